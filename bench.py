@@ -1,0 +1,196 @@
+"""Benchmark of the MI355X MegaMoE layer (one GPU).
+
+Default workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
+one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
+layer forward: router + top-8 + activation cast, dispatch, L1, L2, combine). Also sweeps
+M = 2, 4, 8, 16 and reports each. Before every timed step >= 1 GiB is written so neither
+the 256 MB MALL nor the L2s hold weights; the timed region is the layer alone, with HIP
+events on the stream the layer runs on.
+
+Prints ONE JSON line (the driver contract). Data are synthetic (seeded randn weights of the
+layer's shape, packed on the GPU with the MXFP4 packer).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+E, H, I, TOPK = 384, 3072, 1280, 8
+MXFP4_EXPERT_BYTES = 6266880          # W1 + W2 values + E8M0 scales of one expert
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_weights(torch, seed, n_experts, chunk=32):
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    p1 = torch.empty((n_experts, 2 * I, H // 2), dtype=torch.uint8, device="cuda")
+    s1 = torch.empty((n_experts, 2 * I, H // 32), dtype=torch.uint8, device="cuda")
+    p2 = torch.empty((n_experts, H, I // 2), dtype=torch.uint8, device="cuda")
+    s2 = torch.empty((n_experts, H, I // 32), dtype=torch.uint8, device="cuda")
+    for e0 in range(0, n_experts, chunk):
+        e1 = min(n_experts, e0 + chunk)
+        w = (torch.randn((e1 - e0, 2 * I, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        p1[e0:e1], s1[e0:e1] = qf.quantize_to_mxfp4(w)
+        w = (torch.randn((e1 - e0, H, I), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        p2[e0:e1], s2[e0:e1] = qf.quantize_to_mxfp4(w)
+        del w
+    t = dgm.transform_mxfp4_weights_for_mega_moe_fused((p1, s1), (p2, s2))
+    torch.cuda.synchronize()
+    return t, (p1, s1, p2, s2)
+
+
+def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True):
+    (t1, t2) = weights
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((M, H), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+
+    def layer():
+        dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=force_balanced)
+        dgm.mxfp4_mega_moe_fused(y, t1, t2, buf)
+
+    for _ in range(warmup):
+        flush.fill_(1)
+        layer()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        flush.fill_(1)
+        starts[i].record(stream)
+        layer()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = np.array([s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)])
+    counts = buf.pool_table()[0]
+    n_active = int((counts > 0).sum())
+    ok = bool(torch.isfinite(y.float()).all())
+    return dict(us_median=float(np.median(us)), us_min=float(us.min()), n_active=n_active,
+                weight_bytes=n_active * MXFP4_EXPERT_BYTES, finite=ok, wall_s=wall, y=y)
+
+
+def cpu_baseline(torch_mod, packed, M=8, sample_routes=4, seed=7):
+    """The oracle (numpy fp32 restatement) on the host cores: router + top-8 + cast for the
+    M tokens, then `sample_routes` of the 8*M expert routes (forced-balanced: one route per
+    active expert), weights dequantised once before timing. Scaled to one layer (8*M routes)."""
+    from oracle import moe, numerics as nu
+    p1, s1, p2, s2 = [t.cpu().numpy() for t in packed]
+    rng = np.random.default_rng(seed)
+    x = nu.round_bf16(rng.standard_normal((M, H)).astype(np.float32))
+    rw = nu.round_bf16(rng.standard_normal((E, H)).astype(np.float32) * np.float32(0.02))
+    idx, w = moe.balanced_routing(M, E, TOPK)
+    routes = [(t, s) for t in range(M) for s in range(TOPK)][:sample_routes]
+    W1 = moe.LazyDequant(p1, s1)
+    W2 = moe.LazyDequant(p2, s2)
+    pre = {int(idx[t, s]): (W1[int(idx[t, s])], W2[int(idx[t, s])]) for t, s in routes}
+    reps = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        logits = moe.router_logits_f32(x, rw)
+        moe.topk_softmax(logits, TOPK)
+        codes, sfb, x_dq = moe.quant_act(x, "mxfp8")
+        t_front = time.perf_counter() - t0
+        t1 = time.perf_counter()
+        for t, s in routes:
+            e = int(idx[t, s])
+            sub_idx = np.full_like(idx, -1)
+            sub_idx[t, s] = e
+            moe.moe_forward(x_dq, sub_idx, w, _One(e, pre[e][0]), _One(e, pre[e][1]), 0, "mxfp8")
+        t_routes = time.perf_counter() - t1
+        reps.append(t_front + t_routes * (M * TOPK) / len(routes))
+    return float(np.median(reps)) * 1e6
+
+
+class _One:
+    """W[e] view of a single pre-dequantised expert (others never touched)."""
+
+    def __init__(self, e, w):
+        self.e, self.w = e, w
+        self.shape = (E,) + w.shape
+
+    def __getitem__(self, i):
+        return self.w
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--m", type=int, default=8)
+    ap.add_argument("--act", default="mxfp8", choices=["mxfp8", "mxfp4"])
+    ap.add_argument("--sweep", default="2,4,8,16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (no multi-GPU path)"}))
+        sys.exit(2)
+    import torch
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    torch.cuda.set_device(0)
+    log("building E384 weights ...")
+    weights, packed = build_weights(torch, 1234, E)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(99)
+    router_w = (torch.randn((E, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    sweep = {}
+    for M in sorted(set([int(v) for v in args.sweep.split(",") if v] + [args.m])):
+        r = time_layer(torch, dgm, M, weights, router_w, args.act, args.steps if M == args.m else 10,
+                       args.warmup, 500 + M)
+        gbs = r["weight_bytes"] / (r["us_median"] * 1e-6) / 1e9
+        sweep[M] = dict(us=round(r["us_median"], 2), us_min=round(r["us_min"], 2), active_experts=r["n_active"],
+                        weight_GBps=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4), finite=r["finite"])
+        log(f"M={M}: {sweep[M]}")
+        if M == args.m:
+            main_r = r
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cores = torch.get_num_threads()
+            us = cpu_baseline(torch, [t for t in packed], M=args.m)
+            cpu = dict(value=round(us, 1), unit="us/layer", cores=cores, kind="port",
+                       sample=f"oracle router+top8+cast for M={args.m} and 4 of {8 * args.m} expert routes, "
+                              f"scaled to {8 * args.m} routes; weights pre-dequantised")
+        except Exception as ex:  # reported, never fatal
+            cpu = dict(value=None, unit="us/layer", cores=None, kind="port", sample=f"failed: {ex}")
+    us = main_r["us_median"]
+    achieved = main_r["weight_bytes"] / (us * 1e-6) / 1e9
+    line = {
+        "metric": "us per MoE layer at M=2/4/8/16 (E384 H3072 I1280 top-8); weight HBM GB/s",
+        "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4xmxfp8" if args.act == "mxfp8" else "mxfp4xmxfp4",
+        "data": "synthetic: seeded randn bf16 weights packed to MXFP4 on the GPU, forced-balanced routing",
+        "config": {"workload": f"E384 layer on one GPU, W-MXFP4 x A-{args.act.upper()}, M={args.m}, "
+                               "forced-balanced (BASELINE config 2)",
+                   "M": args.m, "experts": E, "hidden": H, "intermediate": I, "topk": TOPK,
+                   "active_experts": main_r["n_active"], "sweep": sweep, "mall_flush_bytes": 1 << 30},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole layer (frontend + dispatch + L1 + L2 + combine launches)"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,107 @@
+"""ctypes binding of libdgm_megamoe.so (the C ABI declared in include/dgm_megamoe.h).
+
+The library is the product path: there is no CPU fallback. If the shared library is not
+built, or no GPU is present, calls raise instead of computing anything elsewhere.
+"""
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdgm_megamoe.so")
+
+ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1}
+FE_FORCE_BALANCED = 1
+FE_ZERO_ROW_UNROUTED = 2
+
+EXPORTS = [
+    "dgm_version", "dgm_last_error", "dgm_quantize_mxfp4", "dgm_cast_fp4_rows", "dgm_cast_fp8_rows",
+    "dgm_quantize_nvfp4", "dgm_quantize_qoq", "dgm_cast_int8_rows", "dgm_transform_fp4_weights",
+    "dgm_fused_buffer_layout", "dgm_router_topk_launch", "dgm_megamoe_fused_launch",
+    "dgm_device_cu_count", "dgm_probe_mfma_scale",
+]
+
+
+class BufferLayout(ctypes.Structure):
+    _fields_ = [("total_bytes", ctypes.c_size_t), ("x", ctypes.c_size_t), ("x_sf", ctypes.c_size_t),
+                ("topk_idx", ctypes.c_size_t), ("topk_weights", ctypes.c_size_t),
+                ("logits", ctypes.c_size_t), ("pool", ctypes.c_size_t), ("mid", ctypes.c_size_t),
+                ("mid_sf", ctypes.c_size_t), ("partials", ctypes.c_size_t), ("counters", ctypes.c_size_t),
+                ("x_row_bytes", ctypes.c_int32), ("mid_row_bytes", ctypes.c_int32),
+                ("max_routes", ctypes.c_int32)]
+
+
+class MoeArgs(ctypes.Structure):
+    _fields_ = [("num_tokens", ctypes.c_int32), ("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
+                ("num_experts", ctypes.c_int32), ("expert_begin", ctypes.c_int32),
+                ("num_local_experts", ctypes.c_int32), ("topk", ctypes.c_int32),
+                ("act_format", ctypes.c_int32), ("activation_clamp", ctypes.c_float),
+                ("w1_values", ctypes.c_void_p), ("w1_scales", ctypes.c_void_p),
+                ("w2_values", ctypes.c_void_p), ("w2_scales", ctypes.c_void_p),
+                ("recv_stats", ctypes.c_void_p), ("y", ctypes.c_void_p), ("buffer", ctypes.c_void_p),
+                ("layout", ctypes.POINTER(BufferLayout))]
+
+
+_lib = None
+
+
+def load():
+    """Load the shared library (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run `python -m hopper_megamoe_basedondeepgemm_amd.build`")
+    lib = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    sig = {
+        "dgm_version": ([], i32),
+        "dgm_last_error": ([], ctypes.c_char_p),
+        "dgm_quantize_mxfp4": ([vp, i64, i64, i32, vp, vp, vp], i32),
+        "dgm_cast_fp4_rows": ([vp, i64, i64, f32, vp, vp, vp], i32),
+        "dgm_cast_fp8_rows": ([vp, i64, i64, vp, vp, vp], i32),
+        "dgm_quantize_nvfp4": ([vp, i64, i64, vp, vp, vp], i32),
+        "dgm_quantize_qoq": ([vp, i64, i64, vp, vp, vp, vp, vp], i32),
+        "dgm_cast_int8_rows": ([vp, i64, i64, vp, vp, vp], i32),
+        "dgm_transform_fp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
+        "dgm_fused_buffer_layout": ([i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(BufferLayout)], i32),
+        "dgm_router_topk_launch": ([vp, vp, i32, i32, i32, i32, i32, i32, i32, vp,
+                                    ctypes.POINTER(BufferLayout), vp], i32),
+        "dgm_megamoe_fused_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
+        "dgm_device_cu_count": ([], i32),
+        "dgm_probe_mfma_scale": ([vp, vp, vp, vp, vp, i32, i32, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def check(status):
+    if status != 0:
+        msg = load().dgm_last_error().decode(errors="replace")
+        raise RuntimeError(f"dgm error {status}: {msg}")
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("MI355X path: tensors must live on the GPU (no CPU fallback)")
+
+
+def layout(max_tokens, num_experts, num_local_experts, topk, hidden, intermediate, act_format):
+    out = BufferLayout()
+    check(load().dgm_fused_buffer_layout(max_tokens, num_experts, num_local_experts, topk, hidden,
+                                         intermediate, act_format, ctypes.byref(out)))
+    return out

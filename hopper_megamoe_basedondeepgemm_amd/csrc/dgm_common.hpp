@@ -1,0 +1,110 @@
+// Device-side number formats and CDNA4 matrix-core wrappers shared by every kernel.
+// Target: gfx950 (MI355X) only. All helpers are exact integer/bit manipulations or
+// IEEE fp32 operations, so every rounding rule here has a bit-exact CPU counterpart.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DGM_DEV __device__ __forceinline__
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+namespace dgm {
+
+// ---------------------------------------------------------------- bf16
+DGM_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
+DGM_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+DGM_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// ---------------------------------------------------------------- E2M1
+// Midpoint count rule: code = #{b in {.25,.75,1.25,1.75,2.5,3.5,5} : mag > b}; ties go to
+// the smaller magnitude.
+DGM_DEV uint32_t e2m1_mag_code(float a) {
+  return (uint32_t)(a > 0.25f) + (uint32_t)(a > 0.75f) + (uint32_t)(a > 1.25f) +
+         (uint32_t)(a > 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a > 3.5f) + (uint32_t)(a > 5.0f);
+}
+// Activation rule: sign bit only when the magnitude code is non-zero (no -0 code).
+DGM_DEV uint32_t e2m1_ties_down(float x) {
+  uint32_t c = e2m1_mag_code(fabsf(x));
+  return c | ((x < 0.f && c != 0u) ? 8u : 0u);
+}
+// Packer rule: magnitude clamped to 6, sign bit for every negative input (-0 code possible).
+DGM_DEV uint32_t e2m1_bucketize(float x) {
+  uint32_t c = e2m1_mag_code(fminf(fabsf(x), 6.0f));
+  return c | (x < 0.f ? 8u : 0u);
+}
+DGM_DEV float e2m1_value(uint32_t nib) {
+  const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+  float v = mag[nib & 7u];
+  return (nib & 8u) ? -v : v;
+}
+
+// ---------------------------------------------------------------- E8M0
+// Smallest power of two >= |x| by exponent bits, exponent clamped to [1, 254].
+DGM_DEV uint32_t ceil_ue8m0_code(float x) {
+  uint32_t b = __float_as_uint(x) & 0x7fffffffu;
+  uint32_t e = ((b >> 23) & 0xffu) + ((b & 0x7fffffu) != 0u ? 1u : 0u);
+  return e < 1u ? 1u : (e > 254u ? 254u : e);
+}
+DGM_DEV float e8m0_value(uint32_t code) { return __uint_as_float(code << 23); }   // code >= 1
+// 2^(code-127) including code 0 (2^-127, subnormal).
+DGM_DEV float e8m0_value_any(uint32_t code) {
+  return code == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(code << 23);
+}
+// ceil(fp32(log2(x))) with log2 evaluated in double and rounded once to fp32: the
+// behaviour of the log2-based scale rules near powers of two.
+DGM_DEV float ceil_log2_f32(float x) { return ceilf((float)log2((double)x)); }
+
+// ---------------------------------------------------------------- E4M3 (OCP fn)
+// fp32 -> e4m3fn byte, round to nearest even; anything rounding above 448 -> 0x7F (NaN).
+DGM_DEV uint32_t e4m3_encode(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return sign | 0x7fu;
+  float ax = __uint_as_float(a);
+  uint32_t code;
+  if (ax < 0.015625f) {                     // < 2^-6: multiples of 2^-9
+    code = (uint32_t)rintf(ax * 512.0f);
+  } else {
+    int e = (int)(a >> 23) - 127;
+    uint32_t mant = a & 0x7fffffu;
+    uint32_t m3 = mant >> 20, rem = mant & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (m3 & 1u))) m3++;
+    if (m3 == 8u) { m3 = 0u; e++; }
+    int c = ((e + 7) << 3) | (int)m3;
+    code = c > 0x7e ? 0x7fu : (uint32_t)c;
+  }
+  return sign | code;
+}
+
+// ---------------------------------------------------------------- scopes / atomics
+DGM_DEV int atomic_add_acqrel_agent(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+DGM_DEV int atomic_load_acquire_agent(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- matrix cores
+// D(16x16 f32) += A(16x128) * B(128x16) with per-32 E8M0 block scales.
+// fmt: 0 = E4M3, 4 = E2M1. Lane l supplies A row l%16 / B column l%16. E2M1 operands
+// (4 dwords): K = 32*(l/16) .. +32, low nibble first. E4M3 operands (8 dwords): bytes 0-15
+// hold K = 16*(l/16) .. +16 and bytes 16-31 hold K = 64 + 16*(l/16) .. +16. In both cases
+// the scale byte of lane l applies to row/column l%16 over the 32-block K = 32*(l/16) .. +32.
+// Result register i of lane l is D[4*(l/16) + i][l%16]. (Pinned by the probe test.)
+template <int FMT_A, int FMT_B>
+DGM_DEV v4f mfma_scale_16x16x128(v8i a, v8i b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, 0, sb);
+}
+
+}  // namespace dgm

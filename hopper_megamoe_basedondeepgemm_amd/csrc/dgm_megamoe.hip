@@ -1,0 +1,683 @@
+// MegaMoE layer kernels for MI355X (gfx950): router/top-k frontend, dispatch, L1 and L2
+// grouped block-scaled GEMMs on the matrix cores, and the top-k combine.
+//
+// Data layout in HBM (one GPU's share of the EP layer):
+//  * weights: matrix-core fragment order written by dgm_transform_fp4_weights. A 16-row x
+//    128-K tile is 1 KB and lane l of a wave loads bytes [16 l, 16 l + 16) of it with one
+//    16-byte load: the whole wave reads the tile as one contiguous 1 KB run. Per-32 E8M0
+//    scales of 4 consecutive K-tiles sit in one dword per lane.
+//  * activations x: [tokens, H/2] E2M1 (low nibble = even K) or [tokens, H] E4M3, scales
+//    [tokens, H/32]. Routed rows are read in place through the pool table (on one GPU the
+//    per-expert pool is the list of routes; no row copies).
+//  * intermediate (L1 -> L2): [pool row, I/2 | I] codes + [pool row, I/32] scales, pool rows
+//    in (expert asc, token asc, slot asc) order.
+//  * route outputs: fp32 [token * topk + slot, H]; the combine sums valid slots in slot order.
+//
+// Matrix-core use: swap-AB. The weight tile is the 16-row A operand, up to 16 routed tokens
+// form the narrow B operand (one 16-token slab), V_MFMA_SCALE_F32_16X16X128_F8F6F4 applies
+// the E8M0 block scales of both operands in hardware (no dequantisation on the VALU).
+#include "dgm_common.hpp"
+#include "dgm_abi_internal.hpp"
+
+using namespace dgm;
+
+namespace {
+
+struct alignas(16) U4 { uint32_t x, y, z, w; };
+
+DGM_DEV v8i u4_to_v8i(U4 a) { v8i r = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0}; return r; }
+DGM_DEV v8i u8_to_v8i(U4 a, U4 b) {
+  v8i r = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
+  return r;
+}
+
+// ------------------------------------------------------------------ pool table
+struct Pool {
+  int* meta;      // [0] n_active, [1] total routes
+  int* counts;    // [E_local]
+  int* active;    // [n_active] local expert ids, ascending
+  int* offsets;   // [n_active + 1] first pool row of each active expert
+  int* routes;    // [total] route id (token * topk + slot) of each pool row
+};
+
+__host__ __device__ inline size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+__host__ __device__ inline size_t pool_bytes(int E_local, int max_routes) {
+  return 256 + a256((size_t)E_local * 4) * 2 + a256((size_t)(E_local + 1) * 4) + a256((size_t)max_routes * 4);
+}
+
+__host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
+  Pool p;
+  p.meta = (int*)base;
+  p.counts = (int*)(base + 256);
+  p.active = (int*)(base + 256 + a256((size_t)E_local * 4));
+  p.offsets = (int*)(base + 256 + 2 * a256((size_t)E_local * 4));
+  p.routes = (int*)(base + 256 + 2 * a256((size_t)E_local * 4) + a256((size_t)(E_local + 1) * 4));
+  return p;
+}
+
+// ------------------------------------------------------------------ router
+// One wave per (expert, 4-token chunk). Lane l accumulates K = 512 j + 8 l + i (j, then i
+// ascending) with fp32 FMAs of exact bf16 products, then an xor butterfly (32..1) reduces
+// the 64 lane sums. The fixed order makes the fp32 logits reproducible bit for bit.
+template <int J>
+__global__ void __launch_bounds__(256) k_router(const uint16_t* __restrict__ x,
+                                                const uint16_t* __restrict__ w, int M, int E,
+                                                float* __restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t0 = blockIdx.y * 4;
+  if (e >= E) return;
+  constexpr int H = J * 512;
+  U4 wv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const U4*>(w + (size_t)e * H + 512 * j + 8 * lane);
+  U4 xv[4][J];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    int t = t0 + tt < M ? t0 + tt : M - 1;
+#pragma unroll
+    for (int j = 0; j < J; ++j) xv[tt][j] = *reinterpret_cast<const U4*>(x + (size_t)t * H + 512 * j + 8 * lane);
+  }
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      uint32_t xa[4] = {xv[tt][j].x, xv[tt][j].y, xv[tt][j].z, xv[tt][j].w};
+      uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc = fmaf(__uint_as_float(xa[q] << 16), __uint_as_float(wa[q] << 16), acc);
+        acc = fmaf(__uint_as_float(xa[q] & 0xffff0000u), __uint_as_float(wa[q] & 0xffff0000u), acc);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
+    if (lane == 0 && t0 + tt < M) logits[(size_t)(t0 + tt) * E + e] = acc;
+  }
+}
+
+// ------------------------------------------------------------------ top-k + softmax + activation cast
+// One wave per token: keys orderable(bf16(logit)) << 16 | (0xFFFF - e) (-0 -> +0), k rounds
+// of a wave-wide max select; softmax w_k = exp(v_k - v_0) / sum (sequential sum).
+DGM_DEV uint32_t topk_key(float logit, int e) {
+  uint32_t b = f32_to_bf16(logit);
+  if (b == 0x8000u) b = 0u;
+  uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (o << 16) | (0xffffu - (uint32_t)e);
+}
+DGM_DEV float key_value(uint32_t key) {
+  uint32_t o = key >> 16;
+  uint32_t b = (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
+  return bf16_to_f32((uint16_t)b);
+}
+
+__global__ void __launch_bounds__(256) k_select(const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
+                                                int M, int H, int E, int topk, int flags, int token_offset,
+                                                int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= M) return;
+  bool zero_row = false;
+  if (flags & DGM_FE_ZERO_ROW_UNROUTED) {
+    uint32_t any = 0;
+    for (int k = lane; k < H; k += 64) any |= hidden[(size_t)t * H + k] & 0x7fffu;
+    zero_row = !__any(any != 0);
+  }
+  if (zero_row) {
+    if (lane < topk) { topk_idx[(size_t)t * topk + lane] = -1; topk_w[(size_t)t * topk + lane] = 0.f; }
+    return;
+  }
+  if (flags & DGM_FE_FORCE_BALANCED) {
+    if (lane < topk) {
+      int G = E / topk;
+      int g = token_offset + t;
+      topk_idx[(size_t)t * topk + lane] = (int64_t)(lane * G + (g + 7 * lane) % G);
+      topk_w[(size_t)t * topk + lane] = 1.0f / (float)topk;
+    }
+    return;
+  }
+  constexpr int MAXK = 16;   // E <= 1024
+  uint32_t key[MAXK];
+#pragma unroll
+  for (int i = 0; i < MAXK; ++i) {
+    int e = lane + 64 * i;
+    key[i] = e < E ? topk_key(logits[(size_t)t * E + e], e) : 0u;
+  }
+  float vsel[16];
+  int esel[16];
+  for (int k = 0; k < topk; ++k) {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < MAXK; ++i) m = key[i] > m ? key[i] : m;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      uint32_t o = __shfl_xor(m, off);
+      m = o > m ? o : m;
+    }
+#pragma unroll
+    for (int i = 0; i < MAXK; ++i) key[i] = key[i] == m ? 0u : key[i];
+    vsel[k] = key_value(m);
+    esel[k] = (int)(0xffffu - (m & 0xffffu));
+  }
+  if (lane == 0) {
+    float ex[16];
+    float s = 0.f;
+    for (int k = 0; k < topk; ++k) { ex[k] = expf(vsel[k] - vsel[0]); s = s + ex[k]; }
+    for (int k = 0; k < topk; ++k) {
+      topk_idx[(size_t)t * topk + k] = esel[k];
+      topk_w[(size_t)t * topk + k] = ex[k] / s;
+    }
+  }
+}
+
+// Activation cast into the buffer (same rules as dgm_cast_fp4_rows / dgm_cast_fp8_rows):
+// MXFP4 rows with amax floor 1e-30, MXFP8 rows with amax floor 1e-4.
+__global__ void k_cast_act(const uint16_t* __restrict__ x, int64_t groups, int act_format,
+                           uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  float v[32];
+  const U4* p = reinterpret_cast<const U4*>(x + g * 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    U4 r = p[i];
+    uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i * 8 + 2 * j] = __uint_as_float(w[j] << 16);
+      v[i * 8 + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  if (act_format == DGM_ACT_MXFP4) {
+    uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-30f) / 6.0f);
+    float s = e8m0_value(code);
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w |= e2m1_ties_down(v[8 * c + j] / s) << (4 * j);
+      o[c] = w;
+    }
+    reinterpret_cast<U4*>(q)[g] = U4{o[0], o[1], o[2], o[3]};
+    sf[g] = (uint8_t)code;
+  } else {
+    uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-4f) / 448.0f);
+    float inv = 1.0f / e8m0_value(code);
+    uint32_t o[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      uint32_t w = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) w |= e4m3_encode(v[4 * c + b] * inv) << (8 * b);
+      o[c] = w;
+    }
+    U4* d = reinterpret_cast<U4*>(q) + g * 2;
+    d[0] = U4{o[0], o[1], o[2], o[3]};
+    d[1] = U4{o[4], o[5], o[6], o[7]};
+    sf[g] = (uint8_t)code;
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+// One workgroup: per-expert counts, canonical pool order (token asc, slot asc) by rank of
+// the route id among the routes of its expert, exclusive scans over experts, stats update.
+constexpr int DISPATCH_THREADS = 1024;
+constexpr int MAX_ROUTES_DISPATCH = 4096;
+constexpr int MAX_LOCAL_EXPERTS = 1024;
+
+__global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int64_t* __restrict__ topk_idx, int routes_n,
+                                                               int expert_begin, int E_local,
+                                                               uint8_t* __restrict__ pool_base,
+                                                               int* __restrict__ recv_stats) {
+  __shared__ int s_exp[MAX_ROUTES_DISPATCH];
+  __shared__ int s_cnt[MAX_LOCAL_EXPERTS];
+  __shared__ int s_off[MAX_LOCAL_EXPERTS];
+  __shared__ int s_act[MAX_LOCAL_EXPERTS];
+  __shared__ int s_wave[DISPATCH_THREADS / 64][2];
+  Pool P = pool_view(pool_base, E_local);
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E_local; e += DISPATCH_THREADS) s_cnt[e] = 0;
+  for (int r = tid; r < routes_n; r += DISPATCH_THREADS) {
+    int64_t g = topk_idx[r];
+    int64_t l = g - expert_begin;
+    s_exp[r] = (g >= 0 && l >= 0 && l < E_local) ? (int)l : -1;
+  }
+  __syncthreads();
+  for (int r = tid; r < routes_n; r += DISPATCH_THREADS)
+    if (s_exp[r] >= 0) atomicAdd(&s_cnt[s_exp[r]], 1);
+  __syncthreads();
+  // exclusive scans of counts and of the active flags over experts (E_local <= 1024)
+  int c = 0, a = 0;
+  if (tid < E_local) { c = s_cnt[tid]; a = c > 0 ? 1 : 0; }
+  int lane = tid & 63, wv = tid >> 6;
+  int ic = c, ia = a;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int oc = __shfl_up(ic, off), oa = __shfl_up(ia, off);
+    if (lane >= off) { ic += oc; ia += oa; }
+  }
+  if (lane == 63) { s_wave[wv][0] = ic; s_wave[wv][1] = ia; }
+  __syncthreads();
+  int bc = 0, ba = 0;
+  for (int i = 0; i < wv; ++i) { bc += s_wave[i][0]; ba += s_wave[i][1]; }
+  int exc = bc + ic - c, exa = ba + ia - a;
+  if (tid < E_local) {
+    s_off[tid] = exc;
+    P.counts[tid] = c;
+    if (a) { s_act[exa] = tid; P.active[exa] = tid; P.offsets[exa] = exc; }
+    if (recv_stats) recv_stats[tid] += c;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int tot = 0, na = 0;
+    for (int i = 0; i < DISPATCH_THREADS / 64; ++i) { tot += s_wave[i][0]; na += s_wave[i][1]; }
+    P.meta[0] = na;
+    P.meta[1] = tot;
+    P.offsets[na] = tot;
+  }
+  for (int r = tid; r < routes_n; r += DISPATCH_THREADS) {
+    int e = s_exp[r];
+    if (e < 0) continue;
+    int rank = 0;
+    for (int q = 0; q < r; ++q) rank += (s_exp[q] == e) ? 1 : 0;
+    P.routes[s_off[e] + rank] = r;
+  }
+}
+
+// ------------------------------------------------------------------ L1: gate/up + SwiGLU + requant
+// Workgroup = 2 waves; item = (active expert a, 32 intermediate features q). Wave w owns the
+// (gate, up) block pair p = 2q + w (16 features). Both weight tiles of every K-tile are
+// loaded into registers up front (one 1 KB coalesced run per tile), the 16-token B slab is
+// staged once per workgroup in LDS in fragment order, then 2 * KT matrix-core ops run.
+// Epilogue: bf16-round gate/up, clamp, silu(g)*u*w, per-32 requant across the two waves.
+template <int KT, int ACT>
+struct L1Smem {
+  static constexpr int BYTES = ACT == DGM_ACT_MXFP4 ? 16 : 32;
+  static constexpr int KG = (KT + 3) / 4;
+  U4 b[KT][64][BYTES / 16];
+  uint32_t bs[KG][64];
+  float amax[2][16];
+};
+
+template <int KT, int ACT>
+__global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, const uint32_t* __restrict__ w1s,
+                                            const uint8_t* __restrict__ x, const uint8_t* __restrict__ xsf,
+                                            const float* __restrict__ topk_w, uint8_t* __restrict__ pool_base,
+                                            int E_local, int I, int topk, float clamp,
+                                            uint8_t* __restrict__ mid, uint8_t* __restrict__ mid_sf) {
+  constexpr int KG = (KT + 3) / 4;
+  constexpr int XB = ACT == DGM_ACT_MXFP4 ? KT * 64 : KT * 128;   // x row bytes (H/2 or H)
+  constexpr int H = KT * 128;
+  __shared__ L1Smem<KT, ACT> sm;
+  Pool P = pool_view(pool_base, E_local);
+  const int n_active = P.meta[0];
+  const int QN = I / 32;
+  const int NB1 = I / 8;            // 16-row blocks of the 2I-row L1 weight
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int midb = ACT == DGM_ACT_MXFP4 ? I / 2 : I;
+  const int items = n_active * QN;
+  for (int item = blockIdx.x; item < items; item += gridDim.x) {
+    const int a = item / QN, q = item % QN;
+    const int e = P.active[a];
+    const int r0 = P.offsets[a], n = P.offsets[a + 1] - r0;
+    const int p = 2 * q + wv;
+    // ---- A operands: gate tile (block 2p) and up tile (block 2p+1) for every K-tile
+    const uint8_t* gbase = w1v + ((size_t)(e * NB1 + 2 * p) * KT) * 1024 + lane * 16;
+    const uint8_t* ubase = gbase + (size_t)KT * 1024;
+    U4 ag[KT], au[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      ag[kt] = *reinterpret_cast<const U4*>(gbase + kt * 1024);
+      au[kt] = *reinterpret_cast<const U4*>(ubase + kt * 1024);
+    }
+    uint32_t sg[KG], su[KG];
+    const uint32_t* gs = w1s + ((size_t)(e * NB1 + 2 * p) * KG) * 64 + lane;
+#pragma unroll
+    for (int g = 0; g < KG; ++g) { sg[g] = gs[g * 64]; su[g] = gs[(KG + g) * 64]; }
+
+    for (int s0 = 0; s0 < n; s0 += 16) {
+      // ---- stage the B slab (routes s0..s0+15 of this expert) in fragment order
+      __syncthreads();
+      for (int f = threadIdx.x; f < KT * 64; f += 128) {
+        int kt = f >> 6, l = f & 63, c = l & 15;
+        U4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+        if (s0 + c < n) {
+          int t = P.routes[r0 + s0 + c] / topk;
+          if (ACT == DGM_ACT_MXFP4) {
+            v0 = *reinterpret_cast<const U4*>(x + (size_t)t * XB + kt * 64 + (l >> 4) * 16);
+          } else {
+            // E4M3 operand: lane group g holds K = 16 g .. +16 (bytes 0-15) and
+            // K = 64 + 16 g .. +16 (bytes 16-31) of the 128-wide K-tile.
+            const uint8_t* src = x + (size_t)t * XB + kt * 128 + (l >> 4) * 16;
+            v0 = *reinterpret_cast<const U4*>(src);
+            v1 = *reinterpret_cast<const U4*>(src + 64);
+          }
+        }
+        sm.b[kt][l][0] = v0;
+        if (ACT != DGM_ACT_MXFP4) sm.b[kt][l][ACT != DGM_ACT_MXFP4 ? 1 : 0] = v1;
+      }
+      for (int f = threadIdx.x; f < KG * 64; f += 128) {
+        int g = f >> 6, l = f & 63, c = l & 15;
+        uint32_t w = 0x7f7f7f7fu;
+        if (s0 + c < n) {
+          int t = P.routes[r0 + s0 + c] / topk;
+          w = 0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            int kt = 4 * g + j;
+            uint32_t b = kt < KT ? xsf[(size_t)t * (H / 32) + kt * 4 + (l >> 4)] : 127u;
+            w |= b << (8 * j);
+          }
+        }
+        sm.bs[g][l] = w;
+      }
+      __syncthreads();
+      // ---- matrix cores
+      v4f accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        v8i bop;
+        if (ACT == DGM_ACT_MXFP4) bop = u4_to_v8i(sm.b[kt][lane][0]);
+        else bop = u8_to_v8i(sm.b[kt][lane][0], sm.b[kt][lane][ACT != DGM_ACT_MXFP4 ? 1 : 0]);
+        const int sh = 8 * (kt & 3);
+        int sb = (int)(sm.bs[kt >> 2][lane] >> sh);
+        constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;
+        accg = mfma_scale_16x16x128<4, FB>(u4_to_v8i(ag[kt]), bop, accg, (int)(sg[kt >> 2] >> sh), sb);
+        accu = mfma_scale_16x16x128<4, FB>(u4_to_v8i(au[kt]), bop, accu, (int)(su[kt >> 2] >> sh), sb);
+      }
+      // ---- epilogue: lane holds features 16p + 4(l/16) + i for slab column c = l % 16
+      const int c = lane & 15;
+      const bool valid = s0 + c < n;
+      float act[4];
+      float am = 0.f;
+      float wt = 0.f;
+      if (valid) wt = topk_w[P.routes[r0 + s0 + c]];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float g = fminf(round_bf16(accg[i]), clamp);
+        float u = fminf(fmaxf(round_bf16(accu[i]), -clamp), clamp);
+        float sg1 = 1.0f / (1.0f + expf(-g));
+        act[i] = valid ? ((g * sg1) * u) * wt : 0.f;
+        am = fmaxf(am, fabsf(act[i]));
+      }
+      am = fmaxf(am, __shfl_xor(am, 16));
+      am = fmaxf(am, __shfl_xor(am, 32));
+      if (lane < 16) sm.amax[wv][lane] = am;
+      __syncthreads();
+      am = fmaxf(sm.amax[0][c], sm.amax[1][c]);
+      if (valid) {
+        const int row = r0 + s0 + c;
+        const int f0 = 16 * p + 4 * (lane >> 4);
+        if (ACT == DGM_ACT_MXFP4) {
+          uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
+          float s = e8m0_value(code);
+          uint32_t w = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] / s) << (4 * i);
+          *reinterpret_cast<uint16_t*>(mid + (size_t)row * midb + f0 / 2) = (uint16_t)w;
+          if (wv == 0 && lane < 16) mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
+        } else {
+          float ex = ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f);
+          int code = (int)ex + 127;
+          float s = e8m0_value_any((uint32_t)code);
+          uint32_t w = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] / s) << (8 * i);
+          *reinterpret_cast<uint32_t*>(mid + (size_t)row * midb + f0) = w;
+          if (wv == 0 && lane < 16) mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ L2: down projection
+// One wave per item (active expert a, 16 output rows b). A: KT2 tiles in registers; B: the
+// 16-route slab of intermediate rows read straight from L2-resident memory.
+template <int KT, int ACT>
+__global__ void __launch_bounds__(256) k_l2(const uint8_t* __restrict__ w2v, const uint32_t* __restrict__ w2s,
+                                            const uint8_t* __restrict__ mid, const uint8_t* __restrict__ mid_sf,
+                                            uint8_t* __restrict__ pool_base, int E_local, int H,
+                                            float* __restrict__ partials) {
+  constexpr int KG = (KT + 3) / 4;
+  constexpr int I = KT * 128;
+  constexpr int MB = ACT == DGM_ACT_MXFP4 ? I / 2 : I;
+  Pool P = pool_view(pool_base, E_local);
+  const int n_active = P.meta[0];
+  const int NB2 = H / 16;
+  const int lane = threadIdx.x & 63;
+  const int items = n_active * NB2;
+  const int waves = gridDim.x * 4;
+  for (int item = blockIdx.x * 4 + (threadIdx.x >> 6); item < items; item += waves) {
+    const int a = item / NB2, b = item % NB2;
+    const int e = P.active[a];
+    const int r0 = P.offsets[a], n = P.offsets[a + 1] - r0;
+    const uint8_t* base = w2v + ((size_t)(e * NB2 + b) * KT) * 1024 + lane * 16;
+    U4 av[KT];
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) av[kt] = *reinterpret_cast<const U4*>(base + kt * 1024);
+    uint32_t sa[KG];
+    const uint32_t* sp = w2s + ((size_t)(e * NB2 + b) * KG) * 64 + lane;
+#pragma unroll
+    for (int g = 0; g < KG; ++g) sa[g] = sp[g * 64];
+    const int c = lane & 15, kq = lane >> 4;
+    for (int s0 = 0; s0 < n; s0 += 16) {
+      const bool valid = s0 + c < n;
+      const int row = r0 + s0 + (valid ? c : 0);
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        v8i bop;
+        int sb = 127;
+        if (ACT == DGM_ACT_MXFP4) {
+          U4 v = {0, 0, 0, 0};
+          if (valid) v = *reinterpret_cast<const U4*>(mid + (size_t)row * MB + kt * 64 + kq * 16);
+          bop = u4_to_v8i(v);
+        } else {
+          U4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
+          if (valid) {
+            const uint8_t* s = mid + (size_t)row * MB + kt * 128 + kq * 16;
+            v0 = *reinterpret_cast<const U4*>(s);
+            v1 = *reinterpret_cast<const U4*>(s + 64);
+          }
+          bop = u8_to_v8i(v0, v1);
+        }
+        if (valid) sb = mid_sf[(size_t)row * (I / 32) + kt * 4 + kq];
+        constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;
+        acc = mfma_scale_16x16x128<4, FB>(u4_to_v8i(av[kt]), bop, acc, (int)(sa[kt >> 2] >> (8 * (kt & 3))), sb);
+      }
+      if (valid) {
+        const int rid = P.routes[row];
+        float4 o = {acc[0], acc[1], acc[2], acc[3]};
+        *reinterpret_cast<float4*>(partials + (size_t)rid * H + b * 16 + 4 * kq) = o;
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ combine
+// y[t, n] = bf16(sum over valid local slots s ascending of partials[t*topk + s, n]).
+__global__ void k_combine(const float* __restrict__ partials, const int64_t* __restrict__ topk_idx,
+                          int M, int H, int topk, int expert_begin, int E_local, uint16_t* __restrict__ y) {
+  const int t = blockIdx.y;
+  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (t >= M || n >= H) return;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  for (int s = 0; s < topk; ++s) {
+    int64_t g = topk_idx[(size_t)t * topk + s];
+    int64_t l = g - expert_begin;
+    if (g < 0 || l < 0 || l >= E_local) continue;
+    float4 v = *reinterpret_cast<const float4*>(partials + ((size_t)t * topk + s) * H + n);
+    s0 += v.x; s1 += v.y; s2 += v.z; s3 += v.w;
+  }
+  uint32_t lo = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
+  uint32_t hi = (uint32_t)f32_to_bf16(s2) | ((uint32_t)f32_to_bf16(s3) << 16);
+  *reinterpret_cast<uint2*>(y + (size_t)t * H + n) = make_uint2(lo, hi);
+}
+
+int g_cu_count = 0;
+
+int cu_count() {
+  if (g_cu_count == 0) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) == hipSuccess) g_cu_count = prop.multiProcessorCount;
+    if (g_cu_count <= 0) g_cu_count = 256;
+  }
+  return g_cu_count;
+}
+
+template <int KT1, int KT2, int ACT>
+int launch_experts(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, hipStream_t stream) {
+  const int cus = cu_count();
+  uint8_t* pool = buf + L->pool;
+  int items1 = A->num_local_experts * (A->intermediate / 32);
+  int grid1 = items1 < cus * 4 ? items1 : cus * 4;
+  hipLaunchKernelGGL((k_l1<KT1, ACT>), dim3(grid1), dim3(128), 0, stream, (const uint8_t*)A->w1_values,
+                     (const uint32_t*)A->w1_scales, buf + L->x, buf + L->x_sf,
+                     (const float*)(buf + L->topk_weights), pool, A->num_local_experts, A->intermediate,
+                     A->topk, A->activation_clamp, buf + L->mid, buf + L->mid_sf);
+  int st = dgm_last_launch_status();
+  if (st) return st;
+  int items2 = A->num_local_experts * (A->hidden / 16);
+  int grid2 = (items2 + 3) / 4 < cus * 4 ? (items2 + 3) / 4 : cus * 4;
+  hipLaunchKernelGGL((k_l2<KT2, ACT>), dim3(grid2), dim3(256), 0, stream, (const uint8_t*)A->w2_values,
+                     (const uint32_t*)A->w2_scales, buf + L->mid, buf + L->mid_sf, pool, A->num_local_experts,
+                     A->hidden, (float*)(buf + L->partials));
+  return dgm_last_launch_status();
+}
+
+}  // namespace
+
+// ==================================================================== C ABI
+static thread_local char g_err[512];
+void dgm_set_error(const char* msg) {
+  strncpy(g_err, msg, sizeof(g_err) - 1);
+  g_err[sizeof(g_err) - 1] = 0;
+}
+
+extern "C" {
+
+int dgm_version(void) { return 1; }
+const char* dgm_last_error(void) { return g_err; }
+
+int dgm_device_cu_count(void) { return cu_count(); }
+
+int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_experts, int topk,
+                            int hidden, int intermediate, int act_format, DgmBufferLayout* out) {
+  DGM_CHECK_ARG(out != nullptr, "null layout");
+  DGM_CHECK_ARG(max_tokens > 0 && topk > 0 && topk <= 16, "max_tokens > 0, 0 < topk <= 16");
+  DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts in (0, 1024]");
+  DGM_CHECK_ARG(num_local_experts > 0 && num_local_experts <= num_experts, "num_local_experts");
+  DGM_CHECK_ARG(hidden % 512 == 0 && intermediate % 128 == 0, "hidden % 512, intermediate % 128");
+  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8, "act_format");
+  DGM_CHECK_ARG((int64_t)max_tokens * topk <= MAX_ROUTES_DISPATCH, "max_tokens * topk <= 4096");
+  const size_t xb = act_format == DGM_ACT_MXFP4 ? hidden / 2 : hidden;
+  const size_t mb = act_format == DGM_ACT_MXFP4 ? intermediate / 2 : intermediate;
+  const int R = max_tokens * topk;
+  size_t off = 0;
+  memset(out, 0, sizeof(*out));
+  out->x = off; off += dgm_align256((size_t)max_tokens * xb);
+  out->x_sf = off; off += dgm_align256((size_t)max_tokens * (hidden / 32));
+  out->topk_idx = off; off += dgm_align256((size_t)R * 8);
+  out->topk_weights = off; off += dgm_align256((size_t)R * 4);
+  out->logits = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
+  out->pool = off; off += dgm_align256(pool_bytes(num_local_experts, R));
+  out->mid = off; off += dgm_align256((size_t)R * mb);
+  out->mid_sf = off; off += dgm_align256((size_t)R * (intermediate / 32));
+  out->partials = off; off += dgm_align256((size_t)R * hidden * 4);
+  out->counters = off; off += 4096;
+  out->total_bytes = off;
+  out->x_row_bytes = (int32_t)xb;
+  out->mid_row_bytes = (int32_t)mb;
+  out->max_routes = R;
+  return 0;
+}
+
+int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16, int num_tokens,
+                           int hidden, int num_experts, int topk, int act_format, int flags,
+                           int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
+  DGM_CHECK_ARG(hidden_bf16 && router_weight_bf16 && buffer && L, "null pointer");
+  DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
+  DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
+  DGM_CHECK_ARG(num_experts <= 1024, "num_experts <= 1024");
+  DGM_CHECK_ARG(hidden % 512 == 0, "hidden % 512 == 0");
+  DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
+  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8, "act_format");
+  DGM_CHECK_ARG(((uintptr_t)hidden_bf16 & 15) == 0 && ((uintptr_t)router_weight_bf16 & 15) == 0, "16-byte alignment");
+  if (num_tokens == 0) return 0;
+  uint8_t* buf = (uint8_t*)buffer;
+  const int J = hidden / 512;
+  dim3 rg((num_experts + 3) / 4, (num_tokens + 3) / 4);
+  const uint16_t* x = (const uint16_t*)hidden_bf16;
+  const uint16_t* w = (const uint16_t*)router_weight_bf16;
+  float* logits = (float*)(buf + L->logits);
+  switch (J) {
+    case 1: hipLaunchKernelGGL(k_router<1>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
+    case 2: hipLaunchKernelGGL(k_router<2>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
+    case 4: hipLaunchKernelGGL(k_router<4>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
+    case 6: hipLaunchKernelGGL(k_router<6>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
+    case 8: hipLaunchKernelGGL(k_router<8>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
+    default: DGM_CHECK_ARG(false, "hidden must be 512, 1024, 2048, 3072 or 4096");
+  }
+  int st = dgm_last_launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL(k_select, dim3((num_tokens + 3) / 4), dim3(256), 0, stream, x, logits, num_tokens, hidden,
+                     num_experts, topk, flags, token_offset, (int64_t*)(buf + L->topk_idx),
+                     (float*)(buf + L->topk_weights));
+  st = dgm_last_launch_status();
+  if (st) return st;
+  int64_t groups = (int64_t)num_tokens * (hidden / 32);
+  hipLaunchKernelGGL(k_cast_act, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, stream, x, groups, act_format,
+                     buf + L->x, buf + L->x_sf);
+  return dgm_last_launch_status();
+}
+
+int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
+  DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
+  DGM_CHECK_ARG(A->w1_values && A->w1_scales && A->w2_values && A->w2_scales, "null weights");
+  const DgmBufferLayout* L = A->layout;
+  DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
+  DGM_CHECK_ARG(A->num_local_experts > 0 && A->num_local_experts <= MAX_LOCAL_EXPERTS, "num_local_experts");
+  DGM_CHECK_ARG(A->expert_begin >= 0 && A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
+  DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8, "act_format");
+  DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
+  DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 32 == 0, "shape");
+  DGM_CHECK_ARG(A->intermediate % 128 == 0, "intermediate % 128 == 0");
+  if (A->num_tokens == 0) return 0;
+  uint8_t* buf = (uint8_t*)A->buffer;
+  const int routes_n = A->num_tokens * A->topk;
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), 0, stream,
+                     (const int64_t*)(buf + L->topk_idx), routes_n, A->expert_begin, A->num_local_experts,
+                     buf + L->pool, A->recv_stats);
+  int st = dgm_last_launch_status();
+  if (st) return st;
+  const int KT1 = A->hidden / 128, KT2 = A->intermediate / 128;
+  if (KT1 == 24 && KT2 == 10) {
+    st = A->act_format == DGM_ACT_MXFP4 ? launch_experts<24, 10, DGM_ACT_MXFP4>(A, buf, L, stream)
+                                        : launch_experts<24, 10, DGM_ACT_MXFP8>(A, buf, L, stream);
+  } else if (KT1 == 4 && KT2 == 2) {
+    st = A->act_format == DGM_ACT_MXFP4 ? launch_experts<4, 2, DGM_ACT_MXFP4>(A, buf, L, stream)
+                                        : launch_experts<4, 2, DGM_ACT_MXFP8>(A, buf, L, stream);
+  } else if (KT1 == 8 && KT2 == 4) {
+    st = A->act_format == DGM_ACT_MXFP4 ? launch_experts<8, 4, DGM_ACT_MXFP4>(A, buf, L, stream)
+                                        : launch_experts<8, 4, DGM_ACT_MXFP8>(A, buf, L, stream);
+  } else {
+    DGM_CHECK_ARG(false, "supported (hidden, intermediate): (3072, 1280), (512, 256), (1024, 512)");
+  }
+  if (st) return st;
+  dim3 cg((A->hidden / 4 + 255) / 256, A->num_tokens);
+  hipLaunchKernelGGL(k_combine, cg, dim3(256), 0, stream, (const float*)(buf + L->partials),
+                     (const int64_t*)(buf + L->topk_idx), A->num_tokens, A->hidden, A->topk, A->expert_begin,
+                     A->num_local_experts, (uint16_t*)A->y);
+  return dgm_last_launch_status();
+}
+
+}  // extern "C"

@@ -1,0 +1,413 @@
+// Weight packers, activation casts and the weight-layout transform (gfx950).
+//
+// Every kernel restates one reference packer rule bit for bit (citations on each
+// extern "C" entry in include/dgm_megamoe.h). They are memory-bound byte/integer passes:
+// one thread owns one scale group, reads its elements with vector loads and writes the
+// packed bytes with vector stores; no LDS, no matrix cores.
+#include "dgm_common.hpp"
+#include "dgm_abi_internal.hpp"
+
+using namespace dgm;
+
+namespace {
+
+struct alignas(16) U4 { uint32_t x, y, z, w; };
+
+// Load 32 bf16 (64 B) of one group starting at p (16-byte aligned).
+DGM_DEV void load32_bf16(const uint16_t* p, float* v) {
+  const U4* q = reinterpret_cast<const U4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    U4 r = q[i];
+    uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i * 8 + 2 * j] = __uint_as_float(w[j] << 16);
+      v[i * 8 + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+    }
+  }
+}
+
+// Marlin byte order of 8 nibbles n[0..7]: byte b = n[b] << 4 | n[b+4]  -> one u32.
+DGM_DEV uint32_t marlin8(const uint32_t* n) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) w |= ((n[b] << 4) | n[b + 4]) << (8 * b);
+  return w;
+}
+// Low-nibble-first order of 8 nibbles: byte j = n[2j] | n[2j+1] << 4.
+DGM_DEV uint32_t lowfirst8(const uint32_t* n) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w |= (n[2 * j] | (n[2 * j + 1] << 4)) << (8 * j);
+  return w;
+}
+
+// ------------------------------------------------------------------ MXFP4 weight packers
+// rule 0: quantization_mxfp4_fused.quantize_to_mxfp4; rule 1: quantization_mxfp4.quantize_to_mxfp4.
+__global__ void k_quantize_mxfp4(const uint16_t* __restrict__ w, int64_t groups, int rule,
+                                 uint32_t* __restrict__ packed, uint8_t* __restrict__ scale) {
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  float v[32];
+  load32_bf16(w + g * 32, v);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  float sc;
+  uint32_t code;
+  if (rule == 0) {
+    float e = amax > 0.f ? ceil_log2_f32(fmaxf(amax, 1e-38f) / 6.0f) : -127.f;
+    e = fminf(fmaxf(e, -127.f), 127.f);
+    code = (uint32_t)((int)e + 127);
+    sc = e8m0_value_any(code);
+  } else {
+    float d = fminf(fmaxf(fmaxf(amax, 1e-30f) / 6.0f, 0x1p-126f), 0x1p127f);
+    int c = (int)ceil_log2_f32(d) + 127;
+    c = c < 1 ? 1 : (c > 254 ? 254 : c);
+    code = (uint32_t)c;
+    sc = e8m0_value(code);
+  }
+  uint32_t out[4];
+#pragma unroll
+  for (int c8 = 0; c8 < 4; ++c8) {
+    uint32_t n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n[i] = e2m1_bucketize(fminf(fmaxf(v[c8 * 8 + i] / sc, -6.f), 6.f));
+    out[c8] = marlin8(n);
+  }
+  reinterpret_cast<U4*>(packed)[g] = U4{out[0], out[1], out[2], out[3]};
+  scale[g] = (uint8_t)code;
+}
+
+// ------------------------------------------------------------------ row casts (activations)
+// MXFP4 rows: amax >= floor, sf = ceil_ue8m0(amax/6), ties-down E2M1 of x/sf, low-nibble-first.
+__global__ void k_cast_fp4_rows(const uint16_t* __restrict__ x, int64_t groups, float amax_floor,
+                                uint32_t* __restrict__ packed, uint8_t* __restrict__ sf) {
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  float v[32];
+  load32_bf16(x + g * 32, v);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  uint32_t code = ceil_ue8m0_code(fmaxf(amax, amax_floor) / 6.0f);
+  float s = e8m0_value(code);
+  uint32_t out[4];
+#pragma unroll
+  for (int c8 = 0; c8 < 4; ++c8) {
+    uint32_t n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n[i] = e2m1_ties_down(v[c8 * 8 + i] / s);
+    out[c8] = lowfirst8(n);
+  }
+  reinterpret_cast<U4*>(packed)[g] = U4{out[0], out[1], out[2], out[3]};
+  sf[g] = (uint8_t)code;
+}
+
+// MXFP8 rows: amax >= 1e-4, sf = ceil_ue8m0(amax/448), e4m3(x * (1/sf)).
+__global__ void k_cast_fp8_rows(const uint16_t* __restrict__ x, int64_t groups,
+                                uint32_t* __restrict__ q, uint8_t* __restrict__ sf) {
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  float v[32];
+  load32_bf16(x + g * 32, v);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-4f) / 448.0f);
+  float inv = 1.0f / e8m0_value(code);
+  uint32_t out[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) w |= e4m3_encode(v[j * 4 + b] * inv) << (8 * b);
+    out[j] = w;
+  }
+  U4* dst = reinterpret_cast<U4*>(q) + g * 2;
+  dst[0] = U4{out[0], out[1], out[2], out[3]};
+  dst[1] = U4{out[4], out[5], out[6], out[7]};
+  sf[g] = (uint8_t)code;
+}
+
+// ------------------------------------------------------------------ NVFP4 packer
+DGM_DEV uint32_t ue4m3_ceil(float x) {
+  x = fminf(fmaxf(x, 0x1p-9f), 448.0f);
+  int den = (int)ceilf(x / 0x1p-9f);
+  den = den < 1 ? 1 : (den > 7 ? 7 : den);
+  float xn = fmaxf(x, 0x1p-6f);
+  float e = floorf((float)log2((double)xn));
+  int eb = (int)e + 7;
+  float base = exp2f(e);
+  float t = (xn / base - 1.0f) * 8.0f - 1e-6f;
+  int mant = (int)ceilf(t);
+  if (mant > 7) { eb += 1; mant = 0; }
+  mant = mant < 0 ? 0 : (mant > 7 ? 7 : mant);
+  int normal = eb * 8 + mant;
+  normal = normal < 8 ? 8 : (normal > 0x7e ? 0x7e : normal);
+  return x <= 7.0f * 0x1p-9f ? (uint32_t)den : (uint32_t)normal;
+}
+DGM_DEV float ue4m3_value(uint32_t c) {
+  c &= 0x7fu;
+  uint32_t eb = c >> 3, m = c & 7u;
+  if (c == 0x7fu) return 448.0f;
+  if (eb == 0) return (float)m * 0x1p-9f;
+  return (1.0f + (float)m * 0.125f) * exp2f((float)((int)eb - 7));
+}
+
+__global__ void k_quantize_nvfp4(const uint16_t* __restrict__ w, int64_t groups16,
+                                 uint32_t* __restrict__ packed, uint8_t* __restrict__ scale) {
+  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= groups16) return;
+  float v[32];
+  // 16 elements: load 32 B
+  const U4* q = reinterpret_cast<const U4*>(w + g * 16);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    U4 r = q[i];
+    uint32_t ww[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i * 8 + 2 * j] = __uint_as_float(ww[j] << 16);
+      v[i * 8 + 2 * j + 1] = __uint_as_float(ww[j] & 0xffff0000u);
+    }
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  uint32_t code = ue4m3_ceil(fmaxf(amax, 1e-30f) / 6.0f);
+  float s = ue4m3_value(code);
+  uint32_t out[2];
+#pragma unroll
+  for (int c8 = 0; c8 < 2; ++c8) {
+    uint32_t n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n[i] = e2m1_bucketize(fminf(fmaxf(v[c8 * 8 + i] / s, -6.f), 6.f));
+    out[c8] = marlin8(n);
+  }
+  packed[g * 2] = out[0];
+  packed[g * 2 + 1] = out[1];
+  scale[g] = (uint8_t)code;
+}
+
+// ------------------------------------------------------------------ QoQ W4A8 packer
+// One wave per weight row: row amax -> s1 (bf16), then lane-per-K128-group codes.
+__global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int K,
+                               uint8_t* __restrict__ packed, uint8_t* __restrict__ s2o,
+                               uint8_t* __restrict__ zo, float* __restrict__ s1o) {
+  int lane = threadIdx.x & 63;
+  int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* src = w + row * K;
+  float amax = 0.f;
+  for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(src[k])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  float s1 = round_bf16(fmaxf(amax / 120.0f, 1e-30f));
+  if (lane == 0) s1o[row] = s1;
+  int G = K / 128;
+  for (int g = lane; g < G; g += 64) {
+    const uint16_t* p = src + g * 128;
+    float mn = 1e30f, mx = -1e30f;
+    for (int i = 0; i < 128; ++i) {
+      float w8 = fminf(fmaxf(rintf(bf16_to_f32(p[i]) / s1), -112.f), 112.f);
+      mn = fminf(mn, w8);
+      mx = fmaxf(mx, w8);
+    }
+    float s2 = fminf(fmaxf(ceilf((mx - mn) / 15.0f), 1.f), 15.f);
+    float z = fminf(fmaxf(rintf(-mn / s2), 0.f), 15.f);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * (K / 2) + g * 64);
+    for (int c8 = 0; c8 < 16; ++c8) {
+      uint32_t n[8];
+      for (int i = 0; i < 8; ++i) {
+        float w8 = fminf(fmaxf(rintf(bf16_to_f32(p[c8 * 8 + i]) / s1), -112.f), 112.f);
+        n[i] = (uint32_t)fminf(fmaxf(rintf(w8 / s2 + z), 0.f), 15.f);
+      }
+      dst[c8] = marlin8(n);
+    }
+    s2o[row * G + g] = (uint8_t)s2;
+    zo[row * G + g] = (uint8_t)z;
+  }
+}
+
+// Per-token int8: sf = max(amax, 1e-30)/127, q = clamp(rne(x/sf), +-127). One wave per row.
+__global__ void k_cast_int8_rows(const uint16_t* __restrict__ x, int64_t rows, int K,
+                                 int8_t* __restrict__ q, float* __restrict__ sf) {
+  int lane = threadIdx.x & 63;
+  int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* src = x + row * K;
+  float amax = 0.f;
+  for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(src[k])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  float s = fmaxf(amax, 1e-30f) / 127.0f;
+  if (lane == 0) sf[row] = s;
+  for (int k = lane; k < K; k += 64)
+    q[row * K + k] = (int8_t)fminf(fmaxf(rintf(bf16_to_f32(src[k]) / s), -127.f), 127.f);
+}
+
+// ------------------------------------------------------------------ FP4 weight-layout transform
+// Source: packed [E][N][K/2] (Marlin or low-first order), scale [E][N][K/32] E8M0 bytes.
+// Destination (matrix-core fragment order, see dgm_layout in dgm_abi_internal.hpp):
+//   values [E][N/16][K/128][64 lanes][16 B]: lane l = row l%16 of the 16-row block,
+//          K = 128*kt + 32*(l/16) .. +32, byte j = K[2j] | K[2j+1] << 4.
+//   scales [E][N/16][ceil(K/512)][64 lanes][4 B]: byte j = scale of K-tile 4*g + j.
+// l1_interleave: native block q holds gate rows 16*(q/2).. (q even) or up rows
+// N/2 + 16*(q/2).. (q odd), so a (gate, up) pair of blocks covers the same 16 features.
+__global__ void k_transform_fp4(const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
+                                int E, int N, int K, int src_order, int l1_interleave,
+                                uint8_t* __restrict__ dst, uint8_t* __restrict__ sdst) {
+  int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int KT = K / 128, NB = N / 16, KG = (KT + 3) / 4;
+  int64_t total = (int64_t)E * NB * KT * 64;
+  if (tid >= total) return;
+  int lane = (int)(tid & 63);
+  int64_t t = tid >> 6;
+  int kt = (int)(t % KT); t /= KT;
+  int q = (int)(t % NB);
+  int e = (int)(t / NB);
+  int r = lane & 15, kq = lane >> 4;
+  int src_row;
+  if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
+  else src_row = 16 * q + r;
+  const uint8_t* s = src + ((int64_t)e * N + src_row) * (K / 2) + kt * 64 + kq * 16;
+  U4 in = *reinterpret_cast<const U4*>(s);
+  uint32_t w[4] = {in.x, in.y, in.z, in.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint32_t n[8];
+    if (src_order == 0) {        // Marlin: byte b = K[b] << 4 | K[b+4]
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        uint32_t byte = (w[c] >> (8 * b)) & 0xffu;
+        n[b] = byte >> 4;
+        n[b + 4] = byte & 0xfu;
+      }
+      o[c] = lowfirst8(n);
+    } else {
+      o[c] = w[c];
+    }
+  }
+  int64_t tile = ((int64_t)e * NB + q) * KT + kt;
+  *reinterpret_cast<U4*>(dst + tile * 1024 + lane * 16) = U4{o[0], o[1], o[2], o[3]};
+  uint8_t sc = ssrc[((int64_t)e * N + src_row) * (K / 32) + kt * 4 + kq];
+  sdst[((((int64_t)e * NB + q) * KG + kt / 4) * 64 + lane) * 4 + (kt & 3)] = sc;
+}
+
+// Fill the padding bytes of the last scale group (K-tiles KT..4*KG-1) with 127 (= 2^0).
+__global__ void k_fill_scale_pad(uint8_t* sdst, int64_t blocks, int KT, int KG) {
+  int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int pad = KG * 4 - KT;
+  if (pad == 0) return;
+  int64_t total = blocks * 64 * pad;
+  if (tid >= total) return;
+  int p = (int)(tid % pad);
+  int64_t t = tid / pad;
+  int lane = (int)(t & 63);
+  int64_t b = t >> 6;
+  int kt = KT + p;
+  sdst[((b * KG + kt / 4) * 64 + lane) * 4 + (kt & 3)] = 127;
+}
+
+inline int grid_for(int64_t n, int bs) { return (int)((n + bs - 1) / bs); }
+
+}  // namespace
+
+// ==================================================================== C ABI
+extern "C" {
+
+int dgm_quantize_mxfp4(const void* w_bf16, int64_t rows, int64_t K, int rule,
+                       void* packed, void* scale_e8m0, hipStream_t stream) {
+  DGM_CHECK_ARG(w_bf16 && packed && scale_e8m0, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 32 == 0, "K must be a positive multiple of 32");
+  DGM_CHECK_ARG(rule == 0 || rule == 1, "rule must be 0 (fused) or 1 (split)");
+  DGM_CHECK_ARG(((uintptr_t)w_bf16 & 15) == 0 && ((uintptr_t)packed & 15) == 0, "16-byte alignment");
+  int64_t groups = rows * (K / 32);
+  if (groups == 0) return 0;
+  hipLaunchKernelGGL(k_quantize_mxfp4, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
+                     (const uint16_t*)w_bf16, groups, rule, (uint32_t*)packed, (uint8_t*)scale_e8m0);
+  return dgm_last_launch_status();
+}
+
+int dgm_cast_fp4_rows(const void* x_bf16, int64_t rows, int64_t K, float amax_floor,
+                      void* packed, void* sf_e8m0, hipStream_t stream) {
+  DGM_CHECK_ARG(x_bf16 && packed && sf_e8m0, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 32 == 0, "K must be a positive multiple of 32");
+  DGM_CHECK_ARG(((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)packed & 15) == 0, "16-byte alignment");
+  int64_t groups = rows * (K / 32);
+  if (groups == 0) return 0;
+  hipLaunchKernelGGL(k_cast_fp4_rows, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
+                     (const uint16_t*)x_bf16, groups, amax_floor, (uint32_t*)packed, (uint8_t*)sf_e8m0);
+  return dgm_last_launch_status();
+}
+
+int dgm_cast_fp8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_e4m3, void* sf_e8m0,
+                      hipStream_t stream) {
+  DGM_CHECK_ARG(x_bf16 && q_e4m3 && sf_e8m0, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 32 == 0, "K must be a positive multiple of 32");
+  DGM_CHECK_ARG(((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)q_e4m3 & 15) == 0, "16-byte alignment");
+  int64_t groups = rows * (K / 32);
+  if (groups == 0) return 0;
+  hipLaunchKernelGGL(k_cast_fp8_rows, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
+                     (const uint16_t*)x_bf16, groups, (uint32_t*)q_e4m3, (uint8_t*)sf_e8m0);
+  return dgm_last_launch_status();
+}
+
+int dgm_quantize_nvfp4(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* scale_ue4m3,
+                       hipStream_t stream) {
+  DGM_CHECK_ARG(w_bf16 && packed && scale_ue4m3, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 16 == 0, "K must be a positive multiple of 16");
+  DGM_CHECK_ARG(((uintptr_t)w_bf16 & 15) == 0 && ((uintptr_t)packed & 7) == 0, "alignment");
+  int64_t groups = rows * (K / 16);
+  if (groups == 0) return 0;
+  hipLaunchKernelGGL(k_quantize_nvfp4, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
+                     (const uint16_t*)w_bf16, groups, (uint32_t*)packed, (uint8_t*)scale_ue4m3);
+  return dgm_last_launch_status();
+}
+
+int dgm_quantize_qoq(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* s2, void* z,
+                     void* s1_f32, hipStream_t stream) {
+  DGM_CHECK_ARG(w_bf16 && packed && s2 && z && s1_f32, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 128 == 0, "K must be a positive multiple of 128");
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(k_quantize_qoq, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
+                     (const uint16_t*)w_bf16, rows, (int)K, (uint8_t*)packed, (uint8_t*)s2,
+                     (uint8_t*)z, (float*)s1_f32);
+  return dgm_last_launch_status();
+}
+
+int dgm_cast_int8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_i8, void* sf_f32,
+                       hipStream_t stream) {
+  DGM_CHECK_ARG(x_bf16 && q_i8 && sf_f32, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0, "bad shape");
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(k_cast_int8_rows, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
+                     (const uint16_t*)x_bf16, rows, (int)K, (int8_t*)q_i8, (float*)sf_f32);
+  return dgm_last_launch_status();
+}
+
+int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E, int N, int K,
+                              int src_order, int l1_interleave, void* dst_values, void* dst_scales,
+                              hipStream_t stream) {
+  DGM_CHECK_ARG(packed && scale_e8m0 && dst_values && dst_scales, "null pointer");
+  DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 32 == 0 && K % 128 == 0, "N % 32, K % 128");
+  DGM_CHECK_ARG(src_order == 0 || src_order == 1, "src_order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(((uintptr_t)packed & 15) == 0 && ((uintptr_t)dst_values & 15) == 0, "16-byte alignment");
+  int KT = K / 128, NB = N / 16, KG = (KT + 3) / 4;
+  int64_t total = (int64_t)E * NB * KT * 64;
+  hipLaunchKernelGGL(k_transform_fp4, dim3(grid_for(total, 256)), dim3(256), 0, stream,
+                     (const uint8_t*)packed, (const uint8_t*)scale_e8m0, E, N, K, src_order,
+                     l1_interleave, (uint8_t*)dst_values, (uint8_t*)dst_scales);
+  int st = dgm_last_launch_status();
+  if (st) return st;
+  int64_t pad_total = (int64_t)E * NB * 64 * (KG * 4 - KT);
+  if (pad_total > 0)
+    hipLaunchKernelGGL(k_fill_scale_pad, dim3(grid_for(pad_total, 256)), dim3(256), 0, stream,
+                       (uint8_t*)dst_scales, (int64_t)E * NB, KT, KG);
+  return dgm_last_launch_status();
+}
+
+}  // extern "C"

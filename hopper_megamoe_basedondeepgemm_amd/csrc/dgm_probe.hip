@@ -1,0 +1,31 @@
+// Diagnostic: one block-scaled matrix-core op on caller-provided lane fragments, so the
+// tests can check the lane layout the kernels assume (A row l%16 / B column l%16, K chunk
+// 32*(l/16), scale byte of that 32-block; D[4*(l/16)+i][l%16] in result register i).
+#include "dgm_common.hpp"
+#include "dgm_abi_internal.hpp"
+
+using namespace dgm;
+
+template <int FA, int FB>
+__global__ void k_probe(const v8i* a, const v8i* b, const int* sa, const int* sb, float* out) {
+  int l = threadIdx.x;
+  v4f c = {0.f, 0.f, 0.f, 0.f};
+  c = mfma_scale_16x16x128<FA, FB>(a[l], b[l], c, sa[l], sb[l]);
+  for (int i = 0; i < 4; ++i) out[l * 4 + i] = c[i];
+}
+
+extern "C" int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const void* sb,
+                                    void* out, int fmt_a, int fmt_b, hipStream_t stream) {
+  DGM_CHECK_ARG(a && b && sa && sb && out, "null pointer");
+  const v8i* A = (const v8i*)a;
+  const v8i* B = (const v8i*)b;
+  if (fmt_a == 4 && fmt_b == 4)
+    hipLaunchKernelGGL((k_probe<4, 4>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out);
+  else if (fmt_a == 4 && fmt_b == 0)
+    hipLaunchKernelGGL((k_probe<4, 0>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out);
+  else if (fmt_a == 0 && fmt_b == 0)
+    hipLaunchKernelGGL((k_probe<0, 0>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out);
+  else
+    DGM_CHECK_ARG(false, "fmt pairs (4,4), (4,0), (0,0)");
+  return dgm_last_launch_status();
+}

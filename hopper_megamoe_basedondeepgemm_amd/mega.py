@@ -1,0 +1,214 @@
+"""MegaMoE Python API on MI355X: buffers, weight transforms, frontend and the fused layer.
+
+Mirrors the reference entry points (deep_gemm/mega/fused.py, deep_gemm/mega/__init__.py)
+with the same names and argument meaning. ``group=None`` means one GPU. Work runs in the
+HIP library (libdgm_megamoe.so) on the current torch stream; nothing here computes.
+"""
+import ctypes
+import os
+import types
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+
+# ----------------------------------------------------------------------------- buffer
+class FusedSymmBuffer:
+    """Single-process counterpart of deep_gemm/mega/fused.py:79 ``FusedSymmBuffer``.
+
+    One device allocation holds every view the layer uses. On one GPU no symmetric memory
+    or rendezvous is needed; ``ep_size`` / ``ep_rank`` select which expert-parallel share
+    the layer computes (local experts ``[ep_rank * E / ep_size, (ep_rank + 1) * E / ep_size)``),
+    so one GPU can run exactly one rank's share of an EP layer.
+
+    Views: x, x_sf, topk_idx, topk_weights (frontend outputs / layer inputs), l1_acts and
+    l1_acts_sf (aliases of x / x_sf: routed rows are read in place), l2_acts / l2_acts_sf
+    (L1 -> L2 activations in pool order), combine_partials (fp32 [tokens, topk, H] route
+    outputs), logits (fp32 router logits) and pool (dispatch table, int32)."""
+
+    def __init__(self, group, num_experts, max_tokens, topk, hidden, intermediate,
+                 act_format="mxfp4", ep_size=None, ep_rank=None, device=None):
+        if group is not None:
+            ep_size = group.size() if ep_size is None else ep_size
+            ep_rank = group.rank() if ep_rank is None else ep_rank
+        ep_size = 1 if ep_size is None else int(ep_size)
+        ep_rank = 0 if ep_rank is None else int(ep_rank)
+        assert num_experts % ep_size == 0 and 0 <= ep_rank < ep_size
+        self.group = group
+        self.num_experts = num_experts
+        self.num_max_tokens_per_rank = max_tokens
+        self.num_topk = topk
+        self.hidden = hidden
+        self.intermediate_hidden = intermediate
+        self.act_format = act_format
+        self.act_code = _lib.ACT_FORMATS[act_format]
+        self.ep_size, self.ep_rank = ep_size, ep_rank
+        self.num_local_experts = num_experts // ep_size
+        self.expert_begin = ep_rank * self.num_local_experts
+        self.layout = _lib.layout(max_tokens, num_experts, self.num_local_experts, topk, hidden,
+                                  intermediate, self.act_code)
+        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.buffer = torch.zeros(self.layout.total_bytes, dtype=torch.uint8, device=dev)
+        L, b = self.layout, self.buffer
+        R = max_tokens * topk
+
+        def view(off, n, dtype, shape):
+            return b[off:off + n * torch.tensor([], dtype=dtype).element_size()].view(dtype).view(*shape)
+
+        xb = L.x_row_bytes
+        self.x = view(L.x, max_tokens * xb, torch.uint8, (max_tokens, xb))
+        self.x_sf = view(L.x_sf, max_tokens * (hidden // 32), torch.uint8, (max_tokens, hidden // 32))
+        self.topk_idx = view(L.topk_idx, R, torch.int64, (max_tokens, topk))
+        self.topk_weights = view(L.topk_weights, R, torch.float32, (max_tokens, topk))
+        self.logits = view(L.logits, max_tokens * num_experts, torch.float32, (max_tokens, num_experts))
+        mb = L.mid_row_bytes
+        self.l2_acts = view(L.mid, R * mb, torch.uint8, (R, mb))
+        self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 32), torch.uint8, (R, intermediate // 32))
+        self.combine_partials = view(L.partials, R * hidden, torch.float32, (max_tokens, topk, hidden))
+        self.l1_acts, self.l1_acts_sf = self.x, self.x_sf
+        self.handle = types.SimpleNamespace(buffer_ptrs=[b.data_ptr()])
+
+    def pool_table(self):
+        """(counts [E_local], active experts, offsets [n_active+1], routes [total]) as CPU
+        tensors, read back from the device dispatch table."""
+        E = self.num_local_experts
+        a256 = lambda v: (v + 255) // 256 * 256
+        base = self.layout.pool
+        raw = self.buffer[base:base + 256 + 2 * a256(E * 4) + a256((E + 1) * 4) +
+                          a256(self.num_max_tokens_per_rank * self.num_topk * 4)].cpu()
+        meta = raw[:256].view(torch.int32)
+        n_active, total = int(meta[0]), int(meta[1])
+        o = 256
+        counts = raw[o:o + 4 * E].view(torch.int32).clone(); o += a256(E * 4)
+        active = raw[o:o + 4 * n_active].view(torch.int32).clone(); o += a256(E * 4)
+        offsets = raw[o:o + 4 * (n_active + 1)].view(torch.int32).clone(); o += a256((E + 1) * 4)
+        routes = raw[o:o + 4 * total].view(torch.int32).clone()
+        return counts, active, offsets, routes
+
+    def destroy(self):
+        self.buffer = None
+        self.handle = None
+        self.group = None
+
+
+def get_fused_symm_buffer_for_mega_moe(group, num_experts, max_tokens, topk, hidden, intermediate,
+                                       act_format="mxfp4", ep_size=None, ep_rank=None):
+    """deep_gemm/mega/fused.py:88 (``group=None`` -> one GPU)."""
+    return FusedSymmBuffer(group, num_experts, max_tokens, topk, hidden, intermediate, act_format,
+                           ep_size=ep_size, ep_rank=ep_rank)
+
+
+# ----------------------------------------------------------------------------- weight transform
+def _transform_one(packed, scale, l1_interleave, src_order):
+    _lib.require_gpu(packed, scale)
+    assert packed.dtype == torch.uint8 and scale.dtype == torch.uint8 and packed.dim() == 3
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert scale.shape == (E, N, K // 32)
+    KT, NB = K // 128, N // 16
+    KG = (KT + 3) // 4
+    vals = torch.empty((E, NB, KT, 64, 16), dtype=torch.uint8, device=packed.device)
+    scl = torch.empty((E, NB, KG, 64, 4), dtype=torch.uint8, device=packed.device)
+    _lib.check(_lib.load().dgm_transform_fp4_weights(
+        _lib.ptr(packed.contiguous()), _lib.ptr(scale.contiguous()), E, N, K, src_order,
+        int(l1_interleave), _lib.ptr(vals), _lib.ptr(scl), _lib.stream()))
+    return vals, scl, None
+
+
+def transform_mxfp4_weights_for_mega_moe_fused(l1, l2, src_order="marlin"):
+    """deep_gemm/mega/fused.py:64. Inputs: ``(packed [E, 2I, H/2], scale_e8m0 [E, 2I, H/32])``
+    and ``(packed [E, H, I/2], scale [E, H, I/32])`` from ``quantize_to_mxfp4`` (Marlin order;
+    ``src_order="low_first"`` accepts OCP low-nibble-first packing). Returns
+    ``((w1_values, w1_scales, None), (w2_values, w2_scales, None))`` in matrix-core fragment
+    order; the third item (the reference's per-row 2^e_ref) is None because the E8M0 scales
+    are applied exactly by the matrix cores. Invariant kept from the reference:
+    dequant(transform(q)) == interleave(dequant(q))."""
+    so = {"marlin": 0, "low_first": 1}[src_order]
+    return _transform_one(l1[0], l1[1], True, so), _transform_one(l2[0], l2[1], False, so)
+
+
+def transform_weights_for_mega_moe(l1, l2):
+    """sm100_b200 style inputs (low-nibble-first packing from per_token_cast_to_fp4)."""
+    return transform_mxfp4_weights_for_mega_moe_fused(l1, l2, src_order="low_first")
+
+
+# ----------------------------------------------------------------------------- frontend
+def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.Tensor, sym_buffer,
+                                     quant: Optional[str] = None, stamps=None, l2_persist=None,
+                                     wlayout=None, select_in_mega=None, zero_row_unrouted=None,
+                                     force_balanced=None, token_offset: int = 0):
+    """deep_gemm/mega/__init__.py:671: router GEMV (bf16 in, fp32 accumulate, bf16 logits) ->
+    top-k (value desc, index asc) -> fp32 softmax of the k logits -> activation cast into
+    ``sym_buffer.x / x_sf / topk_idx / topk_weights``. ``quant`` defaults to the buffer's
+    activation format. ``force_balanced`` (env DG_FE_FORCE_BALANCED) replaces the routing by
+    the forced-balanced rule after the router ran; ``zero_row_unrouted`` (env
+    DG_FE_ZERO_ROW_UNROUTED, default 1) leaves all-zero rows unrouted. ``stamps``,
+    ``l2_persist`` and ``wlayout`` are H20 tuning knobs with no effect here."""
+    b = sym_buffer
+    _lib.require_gpu(hidden, router_weight)
+    assert hidden.dtype == torch.bfloat16 and router_weight.dtype == torch.bfloat16
+    m, h = hidden.shape
+    e = router_weight.size(0)
+    assert h == b.hidden and e == b.num_experts and router_weight.size(1) == h
+    assert m <= b.num_max_tokens_per_rank
+    if quant is not None and quant != b.act_format:
+        raise ValueError(f"buffer was sized for {b.act_format!r}, got quant={quant!r}")
+    if force_balanced is None:
+        force_balanced = os.environ.get("DG_FE_FORCE_BALANCED", "0") == "1"
+    if zero_row_unrouted is None:
+        zero_row_unrouted = os.environ.get("DG_FE_ZERO_ROW_UNROUTED", "1") == "1"
+    flags = (_lib.FE_FORCE_BALANCED if force_balanced else 0) | \
+            (_lib.FE_ZERO_ROW_UNROUTED if zero_row_unrouted else 0)
+    hidden = hidden.contiguous()
+    router_weight = router_weight.contiguous()
+    _lib.check(_lib.load().dgm_router_topk_launch(
+        _lib.ptr(hidden), _lib.ptr(router_weight), m, h, e, b.num_topk, b.act_code, flags,
+        int(token_offset), _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
+
+
+# ----------------------------------------------------------------------------- fused layer
+def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None):
+    w1, sf1, _ = l1
+    w2, sf2, _ = l2
+    _lib.require_gpu(y, w1, sf1, w2, sf2, stats)
+    assert y.dtype == torch.bfloat16 and y.is_contiguous() and y.size(1) == b.hidden
+    m = y.size(0) if num_tokens is None else num_tokens
+    assert m <= b.num_max_tokens_per_rank
+    E_l, H, I = b.num_local_experts, b.hidden, b.intermediate_hidden
+    kg = lambda k: (k // 128 + 3) // 4
+    assert tuple(w1.shape) == (E_l, 2 * I // 16, H // 128, 64, 16) and w1.dtype == torch.uint8, w1.shape
+    assert tuple(sf1.shape) == (E_l, 2 * I // 16, kg(H), 64, 4) and sf1.dtype == torch.uint8, sf1.shape
+    assert tuple(w2.shape) == (E_l, H // 16, I // 128, 64, 16) and w2.dtype == torch.uint8, w2.shape
+    assert tuple(sf2.shape) == (E_l, H // 16, kg(I), 64, 4) and sf2.dtype == torch.uint8, sf2.shape
+    assert all(t.is_contiguous() for t in (w1, sf1, w2, sf2))
+    if stats is not None:
+        assert stats.dtype == torch.int32 and stats.numel() == E_l
+    args = _lib.MoeArgs(num_tokens=m, hidden=b.hidden, intermediate=b.intermediate_hidden,
+                        num_experts=b.num_experts, expert_begin=b.expert_begin, num_local_experts=E_l,
+                        topk=b.num_topk, act_format=b.act_code,
+                        activation_clamp=float(activation_clamp if activation_clamp is not None else 3.0e38),
+                        w1_values=w1.data_ptr(), w1_scales=sf1.data_ptr(), w2_values=w2.data_ptr(),
+                        w2_scales=sf2.data_ptr(), recv_stats=stats.data_ptr() if stats is not None else None,
+                        y=y.data_ptr(), buffer=b.buffer.data_ptr(), layout=ctypes.pointer(b.layout))
+    _lib.check(_lib.load().dgm_megamoe_fused_launch(ctypes.byref(args), _lib.stream()))
+
+
+def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
+                         fast_math=True, phase_stamps=None, fe_keys=None):
+    """deep_gemm/mega/fused.py:97: the layer over the routing and activations already in the
+    buffer (written by ``fable_router_quant_topk_frontend`` or by the caller): dispatch,
+    L1 + SwiGLU + requant, L2, top-k combine into ``y`` (bf16 [tokens, H]).
+    ``fast_math`` / ``phase_stamps`` / ``fe_keys`` are accepted for signature compatibility."""
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp)
+
+
+def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
+                             cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
+                             force_balanced=None, token_offset=0, **_):
+    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states."""
+    fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
+                                     token_offset=token_offset)
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp)
+    return y

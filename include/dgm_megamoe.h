@@ -1,0 +1,141 @@
+/* dgm_megamoe.h - C ABI of the MI355X (gfx950) MegaMoE layer.
+ *
+ * Plain pointers, sizes and a HIP stream; no torch types. Every call enqueues work on
+ * `stream` and returns without host synchronisation. Return value: 0 on success,
+ * DGM_ERR_INVALID_ARGUMENT (-1) when a host-side check fails (the message is available
+ * from dgm_last_error()), or a positive hipError_t when a launch fails.
+ *
+ * Each entry cites the reference interface it replaces (path:line in the DeepGEMM
+ * MegaMoE fork the interface mirrors).
+ */
+#ifndef DGM_MEGAMOE_H
+#define DGM_MEGAMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DGM_ERR_INVALID_ARGUMENT (-1)
+
+/* activation formats (the "act_format" of sm100_b200/test_mega_moe.py:57) */
+#define DGM_ACT_MXFP4 0 /* E2M1 + UE8M0 per 32 (W4A4)          */
+#define DGM_ACT_MXFP8 1 /* E4M3 + UE8M0 per 32 (W-MXFP4 x A-FP8) */
+
+/* frontend flags */
+#define DGM_FE_FORCE_BALANCED 1     /* DG_FE_FORCE_BALANCED: tests/test_four_api_correctness.py:125-144 */
+#define DGM_FE_ZERO_ROW_UNROUTED 2  /* DG_FE_ZERO_ROW_UNROUTED: deep_gemm/mega/__init__.py:693-696 */
+
+/* Library version and the message of the last failed host-side check (thread-local). */
+int dgm_version(void);
+const char* dgm_last_error(void);
+
+/* ------------------------------------------------------------------ packers
+ * Replaces deep_gemm/quantization_mxfp4_fused.py:29 quantize_to_mxfp4 (rule 0) and
+ * deep_gemm/quantization_mxfp4.py:52 quantize_to_mxfp4 (rule 1).
+ * w_bf16 [rows, K] -> packed [rows, K/2] (Marlin nibble order), scale_e8m0 [rows, K/32]. */
+int dgm_quantize_mxfp4(const void* w_bf16, int64_t rows, int64_t K, int rule,
+                       void* packed, void* scale_e8m0, hipStream_t stream);
+
+/* Replaces sm100_b200/test_mega_moe.py:78 cast_to_fp4_rows (amax_floor 1e-30) and
+ * deep_gemm/utils/math.py:85 per_token_cast_to_fp4(use_ue8m0=True, gran_k=32) (amax_floor 1e-4).
+ * x_bf16 [rows, K] -> packed [rows, K/2] (low nibble = even K), sf_e8m0 [rows, K/32]. */
+int dgm_cast_fp4_rows(const void* x_bf16, int64_t rows, int64_t K, float amax_floor,
+                      void* packed, void* sf_e8m0, hipStream_t stream);
+
+/* Replaces deep_gemm/utils/math.py:26 per_token_cast_to_fp8(use_ue8m0=True, gran_k=32).
+ * x_bf16 [rows, K] -> q_e4m3 [rows, K], sf_e8m0 [rows, K/32]. */
+int dgm_cast_fp8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_e4m3, void* sf_e8m0,
+                      hipStream_t stream);
+
+/* Replaces deep_gemm/quantization_nvfp4.py:62 quantize_to_nvfp4.
+ * w_bf16 [rows, K] -> packed [rows, K/2] (Marlin), scale_ue4m3 [rows, K/16]. */
+int dgm_quantize_nvfp4(const void* w_bf16, int64_t rows, int64_t K, void* packed,
+                       void* scale_ue4m3, hipStream_t stream);
+
+/* Replaces deep_gemm/quantization_qoq_fused.py:18 quantize_to_qoq.
+ * w_bf16 [rows, K] -> packed [rows, K/2] (Marlin), s2 u8 [rows, K/128], z u8 [rows, K/128],
+ * s1 f32 [rows]. */
+int dgm_quantize_qoq(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* s2,
+                     void* z, void* s1_f32, hipStream_t stream);
+
+/* Replaces deep_gemm/quantization_qoq_fused.py:78 per_token_cast_to_int8.
+ * x_bf16 [rows, K] -> q_i8 [rows, K], sf_f32 [rows]. */
+int dgm_cast_int8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_i8, void* sf_f32,
+                       hipStream_t stream);
+
+/* ------------------------------------------------------------------ weight layout
+ * Replaces deep_gemm/mega/fused.py:64 transform_mxfp4_weights_for_mega_moe_fused (one
+ * matrix per call). packed [E, N, K/2] (src_order 0 = Marlin, 1 = low-nibble-first),
+ * scale_e8m0 [E, N, K/32] -> dst_values [E, N/16, K/128, 64, 16] and
+ * dst_scales [E, N/16, ceil(K/512), 64, 4] (matrix-core fragment order). l1_interleave
+ * pairs gate block j with up block j (16 rows each) as the kernel's SwiGLU needs. */
+int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E, int N, int K,
+                              int src_order, int l1_interleave, void* dst_values,
+                              void* dst_scales, hipStream_t stream);
+
+/* ------------------------------------------------------------------ fused buffer
+ * Replaces csrc/apis/mega_fused.hpp:31-76 get_symm_buffer_size_for_fused_mega_moe:
+ * byte offsets of every view inside one device buffer (single GPU, no symmetric memory). */
+typedef struct DgmBufferLayout {
+  size_t total_bytes;
+  size_t x, x_sf, topk_idx, topk_weights;       /* frontend outputs / fused-layer inputs  */
+  size_t logits;                                /* fp32 router logits [max_tokens, E]      */
+  size_t pool;                                  /* dispatch table (see DgmPoolTable)       */
+  size_t mid, mid_sf;                           /* L1 -> L2 activations (pool-row order)   */
+  size_t partials;                              /* fp32 [max_tokens * topk, H] route outputs */
+  size_t counters;                              /* int32 scratch counters                  */
+  int32_t x_row_bytes, mid_row_bytes, max_routes;
+} DgmBufferLayout;
+
+int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_experts, int topk,
+                            int hidden, int intermediate, int act_format, DgmBufferLayout* out);
+
+/* ------------------------------------------------------------------ frontend
+ * Replaces csrc/fable_frontend.h:49-53 launch_router_quant_topk_frontend (and the Python
+ * deep_gemm/mega/__init__.py:671 fable_router_quant_topk_frontend): bf16 router GEMV with
+ * fp32 accumulation in a fixed order, bf16 logits, top-k (value desc, index asc), fp32
+ * softmax of the k logits, activation cast, into the buffer views x / x_sf / topk_idx /
+ * topk_weights (and fp32 logits). token_offset = global id of row 0 (forced-balanced rule). */
+int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16,
+                           int num_tokens, int hidden, int num_experts, int topk, int act_format,
+                           int flags, int token_offset, void* buffer,
+                           const DgmBufferLayout* layout, hipStream_t stream);
+
+/* ------------------------------------------------------------------ fused layer
+ * Replaces csrc/apis/mega_fused.hpp:78-102 run_fused / _C.mxfp4_mega_moe_fused and
+ * deep_gemm/mega/fused.py:97 mxfp4_mega_moe_fused for one GPU's share of the layer:
+ * dispatch of the buffer's topk_idx into per-expert pools (token asc, slot asc), L1
+ * grouped GEMM (gate/up) + SwiGLU + requant, L2 grouped GEMM, top-k weighted combine. */
+typedef struct DgmMoeArgs {
+  int32_t num_tokens, hidden, intermediate, num_experts, expert_begin, num_local_experts, topk;
+  int32_t act_format;
+  float activation_clamp;
+  const void* w1_values;  /* [E_local, 2I/16, H/128, 64, 16] */
+  const void* w1_scales;  /* [E_local, 2I/16, ceil(H/512), 64, 4] */
+  const void* w2_values;  /* [E_local, H/16, I/128, 64, 16] */
+  const void* w2_scales;  /* [E_local, H/16, ceil(I/512), 64, 4] */
+  int32_t* recv_stats;    /* [E_local] cumulative_local_expert_recv_stats, may be NULL */
+  void* y;                /* bf16 [num_tokens, hidden] */
+  void* buffer;
+  const DgmBufferLayout* layout;
+} DgmMoeArgs;
+
+int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
+
+/* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the
+ * current device. dgm_probe_mfma_scale: runs one V_MFMA_SCALE_F32_16X16X128_F8F6F4 on 64
+ * caller-provided lane fragments (a, b: 64 x 32 bytes; sa, sb: 64 int32 scale words;
+ * out: 64 x 4 fp32) so tests can pin the lane layout the kernels assume. fmt 4 = E2M1,
+ * 0 = E4M3; pairs (4,4), (4,0), (0,0). */
+int dgm_device_cu_count(void);
+int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const void* sb, void* out,
+                         int fmt_a, int fmt_b, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DGM_MEGAMOE_H */

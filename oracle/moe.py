@@ -149,8 +149,26 @@ def requant_mid(a, act_format):
 
 
 def silu(x):
+    """x * sigmoid(x) with sigmoid = 1 / (1 + exp(-x)), the reference's
+    ``gate * torch.sigmoid(gate)`` (sm100_b200/test_mega_moe.py:459)."""
     x = as_f32(x)
-    return (x / (np.float32(1.0) + np.exp(-x))).astype(np.float32)
+    return (x * (np.float32(1.0) / (np.float32(1.0) + np.exp(-x)))).astype(np.float32)
+
+
+class LazyDequant:
+    """Per-expert dequantisation on access (``W[e]`` -> f32 [N, K]) so the layer oracle can
+    run at full layer shapes while touching only the routed experts."""
+
+    def __init__(self, packed, scale, fn=None):
+        self.packed, self.scale = packed, scale
+        self.fn = fn or packers.dequantize_mxfp4_marlin
+        E, N, Kh = packed.shape
+        self.shape = (E, N, Kh * 2)
+
+    def __getitem__(self, e):
+        if isinstance(e, slice):
+            return LazyDequant(self.packed[e], self.scale[e], self.fn)
+        return self.fn(self.packed[e], self.scale[e])
 
 
 # ----------------------------------------------------------------------------- layer
@@ -172,15 +190,16 @@ def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=
         t_ids, s_ids = np.nonzero(topk_idx == expert_begin + e)
         if t_ids.size == 0:
             continue
-        h = (x_dq[t_ids] @ W1[e].T).astype(np.float32)
+        w1e, w2e = W1[e], W2[e]
+        h = (x_dq[t_ids] @ w1e.T).astype(np.float32)
         gate, up = h[:, :I], h[:, I:]
         if bf16_gate_up:
             gate, up = round_bf16(gate), round_bf16(up)
         gate = np.minimum(gate, c)
         up = np.clip(up, -c, c)
-        act = (silu(gate) * up * topk_w[t_ids, s_ids][:, None]).astype(np.float32)
+        act = ((silu(gate) * up).astype(np.float32) * topk_w[t_ids, s_ids][:, None]).astype(np.float32)
         act = requant_mid(act, act_format)
-        out = (act @ W2[e].T).astype(np.float32)
+        out = (act @ w2e.T).astype(np.float32)
         for n, (t, s) in enumerate(zip(t_ids, s_ids)):
             routes[int(t) * topk + int(s)] = out[n]
             y[t] = (y[t] + out[n]).astype(np.float32)

@@ -1,0 +1,161 @@
+"""GPU parity of the frontend and the fused layer against the oracle.
+
+Bit-exact: fp32 router logits (fixed accumulation order), top-k indices and slot order,
+activation codes and scales, pool membership and order, recv stats. Tolerance (the bar the
+north star states): per-row cos >= 0.9999 and rel-RMSE <= 0.5 % of the bf16 output against
+the fp32-accumulated oracle (the intermediate requant codes depend on the fp32 order)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nu
+from oracle import packers as pk
+from oracle import moe
+from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+REL_RMSE_MAX = 0.005
+
+
+def make_weights(E, H, I, seed, scale=0.02):
+    """bf16 weights drawn on the GPU (seeded), packed on the GPU by the HIP packer; returns
+    the transformed weights and lazily dequantised oracle views of the packed bytes."""
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    w1 = (torch.randn((E, 2 * I, H), generator=g, device="cuda", dtype=torch.float32) * scale).to(torch.bfloat16)
+    q1 = qf.quantize_to_mxfp4(w1)
+    del w1
+    w2 = (torch.randn((E, H, I), generator=g, device="cuda", dtype=torch.float32) * scale).to(torch.bfloat16)
+    q2 = qf.quantize_to_mxfp4(w2)
+    del w2
+    t = dgm.transform_mxfp4_weights_for_mega_moe_fused(q1, q2)
+    W1 = moe.LazyDequant(q1[0].cpu().numpy(), q1[1].cpu().numpy())
+    W2 = moe.LazyDequant(q2[0].cpu().numpy(), q2[1].cpu().numpy())
+    return t, W1, W2
+
+
+def run_layer(M, E, E_local, expert_begin, H, I, topk, fmt, seed, force_balanced=False, zero_rows=(),
+              max_tokens=None, weights=None, ep=None):
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    rng = np.random.default_rng(seed)
+    x = randn_bf16(rng, (M, H))
+    for r in zero_rows:
+        x[r] = 0.0
+    rw = randn_bf16(rng, (E, H), 0.02)
+    if weights is None:
+        weights = make_weights(E_local, H, I, seed + 1)
+    (t1, t2), W1, W2 = weights
+    ep_size, ep_rank = ep if ep else (E // E_local, expert_begin // E_local)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, max_tokens or M, topk, H, I, act_format=fmt,
+                                                 ep_size=ep_size, ep_rank=ep_rank)
+    xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
+    stats = torch.arange(E_local, dtype=torch.int32, device="cuda")
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    dgm.fable_router_quant_topk_frontend(xs, rws, buf, force_balanced=force_balanced)
+    dgm.mxfp4_mega_moe_fused(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats)
+    torch.cuda.synchronize()
+    # ---- oracle
+    logits = moe.router_logits_f32(x, rw)
+    idx, w, _ = moe.topk_softmax(logits, topk)
+    if force_balanced:
+        idx, w = moe.balanced_routing(M, E, topk)
+    for r in zero_rows:
+        idx[r] = -1
+        w[r] = 0.0
+    codes, sfb, x_dq = moe.quant_act(x, fmt)
+    ref, _ = moe.moe_forward(x_dq, idx, w, W1, W2, expert_begin, fmt)
+    return dict(buf=buf, y=y.float().cpu().numpy(), ref=ref, logits=logits, idx=idx, w=w, codes=codes,
+                sfb=sfb, stats=stats.cpu().numpy(), x=x)
+
+
+def check_frontend(r, fmt, M, force_balanced=False, zero_rows=()):
+    b = r["buf"]
+    if not force_balanced:
+        got = b.logits[:M].cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), r["logits"].view(np.uint32))
+    np.testing.assert_array_equal(b.topk_idx[:M].cpu().numpy(), r["idx"])
+    np.testing.assert_allclose(b.topk_weights[:M].cpu().numpy(), r["w"], rtol=1e-6, atol=0)
+    np.testing.assert_array_equal(b.x[:M].cpu().numpy(), r["codes"])
+    np.testing.assert_array_equal(b.x_sf[:M].cpu().numpy(), r["sfb"])
+
+
+def check_pool(r, E_local, expert_begin):
+    counts, active, offsets, routes = r["buf"].pool_table()
+    rc, ra, ro, rr = moe.dispatch(r["idx"], expert_begin, E_local)
+    np.testing.assert_array_equal(counts.numpy(), rc)
+    np.testing.assert_array_equal(active.numpy(), ra)
+    np.testing.assert_array_equal(offsets.numpy(), ro)
+    np.testing.assert_array_equal(routes.numpy(), rr)
+    np.testing.assert_array_equal(r["stats"], np.arange(E_local) + rc)
+
+
+def check_y(r, zero_rows=()):
+    m = moe.metrics(r["y"], r["ref"])
+    for zr in zero_rows:
+        assert (r["y"][zr] == 0).all()
+    keep = [i for i in range(r["y"].shape[0]) if i not in zero_rows]
+    m = moe.metrics(r["y"][keep], r["ref"][keep])
+    assert m["cos_min"] >= COS_MIN and m["rel_rmse"] <= REL_RMSE_MAX, m
+    return m
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8"])
+def test_small_layer(fmt):
+    need_gpu()
+    M, E, H, I, topk = 6, 16, 512, 256, 4
+    r = run_layer(M, E, E, 0, H, I, topk, fmt, seed=100)
+    check_frontend(r, fmt, M)
+    check_pool(r, E, 0)
+    print(fmt, check_y(r))
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8"])
+def test_config0_shape(fmt):
+    """E=48, H=3072, I=1280, top-8, M=2, real (unbalanced) routing."""
+    need_gpu()
+    r = run_layer(2, 48, 48, 0, 3072, 1280, 8, fmt, seed=200)
+    check_frontend(r, fmt, 2)
+    check_pool(r, 48, 0)
+    print(fmt, check_y(r))
+
+
+def test_config1_ep_share():
+    """384-way router, forced-balanced, one EP rank's share (experts 0..47)
+    on one GPU, M=8 -> 8 rows over 48 local experts, output = the local partial."""
+    need_gpu()
+    r = run_layer(8, 384, 48, 0, 3072, 1280, 8, "mxfp4", seed=300, force_balanced=True)
+    check_frontend(r, "mxfp4", 8, force_balanced=True)
+    check_pool(r, 48, 0)
+    assert int((r["buf"].pool_table()[0] > 0).sum()) == 8
+    print(check_y(r))
+
+
+def test_zero_rows_and_multi_slab():
+    """All-zero rows are unrouted and give y == 0 exactly; 40 tokens on 8 experts put > 16
+    routes on an expert (several 16-token slabs)."""
+    need_gpu()
+    r = run_layer(40, 8, 8, 0, 512, 256, 4, "mxfp4", seed=400, zero_rows=(3, 17))
+    check_frontend(r, "mxfp4", 40, zero_rows=(3, 17))
+    check_pool(r, 8, 0)
+    assert r["buf"].pool_table()[0].max() > 16
+    print(check_y(r, zero_rows=(3, 17)))
+
+
+def test_second_ep_rank_and_replay():
+    """A rank other than 0 (experts 16..31 of 64) and two calls in a row (stats accumulate,
+    the result is identical)."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    weights = make_weights(16, 512, 256, 501)
+    r = run_layer(5, 64, 16, 16, 512, 256, 4, "mxfp8", seed=500, weights=weights)
+    check_pool(r, 16, 16)
+    check_y(r)
+    (t1, t2), _, _ = weights
+    y2 = torch.empty((5, 512), dtype=torch.bfloat16, device="cuda")
+    dgm.mxfp4_mega_moe_fused(y2, t1, t2, r["buf"])
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])

@@ -1,0 +1,145 @@
+"""GPU parity: matrix-core lane layout, packers and the weight-layout transform (bit-exact)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as nu
+from oracle import packers as pk
+from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16, decode_native, interleave16
+
+pytestmark = pytest.mark.gpu
+
+
+def _probe(fa, fb, seed):
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    rng = np.random.default_rng(seed)
+    nbytes_a = 16 if fa == 4 else 32
+    nbytes_b = 16 if fb == 4 else 32
+    a = np.zeros((64, 32), np.uint8)
+    b = np.zeros((64, 32), np.uint8)
+    if fa == 4:
+        a[:, :16] = rng.integers(0, 256, (64, 16), dtype=np.uint8)
+    else:
+        a[:, :] = nu.e4m3_encode(rng.standard_normal((64, 32)).astype(np.float32))
+    if fb == 4:
+        b[:, :16] = rng.integers(0, 256, (64, 16), dtype=np.uint8)
+    else:
+        b[:, :] = nu.e4m3_encode(rng.standard_normal((64, 32)).astype(np.float32))
+    sa = rng.integers(120, 134, 64).astype(np.int32)
+    sb = rng.integers(120, 134, 64).astype(np.int32)
+    dev = torch.device("cuda")
+    ta, tb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    tsa, tsb = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
+    out = torch.zeros(64 * 4, dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().dgm_probe_mfma_scale(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
+                                                _lib.ptr(out), fa, fb, _lib.stream()))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(64, 4)
+
+    def vals(x, f):
+        if f == 4:
+            nib = np.stack([x[:, :16] & 0xF, x[:, :16] >> 4], -1).reshape(64, 32)
+            return nu.e2m1_decode(nib).astype(np.float64)
+        return nu.e4m3_decode(x).astype(np.float64)
+    A = np.zeros((16, 128))
+    B = np.zeros((128, 16))
+
+    def kmap(f, l):
+        g = l // 16
+        if f == 4:                      # E2M1: 32 consecutive K per lane
+            return np.arange(32 * g, 32 * g + 32)
+        return np.concatenate([np.arange(16 * g, 16 * g + 16), np.arange(64 + 16 * g, 80 + 16 * g)])
+    for l in range(64):
+        A[l % 16, kmap(fa, l)] = vals(a, fa)[l]
+        B[kmap(fb, l), l % 16] = vals(b, fb)[l]
+    # the scale of lane l applies to row/column l%16 over the 32-block 32*(l//16)
+    for l in range(64):
+        A[l % 16, 32 * (l // 16):32 * (l // 16) + 32] *= nu.e8m0_to_f32(sa[l])
+        B[32 * (l // 16):32 * (l // 16) + 32, l % 16] *= nu.e8m0_to_f32(sb[l])
+    D = A @ B
+    exp = np.zeros((64, 4))
+    for l in range(64):
+        for i in range(4):
+            exp[l, i] = D[4 * (l // 16) + i, l % 16]
+    return got, exp
+
+
+@pytest.mark.parametrize("fa,fb", [(4, 4), (4, 0)])
+def test_mfma_scale_lane_layout(fa, fb):
+    need_gpu()
+    for seed in range(3):
+        got, exp = _probe(fa, fb, seed)
+        np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6 * np.abs(exp).max())
+
+
+def test_packers_bit_exact():
+    need_gpu()
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf, quantization_mxfp4 as qs
+    from hopper_megamoe_basedondeepgemm_amd import quantization_nvfp4 as qn, quantization_qoq_fused as qq
+    from hopper_megamoe_basedondeepgemm_amd import utils as du
+    rng = np.random.default_rng(11)
+    w = randn_bf16(rng, (3, 64, 512), 0.02)
+    w[0, 0, :32] = 0.0
+    w[0, 1, :32] = np.float32(-1e-3)
+    w[0, 1, 5] = np.float32(0.75)
+    w[0, 2] = np.tile(np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5, 6], np.float32) / 8, 64)
+    tw = bf16_cpu(w).cuda()
+    for fn, ref in ((qf.quantize_to_mxfp4, pk.quantize_to_mxfp4_fused),
+                    (qs.quantize_to_mxfp4, pk.quantize_to_mxfp4_split),
+                    (qn.quantize_to_nvfp4, pk.quantize_to_nvfp4)):
+        p, s = fn(tw)
+        rp, rs = ref(w)
+        np.testing.assert_array_equal(s.cpu().numpy(), rs)
+        np.testing.assert_array_equal(p.cpu().numpy(), rp)
+    p, s2, z, s1 = qq.quantize_to_qoq(tw)
+    rp, rs2, rz, rs1 = pk.quantize_to_qoq(w)
+    np.testing.assert_array_equal(s1.cpu().numpy(), rs1)
+    np.testing.assert_array_equal(s2.cpu().numpy(), rs2)
+    np.testing.assert_array_equal(z.cpu().numpy(), rz)
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)
+
+    x = randn_bf16(rng, (5, 3072))
+    x[0, :32] = 0
+    tx = bf16_cpu(x).cuda()
+    q, sf = qq.per_token_cast_to_int8(tx)
+    rq, rsf = pk.per_token_cast_to_int8(x)
+    np.testing.assert_array_equal(q.cpu().numpy(), rq)
+    np.testing.assert_array_equal(sf[:, 0].cpu().numpy(), rsf)
+    p4, sf4 = du.per_token_cast_to_fp4(tx)
+    rp4, rsf4 = pk.per_token_cast_to_fp4(x)
+    np.testing.assert_array_equal(p4.cpu().numpy(), rp4)
+    np.testing.assert_array_equal(sf4.cpu().numpy(), rsf4)
+    p4, sf4 = du.per_token_cast_to_fp4(tx, amax_floor=1e-30)
+    rp4, rsf4, _ = pk.cast_to_fp4_rows(x)
+    np.testing.assert_array_equal(p4.cpu().numpy(), rp4)
+    np.testing.assert_array_equal(sf4.cpu().numpy(), rsf4)
+    q8, sf8 = du.per_token_cast_to_fp8(tx)
+    rq8, rsf8 = pk.per_token_cast_to_fp8_ue8m0(x)
+    np.testing.assert_array_equal(q8.view(torch.uint8).cpu().numpy(), rq8)
+    np.testing.assert_array_equal(sf8.cpu().numpy(), rsf8)
+
+
+def test_transform_dequant_invariant():
+    """dequant(transform(q)) == interleave(dequant(q)) (the reference's transform check,
+    tests/test_mxfp4_mega_moe_sm90_correctness.py:153-182), for L1 (interleaved) and L2."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf
+    rng = np.random.default_rng(12)
+    w1 = randn_bf16(rng, (2, 64, 640), 0.05)      # K = 640: 5 K-tiles, padded scale group
+    w2 = randn_bf16(rng, (2, 32, 256), 0.05)
+    q1 = qf.quantize_to_mxfp4(bf16_cpu(w1).cuda())
+    q2 = qf.quantize_to_mxfp4(bf16_cpu(w2).cuda())
+    (v1, s1, _), (v2, s2, _) = dgm.transform_mxfp4_weights_for_mega_moe_fused(q1, q2)
+    torch.cuda.synchronize()
+    d1 = pk.dequantize_mxfp4_marlin(q1[0].cpu().numpy(), q1[1].cpu().numpy())
+    d2 = pk.dequantize_mxfp4_marlin(q2[0].cpu().numpy(), q2[1].cpu().numpy())
+    np.testing.assert_array_equal(decode_native(v1.cpu().numpy(), s1.cpu().numpy()), interleave16(d1))
+    np.testing.assert_array_equal(decode_native(v2.cpu().numpy(), s2.cpu().numpy()), d2)
+    # padding scale bytes of the last (partial) group are 2^0
+    assert (s1.cpu().numpy()[:, :, -1, :, 1:] == 127).all()
+    # low-nibble-first sources give the same layout
+    lf = pk.pack_low_first(pk.unpack_marlin(q2[0].cpu().numpy()))
+    (u1, t1, _), (u2, t2, _) = dgm.transform_mxfp4_weights_for_mega_moe_fused(
+        (q1[0], q1[1]), (torch.from_numpy(lf).cuda(), q2[1]), src_order="low_first")
+    np.testing.assert_array_equal(u2.cpu().numpy(), v2.cpu().numpy())

@@ -1,0 +1,52 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol include/*.h declares, and
+its host-side argument checks reject bad shapes with a message (no GPU work is launched)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        names |= set(re.findall(r"\b(dgm_\w+)\s*\(", txt))
+    return sorted(names)
+
+
+def test_library_exports_every_declared_symbol():
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_lib.EXPORTS)
+
+
+def test_host_checks_and_layout():
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    lib = _lib.load()
+    st = lib.dgm_quantize_mxfp4(ctypes.c_void_p(16), 4, 33, 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert st == -1 and b"multiple of 32" in lib.dgm_last_error()
+    with pytest.raises(RuntimeError, match="topk"):
+        _lib.layout(16, 384, 48, 17, 3072, 1280, 0)
+    L = _lib.layout(16, 384, 48, 8, 3072, 1280, 1)
+    offs = [L.x, L.x_sf, L.topk_idx, L.topk_weights, L.logits, L.pool, L.mid, L.mid_sf, L.partials,
+            L.counters, L.total_bytes]
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert L.x_row_bytes == 3072 and L.mid_row_bytes == 1280 and L.max_routes == 128
+    assert L.partials + 128 * 3072 * 4 <= L.counters
+
+
+def test_product_path_has_no_cpu_fallback():
+    import torch
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    w = torch.zeros((2, 64), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        dgm.quantization_mxfp4_fused.quantize_to_mxfp4(w)
