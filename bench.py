@@ -3,9 +3,10 @@
 Default workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
 layer forward: router + top-8 + activation cast, dispatch, L1, L2, combine). Also sweeps
-M = 2, 4, 8, 16 and reports each. Before every timed step >= 1 GiB is written so neither
-the 256 MB MALL nor the L2s hold weights; the timed region is the layer alone, with HIP
-events on the stream the layer runs on.
+M = 2, 4, 8, 16 and reports each. Before every timed step >= 1 GiB is written and
+then 1 GiB of other data is read, so neither the 256 MB MALL nor the L2s hold weights (and
+no dirty lines are left to drain inside the timed region); the timed region is the layer
+alone, with HIP events on the stream the layer runs on.
 
 Prints ONE JSON line (the driver contract). Data are synthetic (seeded randn weights of the
 layer's shape, packed on the GPU with the MXFP4 packer).
@@ -60,6 +61,14 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     x = torch.randn((M, H), generator=g, device="cuda").to(torch.bfloat16)
     y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
     flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    flush_rd = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+
+    def evict():
+        # >= 1 GiB written, then 1 GiB of other data read: neither the 256 MB MALL nor the
+        # L2s hold weights, and no dirty lines of the write are left to be written back
+        # inside the timed region
+        flush.fill_(1)
+        flush_rd.sum()
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -69,12 +78,12 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
         dgm.mxfp4_mega_moe_fused(y, t1, t2, buf)
 
     for _ in range(warmup):
-        flush.fill_(1)
+        evict()
         layer()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
-        flush.fill_(1)
+        evict()
         starts[i].record(stream)
         layer()
         ends[i].record(stream)

@@ -19,7 +19,9 @@ EXPORTS = [
     "dgm_version", "dgm_last_error", "dgm_quantize_mxfp4", "dgm_cast_fp4_rows", "dgm_cast_fp8_rows",
     "dgm_quantize_nvfp4", "dgm_quantize_qoq", "dgm_cast_int8_rows", "dgm_transform_fp4_weights",
     "dgm_fused_buffer_layout", "dgm_router_topk_launch", "dgm_megamoe_fused_launch",
-    "dgm_device_cu_count", "dgm_probe_mfma_scale",
+    "dgm_megamoe_split_launch",
+    "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_probe_mfma_scale",
+    "dgm_probe_mfma_scale_sel",
 ]
 
 
@@ -40,7 +42,8 @@ class MoeArgs(ctypes.Structure):
                 ("w1_values", ctypes.c_void_p), ("w1_scales", ctypes.c_void_p),
                 ("w2_values", ctypes.c_void_p), ("w2_scales", ctypes.c_void_p),
                 ("recv_stats", ctypes.c_void_p), ("y", ctypes.c_void_p), ("buffer", ctypes.c_void_p),
-                ("layout", ctypes.POINTER(BufferLayout))]
+                ("layout", ctypes.POINTER(BufferLayout)), ("phase_stamps", ctypes.c_void_p),
+                ("phase_stamp_rows", ctypes.c_int32)]
 
 
 _lib = None
@@ -69,8 +72,11 @@ def load():
         "dgm_router_topk_launch": ([vp, vp, i32, i32, i32, i32, i32, i32, i32, vp,
                                     ctypes.POINTER(BufferLayout), vp], i32),
         "dgm_megamoe_fused_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
+        "dgm_megamoe_split_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_device_cu_count": ([], i32),
+        "dgm_fused_workgroups": ([i32, i32, i32], i32),
         "dgm_probe_mfma_scale": ([vp, vp, vp, vp, vp, i32, i32, vp], i32),
+        "dgm_probe_mfma_scale_sel": ([vp, vp, vp, vp, vp, i32, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

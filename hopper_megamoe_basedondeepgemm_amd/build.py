@@ -6,7 +6,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdgm_megamoe.so")
-SOURCES = ["dgm_megamoe.hip", "dgm_packers.hip", "dgm_probe.hip"]
+SOURCES = ["dgm_megamoe.hip", "dgm_fused.hip", "dgm_packers.hip", "dgm_probe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

@@ -4,6 +4,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <utility>
 
 #define DGM_DEV __device__ __forceinline__
 
@@ -12,6 +13,16 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 namespace dgm {
+
+// Compile-time unrolled loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <class F, int... Is>
+DGM_DEV void static_for_impl(F& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+DGM_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // ---------------------------------------------------------------- bf16
 DGM_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
@@ -105,6 +116,11 @@ DGM_DEV int atomic_load_acquire_agent(const int* p) {
 template <int FMT_A, int FMT_B>
 DGM_DEV v4f mfma_scale_16x16x128(v8i a, v8i b, v4f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, 0, sa, 0, sb);
+}
+// Same, with the scale bytes selected from 4-byte scale words: byte OPA of sa, byte OPB of sb.
+template <int FMT_A, int FMT_B, int OPA, int OPB>
+DGM_DEV v4f mfma_scale_16x16x128_sel(v8i a, v8i b, v4f c, int sa, int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, OPA, sa, OPB, sb);
 }
 
 }  // namespace dgm

@@ -1,0 +1,44 @@
+// Parameters and limits of the persistent MegaMoE kernel (dgm_fused.hip).
+#pragma once
+#include <stdint.h>
+#include <hip/hip_runtime.h>
+
+constexpr int FUSED_MAX_ROUTES = 1024;   // tokens * topk per call
+constexpr int FUSED_MAX_LOCAL = 512;     // local experts
+constexpr int FUSED_MAX_TOKENS = 256;    // tokens per call
+constexpr int FUSED_MAX_NB64 = 64;       // hidden / 64 (hidden <= 4096); combine uses hidden / 128
+
+// int32 counters in the buffer's counter region
+constexpr int CNT_EXIT = 0;              // workgroups finished (last one clears everything)
+constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
+constexpr int CNT_CLAIM = 2;             // next unclaimed L1 unit, then [3] next unclaimed L2 unit
+constexpr int CNT_L1 = 64;               // [FUSED_MAX_LOCAL] L1 units done per active expert slot
+constexpr int CNT_TOTAL = CNT_L1 + FUSED_MAX_LOCAL + FUSED_MAX_TOKENS * FUSED_MAX_NB64;  // + combine counters
+
+inline __host__ __device__ int a256i(int x) { return (x + 255) & ~255; }
+
+struct FusedParams {
+  const uint8_t* w1v;
+  const uint32_t* w1s;
+  const uint8_t* w2v;
+  const uint32_t* w2s;
+  const uint8_t* x;
+  const uint8_t* xsf;
+  const int64_t* topk_idx;
+  const float* topk_w;
+  uint8_t* mid;
+  uint8_t* mid_sf;
+  float* partials;
+  uint16_t* y;
+  uint8_t* pool_out;
+  int* recv_stats;
+  int* counters;
+  long long* stamps;     // optional [stamp_rows][8] wall-clock stamps (see k_megamoe)
+  int stamp_rows;
+  int M, topk, expert_begin, E_local;
+  float clamp;
+  int spin_limit;
+};
+
+int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream);
+int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format);

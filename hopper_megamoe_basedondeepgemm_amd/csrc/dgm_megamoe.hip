@@ -18,6 +18,7 @@
 // the E8M0 block scales of both operands in hardware (no dequantisation on the VALU).
 #include "dgm_common.hpp"
 #include "dgm_abi_internal.hpp"
+#include "dgm_fused.hpp"
 
 using namespace dgm;
 
@@ -378,8 +379,10 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         sm.bs[g][l] = w;
       }
       __syncthreads();
-      // ---- matrix cores
+      // ---- matrix cores: two K halves accumulated separately and added (the persistent
+      // kernel's order, so both paths give identical results)
       v4f accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+      v4f accg1 = {0.f, 0.f, 0.f, 0.f}, accu1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < KT; ++kt) {
         v8i bop;
@@ -388,9 +391,16 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         const int sh = 8 * (kt & 3);
         int sb = (int)(sm.bs[kt >> 2][lane] >> sh);
         constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;
-        accg = mfma_scale_16x16x128<4, FB>(u4_to_v8i(ag[kt]), bop, accg, (int)(sg[kt >> 2] >> sh), sb);
-        accu = mfma_scale_16x16x128<4, FB>(u4_to_v8i(au[kt]), bop, accu, (int)(su[kt >> 2] >> sh), sb);
+        if (kt < KT / 2) {
+          accg = mfma_scale_16x16x128<4, FB>(u4_to_v8i(ag[kt]), bop, accg, (int)(sg[kt >> 2] >> sh), sb);
+          accu = mfma_scale_16x16x128<4, FB>(u4_to_v8i(au[kt]), bop, accu, (int)(su[kt >> 2] >> sh), sb);
+        } else {
+          accg1 = mfma_scale_16x16x128<4, FB>(u4_to_v8i(ag[kt]), bop, accg1, (int)(sg[kt >> 2] >> sh), sb);
+          accu1 = mfma_scale_16x16x128<4, FB>(u4_to_v8i(au[kt]), bop, accu1, (int)(su[kt >> 2] >> sh), sb);
+        }
       }
+      accg += accg1;
+      accu += accu1;
       // ---- epilogue: lane holds features 16p + 4(l/16) + i for slab column c = l % 16
       const int c = lane & 15;
       const bool valid = s0 + c < n;
@@ -570,6 +580,10 @@ const char* dgm_last_error(void) { return g_err; }
 
 int dgm_device_cu_count(void) { return cu_count(); }
 
+int dgm_fused_workgroups(int hidden, int intermediate, int act_format) {
+  return dgm_fused_grid_blocks(hidden, intermediate, act_format);
+}
+
 int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_experts, int topk,
                             int hidden, int intermediate, int act_format, DgmBufferLayout* out) {
   DGM_CHECK_ARG(out != nullptr, "null layout");
@@ -593,7 +607,7 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   out->mid = off; off += dgm_align256((size_t)R * mb);
   out->mid_sf = off; off += dgm_align256((size_t)R * (intermediate / 32));
   out->partials = off; off += dgm_align256((size_t)R * hidden * 4);
-  out->counters = off; off += 4096;
+  out->counters = off; off += dgm_align256((size_t)CNT_TOTAL * 4);
   out->total_bytes = off;
   out->x_row_bytes = (int32_t)xb;
   out->mid_row_bytes = (int32_t)mb;
@@ -651,6 +665,44 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
   DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 32 == 0, "shape");
   DGM_CHECK_ARG(A->intermediate % 128 == 0, "intermediate % 128 == 0");
+  if (A->num_tokens == 0) return 0;
+  uint8_t* buf = (uint8_t*)A->buffer;
+  const int routes_n = A->num_tokens * A->topk;
+  if (routes_n <= FUSED_MAX_ROUTES && A->num_local_experts <= FUSED_MAX_LOCAL &&
+      A->num_tokens <= FUSED_MAX_TOKENS && A->hidden / 64 <= FUSED_MAX_NB64) {
+    FusedParams p;
+    p.w1v = (const uint8_t*)A->w1_values;
+    p.w1s = (const uint32_t*)A->w1_scales;
+    p.w2v = (const uint8_t*)A->w2_values;
+    p.w2s = (const uint32_t*)A->w2_scales;
+    p.x = buf + L->x;
+    p.xsf = buf + L->x_sf;
+    p.topk_idx = (const int64_t*)(buf + L->topk_idx);
+    p.topk_w = (const float*)(buf + L->topk_weights);
+    p.mid = buf + L->mid;
+    p.mid_sf = buf + L->mid_sf;
+    p.partials = (float*)(buf + L->partials);
+    p.y = (uint16_t*)A->y;
+    p.pool_out = buf + L->pool;
+    p.recv_stats = A->recv_stats;
+    p.counters = (int*)(buf + L->counters);
+    p.M = A->num_tokens;
+    p.topk = A->topk;
+    p.expert_begin = A->expert_begin;
+    p.E_local = A->num_local_experts;
+    p.clamp = A->activation_clamp;
+    p.spin_limit = 1 << 22;
+    p.stamps = (long long*)A->phase_stamps;
+    p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;
+    return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
+  }
+  return dgm_megamoe_split_launch(A, stream);
+}
+
+int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
+  DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
+  const DgmBufferLayout* L = A->layout;
+  DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   if (A->num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)A->buffer;
   const int routes_n = A->num_tokens * A->topk;

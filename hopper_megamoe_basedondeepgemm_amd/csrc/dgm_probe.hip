@@ -14,6 +14,29 @@ __global__ void k_probe(const v8i* a, const v8i* b, const int* sa, const int* sb
   for (int i = 0; i < 4; ++i) out[l * 4 + i] = c[i];
 }
 
+template <int SEL>
+__global__ void k_probe_sel(const v8i* a, const v8i* b, const int* sa, const int* sb, float* out) {
+  int l = threadIdx.x;
+  v4f c = {0.f, 0.f, 0.f, 0.f};
+  c = mfma_scale_16x16x128_sel<4, 4, SEL, SEL>(a[l], b[l], c, sa[l], sb[l]);
+  for (int i = 0; i < 4; ++i) out[l * 4 + i] = c[i];
+}
+
+// Byte select of the scale words (E2M1 x E2M1): the scale used is byte `sel` of sa / sb.
+extern "C" int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void* sa, const void* sb,
+                                        void* out, int sel, hipStream_t stream) {
+  DGM_CHECK_ARG(a && b && sa && sb && out && sel >= 0 && sel < 4, "bad argument");
+  const v8i* A = (const v8i*)a;
+  const v8i* B = (const v8i*)b;
+  switch (sel) {
+    case 0: hipLaunchKernelGGL((k_probe_sel<0>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out); break;
+    case 1: hipLaunchKernelGGL((k_probe_sel<1>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out); break;
+    case 2: hipLaunchKernelGGL((k_probe_sel<2>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out); break;
+    default: hipLaunchKernelGGL((k_probe_sel<3>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out); break;
+  }
+  return dgm_last_launch_status();
+}
+
 extern "C" int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const void* sb,
                                     void* out, int fmt_a, int fmt_b, hipStream_t stream) {
   DGM_CHECK_ARG(a && b && sa && sb && out, "null pointer");

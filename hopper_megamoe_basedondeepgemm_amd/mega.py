@@ -87,6 +87,10 @@ class FusedSymmBuffer:
         routes = raw[o:o + 4 * total].view(torch.int32).clone()
         return counts, active, offsets, routes
 
+    def kernel_error(self):
+        """Error flag of the persistent kernel (1 when a bounded wait expired). Synchronises."""
+        return int(self.buffer[self.layout.counters + 4:self.layout.counters + 8].view(torch.int32).item())
+
     def destroy(self):
         self.buffer = None
         self.handle = None
@@ -169,7 +173,7 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
 
 
 # ----------------------------------------------------------------------------- fused layer
-def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None):
+def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None):
     w1, sf1, _ = l1
     w2, sf2, _ = l2
     _lib.require_gpu(y, w1, sf1, w2, sf2, stats)
@@ -191,8 +195,13 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None):
                         activation_clamp=float(activation_clamp if activation_clamp is not None else 3.0e38),
                         w1_values=w1.data_ptr(), w1_scales=sf1.data_ptr(), w2_values=w2.data_ptr(),
                         w2_scales=sf2.data_ptr(), recv_stats=stats.data_ptr() if stats is not None else None,
-                        y=y.data_ptr(), buffer=b.buffer.data_ptr(), layout=ctypes.pointer(b.layout))
-    _lib.check(_lib.load().dgm_megamoe_fused_launch(ctypes.byref(args), _lib.stream()))
+                        y=y.data_ptr(), buffer=b.buffer.data_ptr(), layout=ctypes.pointer(b.layout),
+                        phase_stamps=phase_stamps.data_ptr() if phase_stamps is not None else None,
+                        phase_stamp_rows=phase_stamps.numel() // 8 if phase_stamps is not None else 0)
+    if phase_stamps is not None:
+        assert phase_stamps.dtype == torch.int64 and phase_stamps.is_cuda and phase_stamps.is_contiguous()
+    fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
+    _lib.check(fn(ctypes.byref(args), _lib.stream()))
 
 
 def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
@@ -200,8 +209,23 @@ def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
     """deep_gemm/mega/fused.py:97: the layer over the routing and activations already in the
     buffer (written by ``fable_router_quant_topk_frontend`` or by the caller): dispatch,
     L1 + SwiGLU + requant, L2, top-k combine into ``y`` (bf16 [tokens, H]).
-    ``fast_math`` / ``phase_stamps`` / ``fe_keys`` are accepted for signature compatibility."""
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp)
+    ``phase_stamps`` (optional int64 CUDA tensor [rows, 8]; workgroups >= rows skip): per-workgroup
+    100 MHz wall-clock stamps: entry, dispatch ready, L1 done, first L1 arrival seen, L2
+    done, exit, fence ticks, units (see ``fused_workgroups``). ``fast_math`` / ``fe_keys`` are
+    accepted for signature compatibility."""
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps)
+
+
+def fused_workgroups(b):
+    """Workgroups of the persistent kernel for this buffer's shape (after its first launch)."""
+    return _lib.load().dgm_fused_workgroups(b.hidden, b.intermediate_hidden, b.act_code)
+
+
+def mxfp4_mega_moe_split(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
+                         fast_math=True, **_):
+    """deep_gemm/mega/__init__.py:579 split API: the same layer as separate launches
+    (dispatch, L1 + SwiGLU + requant, L2, combine) with the fused path's numerics."""
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, split=True)
 
 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,

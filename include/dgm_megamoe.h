@@ -122,9 +122,18 @@ typedef struct DgmMoeArgs {
   void* y;                /* bf16 [num_tokens, hidden] */
   void* buffer;
   const DgmBufferLayout* layout;
+  int64_t* phase_stamps;  /* optional [phase_stamp_rows, 8] wall-clock stamps (phase_stamps of
+                             deep_gemm/mega/fused.py:97); NULL = off. Workgroups beyond
+                             phase_stamp_rows record nothing. */
+  int32_t phase_stamp_rows;
 } DgmMoeArgs;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
+
+/* Replaces csrc/apis/mega.hpp:550 _C.mxfp4_mega_moe_split / deep_gemm/mega/__init__.py:579
+ * mxfp4_mega_moe_split: the same layer as separate launches (dispatch, L1, L2, combine)
+ * instead of one persistent kernel; identical numerics. */
+int dgm_megamoe_split_launch(const DgmMoeArgs* args, hipStream_t stream);
 
 /* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the
  * current device. dgm_probe_mfma_scale: runs one V_MFMA_SCALE_F32_16X16X128_F8F6F4 on 64
@@ -132,8 +141,13 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
  * out: 64 x 4 fp32) so tests can pin the lane layout the kernels assume. fmt 4 = E2M1,
  * 0 = E4M3; pairs (4,4), (4,0), (0,0). */
 int dgm_device_cu_count(void);
+/* Workgroups of the persistent kernel for a shape (0 before its first launch). */
+int dgm_fused_workgroups(int hidden, int intermediate, int act_format);
 int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const void* sb, void* out,
                          int fmt_a, int fmt_b, hipStream_t stream);
+/* Same with E2M1 x E2M1 operands and the scale taken from byte `sel` (0..3) of sa / sb. */
+int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void* sa, const void* sb, void* out,
+                             int sel, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -10,7 +10,7 @@ from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16, decode_native, inte
 pytestmark = pytest.mark.gpu
 
 
-def _probe(fa, fb, seed):
+def _probe(fa, fb, seed, sel=None):
     from hopper_megamoe_basedondeepgemm_amd import _lib
     rng = np.random.default_rng(seed)
     nbytes_a = 16 if fa == 4 else 32
@@ -31,8 +31,19 @@ def _probe(fa, fb, seed):
     ta, tb = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
     tsa, tsb = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
     out = torch.zeros(64 * 4, dtype=torch.float32, device=dev)
-    _lib.check(_lib.load().dgm_probe_mfma_scale(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
-                                                _lib.ptr(out), fa, fb, _lib.stream()))
+    if sel is None:
+        _lib.check(_lib.load().dgm_probe_mfma_scale(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
+                                                    _lib.ptr(out), fa, fb, _lib.stream()))
+    else:
+        # the scale sits in byte `sel` of each word; the other bytes hold other (wrong) codes
+        noise = rng.integers(100, 150, (2, 64, 4)).astype(np.int64)
+        noise[0, :, sel] = sa
+        noise[1, :, sel] = sb
+        wa = (noise[0] << np.array([0, 8, 16, 24])).sum(-1).astype(np.uint32).view(np.int32)
+        wb = (noise[1] << np.array([0, 8, 16, 24])).sum(-1).astype(np.uint32).view(np.int32)
+        tsa, tsb = torch.from_numpy(wa).to(dev), torch.from_numpy(wb).to(dev)
+        _lib.check(_lib.load().dgm_probe_mfma_scale_sel(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
+                                                        _lib.ptr(out), sel, _lib.stream()))
     torch.cuda.synchronize()
     got = out.cpu().numpy().reshape(64, 4)
 
@@ -70,6 +81,14 @@ def test_mfma_scale_lane_layout(fa, fb):
     for seed in range(3):
         got, exp = _probe(fa, fb, seed)
         np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6 * np.abs(exp).max())
+
+
+@pytest.mark.parametrize("sel", [0, 1, 2, 3])
+def test_mfma_scale_byte_select(sel):
+    """op_sel of the block-scale operands picks byte `sel` of the 32-bit scale word."""
+    need_gpu()
+    got, exp = _probe(4, 4, 10 + sel, sel=sel)
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-6 * np.abs(exp).max())
 
 
 def test_packers_bit_exact():
