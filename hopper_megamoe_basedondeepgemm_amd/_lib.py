@@ -39,6 +39,7 @@ class MoeArgs(ctypes.Structure):
                 ("num_experts", ctypes.c_int32), ("expert_begin", ctypes.c_int32),
                 ("num_local_experts", ctypes.c_int32), ("topk", ctypes.c_int32),
                 ("act_format", ctypes.c_int32), ("activation_clamp", ctypes.c_float),
+                ("fast_math", ctypes.c_int32),
                 ("w1_values", ctypes.c_void_p), ("w1_scales", ctypes.c_void_p),
                 ("w2_values", ctypes.c_void_p), ("w2_scales", ctypes.c_void_p),
                 ("recv_stats", ctypes.c_void_p), ("y", ctypes.c_void_p), ("buffer", ctypes.c_void_p),

@@ -71,6 +71,11 @@ DGM_DEV float e8m0_value(uint32_t code) { return __uint_as_float(code << 23); } 
 DGM_DEV float e8m0_value_any(uint32_t code) {
   return code == 0u ? __uint_as_float(0x00400000u) : __uint_as_float(code << 23);
 }
+// 2^(127 - code): the exact reciprocal of the E8M0 value (code 254 gives the subnormal 2^-127),
+// so x * e8m0_inv(code) == x / e8m0_value_any(code) bit for bit.
+DGM_DEV float e8m0_inv(uint32_t code) {
+  return code >= 254u ? __uint_as_float(0x00400000u) : __uint_as_float((254u - code) << 23);
+}
 // ceil(fp32(log2(x))) with log2 evaluated in double and rounded once to fp32: the
 // behaviour of the log2-based scale rules near powers of two.
 DGM_DEV float ceil_log2_f32(float x) { return ceilf((float)log2((double)x)); }
@@ -96,6 +101,16 @@ DGM_DEV uint32_t e4m3_encode(float x) {
     code = c > 0x7e ? 0x7fu : (uint32_t)c;
   }
   return sign | code;
+}
+
+// ---------------------------------------------------------------- SwiGLU
+// sigmoid(g) = 1 / (1 + e^-g). fast: e^-g = 2^(-g log2 e) on the hardware exp2 and the
+// hardware reciprocal (the reference's fast_math=True path is an approximate exp and an
+// approximate reciprocal too); otherwise IEEE expf and a correctly rounded division.
+template <bool FAST>
+DGM_DEV float sigmoid(float g) {
+  if (FAST) return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+  return 1.0f / (1.0f + expf(-g));
 }
 
 // ---------------------------------------------------------------- scopes / atomics

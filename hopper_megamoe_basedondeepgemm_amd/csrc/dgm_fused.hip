@@ -50,6 +50,14 @@ DGM_DEV v8i as_v8i(U4 a, U4 b) {
   return r;
 }
 
+// Weight tiles are read exactly once: non-temporal loads ("nt") keep them from allocating in
+// the L2 / MALL, which lifts streaming bandwidth from ~5.4 to ~7 TB/s on MI355X.
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+DGM_DEV U4 ld_stream(const uint8_t* p) {
+  v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+  return U4{v.x, v.y, v.z, v.w};
+}
+
 // agent-coherent (write-through / L2-bypassing) accesses for cross-workgroup hand-offs
 DGM_DEV void st_agent64(void* p, uint64_t v) {
   __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -63,6 +71,12 @@ DGM_DEV uint32_t ld_agent8(const uint8_t* p) {
 }
 DGM_DEV float ld_agent_f32(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Compiler-only ordering point: memory operations after it stay after the matrix-core ops
+// that produced `acc` (otherwise the next unit's tile loads may be hoisted above them and
+// need a second register set).
+DGM_DEV void after_mfma(v4f acc) {
+  asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]) : "memory");
 }
 // all of this wave's memory operations have completed (stores acknowledged)
 DGM_DEV void wait_mem() {
@@ -100,7 +114,7 @@ struct FusedSmem {
   int last[FUSED_MAX_TOKENS];
   int nlast;
   int is_last;
-  int claim;
+  int claimv[2];
 };
 
 // Exclusive scan of (count, active flag) over n <= FUSED_MAX_LOCAL experts.
@@ -214,7 +228,8 @@ DGM_DEV void stage_slab(S& s, const uint8_t* __restrict__ src, const uint8_t* __
 
 // Phase stamps (the reference's phase_stamps facility): per workgroup, 100 MHz wall clock at
 // [0] entry, [1] dispatch table ready, [2] L1 units done, [3] first L1 arrival observed,
-// [4] L2 units done, [5] exit; [6] wall ticks spent waiting on L1 arrivals, [7] reserved.
+// [4] L2 units done, [5] exit; [6] wall ticks from L1 unit start to its matrix-core ops done
+// (weights landed), [7] wall ticks in L1 arrival signalling (store completion + barrier).
 DGM_DEV long long wall_clock() { return (long long)__builtin_amdgcn_s_memrealtime(); }
 
 template <int KT1, int KT2, int ACT>
@@ -236,7 +251,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   int* l1_done = p.counters + CNT_L1;
   int* comb = p.counters + CNT_L1 + FUSED_MAX_LOCAL;
   long long* st = (p.stamps && (int)blockIdx.x < p.stamp_rows) ? p.stamps + (size_t)blockIdx.x * 8 : nullptr;
-  long long wait_ticks = 0;
+  long long wait_ticks = 0, l1_load_ticks = 0, l1_sig_ticks = 0;
   if (st && tid == 0) st[0] = wall_clock();
 
   // ---------------------------------------------------------------- dispatch (every WG)
@@ -293,6 +308,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // from one counter, then L2 units (active expert a, 128 output rows b) from another. A
   // workgroup starts on L2 units only after the L1 counter ran out, so an L2 unit's wait is
   // only on L1 units already claimed by running workgroups, which never wait.
+  //
+  // Software pipeline: right after a unit's last matrix-core ops the next unit's weight tiles
+  // are issued into the same registers (dead by then), so they stream in
+  // while the unit's epilogue, stores and hand-offs run. A unit's arrival signal (L1) or
+  // combine arrivals (L2) are sent one unit later, after the next unit's matrix-core ops,
+  // when the unit's own stores have long completed (the wait for them is then free).
   const int U1 = n_active * QN, U2 = n_active * NBL2;
   constexpr int CH = 2;
   const int c = lane & 15, kq = lane >> 4;
@@ -300,38 +321,50 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // (gate or up), K half kh = w >> 2. L2: wave w owns rows 16 (NW b + w) .. +16, full K.
   const int pp = wv & 1, gu = (wv >> 1) & 1, kh = wv >> 2;
   constexpr int NSD = (KH + 3) / 4 + 1;                     // L1 scale dwords per K half
+  const int g_lo = (kh * KH) >> 2;
   int staged = -1;          // (phase, a, slab) currently in s.bst
+  int par = 0;              // LDS slot of the next chunk broadcast (alternates)
+
+  // ================================================================ L1 phase
   {
-    int* claim = p.counters + CNT_CLAIM + 0;
-    int next_claim = 0;
-    if (tid == 0) next_claim = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (;;) {
-      if (tid == 0) s.claim = next_claim;
-      __syncthreads();
-      const int base = __builtin_amdgcn_readfirstlane(s.claim);   // uniform: keep it scalar
-      __syncthreads();
-      if (base >= U1) break;
-      // claim the next chunk now; its value is needed only after this chunk
-      if (tid == 0) next_claim = base + CH < U1 ? __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
-      const int top = base + CH < U1 ? base + CH : U1;
-      for (int u = base; u < top; ++u) {
-      // ============================================================ L1 unit
+    int* claim = p.counters + CNT_CLAIM;
+    const uint8_t* w1v = p.w1v;
+    const uint32_t* w1s = p.w1s;
+    auto load1 = [w1v, w1s, lane, pp, gu, kh, g_lo](int u, U4 (&w)[KH], uint32_t (&sw)[NSD]) {
       const int a = u / QN, q = u % QN;
-      U4 wt[KH];
-      uint32_t sd[NSD];
-      {
-        const size_t blk = (size_t)s.act[a] * NB1 + 2 * (2 * q + pp) + gu;
-        const uint8_t* base_w = p.w1v + (blk * KT1 + kh * KH) * 1024 + lane * 16;
+      const size_t blk = (size_t)s.act[a] * NB1 + 2 * (2 * q + pp) + gu;
+      const uint8_t* bw = w1v + (blk * KT1 + kh * KH) * 1024 + lane * 16;
 #pragma unroll
-        for (int k = 0; k < KH; ++k) wt[k] = *reinterpret_cast<const U4*>(base_w + k * 1024);
-        const int g_lo = (kh * KH) >> 2;
-        const uint32_t* sb = p.w1s + (blk * KG1 + g_lo) * 64 + lane;
+      for (int k = 0; k < KH; ++k) w[k] = ld_stream(bw + k * 1024);
+      const uint32_t* sb = w1s + (blk * KG1 + g_lo) * 64 + lane;
 #pragma unroll
-        for (int j = 0; j < NSD; ++j) sd[j] = g_lo + j < KG1 ? sb[j * 64] : 0u;
-      }
+      for (int j = 0; j < NSD; ++j) sw[j] = g_lo + j < KG1 ? __builtin_nontemporal_load(sb + j * 64) : 0u;
+    };
+    if (tid == 0) s.claimv[par] = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    int cur = __builtin_amdgcn_readfirstlane(s.claimv[par]);
+    par ^= 1;
+    int top = cur + CH < U1 ? cur + CH : U1;
+    int ahead = U1;           // thread 0: the chunk claimed one chunk ahead
+    if (tid == 0 && cur + CH < U1) ahead = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    U4 wt[KH];
+    uint32_t sd[NSD];
+    if (cur < U1) load1(cur, wt, sd);
+    int pending = -1;         // expert slot of the previous unit; its arrival is not sent yet
+    while (cur < U1) {
+      const int a = cur / QN, q = cur % QN;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const int pr = 2 * q + pp;                       // (gate, up) block pair of this wave
-      const int g_lo = (kh * KH) >> 2;
+      int nxt = cur + 1;
+      if (nxt >= top) {       // next chunk: the one claimed ahead, broadcast through LDS
+        if (tid == 0) s.claimv[par] = ahead;
+        __syncthreads();
+        nxt = __builtin_amdgcn_readfirstlane(s.claimv[par]);
+        par ^= 1;
+        top = nxt + CH < U1 ? nxt + CH : U1;
+        if (tid == 0) ahead = nxt + CH < U1 ? __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
+      }
+      const long long t_u0 = st ? wall_clock() : 0;
       for (int s0 = 0; s0 < n; s0 += 16) {
         const int key = (a << 16) | s0;
         if (key != staged) {
@@ -366,17 +399,26 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if constexpr ((k & (ACT == DGM_ACT_MXFP4 ? 3 : 1)) == (ACT == DGM_ACT_MXFP4 ? 3 : 1))
             __builtin_amdgcn_sched_barrier(0);
         });
+        after_mfma(acc);
+        if (st) l1_load_ticks += wall_clock() - t_u0;
+        const bool signal = s0 == 0 && pending >= 0;
+        if (signal) wait_mem();                        // the previous unit's stores completed
+        // the last slab's matrix-core ops were the last readers: reuse the registers
+        if (s0 + 16 >= n && nxt < U1) load1(nxt, wt, sd);
+        __builtin_amdgcn_sched_barrier(0);
 
         if (kh == 1) {
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 4; ++i) s.red[pp][gu][lane][i] = acc[i];
         }
         __syncthreads();
+        // every wave waited for its stores before the barrier: the previous unit has arrived
+        if (signal && tid == 0) __hip_atomic_fetch_add(&l1_done[pending], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (kh == 0) {
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 4; ++i) acc[i] = acc[i] + s.red[pp][gu][lane][i];
           if (gu == 1) {
-  #pragma unroll
+#pragma unroll
             for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
           }
         }
@@ -385,11 +427,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         if (kh == 0 && gu == 0) {
           const float wt_r = s.slab_w[c];
           float am = 0.f;
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float g = fminf(round_bf16(acc[i]), p.clamp);
             const float uu = fminf(fmaxf(round_bf16(s.upv[pp][lane][i]), -p.clamp), p.clamp);
-            const float sgm = 1.0f / (1.0f + expf(-g));
+            const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
             act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
             am = fmaxf(am, fabsf(act[i]));
           }
@@ -404,10 +446,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           // lane group kq holds features 16 pr + 4 kq .. +3 of column c
           if (ACT == DGM_ACT_MXFP4) {
             const uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
-            const float sc = e8m0_value(code);
+            const float isc = e8m0_inv(code);
             uint32_t w = 0;
-  #pragma unroll
-            for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] / sc) << (4 * i);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] * isc) << (4 * i);
             // gather the 4 lane groups: 16 features = 8 bytes of the intermediate row
             const uint64_t w64 = (uint64_t)(w & 0xffffu) | ((uint64_t)(__shfl(w, c + 16) & 0xffffu) << 16) |
                                  ((uint64_t)(__shfl(w, c + 32) & 0xffffu) << 32) |
@@ -418,10 +460,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             }
           } else {
             const int code = (int)ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f) + 127;
-            const float sc = e8m0_value_any((uint32_t)code);
+            const float isc = e8m0_inv((uint32_t)code);
             uint32_t w = 0;
-  #pragma unroll
-            for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] / sc) << (8 * i);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] * isc) << (8 * i);
             // lanes 0-15: features 0-7 (groups 0, 1); lanes 16-31: features 8-15 (groups 2, 3)
             const int src_lo = lane < 16 ? c : c + 32, src_hi = lane < 16 ? c + 16 : c + 48;
             const uint64_t w64 = (uint64_t)__shfl(w, src_lo) | ((uint64_t)__shfl(w, src_hi) << 32);
@@ -431,43 +473,98 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             }
           }
         }
+        if (signal) pending = -1;
       }
-      // arrival: this unit's intermediate stores have completed (the wait also covers the
-      // next task's tiles issued above, which the next iteration needs first anyway)
+      pending = a;
+      cur = nxt;
+    }
+    if (pending >= 0) {       // the last unit's arrival
+      const long long t_w0 = st ? wall_clock() : 0;
       wait_mem();
       __syncthreads();
-      if (tid == 0) __hip_atomic_fetch_add(&l1_done[a], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+      if (tid == 0) __hip_atomic_fetch_add(&l1_done[pending], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (st) l1_sig_ticks += wall_clock() - t_w0;
     }
   }
+  if (st && tid == 0) st[2] = wall_clock();
+
+  // ================================================================ L2 phase
   {
     int* claim = p.counters + CNT_CLAIM + 1;
-    int next_claim = 0;
-    if (tid == 0) next_claim = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (st && tid == 0) st[2] = wall_clock();
-    int ready = -1;         // active expert whose L1 arrival has been observed
-    for (;;) {
-      if (tid == 0) s.claim = next_claim;
-      __syncthreads();
-      const int base = __builtin_amdgcn_readfirstlane(s.claim);   // uniform: keep it scalar
-      __syncthreads();
-      if (base >= U2) break;
-      // claim the next chunk now; its value is needed only after this chunk
-      if (tid == 0) next_claim = base + CH < U2 ? __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
-      const int top = base + CH < U2 ? base + CH : U2;
-      for (int v = base; v < top; ++v) {
+    const uint8_t* w2v = p.w2v;
+    const uint32_t* w2s = p.w2s;
+    auto load2 = [w2v, w2s, lane, wv](int v, U4 (&w)[KT2], uint32_t (&sw)[KG2]) {
       const int a = v / NBL2, b = v % NBL2;
-      U4 wt[KT2];
-      uint32_t sd[KG2];
-      {
-        const size_t blk = (size_t)s.act[a] * NB2 + NW * b + wv;
-        const uint8_t* base_w = p.w2v + blk * KT2 * 1024 + lane * 16;
+      const size_t blk = (size_t)s.act[a] * NB2 + NW * b + wv;
+      const uint8_t* bw = w2v + blk * KT2 * 1024 + lane * 16;
 #pragma unroll
-        for (int k = 0; k < KT2; ++k) wt[k] = *reinterpret_cast<const U4*>(base_w + k * 1024);
+      for (int k = 0; k < KT2; ++k) w[k] = ld_stream(bw + k * 1024);
 #pragma unroll
-        for (int g = 0; g < KG2; ++g) sd[g] = p.w2s[(blk * KG2 + g) * 64 + lane];
-      }
+      for (int g = 0; g < KG2; ++g) sw[g] = __builtin_nontemporal_load(w2s + (blk * KG2 + g) * 64 + lane);
+    };
+    __syncthreads();
+    if (tid == 0) s.claimv[par] = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    int cur = __builtin_amdgcn_readfirstlane(s.claimv[par]);
+    par ^= 1;
+    int top = cur + CH < U2 ? cur + CH : U2;
+    int ahead = U2;
+    if (tid == 0 && cur + CH < U2) ahead = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    U4 wt[KT2];
+    uint32_t sd[KG2];
+    if (cur < U2) load2(cur, wt, sd);
+    int ready = -1;           // active expert whose L1 arrival has been observed
+    int pv = -1;              // previous unit; its combine arrivals are not sent yet
+    // Combine: per (token, row block) arrival counter; the arrival that completes it sums the
+    // token's slots in slot order and writes y. The arrivals of unit `v` are two per-thread
+    // atomics at most (an expert holds <= 2 FT routes), issued before the next unit's loads
+    // and consumed after them.
+    static_assert(FUSED_MAX_ROUTES <= 2 * FT, "combine arrivals: two routes per thread at most");
+    auto arrive = [comb, tid](int v, int topk, int& o0, int& o1) {
+      const int a = v / NBL2, b = v % NBL2;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
+      o0 = o1 = -1;
+      if (tid < n)
+        o0 = __hip_atomic_fetch_add(&comb[(s.routes[r0 + tid] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid + FT < n)
+        o1 = __hip_atomic_fetch_add(&comb[(s.routes[r0 + tid + FT] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    auto finish = [&](int v, int o0, int o1) {
+      const int a = v / NBL2, b = v % NBL2;
+      const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
+      if (tid < n) {
+        const int tk = s.routes[r0 + tid] / p.topk;
+        if (o0 == s.nslot[tk] - 1) s.last[atomicAdd(&s.nlast, 1)] = tk;
+      }
+      if (tid + FT < n) {
+        const int tk = s.routes[r0 + tid + FT] / p.topk;
+        if (o1 == s.nslot[tk] - 1) s.last[atomicAdd(&s.nlast, 1)] = tk;
+      }
+      __syncthreads();
+      const int nl = s.nlast;
+      constexpr int RB = 16 * NW;
+      for (int i = tid; i < nl * RB; i += FT) {
+        const int tk = s.last[i / RB], row = b * RB + (i % RB);
+        float sum = 0.f;
+        for (int sl = 0; sl < p.topk; ++sl)
+          if (s.exp_of_route[tk * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)tk * p.topk + sl) * H + row);
+        p.y[(size_t)tk * H + row] = f32_to_bf16(sum);
+      }
+      __syncthreads();
+      if (tid == 0) s.nlast = 0;   // the next appends follow at least one more barrier
+    };
+    while (cur < U2) {
+      const int a = cur / NBL2, b = cur % NBL2;
+      const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
+      int nxt = cur + 1;
+      if (nxt >= top) {
+        if (tid == 0) s.claimv[par] = ahead;
+        __syncthreads();
+        nxt = __builtin_amdgcn_readfirstlane(s.claimv[par]);
+        par ^= 1;
+        top = nxt + CH < U2 ? nxt + CH : U2;
+        if (tid == 0) ahead = nxt + CH < U2 ? __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
+      }
       if (a != ready) {
         long long w0 = st ? wall_clock() : 0;
         if (tid == 0) spin_until(&l1_done[a], QN, p.spin_limit, err);
@@ -498,44 +595,43 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if constexpr ((k & (ACT == DGM_ACT_MXFP4 ? 3 : 1)) == (ACT == DGM_ACT_MXFP4 ? 3 : 1))
             __builtin_amdgcn_sched_barrier(0);
         });
+        after_mfma(acc);
+        const bool send = s0 == 0 && pv >= 0;
+        int o0 = -1, o1 = -1;
+        if (send) {
+          wait_mem();                                  // the previous unit's route outputs landed
+          __syncthreads();
+          arrive(pv, p.topk, o0, o1);
+        }
+        if (s0 + 16 >= n && nxt < U2) load2(nxt, wt, sd);
         __builtin_amdgcn_sched_barrier(0);
-        
         if (s0 + c < n) {
-          const int rid = s.routes[r0 + s0 + c];
-          float* dst = p.partials + (size_t)rid * H + (NW * b + wv) * 16 + 4 * kq;
+          float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * b + wv) * 16 + 4 * kq;
           st_agent64(dst, (uint64_t)__float_as_uint(acc[0]) | ((uint64_t)__float_as_uint(acc[1]) << 32));
           st_agent64(dst + 2, (uint64_t)__float_as_uint(acc[2]) | ((uint64_t)__float_as_uint(acc[3]) << 32));
         }
+        if (send) {
+          finish(pv, o0, o1);
+          pv = -1;
+        }
       }
-      // ---- combine: the arrival that completes (token, row block b) writes y
+      pv = cur;
+      cur = nxt;
+    }
+    if (pv >= 0) {            // the last unit's arrivals
       wait_mem();
       __syncthreads();
-      for (int r = tid; r < n; r += FT) {
-        const int tk = s.routes[r0 + r] / p.topk;
-        const int old = __hip_atomic_fetch_add(&comb[tk * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (old == s.nslot[tk] - 1) s.last[atomicAdd(&s.nlast, 1)] = tk;
-      }
-      __syncthreads();
-      const int nl = s.nlast;
-      constexpr int RB = 16 * NW;
-      for (int i = tid; i < nl * RB; i += FT) {
-        const int tk = s.last[i / RB], row = b * RB + (i % RB);
-        float sum = 0.f;
-        for (int sl = 0; sl < p.topk; ++sl)
-          if (s.exp_of_route[tk * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)tk * p.topk + sl) * H + row);
-        p.y[(size_t)tk * H + row] = f32_to_bf16(sum);
-      }
-      __syncthreads();
-      if (tid == 0) s.nlast = 0;
-      }
+      int o0, o1;
+      arrive(pv, p.topk, o0, o1);
+      finish(pv, o0, o1);
     }
   }
 
   // ---------------------------------------------------------------- teardown
   if (st && tid == 0) {
     st[4] = wall_clock();
-    st[6] = wait_ticks;
-    st[7] = 0;
+    st[6] = l1_load_ticks;
+    st[7] = l1_sig_ticks;
   }
   wait_mem();
   __syncthreads();

@@ -37,6 +37,7 @@ struct FusedParams {
   int stamp_rows;
   int M, topk, expert_begin, E_local;
   float clamp;
+  int fast_math;
   int spin_limit;
 };
 

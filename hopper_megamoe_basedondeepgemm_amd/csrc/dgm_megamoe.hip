@@ -310,7 +310,7 @@ template <int KT, int ACT>
 __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, const uint32_t* __restrict__ w1s,
                                             const uint8_t* __restrict__ x, const uint8_t* __restrict__ xsf,
                                             const float* __restrict__ topk_w, uint8_t* __restrict__ pool_base,
-                                            int E_local, int I, int topk, float clamp,
+                                            int E_local, int I, int topk, float clamp, int fast_math,
                                             uint8_t* __restrict__ mid, uint8_t* __restrict__ mid_sf) {
   constexpr int KG = (KT + 3) / 4;
   constexpr int XB = ACT == DGM_ACT_MXFP4 ? KT * 64 : KT * 128;   // x row bytes (H/2 or H)
@@ -412,7 +412,7 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
       for (int i = 0; i < 4; ++i) {
         float g = fminf(round_bf16(accg[i]), clamp);
         float u = fminf(fmaxf(round_bf16(accu[i]), -clamp), clamp);
-        float sg1 = 1.0f / (1.0f + expf(-g));
+        float sg1 = fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
         act[i] = valid ? ((g * sg1) * u) * wt : 0.f;
         am = fmaxf(am, fabsf(act[i]));
       }
@@ -426,19 +426,19 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         const int f0 = 16 * p + 4 * (lane >> 4);
         if (ACT == DGM_ACT_MXFP4) {
           uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
-          float s = e8m0_value(code);
+          float is = e8m0_inv(code);
           uint32_t w = 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] / s) << (4 * i);
+          for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] * is) << (4 * i);
           *reinterpret_cast<uint16_t*>(mid + (size_t)row * midb + f0 / 2) = (uint16_t)w;
           if (wv == 0 && lane < 16) mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
         } else {
           float ex = ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f);
           int code = (int)ex + 127;
-          float s = e8m0_value_any((uint32_t)code);
+          float is = e8m0_inv((uint32_t)code);
           uint32_t w = 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] / s) << (8 * i);
+          for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] * is) << (8 * i);
           *reinterpret_cast<uint32_t*>(mid + (size_t)row * midb + f0) = w;
           if (wv == 0 && lane < 16) mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
         }
@@ -553,7 +553,7 @@ int launch_experts(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, 
   hipLaunchKernelGGL((k_l1<KT1, ACT>), dim3(grid1), dim3(128), 0, stream, (const uint8_t*)A->w1_values,
                      (const uint32_t*)A->w1_scales, buf + L->x, buf + L->x_sf,
                      (const float*)(buf + L->topk_weights), pool, A->num_local_experts, A->intermediate,
-                     A->topk, A->activation_clamp, buf + L->mid, buf + L->mid_sf);
+                     A->topk, A->activation_clamp, A->fast_math, buf + L->mid, buf + L->mid_sf);
   int st = dgm_last_launch_status();
   if (st) return st;
   int items2 = A->num_local_experts * (A->hidden / 16);
@@ -691,6 +691,7 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.expert_begin = A->expert_begin;
     p.E_local = A->num_local_experts;
     p.clamp = A->activation_clamp;
+    p.fast_math = A->fast_math;
     p.spin_limit = 1 << 22;
     p.stamps = (long long*)A->phase_stamps;
     p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;

@@ -173,7 +173,8 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
 
 
 # ----------------------------------------------------------------------------- fused layer
-def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None):
+def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
+           fast_math=True):
     w1, sf1, _ = l1
     w2, sf2, _ = l2
     _lib.require_gpu(y, w1, sf1, w2, sf2, stats)
@@ -193,6 +194,7 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
                         num_experts=b.num_experts, expert_begin=b.expert_begin, num_local_experts=E_l,
                         topk=b.num_topk, act_format=b.act_code,
                         activation_clamp=float(activation_clamp if activation_clamp is not None else 3.0e38),
+                        fast_math=int(bool(fast_math)),
                         w1_values=w1.data_ptr(), w1_scales=sf1.data_ptr(), w2_values=w2.data_ptr(),
                         w2_scales=sf2.data_ptr(), recv_stats=stats.data_ptr() if stats is not None else None,
                         y=y.data_ptr(), buffer=b.buffer.data_ptr(), layout=ctypes.pointer(b.layout),
@@ -210,10 +212,11 @@ def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
     buffer (written by ``fable_router_quant_topk_frontend`` or by the caller): dispatch,
     L1 + SwiGLU + requant, L2, top-k combine into ``y`` (bf16 [tokens, H]).
     ``phase_stamps`` (optional int64 CUDA tensor [rows, 8]; workgroups >= rows skip): per-workgroup
-    100 MHz wall-clock stamps: entry, dispatch ready, L1 done, first L1 arrival seen, L2
-    done, exit, fence ticks, units (see ``fused_workgroups``). ``fast_math`` / ``fe_keys`` are
-    accepted for signature compatibility."""
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps)
+    100 MHz wall-clock stamps (see ``fused_workgroups``). ``fast_math`` (default True, as in the
+    reference): hardware exp2 / reciprocal in SiLU's sigmoid; False = IEEE expf and division.
+    ``fe_keys`` is accepted for signature compatibility."""
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
+           fast_math=fast_math)
 
 
 def fused_workgroups(b):
@@ -225,7 +228,7 @@ def mxfp4_mega_moe_split(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
                          fast_math=True, **_):
     """deep_gemm/mega/__init__.py:579 split API: the same layer as separate launches
     (dispatch, L1 + SwiGLU + requant, L2, combine) with the fused path's numerics."""
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, split=True)
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, split=True, fast_math=fast_math)
 
 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,

@@ -114,6 +114,7 @@ typedef struct DgmMoeArgs {
   int32_t num_tokens, hidden, intermediate, num_experts, expert_begin, num_local_experts, topk;
   int32_t act_format;
   float activation_clamp;
+  int32_t fast_math;      /* 1: hardware exp2 / reciprocal in SiLU (reference default) */
   const void* w1_values;  /* [E_local, 2I/16, H/128, 64, 16] */
   const void* w1_scales;  /* [E_local, 2I/16, ceil(H/512), 64, 4] */
   const void* w2_values;  /* [E_local, H/16, I/128, 64, 16] */
