@@ -1,12 +1,13 @@
 """Benchmark of the MI355X MegaMoE layer (one GPU).
 
-Default workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
+Headline workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
-layer forward: router + top-8 + activation cast, dispatch, L1, L2, combine). Also sweeps
-M = 2, 4, 8, 16 and reports each. Before every timed step >= 1 GiB is written and
+layer forward: router + top-8 + activation cast, then the fused kernel: dispatch, L1, L2,
+combine). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
+one seeded unbalanced-routing run at M=16. Before every timed step >= 1 GiB is written and
 then 1 GiB of other data is read, so neither the 256 MB MALL nor the L2s hold weights (and
-no dirty lines are left to drain inside the timed region); the timed region is the layer
-alone, with HIP events on the stream the layer runs on.
+no dirty lines are left to drain inside the timed region); per step, HIP events on the
+layer's stream bracket the frontend and the fused kernel.
 
 Prints ONE JSON line (the driver contract). Data are synthetic (seeded randn weights of the
 layer's shape, packed on the GPU with the MXFP4 packer).
@@ -26,6 +27,19 @@ sys.path.insert(0, HERE)
 E, H, I, TOPK = 384, 3072, 1280, 8
 MXFP4_EXPERT_BYTES = 6266880          # W1 + W2 values + E8M0 scales of one expert
 HBM_PEAK_GBS = 8000.0
+
+
+def profiled_traffic_bytes():
+    """HBM bytes per launch of the fused kernel at the headline workload, from the committed
+    rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain device copy), or None."""
+    path = os.path.join(HERE, "profiles", "k_megamoe_E384_M8_mxfp8_hbm_traffic.txt")
+    try:
+        for ln in open(path):
+            if ln.strip().startswith("traffic (fetch + write) ="):
+                return int(float(ln.split("=")[1].split()[0]) * 1e6)
+    except OSError:
+        pass
+    return None
 
 
 def log(*a):
@@ -54,6 +68,8 @@ def build_weights(torch, seed, n_experts, chunk=32):
 
 
 def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True):
+    """Times `steps` layer forwards. Per step three HIP events on the layer's stream: before the
+    frontend, between frontend and the fused MoE kernel, after it."""
     (t1, t2) = weights
     buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act)
     g = torch.Generator(device="cuda")
@@ -70,12 +86,14 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
         flush.fill_(1)
         flush_rd.sum()
     stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
 
-    def layer():
+    def layer(e=None):
+        if e: e[0].record(stream)
         dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=force_balanced)
+        if e: e[1].record(stream)
         dgm.mxfp4_mega_moe_fused(y, t1, t2, buf)
+        if e: e[2].record(stream)
 
     for _ in range(warmup):
         evict()
@@ -84,35 +102,47 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     t0 = time.perf_counter()
     for i in range(steps):
         evict()
-        starts[i].record(stream)
-        layer()
-        ends[i].record(stream)
+        layer(ev[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    us = np.array([s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)])
+    us = np.array([e[0].elapsed_time(e[2]) * 1e3 for e in ev])
+    us_fe = np.array([e[0].elapsed_time(e[1]) * 1e3 for e in ev])
+    us_moe = np.array([e[1].elapsed_time(e[2]) * 1e3 for e in ev])
     counts = buf.pool_table()[0]
     n_active = int((counts > 0).sum())
-    ok = bool(torch.isfinite(y.float()).all())
-    return dict(us_median=float(np.median(us)), us_min=float(us.min()), n_active=n_active,
+    ok = bool(torch.isfinite(y.float()).all()) and buf.kernel_error() == 0
+    return dict(us_median=float(np.median(us)), us_min=float(us.min()), fe_us=float(np.median(us_fe)),
+                moe_us=float(np.median(us_moe)), moe_us_min=float(us_moe.min()), n_active=n_active,
                 weight_bytes=n_active * MXFP4_EXPERT_BYTES, finite=ok, wall_s=wall, y=y)
 
 
-def cpu_baseline(torch_mod, packed, M=8, sample_routes=4, seed=7):
+def copy_calibration(torch, mib, reps=3):
+    """A plain device copy of `mib` MiB (read mib, write mib), for scaling HBM counters."""
+    a = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+def cpu_baseline(packed, M=8, sample_routes=16, reps=5, seed=7):
     """The oracle (numpy fp32 restatement) on the host cores: router + top-8 + cast for the
     M tokens, then `sample_routes` of the 8*M expert routes (forced-balanced: one route per
-    active expert), weights dequantised once before timing. Scaled to one layer (8*M routes)."""
+    active expert), weights dequantised once before timing (as the reference's CPU path does).
+    The route time is scaled to one layer (8*M routes). Returns (us per layer, BLAS threads)."""
     from oracle import moe, numerics as nu
-    p1, s1, p2, s2 = [t.cpu().numpy() for t in packed]
     rng = np.random.default_rng(seed)
     x = nu.round_bf16(rng.standard_normal((M, H)).astype(np.float32))
     rw = nu.round_bf16(rng.standard_normal((E, H)).astype(np.float32) * np.float32(0.02))
     idx, w = moe.balanced_routing(M, E, TOPK)
     routes = [(t, s) for t in range(M) for s in range(TOPK)][:sample_routes]
+    used = sorted({int(idx[t, s]) for t, s in routes})
+    p1, s1, p2, s2 = [np.stack([t[e].cpu().numpy() for e in used]) for t in packed]
     W1 = moe.LazyDequant(p1, s1)
     W2 = moe.LazyDequant(p2, s2)
-    pre = {int(idx[t, s]): (W1[int(idx[t, s])], W2[int(idx[t, s])]) for t, s in routes}
-    reps = []
-    for _ in range(3):
+    pre = {e: (W1[i], W2[i]) for i, e in enumerate(used)}
+    times = []
+    for _ in range(reps):
         t0 = time.perf_counter()
         logits = moe.router_logits_f32(x, rw)
         moe.topk_softmax(logits, TOPK)
@@ -125,8 +155,14 @@ def cpu_baseline(torch_mod, packed, M=8, sample_routes=4, seed=7):
             sub_idx[t, s] = e
             moe.moe_forward(x_dq, sub_idx, w, _One(e, pre[e][0]), _One(e, pre[e][1]), 0, "mxfp8")
         t_routes = time.perf_counter() - t1
-        reps.append(t_front + t_routes * (M * TOPK) / len(routes))
-    return float(np.median(reps)) * 1e6
+        times.append(t_front + t_routes * (M * TOPK) / len(routes))
+    threads = 1
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        pass
+    return float(np.median(times)) * 1e6, threads
 
 
 class _One:
@@ -145,13 +181,18 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--m", type=int, default=8)
-    ap.add_argument("--act", default="mxfp8", choices=["mxfp8", "mxfp4"])
-    ap.add_argument("--sweep", default="2,4,8,16")
+    ap.add_argument("--m", type=int, default=8, help="M of the headline line")
+    ap.add_argument("--act", default="mxfp8", choices=["mxfp8", "mxfp4"], help="activation format of the headline line")
+    ap.add_argument("--sweep", default="2,4,8,16", help="M values of the sweep (both activation formats)")
+    ap.add_argument("--sweep-steps", type=int, default=10)
+    ap.add_argument("--no-unbalanced", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (HBM counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; --gpus must be 1 (no multi-GPU path)"}))
+        print(json.dumps({"error": "this build measures one GPU: the MegaMoE layer here has no multi-GPU "
+                                   "path, so --gpus must be 1"}))
         sys.exit(2)
     import torch
     import hopper_megamoe_basedondeepgemm_amd as dgm
@@ -161,41 +202,60 @@ def main():
     g = torch.Generator(device="cuda")
     g.manual_seed(99)
     router_w = (torch.randn((E, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+
+    def entry(r):
+        gbs = r["weight_bytes"] / (r["moe_us"] * 1e-6) / 1e9
+        return dict(us=round(r["us_median"], 2), us_min=round(r["us_min"], 2), frontend_us=round(r["fe_us"], 2),
+                    moe_us=round(r["moe_us"], 2), active_experts=r["n_active"], weight_MB=round(r["weight_bytes"] / 1e6, 1),
+                    moe_weight_GBps=round(gbs, 1), moe_hbm_frac=round(gbs / HBM_PEAK_GBS, 4), ok=r["finite"])
+
+    main_r = time_layer(torch, dgm, args.m, weights, router_w, args.act, args.steps, args.warmup, 500 + args.m)
+    log(f"headline M={args.m} {args.act}: {entry(main_r)}")
     sweep = {}
-    for M in sorted(set([int(v) for v in args.sweep.split(",") if v] + [args.m])):
-        r = time_layer(torch, dgm, M, weights, router_w, args.act, args.steps if M == args.m else 10,
-                       args.warmup, 500 + M)
-        gbs = r["weight_bytes"] / (r["us_median"] * 1e-6) / 1e9
-        sweep[M] = dict(us=round(r["us_median"], 2), us_min=round(r["us_min"], 2), active_experts=r["n_active"],
-                        weight_GBps=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4), finite=r["finite"])
-        log(f"M={M}: {sweep[M]}")
-        if M == args.m:
-            main_r = r
+    for act in ("mxfp8", "mxfp4"):
+        sweep[act] = {}
+        for M in [int(v) for v in args.sweep.split(",") if v]:
+            r = time_layer(torch, dgm, M, weights, router_w, act, args.sweep_steps, args.warmup, 500 + M)
+            sweep[act][M] = entry(r)
+            log(f"M={M} {act}: {sweep[act][M]}")
+    if not args.no_unbalanced:
+        r = time_layer(torch, dgm, 16, weights, router_w, "mxfp8", args.sweep_steps, args.warmup, 777,
+                       force_balanced=False)
+        sweep["mxfp8_unbalanced_M16"] = entry(r)
+        log(f"unbalanced M=16 mxfp8: {sweep['mxfp8_unbalanced_M16']}")
+    if args.copy_calib_mib:
+        copy_calibration(torch, args.copy_calib_mib)
     cpu = None
     if not args.no_cpu_baseline:
         try:
-            cores = torch.get_num_threads()
-            us = cpu_baseline(torch, [t for t in packed], M=args.m)
-            cpu = dict(value=round(us, 1), unit="us/layer", cores=cores, kind="port",
-                       sample=f"oracle router+top8+cast for M={args.m} and 4 of {8 * args.m} expert routes, "
-                              f"scaled to {8 * args.m} routes; weights pre-dequantised")
+            t0 = time.perf_counter()
+            us, threads = cpu_baseline(packed, M=args.m)
+            cpu = dict(value=round(us, 1), unit="us/layer", cores=threads, kind="port",
+                       sample=f"oracle (numpy fp32) router+top8+cast for M={args.m}, then 16 of the {8 * args.m} "
+                              f"expert routes (weights pre-dequantised), median of 5, route time scaled to "
+                              f"{8 * args.m} routes; A-MXFP8; {time.perf_counter() - t0:.1f} s of host time")
+            log(f"cpu baseline: {cpu}")
         except Exception as ex:  # reported, never fatal
             cpu = dict(value=None, unit="us/layer", cores=None, kind="port", sample=f"failed: {ex}")
     us = main_r["us_median"]
-    achieved = main_r["weight_bytes"] / (us * 1e-6) / 1e9
+    moe_us = main_r["moe_us"]
+    achieved = main_r["weight_bytes"] / (moe_us * 1e-6) / 1e9
     line = {
         "metric": "us per MoE layer at M=2/4/8/16 (E384 H3072 I1280 top-8); weight HBM GB/s",
         "value": round(us, 2), "unit": "us/layer", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "mxfp4xmxfp8" if args.act == "mxfp8" else "mxfp4xmxfp4",
         "data": "synthetic: seeded randn bf16 weights packed to MXFP4 on the GPU, forced-balanced routing",
-        "config": {"workload": f"E384 layer on one GPU, W-MXFP4 x A-{args.act.upper()}, M={args.m}, "
-                               "forced-balanced (BASELINE config 2)",
+        "config": {"workload": f"E384 layer on one GPU (BASELINE config 2), W-MXFP4 x A-{args.act.upper()}, "
+                               f"M={args.m}, forced-balanced; value = frontend + fused MoE kernel",
                    "M": args.m, "experts": E, "hidden": H, "intermediate": I, "topk": TOPK,
-                   "active_experts": main_r["n_active"], "sweep": sweep, "mall_flush_bytes": 1 << 30},
+                   "active_experts": main_r["n_active"], "frontend_us": round(main_r["fe_us"], 2),
+                   "moe_kernel_us": round(moe_us, 2), "sweep": sweep, "mall_flush_bytes": 1 << 30},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "whole layer (frontend + dispatch + L1 + L2 + combine launches)"},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic_bytes() if (args.m == 8 and args.act == "mxfp8") else None,
+                     "kernel": "k_megamoe (fused persistent MoE kernel); achieved = active-expert MXFP4 weight "
+                               "bytes (6,266,880 B per expert) / median kernel time (HIP events)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
