@@ -12,6 +12,10 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
     # packed-fp32 VALU forms are kept out of every kernel (see the module docs)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # no wave-level rewriting of atomics: the fused kernel's work-claim atomics return values
+    # that are consumed a whole work item later, and the rewrite (reduce + broadcast) would
+    # consume them at once, i.e. wait for every weight tile still in flight
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-I" + os.path.join(os.path.dirname(HERE), "include"),
 ]
 

@@ -85,6 +85,24 @@ DGM_DEV void wait_mem() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// all but the N youngest of this wave's vector-memory operations have completed (they
+// complete in issue order)
+template <int N>
+DGM_DEV void wait_vm_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Streaming tile load issued only after the matrix-core op that produced `acc` (a register
+// dependency, so the compiler cannot hoist it above that op and needs no second register
+// set for the tile it replaces).
+DGM_DEV U4 ld_stream_after(const uint8_t* base, int off, v4f acc) {
+  asm("" : "+v"(off) : "v"(acc[0]));
+  return ld_stream(base + off);
+}
+
 constexpr int FT = 512;        // threads per workgroup (8 waves)
 constexpr int NW = FT / 64;
 
@@ -108,11 +126,8 @@ struct FusedSmem {
   };
   uint32_t bsc[(KTM + 3) / 4][64];     // its E8M0 scales, 4 K-tiles per dword
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
-  float red[2][2][64][4];              // L1: second-K-half sums [pair][gate/up][lane][i]
-  float upv[2][64][4];                 // L1: reduced up values for the gate waves
-  float amax[2][16];
-  int last[FUSED_MAX_TOKENS];
-  int nlast;
+  float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
+  float amax[4][16];                   // L1: per-token amax of each pair's 16 features
   int is_last;
   int claimv[2];
 };
@@ -226,10 +241,105 @@ DGM_DEV void stage_slab(S& s, const uint8_t* __restrict__ src, const uint8_t* __
   }
 }
 
+// A B slab held in registers between its loads and its LDS stores (the loads are issued
+// early, ahead of the weight tiles they must not queue behind). Same fragments as stage_slab.
+// Values are kept exactly as loaded (vectors, or the 64-bit halves of agent-scope loads) and
+// only combined or masked at the store: doing either earlier would wait for every older load.
+// Every lane loads (from row 0 when it has no row), so no loaded value crosses a divergent
+// branch.
+template <int KT, int ACT, bool COHERENT>
+struct SlabRegs {
+  static constexpr int FR = (KT * 64 + FT - 1) / FT;
+  v4u v0[FR], v1[FR];            // non-coherent fragments
+  uint64_t h[FR][4];             // coherent fragments: 64-bit halves (K bytes 0-15, 64-79)
+  uint32_t sb[4];                // scale dwords of K-tiles 4g .. 4g+3 (byte l/16 is this lane's)
+  uint32_t ok;                   // bit j: fragment j holds a real row; bit 8 + j: scale byte j
+  float w;
+};
+
+template <int KT, int ACT, bool COHERENT, class RowOf, class WeightOf>
+DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
+                       int row_bytes, int n, RowOf row_of, WeightOf weight_of) {
+  const int tid = threadIdx.x;
+  uint32_t ok = 0;
+#pragma unroll
+  for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+    const int f = tid + j * FT;
+    const int l = f & 63, c = l & 15;
+    const bool have = f < KT * 64 && c < n;
+    ok |= have ? 1u << j : 0u;
+    const int kt = have ? f >> 6 : 0;
+    const size_t rr = have ? (size_t)row_of(c) : 0;
+    // E2M1: 16 bytes at K = 32 g; E4M3: K = 16 g .. +16 and K = 64 + 16 g .. +16 (g = l / 16)
+    const uint8_t* q = ACT == DGM_ACT_MXFP4 ? src + rr * row_bytes + kt * 64 + (l >> 4) * 16
+                                            : src + rr * row_bytes + kt * 128 + (l >> 4) * 16;
+    if (COHERENT) {
+      r.h[j][0] = ld_agent64(q);
+      r.h[j][1] = ld_agent64(q + 8);
+      if (ACT != DGM_ACT_MXFP4) {
+        r.h[j][2] = ld_agent64(q + 64);
+        r.h[j][3] = ld_agent64(q + 72);
+      }
+    } else {
+      r.v0[j] = *reinterpret_cast<const v4u*>(q);
+      if (ACT != DGM_ACT_MXFP4) r.v1[j] = *reinterpret_cast<const v4u*>(q + 64);
+    }
+  }
+  constexpr int KG = (KT + 3) / 4;
+  static_assert(KG * 64 <= FT, "one scale word per thread");
+  {
+    const int g = tid >> 6, l = tid & 63, c = l & 15;
+    const bool have = tid < KG * 64 && c < n;
+    const size_t rr = have ? (size_t)row_of(c) : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kt = 4 * g + j;
+      const bool hb = have && kt < KT;
+      ok |= hb ? 1u << (8 + j) : 0u;
+      const uint32_t* q = reinterpret_cast<const uint32_t*>(ssrc + (hb ? rr * (KT * 4) + kt * 4 : 0));
+      r.sb[j] = COHERENT ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *q;
+    }
+  }
+  r.ok = ok;
+  r.w = tid < n && tid < 16 ? weight_of(tid) : 0.f;
+}
+
+template <int KT, int ACT, bool COHERENT, class S>
+DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
+  const int tid = threadIdx.x;
+  const v4u z = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+    const int f = tid + j * FT;
+    if (f < KT * 64) {
+      const bool have = (r.ok >> j) & 1u;
+      v4u* dst = reinterpret_cast<v4u*>(&s.bst[f >> 6][f & 63][0]);
+      if (COHERENT) {
+        const uint64_t* h = r.h[j];
+        dst[0] = have ? v4u{(uint32_t)h[0], (uint32_t)(h[0] >> 32), (uint32_t)h[1], (uint32_t)(h[1] >> 32)} : z;
+        if (ACT != DGM_ACT_MXFP4)
+          dst[S::BV - 1] = have ? v4u{(uint32_t)h[2], (uint32_t)(h[2] >> 32), (uint32_t)h[3], (uint32_t)(h[3] >> 32)} : z;
+      } else {
+        dst[0] = have ? r.v0[j] : z;
+        if (ACT != DGM_ACT_MXFP4) dst[S::BV - 1] = have ? r.v1[j] : z;
+      }
+    }
+  }
+  constexpr int KG = (KT + 3) / 4;
+  if (tid < KG * 64) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w |= ((r.ok >> (8 + j)) & 1u ? (r.sb[j] >> (8 * ((tid & 63) >> 4))) & 0xffu : 127u) << (8 * j);
+    s.bsc[tid >> 6][tid & 63] = w;
+  }
+  if (tid < 16) s.slab_w[tid] = r.w;
+}
+
 // Phase stamps (the reference's phase_stamps facility): per workgroup, 100 MHz wall clock at
 // [0] entry, [1] dispatch table ready, [2] L1 units done, [3] first L1 arrival observed,
-// [4] L2 units done, [5] exit; [6] wall ticks from L1 unit start to its matrix-core ops done
-// (weights landed), [7] wall ticks in L1 arrival signalling (store completion + barrier).
+// [4] L2 units done, [5] exit; [6] wall ticks in L1 K loops (matrix-core ops, including the
+// waits for their weight tiles), [7] wall ticks in L1 epilogues.
 DGM_DEV long long wall_clock() { return (long long)__builtin_amdgcn_s_memrealtime(); }
 
 template <int KT1, int KT2, int ACT>
@@ -242,7 +352,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   constexpr int H = KT1 * 128, I = KT2 * 128;
   constexpr int XB = ACT == DGM_ACT_MXFP4 ? H / 2 : H;     // activation row bytes
   constexpr int MB = ACT == DGM_ACT_MXFP4 ? I / 2 : I;     // intermediate row bytes
-  constexpr int QN = I / 32, NB1 = I / 8, NB2 = H / 16, NBL2 = H / (16 * NW);
+  constexpr int QN1 = I / 64, NB1 = I / 8, NB2 = H / 16, NBL2 = H / (16 * NW);
+  static_assert(I % 64 == 0, "L1 units are 64 intermediate features");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index: scalar
   const int R = p.M * p.topk;
@@ -257,7 +368,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // ---------------------------------------------------------------- dispatch (every WG)
   for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;
   for (int t = tid; t < p.M; t += FT) s.nslot[t] = 0;
-  if (tid == 0) s.nlast = 0;
   for (int r = tid; r < R; r += FT) {
     int64_t g = p.topk_idx[r];
     int64_t l = g - p.expert_begin;
@@ -304,332 +414,398 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   }
   __syncthreads();        // s.cnt / s.eoff (union with the B slab) are dead from here on
 
-  // Units are claimed dynamically, CH at a time: L1 units (active expert a, 32 features q)
-  // from one counter, then L2 units (active expert a, 128 output rows b) from another. A
-  // workgroup starts on L2 units only after the L1 counter ran out, so an L2 unit's wait is
-  // only on L1 units already claimed by running workgroups, which never wait.
-  //
-  // Software pipeline: right after a unit's last matrix-core ops the next unit's weight tiles
-  // are issued into the same registers (dead by then), so they stream in
-  // while the unit's epilogue, stores and hand-offs run. A unit's arrival signal (L1) or
-  // combine arrivals (L2) are sent one unit later, after the next unit's matrix-core ops,
-  // when the unit's own stores have long completed (the wait for them is then free).
-  const int U1 = n_active * QN, U2 = n_active * NBL2;
-  constexpr int CH = 2;
+  // Units are claimed dynamically from one atomic counter per phase, ahead of their use: L1
+  // units (active expert a, 64 intermediate features q), then L2 units (active expert a,
+  // 128 output rows b). A workgroup starts on L2 units only after the L1 counter ran out, so
+  // an L2 unit's wait is only on L1 units already claimed by running workgroups, which never
+  // wait.
+  const int U1 = n_active * QN1, U2 = n_active * NBL2;
   const int c = lane & 15, kq = lane >> 4;
-  // L1 wave roles: pair pp = w & 1 (16 of the unit's 32 features), tile gu = (w >> 1) & 1
-  // (gate or up), K half kh = w >> 2. L2: wave w owns rows 16 (NW b + w) .. +16, full K.
-  const int pp = wv & 1, gu = (wv >> 1) & 1, kh = wv >> 2;
-  constexpr int NSD = (KH + 3) / 4 + 1;                     // L1 scale dwords per K half
-  const int g_lo = (kh * KH) >> 2;
   int staged = -1;          // (phase, a, slab) currently in s.bst
-  int par = 0;              // LDS slot of the next chunk broadcast (alternates)
 
   // ================================================================ L1 phase
+  // Wave w: block pair pp = w & 3 (16 of the unit's 64 features), tile gu = w >> 2 (gate or
+  // up), full K. An L1 item is (unit, 16-route slab); a wave streams its 16-row weight block
+  // through a ring of KR tile registers: after the op on tile t it issues tile t + KR of the
+  // same item or tile t + KR - KT1 of the next item, so HBM reads never pause at item
+  // boundaries. The next item's activation slab (when it differs) is loaded before that
+  // item's tiles and stored to LDS between the epilogue's two barriers. An item's
+  // intermediate stores have completed when the next item's K loop is done (memory ops
+  // complete in order and that loop waited for younger tiles); the unit's arrival is
+  // signalled then.
   {
+    constexpr int KR = KT1 % 12 == 0 ? 12 : KT1;   // ring depth: tiles in flight per wave
+    static_assert(KT1 % KR == 0, "the ring depth divides the K-tile count");
+    const int pp = wv & 3, gu = wv >> 2;
     int* claim = p.counters + CNT_CLAIM;
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
-    auto load1 = [w1v, w1s, lane, pp, gu, kh, g_lo](int u, U4 (&w)[KH], uint32_t (&sw)[NSD]) {
-      const int a = u / QN, q = u % QN;
-      const size_t blk = (size_t)s.act[a] * NB1 + 2 * (2 * q + pp) + gu;
-      const uint8_t* bw = w1v + (blk * KT1 + kh * KH) * 1024 + lane * 16;
-#pragma unroll
-      for (int k = 0; k < KH; ++k) w[k] = ld_stream(bw + k * 1024);
-      const uint32_t* sb = w1s + (blk * KG1 + g_lo) * 64 + lane;
-#pragma unroll
-      for (int j = 0; j < NSD; ++j) sw[j] = g_lo + j < KG1 ? __builtin_nontemporal_load(sb + j * 64) : 0u;
+    const int topk = p.topk;
+    auto tile_base = [w1v, lane, pp, gu](int u) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+      return w1v + blk * KT1 * 1024 + lane * 16;
     };
-    if (tid == 0) s.claimv[par] = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    auto load_scales = [w1s, lane, pp, gu](int u, uint32_t (&sw)[KG1]) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+#pragma unroll
+      for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
+    };
+    const uint8_t* xv = p.x;
+    const uint8_t* xs = p.xsf;
+    const float* tw = p.topk_w;
+    auto load_slab = [xv, xs, tw, topk](SlabRegs<KT1, ACT, false>& r, int a, int s0) __attribute__((always_inline)) {
+      const int* rts = s.routes + s.aoff[a] + s0;
+      slab_load<KT1, ACT, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
+                          [rts, topk](int cc) { return rts[cc] / topk; }, [rts, tw](int cc) { return tw[rts[cc]]; });
+    };
+    // Claims take two consecutive units (same expert as a rule: one slab staging for both).
+    // Thread 0 keeps the chunk claimed ahead; it is broadcast one item before it is needed.
+    int ahead = U1;
+    if (tid == 0) {
+      const int c0 = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s.claimv[0] = c0;
+      if (c0 + 2 < U1) ahead = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __syncthreads();
-    int cur = __builtin_amdgcn_readfirstlane(s.claimv[par]);
-    par ^= 1;
-    int top = cur + CH < U1 ? cur + CH : U1;
-    int ahead = U1;           // thread 0: the chunk claimed one chunk ahead
-    if (tid == 0 && cur + CH < U1) ahead = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    U4 wt[KH];
-    uint32_t sd[NSD];
-    if (cur < U1) load1(cur, wt, sd);
-    int pending = -1;         // expert slot of the previous unit; its arrival is not sent yet
-    while (cur < U1) {
-      const int a = cur / QN, q = cur % QN;
-      const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
-      const int pr = 2 * q + pp;                       // (gate, up) block pair of this wave
-      int nxt = cur + 1;
-      if (nxt >= top) {       // next chunk: the one claimed ahead, broadcast through LDS
-        if (tid == 0) s.claimv[par] = ahead;
-        __syncthreads();
-        nxt = __builtin_amdgcn_readfirstlane(s.claimv[par]);
-        par ^= 1;
-        top = nxt + CH < U1 ? nxt + CH : U1;
-        if (tid == 0) ahead = nxt + CH < U1 ? __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
-      }
-      const long long t_u0 = st ? wall_clock() : 0;
-      for (int s0 = 0; s0 < n; s0 += 16) {
-        const int key = (a << 16) | s0;
-        if (key != staged) {
-          __syncthreads();
-          const int topk = p.topk;
-          const int* rts = s.routes + r0 + s0;
-          stage_slab<KT1, ACT, false>(s, p.x, p.xsf, XB, n - s0, [rts, topk](int cc) { return rts[cc] / topk; });
-          if (tid < 16) s.slab_w[tid] = s0 + tid < n ? p.topk_w[rts[tid]] : 0.f;
-          staged = key;
-          __syncthreads();
-        }
-        const bool valid = s0 + c < n;
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-        static_for<KH>([&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          const int kt = kh * KH + k;
-          v8i bop;
-          if (ACT == DGM_ACT_MXFP4) bop = as_v8i(s.bst[kt][lane][0]);
-          else bop = as_v8i(s.bst[kt][lane][0], s.bst[kt][lane][Smem::BV - 1]);
-          const int bsw = (int)s.bsc[kt >> 2][lane];
-          if constexpr (KH % 4 == 0) {
-            // the K half starts on a scale dword: byte k & 3 of dword k / 4 (hardware select)
-            acc = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wt[k]), bop, acc, (int)sd[k >> 2], bsw);
-          } else {       // small shapes
-            const int j = (kt >> 2) - g_lo, sh = 8 * (kt & 3);
-            uint32_t wsa = sd[0];
+    int q0 = __builtin_amdgcn_readfirstlane(s.claimv[0]);     // current unit
+    int q1 = q0 + 1 < U1 ? q0 + 1 : U1;                       // next unit
+    bool q1_first = false;                                    // q1 starts a claimed chunk
+    int s0 = 0;
+    U4 wr[KR];
+    uint32_t sd[KG1], sn[KG1];
+    SlabRegs<KT1, ACT, false> pre;
+    int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
+    if (q0 < U1) {
+      load_slab(pre, q0 / QN1, 0);      // (ahead of the tiles: the store below waits for it only)
+      const uint8_t* b = tile_base(q0);
 #pragma unroll
-            for (int jj = 1; jj < NSD; ++jj) wsa = j == jj ? sd[jj] : wsa;
-            acc = mfma_scale_16x16x128<4, FB>(as_v8i(wt[k]), bop, acc, (int)(wsa >> sh), bsw >> sh);
-          }
-          // keep the LDS reads of the B operand at most a few K-tiles ahead (register budget)
-          if constexpr ((k & (ACT == DGM_ACT_MXFP4 ? 3 : 1)) == (ACT == DGM_ACT_MXFP4 ? 3 : 1))
-            __builtin_amdgcn_sched_barrier(0);
-        });
-        after_mfma(acc);
-        if (st) l1_load_ticks += wall_clock() - t_u0;
-        const bool signal = s0 == 0 && pending >= 0;
-        if (signal) wait_mem();                        // the previous unit's stores completed
-        // the last slab's matrix-core ops were the last readers: reuse the registers
-        if (s0 + 16 >= n && nxt < U1) load1(nxt, wt, sd);
-        __builtin_amdgcn_sched_barrier(0);
-
-        if (kh == 1) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) s.red[pp][gu][lane][i] = acc[i];
-        }
-        __syncthreads();
-        // every wave waited for its stores before the barrier: the previous unit has arrived
-        if (signal && tid == 0) __hip_atomic_fetch_add(&l1_done[pending], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (kh == 0) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[i] = acc[i] + s.red[pp][gu][lane][i];
-          if (gu == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
-          }
-        }
-        __syncthreads();
-        float act[4];
-        if (kh == 0 && gu == 0) {
-          const float wt_r = s.slab_w[c];
-          float am = 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float g = fminf(round_bf16(acc[i]), p.clamp);
-            const float uu = fminf(fmaxf(round_bf16(s.upv[pp][lane][i]), -p.clamp), p.clamp);
-            const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
-            act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
-            am = fmaxf(am, fabsf(act[i]));
-          }
-          am = fmaxf(am, __shfl_xor(am, 16));
-          am = fmaxf(am, __shfl_xor(am, 32));
-          if (lane < 16) s.amax[pp][lane] = am;
-        }
-        __syncthreads();
-        if (kh == 0 && gu == 0) {
-          const float am = fmaxf(s.amax[0][c], s.amax[1][c]);
-          const int row = r0 + s0 + c;
-          // lane group kq holds features 16 pr + 4 kq .. +3 of column c
-          if (ACT == DGM_ACT_MXFP4) {
-            const uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
-            const float isc = e8m0_inv(code);
-            uint32_t w = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] * isc) << (4 * i);
-            // gather the 4 lane groups: 16 features = 8 bytes of the intermediate row
-            const uint64_t w64 = (uint64_t)(w & 0xffffu) | ((uint64_t)(__shfl(w, c + 16) & 0xffffu) << 16) |
-                                 ((uint64_t)(__shfl(w, c + 32) & 0xffffu) << 32) |
-                                 ((uint64_t)(__shfl(w, c + 48) & 0xffffu) << 48);
-            if (valid && lane < 16) {
-              st_agent64(p.mid + (size_t)row * MB + 8 * pr, w64);
-              if (pp == 0) st_agent8(p.mid_sf + (size_t)row * (I / 32) + q, (uint8_t)code);
-            }
-          } else {
-            const int code = (int)ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f) + 127;
-            const float isc = e8m0_inv((uint32_t)code);
-            uint32_t w = 0;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] * isc) << (8 * i);
-            // lanes 0-15: features 0-7 (groups 0, 1); lanes 16-31: features 8-15 (groups 2, 3)
-            const int src_lo = lane < 16 ? c : c + 32, src_hi = lane < 16 ? c + 16 : c + 48;
-            const uint64_t w64 = (uint64_t)__shfl(w, src_lo) | ((uint64_t)__shfl(w, src_hi) << 32);
-            if (valid && lane < 32) {
-              st_agent64(p.mid + (size_t)row * MB + 16 * pr + (lane < 16 ? 0 : 8), w64);
-              if (pp == 0 && lane < 16) st_agent8(p.mid_sf + (size_t)row * (I / 32) + q, (uint8_t)code);
-            }
-          }
-        }
-        if (signal) pending = -1;
-      }
-      pending = a;
-      cur = nxt;
-    }
-    if (pending >= 0) {       // the last unit's arrival
-      const long long t_w0 = st ? wall_clock() : 0;
-      wait_mem();
+      for (int k = 0; k < KR; ++k) wr[k] = ld_stream(b + k * 1024);
+      load_scales(q0, sd);
+      slab_store(s, pre);
+      staged = (q0 / QN1) << 16;
       __syncthreads();
-      if (tid == 0) __hip_atomic_fetch_add(&l1_done[pending], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (st) l1_sig_ticks += wall_clock() - t_w0;
     }
+    while (q0 < U1) {
+      const int a = q0 / QN1, q = q0 % QN1;
+      const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
+      const bool last_slab = s0 + 16 >= n;
+      const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
+      const bool has_next = nq < U1;
+      const int na = has_next ? nq / QN1 : -1;
+      const int nkey = (na << 16) | ns0;
+      const bool restage = has_next && nkey != staged;
+      const uint8_t* cb = tile_base(q0);
+      const uint8_t* nb = !has_next ? w1v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
+      if (has_next && nq != q0) load_scales(nq, sn);
+      if (restage) load_slab(pre, na, ns0);
+      const float wt_r = s.slab_w[c];
+      const long long t_k0 = st ? wall_clock() : 0;
+      // ---- K loop over the ring
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      // B operands are read from LDS two K-tiles ahead of their matrix-core op
+      auto bfrag = [lane](int t) __attribute__((always_inline)) {
+        return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
+      };
+      v8i bq0 = bfrag(0), bq1 = KT1 > 1 ? bfrag(1) : bq0;
+      uint32_t bs = s.bsc[0][lane];
+      static_for<KT1>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        const v8i bop = bq0;
+        const uint32_t bsw = bs;
+        bq0 = bq1;
+        if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
+        if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
+        acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, acc, (int)sd[t >> 2], (int)bsw);
+        if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
+        else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
+      });
+      // all but this loop's KR youngest tile loads are done: the previous item's stores too
+      wait_vm_le<KR>();
+      const long long t_e0 = st ? wall_clock() : 0;
+      if (st) l1_load_ticks += t_e0 - t_k0;
+      if (gu == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
+      }
+      // the unit after q1: its pair, or the chunk claimed ahead (broadcast here)
+      const bool bcast = last_slab && q1 < U1 && !q1_first;
+      if (tid == 0 && bcast) s.claimv[0] = ahead;
+      __syncthreads();                                   // (1) up sums visible, slab free
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pend = -1;
+      int q2 = U1;
+      bool q2_first = false;
+      if (bcast) {
+        q2 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
+        q2_first = true;
+        if (tid == 0) ahead = q2 + 2 < U1 ? __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
+      } else if (last_slab && q1 < U1) {
+        q2 = q1 + 1 < U1 ? q1 + 1 : U1;
+      }
+      if (restage) {
+        slab_store(s, pre);
+        staged = nkey;
+      }
+      const bool valid = s0 + c < n;
+      const int pr = 4 * q + pp;                         // 16-feature block of this pair
+      float act[4];
+      if (gu == 0) {
+        float am = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g = fminf(round_bf16(acc[i]), p.clamp);
+          const float uu = fminf(fmaxf(round_bf16(s.upv[pp][lane][i]), -p.clamp), p.clamp);
+          const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
+          act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
+          am = fmaxf(am, fabsf(act[i]));
+        }
+        am = fmaxf(am, __shfl_xor(am, 16));
+        am = fmaxf(am, __shfl_xor(am, 32));
+        if (lane < 16) s.amax[pp][lane] = am;
+      }
+      __syncthreads();                                   // (2) amax visible, next slab staged
+      if (gu == 0) {
+        const float am = fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
+        const int row = r0 + s0 + c;
+        // lane group kq holds features 16 pr + 4 kq .. +3 of column c
+        if (ACT == DGM_ACT_MXFP4) {
+          const uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
+          const float isc = e8m0_inv(code);
+          uint32_t w = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] * isc) << (4 * i);
+          // gather the 4 lane groups: 16 features = 8 bytes of the intermediate row
+          const uint64_t w64 = (uint64_t)(w & 0xffffu) | ((uint64_t)(__shfl(w, c + 16) & 0xffffu) << 16) |
+                               ((uint64_t)(__shfl(w, c + 32) & 0xffffu) << 32) |
+                               ((uint64_t)(__shfl(w, c + 48) & 0xffffu) << 48);
+          if (valid && lane < 16) {
+            st_agent64(p.mid + (size_t)row * MB + 8 * pr, w64);
+            if ((pp & 1) == 0) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
+          }
+        } else {
+          const int code = (int)ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f) + 127;
+          const float isc = e8m0_inv((uint32_t)code);
+          uint32_t w = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] * isc) << (8 * i);
+          // lanes 0-15: features 0-7 (groups 0, 1); lanes 16-31: features 8-15 (groups 2, 3)
+          const int src_lo = lane < 16 ? c : c + 32, src_hi = lane < 16 ? c + 16 : c + 48;
+          const uint64_t w64 = (uint64_t)__shfl(w, src_lo) | ((uint64_t)__shfl(w, src_hi) << 32);
+          if (valid && lane < 32) {
+            st_agent64(p.mid + (size_t)row * MB + 16 * pr + (lane < 16 ? 0 : 8), w64);
+            if ((pp & 1) == 0 && lane < 16) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
+          }
+        }
+      }
+      if (st) l1_sig_ticks += wall_clock() - t_e0;
+      if (last_slab) {
+        pend = a;
+        if (nq != q0) {
+#pragma unroll
+          for (int g = 0; g < KG1; ++g) sd[g] = sn[g];
+        }
+        q0 = q1;
+        q1 = q2;
+        q1_first = q2_first;
+        s0 = 0;
+      } else {
+        s0 += 16;
+      }
+    }
+    wait_mem();               // the last item's stores (and the dummy ring reads)
+    __syncthreads();
+    if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (st && tid == 0) st[2] = wall_clock();
 
   // ================================================================ L2 phase
+  // Wave w owns rows 16 (NW b + w) .. +16 of unit (a, b) over the full K (KT2 tiles, all in
+  // registers); right after the op on tile t it issues tile t of the next item. The next
+  // item's slab (intermediate rows of another expert) is loaded ahead when that expert's L1
+  // arrival is already complete, else staged at the item's start after a bounded wait. Route
+  // outputs (fp32) go to `partials`; one item later, when they have completed, each route
+  // bumps its (token, 128-row block) arrival counter (no return value: nothing waits here).
   {
+    static_assert(KT2 <= 16, "L2 keeps a unit's K-tiles in registers");
     int* claim = p.counters + CNT_CLAIM + 1;
     const uint8_t* w2v = p.w2v;
     const uint32_t* w2s = p.w2s;
-    auto load2 = [w2v, w2s, lane, wv](int v, U4 (&w)[KT2], uint32_t (&sw)[KG2]) {
-      const int a = v / NBL2, b = v % NBL2;
-      const size_t blk = (size_t)s.act[a] * NB2 + NW * b + wv;
-      const uint8_t* bw = w2v + blk * KT2 * 1024 + lane * 16;
-#pragma unroll
-      for (int k = 0; k < KT2; ++k) w[k] = ld_stream(bw + k * 1024);
+    const int topk = p.topk;
+    auto tile_base = [w2v, lane, wv](int v) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[v / NBL2] * NB2 + NW * (v % NBL2) + wv;
+      return w2v + blk * KT2 * 1024 + lane * 16;
+    };
+    auto load_scales = [w2s, lane, wv](int v, uint32_t (&sw)[KG2]) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[v / NBL2] * NB2 + NW * (v % NBL2) + wv;
 #pragma unroll
       for (int g = 0; g < KG2; ++g) sw[g] = __builtin_nontemporal_load(w2s + (blk * KG2 + g) * 64 + lane);
     };
+    const uint8_t* midv = p.mid;
+    const uint8_t* mids = p.mid_sf;
+    auto load_slab = [midv, mids](SlabRegs<KT2, ACT, true>& r, int a, int s0) __attribute__((always_inline)) {
+      const int rb = s.aoff[a] + s0;
+      slab_load<KT2, ACT, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
+                                [](int) { return 0.f; });
+    };
+    // arrivals of item (unit v, slab s0): its routes' outputs for row block v % NBL2 are complete
+    auto arrive = [comb, tid, topk](int v, int s0) __attribute__((always_inline)) {
+      const int a = v / NBL2, b = v % NBL2;
+      const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
+      for (int r = tid; r < n && r < 16; r += FT)
+        __hip_atomic_fetch_add(&comb[(s.routes[r0 + r] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     __syncthreads();
-    if (tid == 0) s.claimv[par] = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    int cur = __builtin_amdgcn_readfirstlane(s.claimv[par]);
-    par ^= 1;
-    int top = cur + CH < U2 ? cur + CH : U2;
     int ahead = U2;
-    if (tid == 0 && cur + CH < U2) ahead = __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    U4 wt[KT2];
-    uint32_t sd[KG2];
-    if (cur < U2) load2(cur, wt, sd);
-    int ready = -1;           // active expert whose L1 arrival has been observed
-    int pv = -1;              // previous unit; its combine arrivals are not sent yet
-    // Combine: per (token, row block) arrival counter; the arrival that completes it sums the
-    // token's slots in slot order and writes y. The arrivals of unit `v` are two per-thread
-    // atomics at most (an expert holds <= 2 FT routes), issued before the next unit's loads
-    // and consumed after them.
-    static_assert(FUSED_MAX_ROUTES <= 2 * FT, "combine arrivals: two routes per thread at most");
-    auto arrive = [comb, tid](int v, int topk, int& o0, int& o1) {
-      const int a = v / NBL2, b = v % NBL2;
+    if (tid == 0) {
+      const int c0 = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s.claimv[0] = c0;
+      if (c0 + 2 < U2) ahead = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    int q0 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
+    int q1 = q0 + 1 < U2 ? q0 + 1 : U2;
+    bool q1_first = false;
+    int s0 = 0;
+    U4 wr[KT2];
+    uint32_t sd[KG2], sn[KG2];
+    SlabRegs<KT2, ACT, true> pre;
+    int ready = -1;           // an active expert whose L1 arrival is known complete
+    bool seen = false;        // (stamps) first L1 arrival observed
+    int pv = -1, ps0 = 0;     // the previous item, whose arrivals are not sent yet
+    if (q0 < U2) {
+      const uint8_t* b = tile_base(q0);
+#pragma unroll
+      for (int k = 0; k < KT2; ++k) wr[k] = ld_stream(b + k * 1024);
+      load_scales(q0, sd);
+    }
+    while (q0 < U2) {
+      const int a = q0 / NBL2, b = q0 % NBL2;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
-      o0 = o1 = -1;
-      if (tid < n)
-        o0 = __hip_atomic_fetch_add(&comb[(s.routes[r0 + tid] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid + FT < n)
-        o1 = __hip_atomic_fetch_add(&comb[(s.routes[r0 + tid + FT] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    auto finish = [&](int v, int o0, int o1) {
-      const int a = v / NBL2, b = v % NBL2;
-      const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
-      if (tid < n) {
-        const int tk = s.routes[r0 + tid] / p.topk;
-        if (o0 == s.nslot[tk] - 1) s.last[atomicAdd(&s.nlast, 1)] = tk;
-      }
-      if (tid + FT < n) {
-        const int tk = s.routes[r0 + tid + FT] / p.topk;
-        if (o1 == s.nslot[tk] - 1) s.last[atomicAdd(&s.nlast, 1)] = tk;
-      }
-      __syncthreads();
-      const int nl = s.nlast;
-      constexpr int RB = 16 * NW;
-      for (int i = tid; i < nl * RB; i += FT) {
-        const int tk = s.last[i / RB], row = b * RB + (i % RB);
-        float sum = 0.f;
-        for (int sl = 0; sl < p.topk; ++sl)
-          if (s.exp_of_route[tk * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)tk * p.topk + sl) * H + row);
-        p.y[(size_t)tk * H + row] = f32_to_bf16(sum);
-      }
-      __syncthreads();
-      if (tid == 0) s.nlast = 0;   // the next appends follow at least one more barrier
-    };
-    while (cur < U2) {
-      const int a = cur / NBL2, b = cur % NBL2;
-      const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
-      int nxt = cur + 1;
-      if (nxt >= top) {
-        if (tid == 0) s.claimv[par] = ahead;
-        __syncthreads();
-        nxt = __builtin_amdgcn_readfirstlane(s.claimv[par]);
-        par ^= 1;
-        top = nxt + CH < U2 ? nxt + CH : U2;
-        if (tid == 0) ahead = nxt + CH < U2 ? __hip_atomic_fetch_add(claim, CH, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
-      }
-      if (a != ready) {
-        long long w0 = st ? wall_clock() : 0;
-        if (tid == 0) spin_until(&l1_done[a], QN, p.spin_limit, err);
+      const int key = (1 << 30) | (a << 16) | s0;
+      if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
+        const long long w0 = st ? wall_clock() : 0;
+        if (a != ready) {
+          if (tid == 0) spin_until(&l1_done[a], QN1, p.spin_limit, err);
+          ready = a;
+        }
         __syncthreads();
         if (st) {
           wait_ticks += wall_clock() - w0;
-          if (tid == 0 && ready == -1) st[3] = wall_clock();
+          if (tid == 0 && !seen) st[3] = wall_clock();
+          seen = true;
         }
-        ready = a;
+        const int rb = r0 + s0;
+        stage_slab<KT2, ACT, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
+        staged = key;
+        __syncthreads();
       }
-      for (int s0 = 0; s0 < n; s0 += 16) {
-        const int key = (1 << 30) | (a << 16) | s0;
-        if (key != staged) {
-          __syncthreads();
-          const int rb = r0 + s0;
-          stage_slab<KT2, ACT, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
-          staged = key;
-          __syncthreads();
-        }
-        v4f acc = {0.f, 0.f, 0.f, 0.f};
-        static_for<KT2>([&](auto kc) {
-          constexpr int k = decltype(kc)::value;
-          v8i bop;
-          if (ACT == DGM_ACT_MXFP4) bop = as_v8i(s.bst[k][lane][0]);
-          else bop = as_v8i(s.bst[k][lane][0], s.bst[k][lane][Smem::BV - 1]);
-          acc = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wt[k]), bop, acc, (int)sd[k >> 2],
-                                                              (int)s.bsc[k >> 2][lane]);
-          if constexpr ((k & (ACT == DGM_ACT_MXFP4 ? 3 : 1)) == (ACT == DGM_ACT_MXFP4 ? 3 : 1))
-            __builtin_amdgcn_sched_barrier(0);
-        });
-        after_mfma(acc);
-        const bool send = s0 == 0 && pv >= 0;
-        int o0 = -1, o1 = -1;
-        if (send) {
-          wait_mem();                                  // the previous unit's route outputs landed
-          __syncthreads();
-          arrive(pv, p.topk, o0, o1);
-        }
-        if (s0 + 16 >= n && nxt < U2) load2(nxt, wt, sd);
-        __builtin_amdgcn_sched_barrier(0);
-        if (s0 + c < n) {
-          float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * b + wv) * 16 + 4 * kq;
-          st_agent64(dst, (uint64_t)__float_as_uint(acc[0]) | ((uint64_t)__float_as_uint(acc[1]) << 32));
-          st_agent64(dst + 2, (uint64_t)__float_as_uint(acc[2]) | ((uint64_t)__float_as_uint(acc[3]) << 32));
-        }
-        if (send) {
-          finish(pv, o0, o1);
-          pv = -1;
+      const bool last_slab = s0 + 16 >= n;
+      const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
+      const bool has_next = nq < U2;
+      const int na = has_next ? nq / NBL2 : -1;
+      const int nkey = (1 << 30) | (na << 16) | ns0;
+      // prefetch the next item's slab if it differs and its expert's L1 is complete
+      bool pf = false;
+      if (has_next && nkey != key) {
+        if (tid == 0)
+          s.claimv[1] = na == ready || __hip_atomic_load(&l1_done[na], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
+        __syncthreads();
+        pf = __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0;
+        if (pf) {
+          ready = na;
+          load_slab(pre, na, ns0);
         }
       }
-      pv = cur;
-      cur = nxt;
+      const uint8_t* cb = tile_base(q0);
+      const uint8_t* nb = !has_next ? w2v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
+      if (has_next && nq != q0) load_scales(nq, sn);
+      // ---- K loop: B operands read from LDS two K-tiles ahead
+      v4f acc = {0.f, 0.f, 0.f, 0.f};
+      auto bfrag = [lane](int t) __attribute__((always_inline)) {
+        return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
+      };
+      v8i bq0 = bfrag(0), bq1 = KT2 > 1 ? bfrag(1) : bq0;
+      uint32_t bs = s.bsc[0][lane];
+      static_for<KT2>([&](auto tc) {
+        constexpr int t = decltype(tc)::value;
+        const v8i bop = bq0;
+        const uint32_t bsw = bs;
+        bq0 = bq1;
+        if constexpr (t + 2 < KT2) bq1 = bfrag(t + 2);
+        if constexpr ((t & 3) == 3 && t + 1 < KT2) bs = s.bsc[(t + 1) >> 2][lane];
+        acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t]), bop, acc, (int)sd[t >> 2], (int)bsw);
+        wr[t] = ld_stream_after(nb, t * 1024, acc);
+      });
+      // all but this loop's KT2 youngest tile loads are done: the previous item's stores too
+      wait_vm_le<KT2>();
+      if (s0 + c < n) {
+        float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * b + wv) * 16 + 4 * kq;
+        st_agent64(dst, (uint64_t)__float_as_uint(acc[0]) | ((uint64_t)__float_as_uint(acc[1]) << 32));
+        st_agent64(dst + 2, (uint64_t)__float_as_uint(acc[2]) | ((uint64_t)__float_as_uint(acc[3]) << 32));
+      }
+      const bool bcast = last_slab && q1 < U2 && !q1_first;
+      if (tid == 0 && bcast) s.claimv[0] = ahead;
+      __syncthreads();                                   // (1) previous outputs complete, slab free
+      if (pv >= 0) arrive(pv, ps0);
+      pv = q0;
+      ps0 = s0;
+      int q2 = U2;
+      bool q2_first = false;
+      if (bcast) {
+        q2 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
+        q2_first = true;
+        if (tid == 0) ahead = q2 + 2 < U2 ? __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
+      } else if (last_slab && q1 < U2) {
+        q2 = q1 + 1 < U2 ? q1 + 1 : U2;
+      }
+      if (pf) {
+        slab_store(s, pre);
+        staged = nkey;
+      }
+      __syncthreads();                                   // (2) next slab visible
+      if (last_slab) {
+        if (nq != q0) {
+#pragma unroll
+          for (int g = 0; g < KG2; ++g) sd[g] = sn[g];
+        }
+        q0 = q1;
+        q1 = q2;
+        q1_first = q2_first;
+        s0 = 0;
+      } else {
+        s0 += 16;
+      }
     }
-    if (pv >= 0) {            // the last unit's arrivals
-      wait_mem();
+    wait_mem();               // the last item's outputs (and the dummy reads)
+    __syncthreads();
+    if (pv >= 0) arrive(pv, ps0);
+  }
+  if (st && tid == 0) st[4] = wall_clock();
+
+  // ================================================================ combine
+  // (token t, 128-row block b) pairs, round robin over the workgroups: wait until every local
+  // route of t has delivered block b, then sum the routes in slot order (fp32) -> bf16 y. The
+  // wait is only on L2 items, which never wait on this phase.
+  {
+    constexpr int RB = 16 * NW;
+    for (int i = blockIdx.x; i < p.M * NBL2; i += gridDim.x) {
+      const int t = i / NBL2, b = i % NBL2;
+      const int need = s.nslot[t];
+      if (need == 0) continue;                           // (y row zeroed by workgroup 0)
+      if (tid == 0) spin_until(&comb[i], need, p.spin_limit, err);
       __syncthreads();
-      int o0, o1;
-      arrive(pv, p.topk, o0, o1);
-      finish(pv, o0, o1);
+      for (int j = tid; j < RB; j += FT) {
+        const int row = b * RB + j;
+        float sum = 0.f;
+        for (int sl = 0; sl < p.topk; ++sl)
+          if (s.exp_of_route[t * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)t * p.topk + sl) * H + row);
+        p.y[(size_t)t * H + row] = f32_to_bf16(sum);
+      }
     }
   }
 
   // ---------------------------------------------------------------- teardown
   if (st && tid == 0) {
-    st[4] = wall_clock();
     st[6] = l1_load_ticks;
     st[7] = l1_sig_ticks;
   }
