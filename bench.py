@@ -90,7 +90,7 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
 
     def layer(e=None):
         if e: e[0].record(stream)
-        dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=force_balanced)
+        dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=force_balanced, select_in_mega=True)
         if e: e[1].record(stream)
         dgm.mxfp4_mega_moe_fused(y, t1, t2, buf)
         if e: e[2].record(stream)

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(_HERE, "libdgm_megamoe.so")
 ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1}
 FE_FORCE_BALANCED = 1
 FE_ZERO_ROW_UNROUTED = 2
+FE_SELECT_IN_MEGA = 4
 
 EXPORTS = [
     "dgm_version", "dgm_last_error", "dgm_quantize_mxfp4", "dgm_cast_fp4_rows", "dgm_cast_fp8_rows",
@@ -28,7 +29,8 @@ EXPORTS = [
 class BufferLayout(ctypes.Structure):
     _fields_ = [("total_bytes", ctypes.c_size_t), ("x", ctypes.c_size_t), ("x_sf", ctypes.c_size_t),
                 ("topk_idx", ctypes.c_size_t), ("topk_weights", ctypes.c_size_t),
-                ("logits", ctypes.c_size_t), ("pool", ctypes.c_size_t), ("mid", ctypes.c_size_t),
+                ("logits", ctypes.c_size_t), ("token_flags", ctypes.c_size_t), ("pool", ctypes.c_size_t),
+                ("mid", ctypes.c_size_t),
                 ("mid_sf", ctypes.c_size_t), ("partials", ctypes.c_size_t), ("counters", ctypes.c_size_t),
                 ("x_row_bytes", ctypes.c_int32), ("mid_row_bytes", ctypes.c_int32),
                 ("max_routes", ctypes.c_int32)]
@@ -39,7 +41,8 @@ class MoeArgs(ctypes.Structure):
                 ("num_experts", ctypes.c_int32), ("expert_begin", ctypes.c_int32),
                 ("num_local_experts", ctypes.c_int32), ("topk", ctypes.c_int32),
                 ("act_format", ctypes.c_int32), ("activation_clamp", ctypes.c_float),
-                ("fast_math", ctypes.c_int32),
+                ("fast_math", ctypes.c_int32), ("select_in_mega", ctypes.c_int32), ("fe_flags", ctypes.c_int32),
+                ("token_offset", ctypes.c_int32),
                 ("w1_values", ctypes.c_void_p), ("w1_scales", ctypes.c_void_p),
                 ("w2_values", ctypes.c_void_p), ("w2_scales", ctypes.c_void_p),
                 ("recv_stats", ctypes.c_void_p), ("y", ctypes.c_void_p), ("buffer", ctypes.c_void_p),

@@ -113,6 +113,82 @@ DGM_DEV float sigmoid(float g) {
   return 1.0f / (1.0f + expf(-g));
 }
 
+// ---------------------------------------------------------------- top-k selection
+// Key order of the router top-k: orderable(bf16(logit)) << 16 | (0xFFFF - e), -0 -> +0, so
+// larger keys are larger values and, on ties, lower expert ids.
+DGM_DEV uint32_t topk_key(float logit, int e) {
+  uint32_t b = f32_to_bf16(logit);
+  if (b == 0x8000u) b = 0u;
+  uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (o << 16) | (0xffffu - (uint32_t)e);
+}
+DGM_DEV float key_value(uint32_t key) {
+  uint32_t o = key >> 16;
+  uint32_t b = (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
+  return bf16_to_f32((uint16_t)b);
+}
+
+// Top-k of one token's fp32 logits row (E <= 1024, topk <= 16) by one wave: k rounds of a
+// wave-wide max over the keys, then w_k = exp(v_k - v_0) / sum_k (sequential sum). Lane k <
+// topk receives slot k. zero_row: every slot -1 / 0. balanced: slot s -> s G + (g + 7 s) % G,
+// G = E / topk, weight 1 / topk (g = the token's global index).
+template <class LoadLogit>
+DGM_DEV void select_topk_wave(LoadLogit load, int E, int topk, bool balanced, int g, bool zero_row, int lane,
+                              int& idx, float& wt) {
+  idx = -1;
+  wt = 0.f;
+  if (zero_row) return;
+  if (balanced) {
+    const int G = E / topk;
+    if (lane < topk) {
+      idx = lane * G + (g + 7 * lane) % G;
+      wt = 1.0f / (float)topk;
+    }
+    return;
+  }
+  constexpr int MAXK = 16;
+  uint32_t key[MAXK];
+#pragma unroll
+  for (int i = 0; i < MAXK; ++i) {
+    const int e = lane + 64 * i;
+    key[i] = e < E ? topk_key(load(e), e) : 0u;
+  }
+  float vsel[16], ex[16];
+  int esel[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if (k < topk) {
+      uint32_t m = 0u;
+#pragma unroll
+      for (int i = 0; i < MAXK; ++i) m = key[i] > m ? key[i] : m;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t o = __shfl_xor(m, off);
+        m = o > m ? o : m;
+      }
+#pragma unroll
+      for (int i = 0; i < MAXK; ++i) key[i] = key[i] == m ? 0u : key[i];
+      vsel[k] = key_value(m);
+      esel[k] = (int)(0xffffu - (m & 0xffffu));
+    }
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if (k < topk) {
+      ex[k] = expf(vsel[k] - vsel[0]);
+      sum = sum + ex[k];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    if (k < topk && k == lane) {
+      idx = esel[k];
+      wt = ex[k] / sum;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- scopes / atomics
 DGM_DEV int atomic_add_acqrel_agent(int* p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);

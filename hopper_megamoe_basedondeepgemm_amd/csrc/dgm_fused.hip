@@ -111,6 +111,7 @@ struct FusedSmem {
   static constexpr int BV = ACT == DGM_ACT_MXFP4 ? 1 : 2;          // U4 per lane per K-tile
   static constexpr int KTM = KT1 > KT2 ? KT1 : KT2;
   int exp_of_route[FUSED_MAX_ROUTES];
+  float route_w[FUSED_MAX_ROUTES];     // routing weight of each route
   int routes[FUSED_MAX_ROUTES];
   int act[FUSED_MAX_LOCAL];
   int aoff[FUSED_MAX_LOCAL + 1];
@@ -368,10 +369,33 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // ---------------------------------------------------------------- dispatch (every WG)
   for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;
   for (int t = tid; t < p.M; t += FT) s.nslot[t] = 0;
-  for (int r = tid; r < R; r += FT) {
-    int64_t g = p.topk_idx[r];
-    int64_t l = g - p.expert_begin;
-    s.exp_of_route[r] = (g >= 0 && l >= 0 && l < p.E_local) ? (int)l : -1;
+  if (p.select) {
+    // top-k from the logits (one wave per token), as the frontend would have done
+    for (int t = wv; t < p.M; t += NW) {
+      int idx;
+      float wt;
+      const float* row = p.logits + (size_t)t * p.E;
+      select_topk_wave([row](int e) { return row[e]; }, p.E, p.topk, (p.fe_flags & DGM_FE_FORCE_BALANCED) != 0,
+                       p.token_offset + t, (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) && (p.token_flags[t] & 1),
+                       lane, idx, wt);
+      if (lane < p.topk) {
+        const int r = t * p.topk + lane;
+        const int l = idx - p.expert_begin;
+        s.exp_of_route[r] = (idx >= 0 && l >= 0 && l < p.E_local) ? l : -1;
+        s.route_w[r] = wt;
+        if (blockIdx.x == 0) {
+          p.topk_idx[r] = idx;
+          p.topk_w[r] = wt;
+        }
+      }
+    }
+  } else {
+    for (int r = tid; r < R; r += FT) {
+      int64_t g = p.topk_idx[r];
+      int64_t l = g - p.expert_begin;
+      s.exp_of_route[r] = (g >= 0 && l >= 0 && l < p.E_local) ? (int)l : -1;
+      s.route_w[r] = p.topk_w[r];
+    }
   }
   __syncthreads();
   for (int r = tid; r < R; r += FT) {
@@ -452,24 +476,20 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     };
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
-    const float* tw = p.topk_w;
-    auto load_slab = [xv, xs, tw, topk](SlabRegs<KT1, ACT, false>& r, int a, int s0) __attribute__((always_inline)) {
+    auto load_slab = [xv, xs, topk](SlabRegs<KT1, ACT, false>& r, int a, int s0) __attribute__((always_inline)) {
       const int* rts = s.routes + s.aoff[a] + s0;
       slab_load<KT1, ACT, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
-                          [rts, topk](int cc) { return rts[cc] / topk; }, [rts, tw](int cc) { return tw[rts[cc]]; });
+                                 [rts, topk](int cc) { return rts[cc] / topk; },
+                                 [rts](int cc) { return s.route_w[rts[cc]]; });
     };
-    // Claims take two consecutive units (same expert as a rule: one slab staging for both).
-    // Thread 0 keeps the chunk claimed ahead; it is broadcast one item before it is needed.
+    // Workgroup g starts with units g and G + g (every workgroup starts at once: claims on
+    // one counter would serialize them); later units are claimed one at a time from a counter
+    // (offset by 2 G), by thread 0, one item before they are needed.
+    const int G = gridDim.x;
     int ahead = U1;
-    if (tid == 0) {
-      const int c0 = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s.claimv[0] = c0;
-      if (c0 + 2 < U1) ahead = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    int q0 = __builtin_amdgcn_readfirstlane(s.claimv[0]);     // current unit
-    int q1 = q0 + 1 < U1 ? q0 + 1 : U1;                       // next unit
-    bool q1_first = false;                                    // q1 starts a claimed chunk
+    if (tid == 0 && 2 * G < U1) ahead = 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
+    int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
     U4 wr[KR];
     uint32_t sd[KG1], sn[KG1];
@@ -527,20 +547,17 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
       }
-      // the unit after q1: its pair, or the chunk claimed ahead (broadcast here)
-      const bool bcast = last_slab && q1 < U1 && !q1_first;
+      // the unit after q1 (claimed one item ago), broadcast here
+      const bool bcast = last_slab && q1 < U1;
       if (tid == 0 && bcast) s.claimv[0] = ahead;
       __syncthreads();                                   // (1) up sums visible, slab free
       if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pend = -1;
       int q2 = U1;
-      bool q2_first = false;
       if (bcast) {
         q2 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        q2_first = true;
-        if (tid == 0) ahead = q2 + 2 < U1 ? __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
-      } else if (last_slab && q1 < U1) {
-        q2 = q1 + 1 < U1 ? q1 + 1 : U1;
+        if (tid == 0)
+          ahead = q2 < U1 ? 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
       }
       if (restage) {
         slab_store(s, pre);
@@ -606,7 +623,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         }
         q0 = q1;
         q1 = q2;
-        q1_first = q2_first;
         s0 = 0;
       } else {
         s0 += 16;
@@ -654,17 +670,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       for (int r = tid; r < n && r < 16; r += FT)
         __hip_atomic_fetch_add(&comb[(s.routes[r0 + r] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
+    // units g and G + g first, then claims (offset by 2 G), as in the L1 phase
     __syncthreads();
+    const int G = gridDim.x;
     int ahead = U2;
-    if (tid == 0) {
-      const int c0 = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s.claimv[0] = c0;
-      if (c0 + 2 < U2) ahead = __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    int q0 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-    int q1 = q0 + 1 < U2 ? q0 + 1 : U2;
-    bool q1_first = false;
+    if (tid == 0 && 2 * G < U2) ahead = 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int q0 = (int)blockIdx.x < U2 ? (int)blockIdx.x : U2;
+    int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
     U4 wr[KT2];
     uint32_t sd[KG2], sn[KG2];
@@ -743,20 +755,17 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         st_agent64(dst, (uint64_t)__float_as_uint(acc[0]) | ((uint64_t)__float_as_uint(acc[1]) << 32));
         st_agent64(dst + 2, (uint64_t)__float_as_uint(acc[2]) | ((uint64_t)__float_as_uint(acc[3]) << 32));
       }
-      const bool bcast = last_slab && q1 < U2 && !q1_first;
+      const bool bcast = last_slab && q1 < U2;
       if (tid == 0 && bcast) s.claimv[0] = ahead;
       __syncthreads();                                   // (1) previous outputs complete, slab free
       if (pv >= 0) arrive(pv, ps0);
       pv = q0;
       ps0 = s0;
       int q2 = U2;
-      bool q2_first = false;
       if (bcast) {
         q2 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        q2_first = true;
-        if (tid == 0) ahead = q2 + 2 < U2 ? __hip_atomic_fetch_add(claim, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
-      } else if (last_slab && q1 < U2) {
-        q2 = q1 + 1 < U2 ? q1 + 1 : U2;
+        if (tid == 0)
+          ahead = q2 < U2 ? 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
       }
       if (pf) {
         slab_store(s, pre);
@@ -770,7 +779,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         }
         q0 = q1;
         q1 = q2;
-        q1_first = q2_first;
         s0 = 0;
       } else {
         s0 += 16;

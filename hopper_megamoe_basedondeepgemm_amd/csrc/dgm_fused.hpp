@@ -14,6 +14,9 @@ constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
 constexpr int CNT_CLAIM = 2;             // next unclaimed L1 unit, then [3] next unclaimed L2 unit
 constexpr int CNT_L1 = 64;               // [FUSED_MAX_LOCAL] L1 units done per active expert slot
 constexpr int CNT_TOTAL = CNT_L1 + FUSED_MAX_LOCAL + FUSED_MAX_TOKENS * FUSED_MAX_NB64;  // + combine counters
+constexpr int CNT_FE = CNT_TOTAL;        // frontend: arrival counters of 4-token chunks
+constexpr int CNT_FE_CHUNKS = 1024;
+constexpr int CNT_ALL = CNT_FE + CNT_FE_CHUNKS;
 
 inline __host__ __device__ int a256i(int x) { return (x + 255) & ~255; }
 
@@ -24,8 +27,10 @@ struct FusedParams {
   const uint32_t* w2s;
   const uint8_t* x;
   const uint8_t* xsf;
-  const int64_t* topk_idx;
-  const float* topk_w;
+  int64_t* topk_idx;        // read, or written by workgroup 0 when select != 0
+  float* topk_w;
+  const float* logits;      // select != 0: fp32 router logits [M, E] and token flags [M]
+  const int* token_flags;
   uint8_t* mid;
   uint8_t* mid_sf;
   float* partials;
@@ -36,6 +41,7 @@ struct FusedParams {
   long long* stamps;     // optional [stamp_rows][8] wall-clock stamps (see k_megamoe)
   int stamp_rows;
   int M, topk, expert_begin, E_local;
+  int select, fe_flags, token_offset, E;   // select the top-k in the prologue (DGM_FE_* flags)
   float clamp;
   int fast_math;
   int spin_limit;

@@ -57,171 +57,113 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
   return p;
 }
 
-// ------------------------------------------------------------------ router
-// One wave per (expert, 4-token chunk). Lane l accumulates K = 512 j + 8 l + i (j, then i
-// ascending) with fp32 FMAs of exact bf16 products, then an xor butterfly (32..1) reduces
-// the 64 lane sums. The fixed order makes the fp32 logits reproducible bit for bit.
+// ------------------------------------------------------------------ frontend
+// Router: wave w of workgroup (bx, by) computes the logits of expert 4 bx + w for tokens
+// 4 by .. +3. Lane l accumulates K = 512 j + 8 l + i (j, then i ascending) with fp32 FMAs of
+// exact bf16 products, then an xor butterfly (32..1) reduces the 64 lane sums: a fixed
+// order, so the fp32 logits are reproducible bit for bit. Workgroups with bx == 0 also record
+// each token's all-zero flag (token_flags bit 0) from the rows they hold.
+// Cast: 8 lanes per 32-element activation group, 4 elements per lane (MXFP4 rows with amax
+// floor 1e-30, MXFP8 rows with amax floor 1e-4: the rules of dgm_cast_fp4_rows /
+// dgm_cast_fp8_rows), spread over the whole grid after the router work.
 template <int J>
-__global__ void __launch_bounds__(256) k_router(const uint16_t* __restrict__ x,
-                                                const uint16_t* __restrict__ w, int M, int E,
-                                                float* __restrict__ logits) {
-  const int lane = threadIdx.x & 63;
-  const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int t0 = blockIdx.y * 4;
-  if (e >= E) return;
+__global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                  int M, int E, int act_format, float* __restrict__ logits,
+                                                  int* __restrict__ token_flags, uint8_t* __restrict__ q,
+                                                  uint8_t* __restrict__ sf) {
   constexpr int H = J * 512;
-  U4 wv[J];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // ---- router logits
+  const int e = blockIdx.x * 4 + wave;
+  const int t0 = blockIdx.y * 4;
+  {
+    U4 wv[J];
+    const int ee = e < E ? e : E - 1;
 #pragma unroll
-  for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const U4*>(w + (size_t)e * H + 512 * j + 8 * lane);
-  U4 xv[4][J];
+    for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const U4*>(w + (size_t)ee * H + 512 * j + 8 * lane);
+    U4 xv[4][J];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    int t = t0 + tt < M ? t0 + tt : M - 1;
+    for (int tt = 0; tt < 4; ++tt) {
+      int t = t0 + tt < M ? t0 + tt : M - 1;
 #pragma unroll
-    for (int j = 0; j < J; ++j) xv[tt][j] = *reinterpret_cast<const U4*>(x + (size_t)t * H + 512 * j + 8 * lane);
-  }
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      uint32_t xa[4] = {xv[tt][j].x, xv[tt][j].y, xv[tt][j].z, xv[tt][j].w};
-      uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc = fmaf(__uint_as_float(xa[q] << 16), __uint_as_float(wa[q] << 16), acc);
-        acc = fmaf(__uint_as_float(xa[q] & 0xffff0000u), __uint_as_float(wa[q] & 0xffff0000u), acc);
-      }
+      for (int j = 0; j < J; ++j) xv[tt][j] = *reinterpret_cast<const U4*>(x + (size_t)t * H + 512 * j + 8 * lane);
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
-    if (lane == 0 && t0 + tt < M) logits[(size_t)(t0 + tt) * E + e] = acc;
+    for (int tt = 0; tt < 4; ++tt) {
+      float acc = 0.f;
+      uint32_t any = 0;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        uint32_t xa[4] = {xv[tt][j].x, xv[tt][j].y, xv[tt][j].z, xv[tt][j].w};
+        uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          acc = fmaf(__uint_as_float(xa[qq] << 16), __uint_as_float(wa[qq] << 16), acc);
+          acc = fmaf(__uint_as_float(xa[qq] & 0xffff0000u), __uint_as_float(wa[qq] & 0xffff0000u), acc);
+          any |= xa[qq] & 0x7fff7fffu;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
+      const bool nonzero = __any(any != 0u);
+      if (lane == 0 && t0 + tt < M) {
+        if (e < E) logits[(size_t)(t0 + tt) * E + e] = acc;
+        if (blockIdx.x == 0 && wave == 0) token_flags[t0 + tt] = nonzero ? 0 : 1;
+      }
+    }
+  }
+  // ---- activation cast: 8 lanes per group
+  const int64_t groups = (int64_t)M * (H / 32);
+  const int64_t nlanes = (int64_t)gridDim.x * gridDim.y * 256;
+  for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid; i < groups * 8; i += nlanes) {
+    const int64_t g = i >> 3;
+    const int part = (int)(i & 7);            // elements 4 part .. +3 of the group
+    const uint2 raw = *reinterpret_cast<const uint2*>(x + g * 32 + 4 * part);
+    float v[4] = {__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                  __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    if (act_format == DGM_ACT_MXFP4) {
+      const uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-30f) / 6.0f);
+      const float sc = e8m0_value(code);
+      uint32_t o = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o |= e2m1_ties_down(v[k] / sc) << (4 * k);
+      reinterpret_cast<uint16_t*>(q)[g * 8 + part] = (uint16_t)o;
+      if (part == 0) sf[g] = (uint8_t)code;
+    } else {
+      const uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-4f) / 448.0f);
+      const float inv = 1.0f / e8m0_value(code);
+      uint32_t o = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o |= e4m3_encode(v[k] * inv) << (8 * k);
+      reinterpret_cast<uint32_t*>(q)[g * 8 + part] = o;
+      if (part == 0) sf[g] = (uint8_t)code;
+    }
   }
 }
 
-// ------------------------------------------------------------------ top-k + softmax + activation cast
+// ------------------------------------------------------------------ top-k + softmax
 // One wave per token: keys orderable(bf16(logit)) << 16 | (0xFFFF - e) (-0 -> +0), k rounds
-// of a wave-wide max select; softmax w_k = exp(v_k - v_0) / sum (sequential sum).
-DGM_DEV uint32_t topk_key(float logit, int e) {
-  uint32_t b = f32_to_bf16(logit);
-  if (b == 0x8000u) b = 0u;
-  uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-  return (o << 16) | (0xffffu - (uint32_t)e);
-}
-DGM_DEV float key_value(uint32_t key) {
-  uint32_t o = key >> 16;
-  uint32_t b = (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
-  return bf16_to_f32((uint16_t)b);
-}
-
-__global__ void __launch_bounds__(256) k_select(const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
-                                                int M, int H, int E, int topk, int flags, int token_offset,
+// of a wave-wide max select; softmax w_k = exp(v_k - v_0) / sum (sequential sum). Zero rows
+// (token_flags bit 0, with DGM_FE_ZERO_ROW_UNROUTED) get idx -1 / weight 0; forced-balanced
+// routing (DGM_FE_FORCE_BALANCED) gives slot s -> s G + (g + 7 s) % G with weight 1 / topk.
+__global__ void __launch_bounds__(256) k_select(const float* __restrict__ logits, const int* __restrict__ token_flags,
+                                                int M, int E, int topk, int flags, int token_offset,
                                                 int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= M) return;
-  bool zero_row = false;
-  if (flags & DGM_FE_ZERO_ROW_UNROUTED) {
-    uint32_t any = 0;
-    for (int k = lane; k < H; k += 64) any |= hidden[(size_t)t * H + k] & 0x7fffu;
-    zero_row = !__any(any != 0);
-  }
-  if (zero_row) {
-    if (lane < topk) { topk_idx[(size_t)t * topk + lane] = -1; topk_w[(size_t)t * topk + lane] = 0.f; }
-    return;
-  }
-  if (flags & DGM_FE_FORCE_BALANCED) {
-    if (lane < topk) {
-      int G = E / topk;
-      int g = token_offset + t;
-      topk_idx[(size_t)t * topk + lane] = (int64_t)(lane * G + (g + 7 * lane) % G);
-      topk_w[(size_t)t * topk + lane] = 1.0f / (float)topk;
-    }
-    return;
-  }
-  constexpr int MAXK = 16;   // E <= 1024
-  uint32_t key[MAXK];
-#pragma unroll
-  for (int i = 0; i < MAXK; ++i) {
-    int e = lane + 64 * i;
-    key[i] = e < E ? topk_key(logits[(size_t)t * E + e], e) : 0u;
-  }
-  float vsel[16];
-  int esel[16];
-  for (int k = 0; k < topk; ++k) {
-    uint32_t m = 0u;
-#pragma unroll
-    for (int i = 0; i < MAXK; ++i) m = key[i] > m ? key[i] : m;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      uint32_t o = __shfl_xor(m, off);
-      m = o > m ? o : m;
-    }
-#pragma unroll
-    for (int i = 0; i < MAXK; ++i) key[i] = key[i] == m ? 0u : key[i];
-    vsel[k] = key_value(m);
-    esel[k] = (int)(0xffffu - (m & 0xffffu));
-  }
-  if (lane == 0) {
-    float ex[16];
-    float s = 0.f;
-    for (int k = 0; k < topk; ++k) { ex[k] = expf(vsel[k] - vsel[0]); s = s + ex[k]; }
-    for (int k = 0; k < topk; ++k) {
-      topk_idx[(size_t)t * topk + k] = esel[k];
-      topk_w[(size_t)t * topk + k] = ex[k] / s;
-    }
-  }
-}
-
-// Activation cast into the buffer (same rules as dgm_cast_fp4_rows / dgm_cast_fp8_rows):
-// MXFP4 rows with amax floor 1e-30, MXFP8 rows with amax floor 1e-4.
-__global__ void k_cast_act(const uint16_t* __restrict__ x, int64_t groups, int act_format,
-                           uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
-  int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= groups) return;
-  float v[32];
-  const U4* p = reinterpret_cast<const U4*>(x + g * 32);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    U4 r = p[i];
-    uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[i * 8 + 2 * j] = __uint_as_float(w[j] << 16);
-      v[i * 8 + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-    }
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  if (act_format == DGM_ACT_MXFP4) {
-    uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-30f) / 6.0f);
-    float s = e8m0_value(code);
-    uint32_t o[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) w |= e2m1_ties_down(v[8 * c + j] / s) << (4 * j);
-      o[c] = w;
-    }
-    reinterpret_cast<U4*>(q)[g] = U4{o[0], o[1], o[2], o[3]};
-    sf[g] = (uint8_t)code;
-  } else {
-    uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-4f) / 448.0f);
-    float inv = 1.0f / e8m0_value(code);
-    uint32_t o[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      uint32_t w = 0;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) w |= e4m3_encode(v[4 * c + b] * inv) << (8 * b);
-      o[c] = w;
-    }
-    U4* d = reinterpret_cast<U4*>(q) + g * 2;
-    d[0] = U4{o[0], o[1], o[2], o[3]};
-    d[1] = U4{o[4], o[5], o[6], o[7]};
-    sf[g] = (uint8_t)code;
+  int idx = -1;
+  float wt = 0.f;
+  const float* row = logits + (size_t)t * E;
+  select_topk_wave([row](int e) { return row[e]; }, E, topk, (flags & DGM_FE_FORCE_BALANCED) != 0,
+                   token_offset + t, (flags & DGM_FE_ZERO_ROW_UNROUTED) && (token_flags[t] & 1), lane, idx, wt);
+  if (lane < topk) {
+    topk_idx[(size_t)t * topk + lane] = idx;
+    topk_w[(size_t)t * topk + lane] = wt;
   }
 }
 
@@ -603,11 +545,12 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   out->topk_idx = off; off += dgm_align256((size_t)R * 8);
   out->topk_weights = off; off += dgm_align256((size_t)R * 4);
   out->logits = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
+  out->token_flags = off; off += dgm_align256((size_t)max_tokens * 4);
   out->pool = off; off += dgm_align256(pool_bytes(num_local_experts, R));
   out->mid = off; off += dgm_align256((size_t)R * mb);
   out->mid_sf = off; off += dgm_align256((size_t)R * (intermediate / 32));
   out->partials = off; off += dgm_align256((size_t)R * hidden * 4);
-  out->counters = off; off += dgm_align256((size_t)CNT_TOTAL * 4);
+  out->counters = off; off += dgm_align256((size_t)CNT_ALL * 4);
   out->total_bytes = off;
   out->x_row_bytes = (int32_t)xb;
   out->mid_row_bytes = (int32_t)mb;
@@ -633,26 +576,38 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
   const uint16_t* x = (const uint16_t*)hidden_bf16;
   const uint16_t* w = (const uint16_t*)router_weight_bf16;
   float* logits = (float*)(buf + L->logits);
+  int* tflags = (int*)(buf + L->token_flags);
+#define DGM_FE(JJ)                                                                                              \
+  hipLaunchKernelGGL(k_frontend<JJ>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, act_format, logits, \
+                     tflags, buf + L->x, buf + L->x_sf)
   switch (J) {
-    case 1: hipLaunchKernelGGL(k_router<1>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
-    case 2: hipLaunchKernelGGL(k_router<2>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
-    case 4: hipLaunchKernelGGL(k_router<4>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
-    case 6: hipLaunchKernelGGL(k_router<6>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
-    case 8: hipLaunchKernelGGL(k_router<8>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, logits); break;
+    case 1: DGM_FE(1); break;
+    case 2: DGM_FE(2); break;
+    case 4: DGM_FE(4); break;
+    case 6: DGM_FE(6); break;
+    case 8: DGM_FE(8); break;
     default: DGM_CHECK_ARG(false, "hidden must be 512, 1024, 2048, 3072 or 4096");
   }
+#undef DGM_FE
   int st = dgm_last_launch_status();
-  if (st) return st;
-  hipLaunchKernelGGL(k_select, dim3((num_tokens + 3) / 4), dim3(256), 0, stream, x, logits, num_tokens, hidden,
+  if (st || (flags & DGM_FE_SELECT_IN_MEGA)) return st;
+  hipLaunchKernelGGL(k_select, dim3((num_tokens + 3) / 4), dim3(256), 0, stream, logits, tflags, num_tokens,
                      num_experts, topk, flags, token_offset, (int64_t*)(buf + L->topk_idx),
                      (float*)(buf + L->topk_weights));
-  st = dgm_last_launch_status();
-  if (st) return st;
-  int64_t groups = (int64_t)num_tokens * (hidden / 32);
-  hipLaunchKernelGGL(k_cast_act, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, stream, x, groups, act_format,
-                     buf + L->x, buf + L->x_sf);
   return dgm_last_launch_status();
 }
+
+// Writes topk_idx / topk_weights from the buffer's logits (after a DGM_FE_SELECT_IN_MEGA
+// frontend call) for the paths that read them.
+static int materialize_topk(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, hipStream_t stream) {
+  hipLaunchKernelGGL(k_select, dim3((A->num_tokens + 3) / 4), dim3(256), 0, stream, (const float*)(buf + L->logits),
+                     (const int*)(buf + L->token_flags), A->num_tokens, A->num_experts, A->topk, A->fe_flags,
+                     A->token_offset, (int64_t*)(buf + L->topk_idx), (float*)(buf + L->topk_weights));
+  return dgm_last_launch_status();
+}
+
+// Every workgroup of the fused kernel reads all tokens' logits when it selects the top-k.
+constexpr int SELECT_IN_MEGA_MAX_TOKENS = 64;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
@@ -670,6 +625,11 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   const int routes_n = A->num_tokens * A->topk;
   if (routes_n <= FUSED_MAX_ROUTES && A->num_local_experts <= FUSED_MAX_LOCAL &&
       A->num_tokens <= FUSED_MAX_TOKENS && A->hidden / 64 <= FUSED_MAX_NB64) {
+    const bool sel = A->select_in_mega && A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS;
+    if (A->select_in_mega && !sel) {
+      int st = materialize_topk(A, buf, L, stream);
+      if (st) return st;
+    }
     FusedParams p;
     p.w1v = (const uint8_t*)A->w1_values;
     p.w1s = (const uint32_t*)A->w1_scales;
@@ -677,8 +637,14 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.w2s = (const uint32_t*)A->w2_scales;
     p.x = buf + L->x;
     p.xsf = buf + L->x_sf;
-    p.topk_idx = (const int64_t*)(buf + L->topk_idx);
-    p.topk_w = (const float*)(buf + L->topk_weights);
+    p.topk_idx = (int64_t*)(buf + L->topk_idx);
+    p.topk_w = (float*)(buf + L->topk_weights);
+    p.logits = (const float*)(buf + L->logits);
+    p.token_flags = (const int*)(buf + L->token_flags);
+    p.select = sel ? 1 : 0;
+    p.fe_flags = A->fe_flags;
+    p.token_offset = A->token_offset;
+    p.E = A->num_experts;
     p.mid = buf + L->mid;
     p.mid_sf = buf + L->mid_sf;
     p.partials = (float*)(buf + L->partials);
@@ -707,6 +673,10 @@ int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   if (A->num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)A->buffer;
   const int routes_n = A->num_tokens * A->topk;
+  if (A->select_in_mega) {
+    int st0 = materialize_topk(A, buf, L, stream);
+    if (st0) return st0;
+  }
   hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(DISPATCH_THREADS), 0, stream,
                      (const int64_t*)(buf + L->topk_idx), routes_n, A->expert_begin, A->num_local_experts,
                      buf + L->pool, A->recv_stats);

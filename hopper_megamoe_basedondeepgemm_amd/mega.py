@@ -139,6 +139,8 @@ def transform_weights_for_mega_moe(l1, l2):
 
 
 # ----------------------------------------------------------------------------- frontend
+SELECT_IN_MEGA_MAX_TOKENS = 64    # every workgroup of the fused kernel reads all tokens' logits
+
 def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.Tensor, sym_buffer,
                                      quant: Optional[str] = None, stamps=None, l2_persist=None,
                                      wlayout=None, select_in_mega=None, zero_row_unrouted=None,
@@ -148,7 +150,10 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
     ``sym_buffer.x / x_sf / topk_idx / topk_weights``. ``quant`` defaults to the buffer's
     activation format. ``force_balanced`` (env DG_FE_FORCE_BALANCED) replaces the routing by
     the forced-balanced rule after the router ran; ``zero_row_unrouted`` (env
-    DG_FE_ZERO_ROW_UNROUTED, default 1) leaves all-zero rows unrouted. ``stamps``,
+    DG_FE_ZERO_ROW_UNROUTED, default 1) leaves all-zero rows unrouted. ``select_in_mega`` (env
+    DG_FE_SELECT_IN_MEGA, default 0; tokens <= 64): stop after the logits and the cast; the
+    next ``mxfp4_mega_moe_fused`` on this buffer selects the top-k in its prologue (and writes
+    ``topk_idx / topk_weights``, which are not valid before that call). ``stamps``,
     ``l2_persist`` and ``wlayout`` are H20 tuning knobs with no effect here."""
     b = sym_buffer
     _lib.require_gpu(hidden, router_weight)
@@ -163,8 +168,14 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
         force_balanced = os.environ.get("DG_FE_FORCE_BALANCED", "0") == "1"
     if zero_row_unrouted is None:
         zero_row_unrouted = os.environ.get("DG_FE_ZERO_ROW_UNROUTED", "1") == "1"
+    if select_in_mega is None:
+        select_in_mega = os.environ.get("DG_FE_SELECT_IN_MEGA", "0") == "1"
+    select_in_mega = bool(select_in_mega) and m <= SELECT_IN_MEGA_MAX_TOKENS
     flags = (_lib.FE_FORCE_BALANCED if force_balanced else 0) | \
             (_lib.FE_ZERO_ROW_UNROUTED if zero_row_unrouted else 0)
+    b._fe_select = (flags, int(token_offset)) if select_in_mega else None
+    if select_in_mega:
+        flags |= _lib.FE_SELECT_IN_MEGA
     hidden = hidden.contiguous()
     router_weight = router_weight.contiguous()
     _lib.check(_lib.load().dgm_router_topk_launch(
@@ -190,11 +201,13 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
     assert all(t.is_contiguous() for t in (w1, sf1, w2, sf2))
     if stats is not None:
         assert stats.dtype == torch.int32 and stats.numel() == E_l
+    sel = getattr(b, "_fe_select", None)
     args = _lib.MoeArgs(num_tokens=m, hidden=b.hidden, intermediate=b.intermediate_hidden,
                         num_experts=b.num_experts, expert_begin=b.expert_begin, num_local_experts=E_l,
                         topk=b.num_topk, act_format=b.act_code,
                         activation_clamp=float(activation_clamp if activation_clamp is not None else 3.0e38),
-                        fast_math=int(bool(fast_math)),
+                        fast_math=int(bool(fast_math)), select_in_mega=int(sel is not None),
+                        fe_flags=sel[0] if sel else 0, token_offset=sel[1] if sel else 0,
                         w1_values=w1.data_ptr(), w1_scales=sf1.data_ptr(), w2_values=w2.data_ptr(),
                         w2_scales=sf2.data_ptr(), recv_stats=stats.data_ptr() if stats is not None else None,
                         y=y.data_ptr(), buffer=b.buffer.data_ptr(), layout=ctypes.pointer(b.layout),
@@ -234,8 +247,9 @@ def mxfp4_mega_moe_split(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
                              cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
                              force_balanced=None, token_offset=0, **_):
-    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states."""
+    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states (the top-k
+    is selected in the fused kernel's prologue when the token count allows)."""
     fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
-                                     token_offset=token_offset)
+                                     token_offset=token_offset, select_in_mega=True)
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp)
     return y

@@ -28,6 +28,8 @@ extern "C" {
 /* frontend flags */
 #define DGM_FE_FORCE_BALANCED 1     /* DG_FE_FORCE_BALANCED: tests/test_four_api_correctness.py:125-144 */
 #define DGM_FE_ZERO_ROW_UNROUTED 2  /* DG_FE_ZERO_ROW_UNROUTED: deep_gemm/mega/__init__.py:693-696 */
+#define DGM_FE_SELECT_IN_MEGA 4     /* DG_FE_SELECT_IN_MEGA: deep_gemm/mega/__init__.py:688-692 -- the frontend
+                                       stops after logits + cast; the fused layer selects the top-k */
 
 /* Library version and the message of the last failed host-side check (thread-local). */
 int dgm_version(void);
@@ -84,6 +86,7 @@ typedef struct DgmBufferLayout {
   size_t total_bytes;
   size_t x, x_sf, topk_idx, topk_weights;       /* frontend outputs / fused-layer inputs  */
   size_t logits;                                /* fp32 router logits [max_tokens, E]      */
+  size_t token_flags;                           /* int32 [max_tokens]: bit 0 = all-zero row */
   size_t pool;                                  /* dispatch table (see DgmPoolTable)       */
   size_t mid, mid_sf;                           /* L1 -> L2 activations (pool-row order)   */
   size_t partials;                              /* fp32 [max_tokens * topk, H] route outputs */
@@ -99,7 +102,9 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
  * deep_gemm/mega/__init__.py:671 fable_router_quant_topk_frontend): bf16 router GEMV with
  * fp32 accumulation in a fixed order, bf16 logits, top-k (value desc, index asc), fp32
  * softmax of the k logits, activation cast, into the buffer views x / x_sf / topk_idx /
- * topk_weights (and fp32 logits). token_offset = global id of row 0 (forced-balanced rule). */
+ * topk_weights (and fp32 logits, token flags). token_offset = global id of row 0
+ * (forced-balanced rule). With DGM_FE_SELECT_IN_MEGA the top-k is left to the fused layer
+ * (DgmMoeArgs.select_in_mega); topk_idx / topk_weights are written by that call instead. */
 int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16,
                            int num_tokens, int hidden, int num_experts, int topk, int act_format,
                            int flags, int token_offset, void* buffer,
@@ -115,6 +120,10 @@ typedef struct DgmMoeArgs {
   int32_t act_format;
   float activation_clamp;
   int32_t fast_math;      /* 1: hardware exp2 / reciprocal in SiLU (reference default) */
+  int32_t select_in_mega; /* 1: select the top-k from the buffer's logits / token flags (after a
+                             DGM_FE_SELECT_IN_MEGA frontend call) and write topk_idx / weights */
+  int32_t fe_flags;       /* with select_in_mega: the frontend's DGM_FE_* flags */
+  int32_t token_offset;   /* with select_in_mega: global id of row 0 */
   const void* w1_values;  /* [E_local, 2I/16, H/128, 64, 16] */
   const void* w1_scales;  /* [E_local, 2I/16, ceil(H/512), 64, 4] */
   const void* w2_values;  /* [E_local, H/16, I/128, 64, 16] */

@@ -39,7 +39,7 @@ def make_weights(E, H, I, seed, scale=0.02):
 
 
 def run_layer(M, E, E_local, expert_begin, H, I, topk, fmt, seed, force_balanced=False, zero_rows=(),
-              max_tokens=None, weights=None, ep=None):
+              max_tokens=None, weights=None, ep=None, select_in_mega=False, split=False):
     import hopper_megamoe_basedondeepgemm_amd as dgm
     rng = np.random.default_rng(seed)
     x = randn_bf16(rng, (M, H))
@@ -55,8 +55,9 @@ def run_layer(M, E, E_local, expert_begin, H, I, topk, fmt, seed, force_balanced
     xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
     stats = torch.arange(E_local, dtype=torch.int32, device="cuda")
     y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
-    dgm.fable_router_quant_topk_frontend(xs, rws, buf, force_balanced=force_balanced)
-    dgm.mxfp4_mega_moe_fused(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats)
+    dgm.fable_router_quant_topk_frontend(xs, rws, buf, force_balanced=force_balanced, select_in_mega=select_in_mega)
+    layer = dgm.mxfp4_mega_moe_split if split else dgm.mxfp4_mega_moe_fused
+    layer(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats)
     torch.cuda.synchronize()
     # ---- oracle
     logits = moe.router_logits_f32(x, rw)
@@ -175,3 +176,36 @@ def test_split_matches_fused(fmt):
     dgm.mxfp4_mega_moe_split(y2, t1, t2, r["buf"])
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8"])
+def test_select_in_mega(fmt):
+    """Top-k selected in the fused kernel's prologue (frontend with select_in_mega): the same
+    routing, weights and output; topk_idx / topk_weights are written by the fused call."""
+    need_gpu()
+    M, E, H, I, topk = 6, 16, 512, 256, 4
+    r = run_layer(M, E, E, 0, H, I, topk, fmt, seed=100, select_in_mega=True)
+    check_frontend(r, fmt, M)
+    check_pool(r, E, 0)
+    print(fmt, check_y(r))
+
+
+def test_select_in_mega_zero_rows_multi_slab_and_split():
+    """select_in_mega with zero rows and > 16 routes per expert; and through the split API
+    (which materialises the top-k in a separate launch first)."""
+    need_gpu()
+    for split in (False, True):
+        r = run_layer(40, 8, 8, 0, 512, 256, 4, "mxfp4", seed=400, zero_rows=(3, 17), select_in_mega=True,
+                      split=split)
+        check_frontend(r, "mxfp4", 40, zero_rows=(3, 17))
+        check_pool(r, 8, 0)
+        print(split, check_y(r, zero_rows=(3, 17)))
+
+
+def test_select_in_mega_config1_balanced():
+    """BASELINE config 1 with the forced-balanced rule applied in the fused kernel's prologue."""
+    need_gpu()
+    r = run_layer(8, 384, 48, 0, 3072, 1280, 8, "mxfp4", seed=300, force_balanced=True, select_in_mega=True)
+    check_frontend(r, "mxfp4", 8, force_balanced=True)
+    check_pool(r, 48, 0)
+    print(check_y(r))
