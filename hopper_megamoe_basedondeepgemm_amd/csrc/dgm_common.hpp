@@ -128,6 +128,20 @@ DGM_DEV float key_value(uint32_t key) {
   return bf16_to_f32((uint16_t)b);
 }
 
+// Wave-wide max, uniform result: DPP within rows of 16 lanes (quad xor 1, quad xor 2, half
+// mirror, mirror), then the 4 row results via readlane.
+DGM_DEV uint32_t wave_max_u32(uint32_t v) {
+  auto mx = [](uint32_t a, int b) { return a > (uint32_t)b ? a : (uint32_t)b; };
+  v = mx(v, __builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+  v = mx(v, __builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+  v = mx(v, __builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false));   // row_half_mirror
+  v = mx(v, __builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false));   // row_mirror
+  const uint32_t a = __builtin_amdgcn_readlane((int)v, 15), b = __builtin_amdgcn_readlane((int)v, 31);
+  const uint32_t c = __builtin_amdgcn_readlane((int)v, 47), d = __builtin_amdgcn_readlane((int)v, 63);
+  const uint32_t ab = a > b ? a : b, cd = c > d ? c : d;
+  return ab > cd ? ab : cd;
+}
+
 // Top-k of one token's fp32 logits row (E <= 1024, topk <= 16) by one wave: k rounds of a
 // wave-wide max over the keys, then w_k = exp(v_k - v_0) / sum_k (sequential sum). Lane k <
 // topk receives slot k. zero_row: every slot -1 / 0. balanced: slot s -> s G + (g + 7 s) % G,
@@ -147,11 +161,12 @@ DGM_DEV void select_topk_wave(LoadLogit load, int E, int topk, bool balanced, in
     return;
   }
   constexpr int MAXK = 16;
+  const int nk = (E + 63) >> 6;         // key slots in use (wave-uniform)
   uint32_t key[MAXK];
 #pragma unroll
   for (int i = 0; i < MAXK; ++i) {
     const int e = lane + 64 * i;
-    key[i] = e < E ? topk_key(load(e), e) : 0u;
+    key[i] = i < nk && e < E ? topk_key(load(e), e) : 0u;
   }
   float vsel[16], ex[16];
   int esel[16];
@@ -160,14 +175,12 @@ DGM_DEV void select_topk_wave(LoadLogit load, int E, int topk, bool balanced, in
     if (k < topk) {
       uint32_t m = 0u;
 #pragma unroll
-      for (int i = 0; i < MAXK; ++i) m = key[i] > m ? key[i] : m;
+      for (int i = 0; i < MAXK; ++i)
+        if (i < nk) m = key[i] > m ? key[i] : m;
+      m = wave_max_u32(m);
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t o = __shfl_xor(m, off);
-        m = o > m ? o : m;
-      }
-#pragma unroll
-      for (int i = 0; i < MAXK; ++i) key[i] = key[i] == m ? 0u : key[i];
+      for (int i = 0; i < MAXK; ++i)
+        if (i < nk) key[i] = key[i] == m ? 0u : key[i];
       vsel[k] = key_value(m);
       esel[k] = (int)(0xffffu - (m & 0xffffu));
     }

@@ -367,27 +367,37 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[0] = wall_clock();
 
   // ---------------------------------------------------------------- dispatch (every WG)
-  for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;
   for (int t = tid; t < p.M; t += FT) s.nslot[t] = 0;
   if (p.select) {
-    // top-k from the logits (one wave per token), as the frontend would have done
-    for (int t = wv; t < p.M; t += NW) {
-      int idx;
-      float wt;
-      const float* row = p.logits + (size_t)t * p.E;
-      select_topk_wave([row](int e) { return row[e]; }, p.E, p.topk, (p.fe_flags & DGM_FE_FORCE_BALANCED) != 0,
-                       p.token_offset + t, (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) && (p.token_flags[t] & 1),
-                       lane, idx, wt);
-      if (lane < p.topk) {
-        const int r = t * p.topk + lane;
-        const int l = idx - p.expert_begin;
-        s.exp_of_route[r] = (idx >= 0 && l >= 0 && l < p.E_local) ? l : -1;
-        s.route_w[r] = wt;
-        if (blockIdx.x == 0) {
-          p.topk_idx[r] = idx;
-          p.topk_w[r] = wt;
+    // top-k from the logits, as the frontend would have done: the logits of TC tokens at a
+    // time go through LDS (the slab area, unused until the L1 phase; one coalesced pass),
+    // then one wave selects per token
+    float* lg = reinterpret_cast<float*>(&s.bst[0][0][0]);
+    const int TC = (int)(sizeof(s.bst) / 4) / p.E;
+    for (int t0 = 0; t0 < p.M; t0 += TC) {
+      const int tn = p.M - t0 < TC ? p.M - t0 : TC;
+      for (int i = tid; i < tn * p.E; i += FT) lg[i] = p.logits[(size_t)t0 * p.E + i];
+      __syncthreads();
+      for (int tt = wv; tt < tn; tt += NW) {
+        const int t = t0 + tt;
+        int idx;
+        float wt;
+        const float* row = lg + tt * p.E;
+        select_topk_wave([row](int e) { return row[e]; }, p.E, p.topk, (p.fe_flags & DGM_FE_FORCE_BALANCED) != 0,
+                         p.token_offset + t, (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) && (p.token_flags[t] & 1),
+                         lane, idx, wt);
+        if (lane < p.topk) {
+          const int r = t * p.topk + lane;
+          const int l = idx - p.expert_begin;
+          s.exp_of_route[r] = (idx >= 0 && l >= 0 && l < p.E_local) ? l : -1;
+          s.route_w[r] = wt;
+          if (blockIdx.x == 0) {
+            p.topk_idx[r] = idx;
+            p.topk_w[r] = wt;
+          }
         }
       }
+      __syncthreads();
     }
   } else {
     for (int r = tid; r < R; r += FT) {
@@ -397,6 +407,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       s.route_w[r] = p.topk_w[r];
     }
   }
+  for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;   // (shares LDS with the logits staging)
   __syncthreads();
   for (int r = tid; r < R; r += FT) {
     int e = s.exp_of_route[r];
@@ -443,7 +454,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // 128 output rows b). A workgroup starts on L2 units only after the L1 counter ran out, so
   // an L2 unit's wait is only on L1 units already claimed by running workgroups, which never
   // wait.
-  const int U1 = n_active * QN1, U2 = n_active * NBL2;
+  // L2 items span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks
+  constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2, TI2 = RB2 * KT2;
+  const int U1 = n_active * QN1, U2 = n_active * UPE2;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
 
@@ -486,8 +499,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // one counter would serialize them); later units are claimed one at a time from a counter
     // (offset by 2 G), by thread 0, one item before they are needed.
     const int G = gridDim.x;
-    int ahead = U1;
-    if (tid == 0 && 2 * G < U1) ahead = 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
+    // used as returned (any arithmetic on it here would wait for every load issued before it)
+    int ahead = -1;
+    if (tid == 0 && 2 * G < U1) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
@@ -555,9 +570,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       pend = -1;
       int q2 = U1;
       if (bcast) {
-        q2 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        if (tid == 0)
-          ahead = q2 < U1 ? 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U1;
+        const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
+        q2 = raw >= 0 && 2 * G + raw < U1 ? 2 * G + raw : U1;
+        if (q2 < U1) {
+          if (tid == 0) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          ahead = -1;
+        }
       }
       if (restage) {
         slab_store(s, pre);
@@ -635,26 +654,30 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[2] = wall_clock();
 
   // ================================================================ L2 phase
-  // Wave w owns rows 16 (NW b + w) .. +16 of unit (a, b) over the full K (KT2 tiles, all in
-  // registers); right after the op on tile t it issues tile t of the next item. The next
+  // Unit (a, b) = rows 128 RB2 b .. +128 RB2 of expert a; wave w owns the RB2 16-row blocks
+  // at 16 (NW RB2 b + RB2 w) .. (TI2 contiguous tiles over the full K). The wave streams them
+  // through a ring of KT2 tile registers; the second half of the ring (and all of it at the
+  // end) rolls into the next item's tiles right after the op that consumed a slot. The next
   // item's slab (intermediate rows of another expert) is loaded ahead when that expert's L1
   // arrival is already complete, else staged at the item's start after a bounded wait. Route
   // outputs (fp32) go to `partials`; one item later, when they have completed, each route
-  // bumps its (token, 128-row block) arrival counter (no return value: nothing waits here).
+  // bumps the arrival counters of its (token, 128-row block)s (no return value).
   {
-    static_assert(KT2 <= 16, "L2 keeps a unit's K-tiles in registers");
+    static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
     int* claim = p.counters + CNT_CLAIM + 1;
     const uint8_t* w2v = p.w2v;
     const uint32_t* w2s = p.w2s;
     const int topk = p.topk;
-    auto tile_base = [w2v, lane, wv](int v) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[v / NBL2] * NB2 + NW * (v % NBL2) + wv;
-      return w2v + blk * KT2 * 1024 + lane * 16;
+    auto blk_of = [wv](int v) __attribute__((always_inline)) {
+      return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
     };
-    auto load_scales = [w2s, lane, wv](int v, uint32_t (&sw)[KG2]) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[v / NBL2] * NB2 + NW * (v % NBL2) + wv;
+    auto tile_base = [w2v, lane, blk_of](int v) __attribute__((always_inline)) {
+      return w2v + blk_of(v) * KT2 * 1024 + lane * 16;
+    };
+    auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[RB2 * KG2]) __attribute__((always_inline)) {
+      const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
 #pragma unroll
-      for (int g = 0; g < KG2; ++g) sw[g] = __builtin_nontemporal_load(w2s + (blk * KG2 + g) * 64 + lane);
+      for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
     };
     const uint8_t* midv = p.mid;
     const uint8_t* mids = p.mid_sf;
@@ -663,23 +686,26 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       slab_load<KT2, ACT, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
                                 [](int) { return 0.f; });
     };
-    // arrivals of item (unit v, slab s0): its routes' outputs for row block v % NBL2 are complete
+    // arrivals of item (unit v, slab s0): its routes' outputs for the unit's blocks are complete
     auto arrive = [comb, tid, topk](int v, int s0) __attribute__((always_inline)) {
-      const int a = v / NBL2, b = v % NBL2;
+      const int a = v / UPE2, b = v % UPE2;
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
-      for (int r = tid; r < n && r < 16; r += FT)
-        __hip_atomic_fetch_add(&comb[(s.routes[r0 + r] / topk) * NBL2 + b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = tid; i < 16 * RB2 && i / RB2 < n; i += FT)
+        __hip_atomic_fetch_add(&comb[(s.routes[r0 + i / RB2] / topk) * NBL2 + RB2 * b + i % RB2], 1,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units g and G + g first, then claims (offset by 2 G), as in the L1 phase
     __syncthreads();
     const int G = gridDim.x;
-    int ahead = U2;
-    if (tid == 0 && 2 * G < U2) ahead = 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
+    // used as returned (any arithmetic on it here would wait for every load issued before it)
+    int ahead = -1;
+    if (tid == 0 && 2 * G < U2) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int q0 = (int)blockIdx.x < U2 ? (int)blockIdx.x : U2;
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
     U4 wr[KT2];
-    uint32_t sd[KG2], sn[KG2];
+    uint32_t sd[RB2 * KG2], sn[RB2 * KG2];
     SlabRegs<KT2, ACT, true> pre;
     int ready = -1;           // an active expert whose L1 arrival is known complete
     bool seen = false;        // (stamps) first L1 arrival observed
@@ -691,7 +717,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       load_scales(q0, sd);
     }
     while (q0 < U2) {
-      const int a = q0 / NBL2, b = q0 % NBL2;
+      const int a = q0 / UPE2, b = q0 % UPE2;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const int key = (1 << 30) | (a << 16) | s0;
       if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
@@ -714,7 +740,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
       const bool has_next = nq < U2;
-      const int na = has_next ? nq / NBL2 : -1;
+      const int na = has_next ? nq / UPE2 : -1;
       const int nkey = (1 << 30) | (na << 16) | ns0;
       // prefetch the next item's slab if it differs and its expert's L1 is complete
       bool pf = false;
@@ -731,29 +757,41 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* cb = tile_base(q0);
       const uint8_t* nb = !has_next ? w2v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
       if (has_next && nq != q0) load_scales(nq, sn);
-      // ---- K loop: B operands read from LDS two K-tiles ahead
-      v4f acc = {0.f, 0.f, 0.f, 0.f};
-      auto bfrag = [lane](int t) __attribute__((always_inline)) {
-        return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
+      // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
+      // read from LDS two ops ahead
+      v4f acc[RB2];
+#pragma unroll
+      for (int j = 0; j < RB2; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+      auto bfrag = [lane](int k) __attribute__((always_inline)) {
+        return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[k][lane][0]) : as_v8i(s.bst[k][lane][0], s.bst[k][lane][Smem::BV - 1]);
       };
-      v8i bq0 = bfrag(0), bq1 = KT2 > 1 ? bfrag(1) : bq0;
-      uint32_t bs = s.bsc[0][lane];
-      static_for<KT2>([&](auto tc) {
+      v8i bq0 = bfrag(0), bq1 = bfrag(1 % KT2);
+      uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
+      static_for<TI2>([&](auto tc) {
         constexpr int t = decltype(tc)::value;
+        constexpr int j = t / KT2, k = t % KT2;
         const v8i bop = bq0;
-        const uint32_t bsw = bs;
+        const uint32_t bsw = bs0;
         bq0 = bq1;
-        if constexpr (t + 2 < KT2) bq1 = bfrag(t + 2);
-        if constexpr ((t & 3) == 3 && t + 1 < KT2) bs = s.bsc[(t + 1) >> 2][lane];
-        acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t]), bop, acc, (int)sd[t >> 2], (int)bsw);
-        wr[t] = ld_stream_after(nb, t * 1024, acc);
+        bs0 = bs1;
+        if constexpr (t + 2 < TI2) {
+          bq1 = bfrag((t + 2) % KT2);
+          bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
+        }
+        acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j], (int)sd[j * KG2 + (k >> 2)],
+                                                               (int)bsw);
+        if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+        else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
       });
       // all but this loop's KT2 youngest tile loads are done: the previous item's stores too
       wait_vm_le<KT2>();
       if (s0 + c < n) {
-        float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * b + wv) * 16 + 4 * kq;
-        st_agent64(dst, (uint64_t)__float_as_uint(acc[0]) | ((uint64_t)__float_as_uint(acc[1]) << 32));
-        st_agent64(dst + 2, (uint64_t)__float_as_uint(acc[2]) | ((uint64_t)__float_as_uint(acc[3]) << 32));
+        float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+#pragma unroll
+        for (int j = 0; j < RB2; ++j) {
+          st_agent64(dst + 16 * j, (uint64_t)__float_as_uint(acc[j][0]) | ((uint64_t)__float_as_uint(acc[j][1]) << 32));
+          st_agent64(dst + 16 * j + 2, (uint64_t)__float_as_uint(acc[j][2]) | ((uint64_t)__float_as_uint(acc[j][3]) << 32));
+        }
       }
       const bool bcast = last_slab && q1 < U2;
       if (tid == 0 && bcast) s.claimv[0] = ahead;
@@ -763,9 +801,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       ps0 = s0;
       int q2 = U2;
       if (bcast) {
-        q2 = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        if (tid == 0)
-          ahead = q2 < U2 ? 2 * G + __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : U2;
+        const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
+        q2 = raw >= 0 && 2 * G + raw < U2 ? 2 * G + raw : U2;
+        if (q2 < U2) {
+          if (tid == 0) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          ahead = -1;
+        }
       }
       if (pf) {
         slab_store(s, pre);
@@ -775,7 +817,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (last_slab) {
         if (nq != q0) {
 #pragma unroll
-          for (int g = 0; g < KG2; ++g) sd[g] = sn[g];
+          for (int g = 0; g < RB2 * KG2; ++g) sd[g] = sn[g];
         }
         q0 = q1;
         q1 = q2;
@@ -791,23 +833,27 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[4] = wall_clock();
 
   // ================================================================ combine
-  // (token t, 128-row block b) pairs, round robin over the workgroups: wait until every local
-  // route of t has delivered block b, then sum the routes in slot order (fp32) -> bf16 y. The
-  // wait is only on L2 items, which never wait on this phase.
+  // (token t, 128-row block b) pairs, PG consecutive pairs per pass and workgroup: wait until
+  // every local route of t has delivered block b, then sum the routes in slot order (fp32)
+  // -> bf16 y. The waits are only on L2 items, which never wait on this phase.
   {
-    constexpr int RB = 16 * NW;
-    for (int i = blockIdx.x; i < p.M * NBL2; i += gridDim.x) {
-      const int t = i / NBL2, b = i % NBL2;
-      const int need = s.nslot[t];
-      if (need == 0) continue;                           // (y row zeroed by workgroup 0)
-      if (tid == 0) spin_until(&comb[i], need, p.spin_limit, err);
+    constexpr int CB = 16 * NW, PG = FT / CB;
+    const int P = p.M * NBL2;
+    for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {
+      if (tid < PG && i0 + tid < P) {
+        const int need = s.nslot[(i0 + tid) / NBL2];
+        if (need > 0) spin_until(&comb[i0 + tid], need, p.spin_limit, err);
+      }
       __syncthreads();
-      for (int j = tid; j < RB; j += FT) {
-        const int row = b * RB + j;
-        float sum = 0.f;
-        for (int sl = 0; sl < p.topk; ++sl)
-          if (s.exp_of_route[t * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)t * p.topk + sl) * H + row);
-        p.y[(size_t)t * H + row] = f32_to_bf16(sum);
+      const int i = i0 + tid / CB;
+      if (i < P) {
+        const int t = i / NBL2, row = (i % NBL2) * CB + tid % CB;
+        if (s.nslot[t] > 0) {              // (y rows of tokens without a local route: zeroed by workgroup 0)
+          float sum = 0.f;
+          for (int sl = 0; sl < p.topk; ++sl)
+            if (s.exp_of_route[t * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)t * p.topk + sl) * H + row);
+          p.y[(size_t)t * H + row] = f32_to_bf16(sum);
+        }
       }
     }
   }
