@@ -1,38 +1,41 @@
 // One persistent kernel for one GPU's share of the MegaMoE layer (gfx950):
-// dispatch -> L1 (gate/up, SwiGLU, requant) -> L2 (down) -> top-k combine.
+// [top-k] -> dispatch -> L1 (gate/up, SwiGLU, requant) -> L2 (down) -> top-k combine.
 //
-// Schedule. The grid is sized to what the device keeps resident at once. Work units are
-// L1 units (active expert a, 32 intermediate features q), then L2 units (active expert a,
-// 128 output rows b); workgroups claim them two at a time from one atomic counter per phase
-// (the next claim is issued before the current chunk runs) and move to the L2 phase only
-// when the L1 counter ran out. L1 units never wait, so an L2 unit's wait (on the L1 arrival
-// counter of its expert) is only on units claimed earlier by running workgroups. Every wait
-// is a bounded spin; on expiry the
-// kernel raises an error flag and carries on, so every wave always reaches the end. Units
-// of a chunk share an expert, so the 16-column B slab (routed activations or intermediate
-// rows) is staged in LDS once.
+// Schedule. The grid is what the device keeps resident at once (one 8-wave workgroup per
+// CU). Work units: L1 units (active expert a, 64 intermediate features), then L2 units
+// (active expert a, 256 output rows). Workgroup g starts with units g and G + g of each
+// phase; later units are claimed one at a time from one atomic counter per phase, one unit
+// before they are needed (a shared counter at kernel start would serialize every
+// workgroup). A workgroup moves to L2 only when it ran out of L1 units; L1 units never wait,
+// so an L2 unit's wait (on the L1 arrival counter of its expert) is only on units held by
+// running workgroups. Every wait is a bounded spin; on expiry the kernel raises an error flag
+// and carries on, so every wave always reaches the end. An item is a unit's share of one
+// 16-route slab (units of experts with more than 16 routes have several items).
 //
-// Streaming. A wave keeps one unit's weight tiles in registers (one 1 KB coalesced load per
-// 16x128 tile, <= 12 KB per wave). The next unit's tiles are issued into the same registers
-// right after the current unit's matrix-core ops, so the epilogue, barriers, stores and
-// hand-offs of a unit overlap the next unit's HBM traffic; 8-wave workgroups at 4 waves per
-// SIMD overlap the rest across workgroups.
+// Streaming. Each wave streams its weight rows through a ring of tile registers (one 1 KB
+// coalesced non-temporal load per 16x128 tile): right after the matrix-core op on a tile it
+// issues the load of the tile KR positions later, continuing into the next item, so HBM reads
+// never pause at item boundaries. The next item's activation slab is loaded into registers
+// before the tiles it must not queue behind and stored to LDS between the epilogue's
+// barriers. Loads whose values are only combined later (claims, slab bytes) are kept as
+// returned: consuming them early would wait for every weight tile issued before them.
 //
-// Dispatch. Every workgroup derives the same pool table from topk_idx in LDS (a few hundred
-// routes): per-expert counts, the active-expert list (ascending) and the canonical pool
-// order (token asc, slot asc). Workgroup 0 also publishes it, the recv stats and the zero
-// rows of unrouted tokens.
+// Dispatch. Every workgroup derives the same pool table in LDS (a few hundred routes): under
+// select_in_mega it first selects the top-k from the router logits itself; then per-expert
+// counts, the active-expert list (ascending) and the canonical pool order (token asc, slot
+// asc). Workgroup 0 also publishes the routing and the pool, the recv stats and the zero rows
+// of tokens without a local route.
 //
 // Hand-offs between workgroups go through HBM with agent-coherent accesses only: the data
 // (intermediate codes and scales, fp32 route outputs) is written with relaxed agent-scope
 // atomic stores (write-through, "sc1") and read with agent-scope atomic loads, and the
-// producer waits for its stores to complete (s_waitcnt) before bumping the arrival counter.
-// No agent-scope release/acquire fence is used: on this GPU those write back / invalidate a
+// producer's stores have completed (s_waitcnt) before it bumps an arrival counter. No
+// agent-scope release/acquire fence is used: on this GPU those write back / invalidate a
 // whole L2 and cost tens of microseconds each.
-//   L1 unit -> mid codes + scales of its 32 features, then l1_done[a] += 1
-//   L2 unit waits l1_done[a] == I/32, writes fp32 route outputs, then comb[t][b] += 1 per
-//   route; the arrival that completes token t's block b sums the token's slots in slot order
-//   and writes y (bf16).
+//   L1 unit -> mid codes + scales of its 64 features; one item later l1_done[a] += 1
+//   L2 item -> fp32 route outputs; one item later comb[t][b] += 1 per route and 128-row block
+//   combine -> per (token, block): wait comb == the token's local routes, sum the routes in
+//   slot order (fp32) -> bf16 y
 // The last workgroup to finish clears all counters, so the next launch starts from zero.
 #include "dgm_common.hpp"
 #include "dgm_abi_internal.hpp"
