@@ -4,15 +4,17 @@ re-built on CDNA4 matrix cores behind the same Python entry points.
 Exports mirror deep_gemm/__init__.py:84-110 for the MegaMoE path plus the packers."""
 from . import _lib
 from .mega import (FusedSymmBuffer, get_fused_symm_buffer_for_mega_moe,
-                   transform_mxfp4_weights_for_mega_moe_fused, transform_weights_for_mega_moe,
+                   transform_mxfp4_weights_for_mega_moe_fused, transform_qoq_weights_for_mega_moe_fused,
+                   transform_weights_for_mega_moe,
                    fable_router_quant_topk_frontend, mxfp4_mega_moe_fused, mxfp4_mega_moe_split,
-                   mxfp4_mega_moe_from_bf16)
+                   mxfp4_mega_moe_from_bf16, qoq_mega_moe_fused, qoq_mega_moe_split)
 from . import quantization_mxfp4, quantization_mxfp4_fused, quantization_nvfp4, quantization_qoq_fused
 from .utils import per_token_cast_to_fp4, per_token_cast_to_fp8, ceil_div, align
 
 __all__ = [
     "FusedSymmBuffer", "get_fused_symm_buffer_for_mega_moe", "transform_mxfp4_weights_for_mega_moe_fused",
+    "transform_qoq_weights_for_mega_moe_fused",
     "transform_weights_for_mega_moe", "fable_router_quant_topk_frontend", "mxfp4_mega_moe_fused",
-    "mxfp4_mega_moe_split", "mxfp4_mega_moe_from_bf16", "quantization_mxfp4", "quantization_mxfp4_fused", "quantization_nvfp4",
+    "mxfp4_mega_moe_split", "mxfp4_mega_moe_from_bf16", "qoq_mega_moe_fused", "qoq_mega_moe_split", "quantization_mxfp4", "quantization_mxfp4_fused", "quantization_nvfp4",
     "quantization_qoq_fused", "per_token_cast_to_fp4", "per_token_cast_to_fp8", "ceil_div", "align",
 ]

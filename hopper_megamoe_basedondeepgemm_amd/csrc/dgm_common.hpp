@@ -227,4 +227,25 @@ DGM_DEV v4f mfma_scale_16x16x128_sel(v8i a, v8i b, v4f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, OPA, sa, OPB, sb);
 }
 
+// D(16x16 i32) += A(16x64 int8) * B(64x16 int8), exact. Lane l supplies A row l%16 / B column
+// l%16 with 16 K values (lane group l/16 of both operands pairs byte for byte); result
+// register i of lane l is D[4*(l/16) + i][l%16]. (Pinned by the probe test.)
+DGM_DEV v4i mfma_i8_16x16x64(v4i a, v4i b, v4i c) { return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0); }
+
+// QoQ codes: dword d holds K j = b (low nibble of byte b) and 4 + b (high nibble); as int8
+// bytes: (d & 0x0F0F0F0F, (d >> 4) & 0x0F0F0F0F).
+DGM_DEV v4i qoq_codes(uint32_t d0, uint32_t d1) {
+  v4i r = {(int)(d0 & 0x0F0F0F0Fu), (int)((d0 >> 4) & 0x0F0F0F0Fu), (int)(d1 & 0x0F0F0F0Fu),
+           (int)((d1 >> 4) & 0x0F0F0F0Fu)};
+  return r;
+}
+
+// sum of the 16 int8 values of a 16-byte fragment (exact)
+DGM_DEV int i8_sum16(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  int s = __builtin_amdgcn_sdot4((int)a, 0x01010101, 0, false);
+  s = __builtin_amdgcn_sdot4((int)b, 0x01010101, s, false);
+  s = __builtin_amdgcn_sdot4((int)c, 0x01010101, s, false);
+  return __builtin_amdgcn_sdot4((int)d, 0x01010101, s, false);
+}
+
 }  // namespace dgm

@@ -105,6 +105,28 @@ DGM_DEV U4 ld_stream_after(const uint8_t* base, int off, v4f acc) {
   asm("" : "+v"(off) : "v"(acc[0]));
   return ld_stream(base + off);
 }
+DGM_DEV U4 ld_stream_after(const uint8_t* base, int off, v4i acc) {
+  asm("" : "+v"(off) : "v"(acc[0]));
+  return ld_stream(base + off);
+}
+DGM_DEV void st_agent32(void* p, uint32_t v) {
+  __hip_atomic_store((uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// QoQ: the zero point and group scale of the four accumulator rows 4 kq .. +3 of K-tile u
+// (one meta dword per lane group), from the wave's per-item meta registers (dword 4 u + kq of
+// the item's meta is held by lane (4 u + kq) % 64 in register (4 u + kq) / 64)
+template <int U>
+DGM_DEV uint32_t qoq_meta(const uint32_t* md, int kq) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(((4 * U + kq) & 63) * 4, (int)md[U >> 4]);
+}
+DGM_DEV v4i lo4(v8i v) { return __builtin_shufflevector(v, v, 0, 1, 2, 3); }
+// Compiler-only ordering point: the matrix-core ops that use `b` come after the VALU work that
+// produced `q` (otherwise the scheduler issues every op of a loop first and keeps all their
+// results live until the end)
+template <class T>
+DGM_DEV void after_values(v8i& b, T q) { asm("" : "+v"(b) : "v"(q)); }
+DGM_DEV v4i hi4(v8i v) { return __builtin_shufflevector(v, v, 4, 5, 6, 7); }
 
 constexpr int FT = 512;        // threads per workgroup (8 waves)
 constexpr int NW = FT / 64;
@@ -129,6 +151,11 @@ struct FusedSmem {
     U4 bst[KTM][64][BV];               // B slab in matrix-core fragment order
   };
   uint32_t bsc[(KTM + 3) / 4][64];     // its E8M0 scales, 4 K-tiles per dword
+  // QoQ slab extras: per column and 64-K chunk the sum of the column's int8 values (for the
+  // zero-point term), and per chunk and column the activation scale (chunk 0 only for the
+  // per-token scale of the input activations)
+  alignas(16) int xsum[ACT == DGM_ACT_QOQ ? 16 : 1][ACT == DGM_ACT_QOQ ? 2 * KTM : 1];
+  alignas(16) float csc[ACT == DGM_ACT_QOQ ? 16 : 1][ACT == DGM_ACT_QOQ ? 2 * KTM : 1];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
@@ -258,6 +285,7 @@ struct SlabRegs {
   uint64_t h[FR][4];             // coherent fragments: 64-bit halves (K bytes 0-15, 64-79)
   uint32_t sb[4];                // scale dwords of K-tiles 4g .. 4g+3 (byte l/16 is this lane's)
   uint32_t ok;                   // bit j: fragment j holds a real row; bit 8 + j: scale byte j
+  float fsc;                     // QoQ: an activation scale (see slab_load)
   float w;
 };
 
@@ -291,7 +319,18 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
   }
   constexpr int KG = (KT + 3) / 4;
   static_assert(KG * 64 <= FT, "one scale word per thread");
-  {
+  if constexpr (ACT == DGM_ACT_QOQ) {
+    // activations: one fp32 scale per token (row pitch KT * 4 bytes: the reference's
+    // [M, K/128] copies), thread c < 16; intermediate rows (COHERENT): one per 64-K chunk (row
+    // pitch KT * 8 bytes), thread 16 ch + c
+    static_assert(!COHERENT || 32 * KT <= FT, "one chunk scale per thread");
+    const int c = tid & 15, ch = tid >> 4;
+    const bool have = c < n && (COHERENT ? ch < 2 * KT : ch == 0);
+    const size_t rr = have ? (size_t)row_of(c) : 0;
+    const float* q = reinterpret_cast<const float*>(ssrc + rr * (COHERENT ? KT * 8 : KT * 4)) + (have ? ch : 0);
+    r.fsc = COHERENT ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *q;
+    ok |= have ? 1u << 8 : 0u;
+  } else {
     const int g = tid >> 6, l = tid & 63, c = l & 15;
     const bool have = tid < KG * 64 && c < n;
     const size_t rr = have ? (size_t)row_of(c) : 0;
@@ -310,7 +349,10 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
 
 template <int KT, int ACT, bool COHERENT, class S>
 DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
-  const int tid = threadIdx.x;
+  // (the thread index is made opaque so that the LDS addresses below are recomputed here
+  // rather than hoisted out of the work loop and kept live, or spilled, across it)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   const v4u z = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
@@ -330,7 +372,37 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
     }
   }
   constexpr int KG = (KT + 3) / 4;
-  if (tid < KG * 64) {
+  if constexpr (ACT == DGM_ACT_QOQ) {
+#pragma unroll
+    for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+      const int f = tid + j * FT;
+      if (f < KT * 64) {
+        const bool have = (r.ok >> j) & 1u;
+        const int kt = f >> 6, l = f & 63;
+        int s0, s1;
+        if (COHERENT) {
+          const uint64_t* h = r.h[j];
+          s0 = i8_sum16((uint32_t)h[0], (uint32_t)(h[0] >> 32), (uint32_t)h[1], (uint32_t)(h[1] >> 32));
+          s1 = i8_sum16((uint32_t)h[2], (uint32_t)(h[2] >> 32), (uint32_t)h[3], (uint32_t)(h[3] >> 32));
+        } else {
+          s0 = i8_sum16(r.v0[j].x, r.v0[j].y, r.v0[j].z, r.v0[j].w);
+          s1 = i8_sum16(r.v1[j].x, r.v1[j].y, r.v1[j].z, r.v1[j].w);
+        }
+        s0 = have ? s0 : 0;
+        s1 = have ? s1 : 0;
+        // (the branch is wave-uniform: a wave's 64 lanes are the 4 lane groups of one K-tile)
+        s0 += __shfl_xor(s0, 16);
+        s0 += __shfl_xor(s0, 32);
+        s1 += __shfl_xor(s1, 16);
+        s1 += __shfl_xor(s1, 32);
+        if (l < 16) {
+          s.xsum[l][2 * kt] = s0;
+          s.xsum[l][2 * kt + 1] = s1;
+        }
+      }
+    }
+    if (COHERENT ? tid < 32 * KT : tid < 16) s.csc[tid & 15][tid >> 4] = (r.ok >> 8) & 1u ? r.fsc : 0.f;
+  } else if (tid < KG * 64) {
     uint32_t w = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -480,15 +552,32 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int* claim = p.counters + CNT_CLAIM;
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
+    const float* w1r = p.w1r;
     const int topk = p.topk;
     auto tile_base = [w1v, lane, pp, gu](int u) __attribute__((always_inline)) {
       const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
       return w1v + blk * KT1 * 1024 + lane * 16;
     };
-    auto load_scales = [w1s, lane, pp, gu](int u, uint32_t (&sw)[KG1]) __attribute__((always_inline)) {
+    // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block; QoQ:
+    // its meta dwords (4 per K-tile, spread over the lanes) and the s1 of the lane's 4 rows
+    constexpr int MR1 = (4 * KT1 + 63) / 64;
+    constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : KG1;
+    auto load_scales = [w1s, w1r, lane, pp, gu](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
       const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+      if constexpr (ACT == DGM_ACT_QOQ) {
+        const uint32_t* mb = w1s + blk * KT1 * 4;
 #pragma unroll
-      for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
+        for (int j = 0; j < MR1; ++j)
+          sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * KT1 ? 64 * j + lane : 4 * KT1 - 1));
+        const v4u r = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w1r + blk * 16 + 4 * (lane >> 4)));
+        sw[MR1] = r.x;
+        sw[MR1 + 1] = r.y;
+        sw[MR1 + 2] = r.z;
+        sw[MR1 + 3] = r.w;
+      } else {
+#pragma unroll
+        for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
+      }
     };
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
@@ -510,7 +599,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
     U4 wr[KR];
-    uint32_t sd[KG1], sn[KG1];
+    uint32_t sd[SW1], sn[SW1];
     SlabRegs<KT1, ACT, false> pre;
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
     if (q0 < U1) {
@@ -537,6 +626,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (has_next && nq != q0) load_scales(nq, sn);
       if (restage) load_slab(pre, na, ns0);
       const float wt_r = s.slab_w[c];
+      const float sx = ACT == DGM_ACT_QOQ ? s.csc[c][0] : 1.f;     // QoQ: the token's activation scale
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -545,18 +635,53 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
       };
       v8i bq0 = bfrag(0), bq1 = KT1 > 1 ? bfrag(1) : bq0;
-      uint32_t bs = s.bsc[0][lane];
-      static_for<KT1>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        const v8i bop = bq0;
-        const uint32_t bsw = bs;
-        bq0 = bq1;
-        if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
-        if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
-        acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, acc, (int)sd[t >> 2], (int)bsw);
-        if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
-        else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
-      });
+      if constexpr (ACT == DGM_ACT_QOQ) {
+        // per K-tile: two int8 ops on the raw 4-bit codes (exact int32 sums of code * x), then,
+        // one tile later (off the matrix-core result's latency), the zero-point correction
+        // P = acc - z * sum(x) and the group scale: Q += s2 * P (exact: |Q| < 2^31)
+        v4i qa = {0, 0, 0, 0}, prev = {0, 0, 0, 0};
+        auto promote = [&](auto uc, v4i a) __attribute__((always_inline)) {
+          constexpr int u = decltype(uc)::value;
+          const int2 xx = *reinterpret_cast<const int2*>(&s.xsum[c][2 * u]);
+          const int X = xx.x + xx.y;
+          const uint32_t md = qoq_meta<u>(sd, kq);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int z = (int)((md >> (8 * i)) & 15u), s2 = (int)((md >> (8 * i + 4)) & 15u);
+            qa[i] += (a[i] - z * X) * s2;
+          }
+        };
+        static_for<KT1>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          v8i bop = bq0;
+          bq0 = bq1;
+          if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
+          if constexpr (t >= 2) after_values(bop, qa);      // (tile t - 2 promoted)
+          const U4 w = wr[t % KR];
+          v4i at = mfma_i8_16x16x64(qoq_codes(w.x, w.y), lo4(bop), v4i{0, 0, 0, 0});
+          at = mfma_i8_16x16x64(qoq_codes(w.z, w.w), hi4(bop), at);
+          if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, at);
+          else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, at);
+          if constexpr (t > 0) promote(std::integral_constant<int, t - 1>{}, prev);
+          prev = at;
+        });
+        promote(std::integral_constant<int, KT1 - 1>{}, prev);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = (float)qa[i] * __uint_as_float(sd[MR1 + i]) * sx;
+      } else {
+        uint32_t bs = s.bsc[0][lane];
+        static_for<KT1>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          const v8i bop = bq0;
+          const uint32_t bsw = bs;
+          bq0 = bq1;
+          if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
+          if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
+          acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, acc, (int)sd[t >> 2], (int)bsw);
+          if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
+          else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
+        });
+      }
       // all but this loop's KR youngest tile loads are done: the previous item's stores too
       wait_vm_le<KR>();
       const long long t_e0 = st ? wall_clock() : 0;
@@ -592,8 +717,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         float am = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float g = fminf(round_bf16(acc[i]), p.clamp);
-          const float uu = fminf(fmaxf(round_bf16(s.upv[pp][lane][i]), -p.clamp), p.clamp);
+          // MXFP: gate / up rounded to bf16 (the reference's L1 output); QoQ: fp32
+          const float g = fminf(ACT == DGM_ACT_QOQ ? acc[i] : round_bf16(acc[i]), p.clamp);
+          const float uv = s.upv[pp][lane][i];
+          const float uu = fminf(fmaxf(ACT == DGM_ACT_QOQ ? uv : round_bf16(uv), -p.clamp), p.clamp);
           const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
           act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
           am = fmaxf(am, fabsf(act[i]));
@@ -604,10 +731,27 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       __syncthreads();                                   // (2) amax visible, next slab staged
       if (gu == 0) {
-        const float am = fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
+        const float am = ACT == DGM_ACT_QOQ ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
+                                            : fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
         const int row = r0 + s0 + c;
         // lane group kq holds features 16 pr + 4 kq .. +3 of column c
-        if (ACT == DGM_ACT_MXFP4) {
+        if (ACT == DGM_ACT_QOQ) {
+          // int8 per 64 features (this unit): scale = max(amax / 127, FLT_MIN), round to
+          // nearest even, clamp to +-127
+          const float sc = fmaxf(am / 127.0f, 1.17549435e-38f);
+          uint32_t w = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = fminf(fmaxf(rintf(act[i] / sc), -127.f), 127.f);
+            w |= ((uint32_t)(int)v & 0xffu) << (8 * i);
+          }
+          const int src_lo = lane < 16 ? c : c + 32, src_hi = lane < 16 ? c + 16 : c + 48;
+          const uint64_t w64 = (uint64_t)__shfl(w, src_lo) | ((uint64_t)__shfl(w, src_hi) << 32);
+          if (valid && lane < 32) {
+            st_agent64(p.mid + (size_t)row * MB + 16 * pr + (lane < 16 ? 0 : 8), w64);
+            if (pp == 0 && lane < 16) st_agent32(p.mid_sf + (size_t)row * (I / 16) + 4 * q, __float_as_uint(sc));
+          }
+        } else if (ACT == DGM_ACT_MXFP4) {
           const uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
           const float isc = e8m0_inv(code);
           uint32_t w = 0;
@@ -641,7 +785,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         pend = a;
         if (nq != q0) {
 #pragma unroll
-          for (int g = 0; g < KG1; ++g) sd[g] = sn[g];
+          for (int g = 0; g < SW1; ++g) sd[g] = sn[g];
         }
         q0 = q1;
         q1 = q2;
@@ -670,6 +814,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int* claim = p.counters + CNT_CLAIM + 1;
     const uint8_t* w2v = p.w2v;
     const uint32_t* w2s = p.w2s;
+    const float* w2r = p.w2r;
     const int topk = p.topk;
     auto blk_of = [wv](int v) __attribute__((always_inline)) {
       return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
@@ -677,10 +822,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     auto tile_base = [w2v, lane, blk_of](int v) __attribute__((always_inline)) {
       return w2v + blk_of(v) * KT2 * 1024 + lane * 16;
     };
-    auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[RB2 * KG2]) __attribute__((always_inline)) {
-      const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
+    // per-item scale registers (the wave's RB2 contiguous 16-row blocks), loaded one item
+    // ahead: MXFP: E8M0 scale dwords; QoQ: meta dwords (4 per K-tile)
+    constexpr int MR2 = (4 * TI2 + 63) / 64;
+    constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : RB2 * KG2;
+    auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
+      if constexpr (ACT == DGM_ACT_QOQ) {
+        const uint32_t* mb = w2s + blk_of(v) * KT2 * 4;
 #pragma unroll
-      for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
+        for (int j = 0; j < MR2; ++j)
+          sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * TI2 ? 64 * j + lane : 4 * TI2 - 1));
+      } else {
+        const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
+#pragma unroll
+        for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
+      }
     };
     const uint8_t* midv = p.mid;
     const uint8_t* mids = p.mid_sf;
@@ -691,10 +847,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     };
     // arrivals of item (unit v, slab s0): its routes' outputs for the unit's blocks are complete
     auto arrive = [comb, tid, topk](int v, int s0) __attribute__((always_inline)) {
+      // (topk and the thread index made opaque: what derives from them is computed here, not
+      // kept live across the work loop, where it would cost registers or a spill)
+      int tk = topk, i0 = tid;
+      asm volatile("" : "+s"(tk), "+v"(i0));
       const int a = v / UPE2, b = v % UPE2;
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
-      for (int i = tid; i < 16 * RB2 && i / RB2 < n; i += FT)
-        __hip_atomic_fetch_add(&comb[(s.routes[r0 + i / RB2] / topk) * NBL2 + RB2 * b + i % RB2], 1,
+      for (int i = i0; i < 16 * RB2 && i / RB2 < n; i += FT)
+        __hip_atomic_fetch_add(&comb[(s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2], 1,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units g and G + g first, then claims (offset by 2 G), as in the L1 phase
@@ -708,7 +868,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
     U4 wr[KT2];
-    uint32_t sd[RB2 * KG2], sn[RB2 * KG2];
+    uint32_t sd[SW2], sn[SW2];
     SlabRegs<KT2, ACT, true> pre;
     int ready = -1;           // an active expert whose L1 arrival is known complete
     bool seen = false;        // (stamps) first L1 arrival observed
@@ -735,8 +895,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if (tid == 0 && !seen) st[3] = wall_clock();
           seen = true;
         }
-        const int rb = r0 + s0;
-        stage_slab<KT2, ACT, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
+        if constexpr (ACT == DGM_ACT_QOQ) {
+          load_slab(pre, a, s0);            // (pre holds nothing between items)
+          slab_store(s, pre);
+        } else {
+          const int rb = r0 + s0;
+          stage_slab<KT2, ACT, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
+        }
         staged = key;
         __syncthreads();
       }
@@ -760,6 +925,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* cb = tile_base(q0);
       const uint8_t* nb = !has_next ? w2v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
       if (has_next && nq != q0) load_scales(nq, sn);
+      // QoQ: the row scales s1 of the lane's 4 rows of each block, only used after the K loop
+      // (so loaded for this item, here)
+      v4u s1r[ACT == DGM_ACT_QOQ ? RB2 : 1];
+      if constexpr (ACT == DGM_ACT_QOQ) {
+#pragma unroll
+        for (int jb = 0; jb < RB2; ++jb)
+          s1r[jb] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w2r + (blk_of(q0) + jb) * 16 + 4 * kq));
+      }
       // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
       // read from LDS two ops ahead
       v4f acc[RB2];
@@ -769,23 +942,67 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[k][lane][0]) : as_v8i(s.bst[k][lane][0], s.bst[k][lane][Smem::BV - 1]);
       };
       v8i bq0 = bfrag(0), bq1 = bfrag(1 % KT2);
-      uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
-      static_for<TI2>([&](auto tc) {
-        constexpr int t = decltype(tc)::value;
-        constexpr int j = t / KT2, k = t % KT2;
-        const v8i bop = bq0;
-        const uint32_t bsw = bs0;
-        bq0 = bq1;
-        bs0 = bs1;
-        if constexpr (t + 2 < TI2) {
-          bq1 = bfrag((t + 2) % KT2);
-          bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
+      if constexpr (ACT == DGM_ACT_QOQ) {
+        // per K-tile two int8 ops, one per 64-K chunk (the intermediate's scale changes every
+        // 64 features); one tile later: f += s2 * sum_h float(acc_h - z * sum(x_h)) * scale_h
+        v4i p0 = {0, 0, 0, 0}, p1 = {0, 0, 0, 0};
+        auto promote = [&](auto uc, v4i a0, v4i a1) __attribute__((always_inline)) {
+          constexpr int u = decltype(uc)::value;
+          constexpr int jb = u / KT2, k = u % KT2;
+          const int2 xx = *reinterpret_cast<const int2*>(&s.xsum[c][2 * k]);
+          const float2 sm = *reinterpret_cast<const float2*>(&s.csc[c][2 * k]);
+          const uint32_t md = qoq_meta<u>(sd, kq);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int z = (int)((md >> (8 * i)) & 15u);
+            const float s2 = (float)((md >> (8 * i + 4)) & 15u);
+            const float v = fmaf((float)(a1[i] - z * xx.y), sm.y, (float)(a0[i] - z * xx.x) * sm.x);
+            acc[jb][i] = fmaf(s2, v, acc[jb][i]);
+          }
+        };
+        static_for<TI2>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          constexpr int k = t % KT2;
+          v8i bop = bq0;
+          bq0 = bq1;
+          if constexpr (t + 2 < TI2) bq1 = bfrag((t + 2) % KT2);
+          if constexpr (t >= 2) after_values(bop, acc[(t - 2) / KT2]);   // (tile t - 2 promoted)
+          const U4 w = wr[k];
+          const v4i a0 = mfma_i8_16x16x64(qoq_codes(w.x, w.y), lo4(bop), v4i{0, 0, 0, 0});
+          const v4i a1 = mfma_i8_16x16x64(qoq_codes(w.z, w.w), hi4(bop), v4i{0, 0, 0, 0});
+          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, a1);
+          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, a1);
+          if constexpr (t > 0) promote(std::integral_constant<int, t - 1>{}, p0, p1);
+          p0 = a0;
+          p1 = a1;
+        });
+        promote(std::integral_constant<int, TI2 - 1>{}, p0, p1);
+#pragma unroll
+        for (int j = 0; j < RB2; ++j) {
+          acc[j][0] *= __uint_as_float(s1r[j].x);
+          acc[j][1] *= __uint_as_float(s1r[j].y);
+          acc[j][2] *= __uint_as_float(s1r[j].z);
+          acc[j][3] *= __uint_as_float(s1r[j].w);
         }
-        acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j], (int)sd[j * KG2 + (k >> 2)],
-                                                               (int)bsw);
-        if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
-        else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
-      });
+      } else {
+        uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
+        static_for<TI2>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          constexpr int j = t / KT2, k = t % KT2;
+          const v8i bop = bq0;
+          const uint32_t bsw = bs0;
+          bq0 = bq1;
+          bs0 = bs1;
+          if constexpr (t + 2 < TI2) {
+            bq1 = bfrag((t + 2) % KT2);
+            bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
+          }
+          acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
+                                                                 (int)sd[j * KG2 + (k >> 2)], (int)bsw);
+          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
+        });
+      }
       // all but this loop's KT2 youngest tile loads are done: the previous item's stores too
       wait_vm_le<KT2>();
       if (s0 + c < n) {
@@ -820,7 +1037,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (last_slab) {
         if (nq != q0) {
 #pragma unroll
-          for (int g = 0; g < RB2 * KG2; ++g) sd[g] = sn[g];
+          for (int g = 0; g < SW2; ++g) sd[g] = sn[g];
         }
         q0 = q1;
         q1 = q2;
@@ -911,15 +1128,17 @@ int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format) {
 }
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream) {
-  if (hidden == 3072 && intermediate == 1280)
-    return act == DGM_ACT_MXFP4 ? launch_fused_t<24, 10, DGM_ACT_MXFP4>(prm, 0, stream)
-                                : launch_fused_t<24, 10, DGM_ACT_MXFP8>(prm, 0, stream);
-  if (hidden == 512 && intermediate == 256)
-    return act == DGM_ACT_MXFP4 ? launch_fused_t<4, 2, DGM_ACT_MXFP4>(prm, 1, stream)
-                                : launch_fused_t<4, 2, DGM_ACT_MXFP8>(prm, 1, stream);
-  if (hidden == 1024 && intermediate == 512)
-    return act == DGM_ACT_MXFP4 ? launch_fused_t<8, 4, DGM_ACT_MXFP4>(prm, 2, stream)
-                                : launch_fused_t<8, 4, DGM_ACT_MXFP8>(prm, 2, stream);
+#define DGM_FUSED_SHAPE(H_, I_, SLOT)                                                          \
+  if (hidden == H_ && intermediate == I_) {                                                    \
+    constexpr int KA = H_ / 128, KB = I_ / 128;                                               \
+    return act == DGM_ACT_MXFP4   ? launch_fused_t<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream) \
+           : act == DGM_ACT_MXFP8 ? launch_fused_t<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream) \
+                                  : launch_fused_t<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream);   \
+  }
+  DGM_FUSED_SHAPE(3072, 1280, 0)
+  DGM_FUSED_SHAPE(512, 256, 1)
+  DGM_FUSED_SHAPE(1024, 512, 2)
+#undef DGM_FUSED_SHAPE
   dgm_set_error("fused kernel: supported (hidden, intermediate) are (3072, 1280), (512, 256), (1024, 512)");
   return DGM_ERR_INVALID_ARGUMENT;
 }

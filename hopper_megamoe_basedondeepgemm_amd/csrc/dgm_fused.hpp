@@ -25,6 +25,8 @@ struct FusedParams {
   const uint32_t* w1s;
   const uint8_t* w2v;
   const uint32_t* w2s;
+  const float* w1r;         // QoQ: per-row weight scales s1 [E_local, N] (null for MXFP4)
+  const float* w2r;
   const uint8_t* x;
   const uint8_t* xsf;
   int64_t* topk_idx;        // read, or written by workgroup 0 when select != 0

@@ -65,7 +65,8 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
 // each token's all-zero flag (token_flags bit 0) from the rows they hold.
 // Cast: 8 lanes per 32-element activation group, 4 elements per lane (MXFP4 rows with amax
 // floor 1e-30, MXFP8 rows with amax floor 1e-4: the rules of dgm_cast_fp4_rows /
-// dgm_cast_fp8_rows), spread over the whole grid after the router work.
+// dgm_cast_fp8_rows), spread over the whole grid after the router work; QoQ: one wave per
+// token (per-token int8, the rule of dgm_cast_int8_rows).
 template <int J>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
@@ -111,6 +112,41 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
         if (blockIdx.x == 0 && wave == 0) token_flags[t0 + tt] = nonzero ? 0 : 1;
       }
     }
+  }
+  if (act_format == DGM_ACT_QOQ) {
+    // ---- QoQ activation cast (per_token_cast_to_int8): one wave per token, lane l holds
+    // elements 512 j + 8 l .. +7; sf = max(amax, 1e-30) / 127 (fp32), q = clamp(rne(x / sf),
+    // +-127); the scale is repeated over the row's H / 128 slots
+    const int nwaves = gridDim.x * gridDim.y * 4;
+    for (int t = ((int)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave; t < M; t += nwaves) {
+      U4 xv[J];
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        xv[j] = *reinterpret_cast<const U4*>(x + (size_t)t * H + 512 * j + 8 * lane);
+        const uint32_t d[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(d[k] << 16)), fabsf(__uint_as_float(d[k] & 0xffff0000u))));
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+      const float scale = fmaxf(amax, 1e-30f) / 127.0f;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        uint32_t o[2] = {0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t bits = (k & 1) ? (d[k >> 1] & 0xffff0000u) : (d[k >> 1] << 16);
+          const float v = fminf(fmaxf(rintf(__uint_as_float(bits) / scale), -127.f), 127.f);
+          o[k >> 2] |= ((uint32_t)(int)v & 0xffu) << (8 * (k & 3));
+        }
+        *reinterpret_cast<uint2*>(q + (size_t)t * H + 512 * j + 8 * lane) = make_uint2(o[0], o[1]);
+      }
+      if (lane < H / 128) reinterpret_cast<float*>(sf)[(size_t)t * (H / 128) + lane] = scale;
+    }
+    return;
   }
   // ---- activation cast: 8 lanes per group
   const int64_t groups = (int64_t)M * (H / 32);
@@ -533,10 +569,14 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts in (0, 1024]");
   DGM_CHECK_ARG(num_local_experts > 0 && num_local_experts <= num_experts, "num_local_experts");
   DGM_CHECK_ARG(hidden % 512 == 0 && intermediate % 128 == 0, "hidden % 512, intermediate % 128");
-  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8, "act_format");
+  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8 || act_format == DGM_ACT_QOQ,
+                "act_format");
   DGM_CHECK_ARG((int64_t)max_tokens * topk <= MAX_ROUTES_DISPATCH, "max_tokens * topk <= 4096");
   const size_t xb = act_format == DGM_ACT_MXFP4 ? hidden / 2 : hidden;
   const size_t mb = act_format == DGM_ACT_MXFP4 ? intermediate / 2 : intermediate;
+  // scales: E8M0 bytes per 32 (MXFP); QoQ: fp32 per token repeated over H / 128 slots (the
+  // same H / 32 bytes) and fp32 per 64 intermediate features (I / 16 bytes)
+  const size_t msfb = act_format == DGM_ACT_QOQ ? intermediate / 16 : intermediate / 32;
   const int R = max_tokens * topk;
   size_t off = 0;
   memset(out, 0, sizeof(*out));
@@ -548,7 +588,7 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   out->token_flags = off; off += dgm_align256((size_t)max_tokens * 4);
   out->pool = off; off += dgm_align256(pool_bytes(num_local_experts, R));
   out->mid = off; off += dgm_align256((size_t)R * mb);
-  out->mid_sf = off; off += dgm_align256((size_t)R * (intermediate / 32));
+  out->mid_sf = off; off += dgm_align256((size_t)R * msfb);
   out->partials = off; off += dgm_align256((size_t)R * hidden * 4);
   out->counters = off; off += dgm_align256((size_t)CNT_ALL * 4);
   out->total_bytes = off;
@@ -567,7 +607,8 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
   DGM_CHECK_ARG(num_experts <= 1024, "num_experts <= 1024");
   DGM_CHECK_ARG(hidden % 512 == 0, "hidden % 512 == 0");
   DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
-  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8, "act_format");
+  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8 || act_format == DGM_ACT_QOQ,
+                "act_format");
   DGM_CHECK_ARG(((uintptr_t)hidden_bf16 & 15) == 0 && ((uintptr_t)router_weight_bf16 & 15) == 0, "16-byte alignment");
   if (num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)buffer;
@@ -616,7 +657,10 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(A->num_local_experts > 0 && A->num_local_experts <= MAX_LOCAL_EXPERTS, "num_local_experts");
   DGM_CHECK_ARG(A->expert_begin >= 0 && A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
-  DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8, "act_format");
+  DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8 || A->act_format == DGM_ACT_QOQ,
+                "act_format");
+  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ || (A->w1_row_scales && A->w2_row_scales),
+                "QoQ needs the row scales s1 of both matrices");
   DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
   DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 32 == 0, "shape");
   DGM_CHECK_ARG(A->intermediate % 128 == 0, "intermediate % 128 == 0");
@@ -635,6 +679,8 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.w1s = (const uint32_t*)A->w1_scales;
     p.w2v = (const uint8_t*)A->w2_values;
     p.w2s = (const uint32_t*)A->w2_scales;
+    p.w1r = A->act_format == DGM_ACT_QOQ ? (const float*)A->w1_row_scales : nullptr;
+    p.w2r = A->act_format == DGM_ACT_QOQ ? (const float*)A->w2_row_scales : nullptr;
     p.x = buf + L->x;
     p.xsf = buf + L->x_sf;
     p.topk_idx = (int64_t*)(buf + L->topk_idx);
@@ -663,11 +709,15 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
+  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ,
+                "QoQ layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
   return dgm_megamoe_split_launch(A, stream);
 }
 
 int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
+  DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8,
+                "split path: act_format must be MXFP4 or MXFP8 (the QoQ layer is fused only)");
   const DgmBufferLayout* L = A->layout;
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   if (A->num_tokens == 0) return 0;

@@ -297,6 +297,64 @@ __global__ void k_transform_fp4(const uint8_t* __restrict__ src, const uint8_t* 
   sdst[((((int64_t)e * NB + q) * KG + kt / 4) * 64 + lane) * 4 + (kt & 3)] = sc;
 }
 
+// QoQ (W4A8) weights -> the fused kernel's layout (one thread per (expert, 16-row block,
+// K-tile, lane)). Values [E][N/16][K/128][64][16 B]: lane l = row l%16; its 16 bytes hold the
+// two K=64 int8 operands (op h: K = 64 h + 16 (l/16) + j, j = 0..15) as nibbles: dword 2h
+// byte b = n[b] | n[4+b] << 4, dword 2h+1 byte b = n[8+b] | n[12+b] << 4, so the 16 int8
+// codes come out as (d & 0x0F0F0F0F, (d >> 4) & 0x0F0F0F0F) per dword. Meta [E][N/16][K/128]
+// [16 B]: byte r = z | s2 << 4 of row r (both are 4-bit by construction: z 0..15, s2 1..15),
+// so dword kq holds the four rows 4 kq .. +3 that lane group kq accumulates. s1 [E][N] in the
+// same row order. l1_interleave as for the MXFP4 transform.
+__global__ void k_transform_qoq(const uint8_t* __restrict__ src, const uint8_t* __restrict__ s2,
+                                const uint8_t* __restrict__ z, const float* __restrict__ s1, int E, int N,
+                                int K, int l1_interleave, uint8_t* __restrict__ dst, uint8_t* __restrict__ mdst,
+                                float* __restrict__ s1dst) {
+  int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int KT = K / 128, NB = N / 16;
+  const int64_t total = (int64_t)E * NB * KT * 64;
+  if (tid >= total) return;
+  const int lane = (int)(tid & 63);
+  int64_t t = tid >> 6;
+  const int kt = (int)(t % KT); t /= KT;
+  const int q = (int)(t % NB);
+  const int e = (int)(t / NB);
+  const int r = lane & 15, g = lane >> 4;
+  int src_row;
+  if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
+  else src_row = 16 * q + r;
+  const uint8_t* row = src + ((int64_t)e * N + src_row) * (K / 2);
+  uint32_t o[4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // K = 128 kt + 64 h + 16 g .. +16: two Marlin chunks of 8 (byte b = K[b] << 4 | K[b+4])
+    const uint8_t* c = row + (128 * kt + 64 * h + 16 * g) / 2;
+    uint32_t n[16];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = c[4 * ch + b];
+        n[8 * ch + b] = byte >> 4;
+        n[8 * ch + b + 4] = byte & 0xfu;
+      }
+    uint32_t d0 = 0, d1 = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      d0 |= (n[b] | (n[4 + b] << 4)) << (8 * b);
+      d1 |= (n[8 + b] | (n[12 + b] << 4)) << (8 * b);
+    }
+    o[2 * h] = d0;
+    o[2 * h + 1] = d1;
+  }
+  const int64_t tile = ((int64_t)e * NB + q) * KT + kt;
+  *reinterpret_cast<U4*>(dst + tile * 1024 + lane * 16) = U4{o[0], o[1], o[2], o[3]};
+  if (g == 0) {
+    const int64_t mi = ((int64_t)e * N + src_row) * KT + kt;
+    mdst[tile * 16 + r] = (uint8_t)((z[mi] & 15u) | (s2[mi] << 4));
+    if (kt == 0) s1dst[((int64_t)e * NB + q) * 16 + r] = s1[(int64_t)e * N + src_row];
+  }
+}
+
 // Fill the padding bytes of the last scale group (K-tiles KT..4*KG-1) with 127 (= 2^0).
 __global__ void k_fill_scale_pad(uint8_t* sdst, int64_t blocks, int KT, int KG) {
   int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -407,6 +465,19 @@ int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E,
   if (pad_total > 0)
     hipLaunchKernelGGL(k_fill_scale_pad, dim3(grid_for(pad_total, 256)), dim3(256), 0, stream,
                        (uint8_t*)dst_scales, (int64_t)E * NB, KT, KG);
+  return dgm_last_launch_status();
+}
+
+int dgm_transform_qoq_weights(const void* packed, const void* s2, const void* z, const void* s1, int E, int N,
+                              int K, int l1_interleave, void* dst_values, void* dst_meta, void* dst_s1,
+                              hipStream_t stream) {
+  DGM_CHECK_ARG(packed && s2 && z && s1 && dst_values && dst_meta && dst_s1, "null pointer");
+  DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "E, N, K (N % 16, K % 128)");
+  DGM_CHECK_ARG(!l1_interleave || N % 32 == 0, "l1_interleave needs N % 32 == 0");
+  const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
+  hipLaunchKernelGGL(k_transform_qoq, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)packed,
+                     (const uint8_t*)s2, (const uint8_t*)z, (const float*)s1, E, N, K, l1_interleave,
+                     (uint8_t*)dst_values, (uint8_t*)dst_meta, (float*)dst_s1);
   return dgm_last_launch_status();
 }
 

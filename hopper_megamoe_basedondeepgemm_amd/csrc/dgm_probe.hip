@@ -52,3 +52,18 @@ extern "C" int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa
     DGM_CHECK_ARG(false, "fmt pairs (4,4), (4,0), (0,0)");
   return dgm_last_launch_status();
 }
+
+// One int8 matrix-core op (V_MFMA_I32_16X16X64_I8) on caller-provided lane fragments
+// (a, b: 64 x 16 bytes; out: 64 x 4 int32), to pin the lane layout of the W4A8 path.
+__global__ void k_probe_i8(const v4i* a, const v4i* b, v4i* out) {
+  const int l = threadIdx.x;
+  v4i c = {0, 0, 0, 0};
+  c = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[l], b[l], c, 0, 0, 0);
+  out[l] = c;
+}
+
+extern "C" int dgm_probe_mfma_i8(const void* a, const void* b, void* out, hipStream_t stream) {
+  DGM_CHECK_ARG(a && b && out, "null pointer");
+  hipLaunchKernelGGL(k_probe_i8, dim3(1), dim3(64), 0, stream, (const v4i*)a, (const v4i*)b, (v4i*)out);
+  return dgm_last_launch_status();
+}

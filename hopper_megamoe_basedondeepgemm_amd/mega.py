@@ -26,7 +26,9 @@ class FusedSymmBuffer:
     Views: x, x_sf, topk_idx, topk_weights (frontend outputs / layer inputs), l1_acts and
     l1_acts_sf (aliases of x / x_sf: routed rows are read in place), l2_acts / l2_acts_sf
     (L1 -> L2 activations in pool order), combine_partials (fp32 [tokens, topk, H] route
-    outputs), logits (fp32 router logits) and pool (dispatch table, int32)."""
+    outputs), logits (fp32 router logits) and pool (dispatch table, int32).
+    act_format "mxfp4" / "mxfp8": uint8 codes with E8M0 scale bytes per 32; "qoq": int8 codes,
+    x_sf fp32 [tokens, H/128] (one scale per token, repeated), l2_acts_sf fp32 [routes, I/64]."""
 
     def __init__(self, group, num_experts, max_tokens, topk, hidden, intermediate,
                  act_format="mxfp4", ep_size=None, ep_rank=None, device=None):
@@ -58,14 +60,23 @@ class FusedSymmBuffer:
             return b[off:off + n * torch.tensor([], dtype=dtype).element_size()].view(dtype).view(*shape)
 
         xb = L.x_row_bytes
-        self.x = view(L.x, max_tokens * xb, torch.uint8, (max_tokens, xb))
-        self.x_sf = view(L.x_sf, max_tokens * (hidden // 32), torch.uint8, (max_tokens, hidden // 32))
+        qoq = act_format == "qoq"
+        if qoq:   # int8 codes, fp32 scale per token repeated over the H / 128 slots
+            self.x = view(L.x, max_tokens * xb, torch.int8, (max_tokens, xb))
+            self.x_sf = view(L.x_sf, max_tokens * (hidden // 128), torch.float32, (max_tokens, hidden // 128))
+        else:     # codes, E8M0 scale bytes per 32
+            self.x = view(L.x, max_tokens * xb, torch.uint8, (max_tokens, xb))
+            self.x_sf = view(L.x_sf, max_tokens * (hidden // 32), torch.uint8, (max_tokens, hidden // 32))
         self.topk_idx = view(L.topk_idx, R, torch.int64, (max_tokens, topk))
         self.topk_weights = view(L.topk_weights, R, torch.float32, (max_tokens, topk))
         self.logits = view(L.logits, max_tokens * num_experts, torch.float32, (max_tokens, num_experts))
         mb = L.mid_row_bytes
-        self.l2_acts = view(L.mid, R * mb, torch.uint8, (R, mb))
-        self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 32), torch.uint8, (R, intermediate // 32))
+        if qoq:   # int8 codes, fp32 scale per 64 features
+            self.l2_acts = view(L.mid, R * mb, torch.int8, (R, mb))
+            self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 64), torch.float32, (R, intermediate // 64))
+        else:
+            self.l2_acts = view(L.mid, R * mb, torch.uint8, (R, mb))
+            self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 32), torch.uint8, (R, intermediate // 32))
         self.combine_partials = view(L.partials, R * hidden, torch.float32, (max_tokens, topk, hidden))
         self.l1_acts, self.l1_acts_sf = self.x, self.x_sf
         self.handle = types.SimpleNamespace(buffer_ptrs=[b.data_ptr()])
@@ -133,6 +144,38 @@ def transform_mxfp4_weights_for_mega_moe_fused(l1, l2, src_order="marlin"):
     return _transform_one(l1[0], l1[1], True, so), _transform_one(l2[0], l2[1], False, so)
 
 
+def _transform_qoq_one(q, l1_interleave):
+    packed, s2, z, s1 = q
+    _lib.require_gpu(packed, s2, z, s1)
+    assert packed.dtype == torch.uint8 and s2.dtype == torch.uint8 and z.dtype == torch.uint8
+    assert s1.dtype == torch.float32 and packed.dim() == 3
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert s2.shape == (E, N, K // 128) and z.shape == (E, N, K // 128) and s1.shape == (E, N)
+    assert N % 16 == 0 and K % 128 == 0, (N, K)
+    # the fused layout keeps z and s2 as one nibble each (quantize_to_qoq: z 0..15, s2 1..15)
+    if int(torch.maximum(s2.max(), z.max()).item()) > 15:
+        raise ValueError("QoQ meta out of range: z and s2 must be < 16")
+    KT, NB = K // 128, N // 16
+    vals = torch.empty((E, NB, KT, 64, 16), dtype=torch.uint8, device=packed.device)
+    meta = torch.empty((E, NB, KT, 16), dtype=torch.uint8, device=packed.device)
+    rs = torch.empty((E, N), dtype=torch.float32, device=packed.device)
+    _lib.check(_lib.load().dgm_transform_qoq_weights(
+        _lib.ptr(packed.contiguous()), _lib.ptr(s2.contiguous()), _lib.ptr(z.contiguous()),
+        _lib.ptr(s1.contiguous()), E, N, K, int(l1_interleave), _lib.ptr(vals), _lib.ptr(meta), _lib.ptr(rs),
+        _lib.stream()))
+    return vals, meta, rs
+
+
+def transform_qoq_weights_for_mega_moe_fused(l1, l2):
+    """deep_gemm/mega/fused.py:71. Inputs: ``quantize_to_qoq`` tuples ``(packed [E, N, K/2],
+    s2 [E, N, K/128], z [E, N, K/128], s1 [E, N])`` for W1 [E, 2I, H] and W2 [E, H, I].
+    Returns ``((w1_values, w1_meta, w1_s1), (w2_values, w2_meta, w2_s1))``: 4-bit codes in
+    int8 matrix-core fragment order, per (row, K128) zero points and group scales, per-row
+    scales. Invariant: dequant(transform(q)) == interleave(dequant(q))."""
+    return _transform_qoq_one(l1, True), _transform_qoq_one(l2, False)
+
+
 def transform_weights_for_mega_moe(l1, l2):
     """sm100_b200 style inputs (low-nibble-first packing from per_token_cast_to_fp4)."""
     return transform_mxfp4_weights_for_mega_moe_fused(l1, l2, src_order="low_first")
@@ -185,9 +228,12 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
 
 # ----------------------------------------------------------------------------- fused layer
 def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
-           fast_math=True):
-    w1, sf1, _ = l1
-    w2, sf2, _ = l2
+           fast_math=True, qoq=False):
+    if qoq != (b.act_format == "qoq"):
+        raise ValueError(f"buffer was sized for {b.act_format!r}: use "
+                         f"{'qoq' if b.act_format == 'qoq' else 'mxfp4'}_mega_moe_*")
+    w1, sf1, rs1 = l1
+    w2, sf2, rs2 = l2
     _lib.require_gpu(y, w1, sf1, w2, sf2, stats)
     assert y.dtype == torch.bfloat16 and y.is_contiguous() and y.size(1) == b.hidden
     m = y.size(0) if num_tokens is None else num_tokens
@@ -195,9 +241,16 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
     E_l, H, I = b.num_local_experts, b.hidden, b.intermediate_hidden
     kg = lambda k: (k // 128 + 3) // 4
     assert tuple(w1.shape) == (E_l, 2 * I // 16, H // 128, 64, 16) and w1.dtype == torch.uint8, w1.shape
-    assert tuple(sf1.shape) == (E_l, 2 * I // 16, kg(H), 64, 4) and sf1.dtype == torch.uint8, sf1.shape
     assert tuple(w2.shape) == (E_l, H // 16, I // 128, 64, 16) and w2.dtype == torch.uint8, w2.shape
-    assert tuple(sf2.shape) == (E_l, H // 16, kg(I), 64, 4) and sf2.dtype == torch.uint8, sf2.shape
+    if qoq:   # meta [E, N/16, K/128, 16] (z | s2 << 4 per row), row scales s1 [E, N]
+        _lib.require_gpu(rs1, rs2)
+        assert tuple(sf1.shape) == (E_l, 2 * I // 16, H // 128, 16) and sf1.dtype == torch.uint8, sf1.shape
+        assert tuple(sf2.shape) == (E_l, H // 16, I // 128, 16) and sf2.dtype == torch.uint8, sf2.shape
+        assert tuple(rs1.shape) == (E_l, 2 * I) and rs1.dtype == torch.float32 and rs1.is_contiguous(), rs1.shape
+        assert tuple(rs2.shape) == (E_l, H) and rs2.dtype == torch.float32 and rs2.is_contiguous(), rs2.shape
+    else:
+        assert tuple(sf1.shape) == (E_l, 2 * I // 16, kg(H), 64, 4) and sf1.dtype == torch.uint8, sf1.shape
+        assert tuple(sf2.shape) == (E_l, H // 16, kg(I), 64, 4) and sf2.dtype == torch.uint8, sf2.shape
     assert all(t.is_contiguous() for t in (w1, sf1, w2, sf2))
     if stats is not None:
         assert stats.dtype == torch.int32 and stats.numel() == E_l
@@ -212,7 +265,9 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
                         w2_scales=sf2.data_ptr(), recv_stats=stats.data_ptr() if stats is not None else None,
                         y=y.data_ptr(), buffer=b.buffer.data_ptr(), layout=ctypes.pointer(b.layout),
                         phase_stamps=phase_stamps.data_ptr() if phase_stamps is not None else None,
-                        phase_stamp_rows=phase_stamps.numel() // 8 if phase_stamps is not None else 0)
+                        phase_stamp_rows=phase_stamps.numel() // 8 if phase_stamps is not None else 0,
+                        w1_row_scales=rs1.data_ptr() if qoq else None,
+                        w2_row_scales=rs2.data_ptr() if qoq else None)
     if phase_stamps is not None:
         assert phase_stamps.dtype == torch.int64 and phase_stamps.is_cuda and phase_stamps.is_contiguous()
     fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
@@ -230,6 +285,23 @@ def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
     ``fe_keys`` is accepted for signature compatibility."""
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
            fast_math=fast_math)
+
+
+def qoq_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
+                       fast_math=True, phase_stamps=None, fe_keys=None):
+    """deep_gemm/mega/fused.py:102: the QoQ W4A8 layer (``get_fused_symm_buffer_for_mega_moe(...,
+    act_format="qoq")``, weights from ``transform_qoq_weights_for_mega_moe_fused``): int8
+    activations with one scale per token, 4-bit weight codes with per-(row, K128) zero point and
+    integer scale and per-row fp32 scale, exact int32 group sums; fp32 gate / up, SiLU * up *
+    routing weight, int8 requant per 64 features, L2, fp32 combine -> bf16 ``y``."""
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
+           fast_math=fast_math, qoq=True)
+
+
+def qoq_mega_moe_split(*_, **__):
+    """deep_gemm/mega/__init__.py:584 (the sm90 legacy buffer and QoQ int4 layout). Not provided:
+    the QoQ layer runs as the fused kernel only (``qoq_mega_moe_fused``)."""
+    raise NotImplementedError("qoq_mega_moe_split: use qoq_mega_moe_fused on a qoq buffer")
 
 
 def fused_workgroups(b):
@@ -251,5 +323,6 @@ def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
     is selected in the fused kernel's prologue when the token count allows)."""
     fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
                                      token_offset=token_offset, select_in_mega=True)
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp)
+    # (a qoq buffer runs the QoQ layer: the reference's DG_W4A8_INT=1 route)
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, qoq=b.act_format == "qoq")
     return y

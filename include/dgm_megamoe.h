@@ -24,6 +24,8 @@ extern "C" {
 /* activation formats (the "act_format" of sm100_b200/test_mega_moe.py:57) */
 #define DGM_ACT_MXFP4 0 /* E2M1 + UE8M0 per 32 (W4A4)          */
 #define DGM_ACT_MXFP8 1 /* E4M3 + UE8M0 per 32 (W-MXFP4 x A-FP8) */
+#define DGM_ACT_QOQ 2   /* QoQ W4A8: int8 activations with one fp32 scale per token, QoQ weights
+                           (deep_gemm/quantization_qoq_fused.py:1-11) */
 
 /* frontend flags */
 #define DGM_FE_FORCE_BALANCED 1     /* DG_FE_FORCE_BALANCED: tests/test_four_api_correctness.py:125-144 */
@@ -79,6 +81,15 @@ int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E,
                               int src_order, int l1_interleave, void* dst_values,
                               void* dst_scales, hipStream_t stream);
 
+/* Replaces deep_gemm/mega/fused.py:71 transform_qoq_weights_for_mega_moe_fused (one matrix per
+ * call). packed [E, N, K/2] (Marlin), s2 / z u8 [E, N, K/128], s1 f32 [E, N] ->
+ * dst_values [E, N/16, K/128, 64, 16] (int8 matrix-core fragment order, 4-bit codes),
+ * dst_meta [E, N/16, K/128, 16] (byte r = z | s2 << 4 of row r; z and s2 must be < 16), dst_s1 f32 [E, N] (row order of
+ * dst_values; l1_interleave pairs gate / up 16-row blocks). */
+int dgm_transform_qoq_weights(const void* packed, const void* s2, const void* z, const void* s1, int E, int N,
+                              int K, int l1_interleave, void* dst_values, void* dst_meta, void* dst_s1,
+                              hipStream_t stream);
+
 /* ------------------------------------------------------------------ fused buffer
  * Replaces csrc/apis/mega_fused.hpp:31-76 get_symm_buffer_size_for_fused_mega_moe:
  * byte offsets of every view inside one device buffer (single GPU, no symmetric memory). */
@@ -125,9 +136,9 @@ typedef struct DgmMoeArgs {
   int32_t fe_flags;       /* with select_in_mega: the frontend's DGM_FE_* flags */
   int32_t token_offset;   /* with select_in_mega: global id of row 0 */
   const void* w1_values;  /* [E_local, 2I/16, H/128, 64, 16] */
-  const void* w1_scales;  /* [E_local, 2I/16, ceil(H/512), 64, 4] */
+  const void* w1_scales;  /* MXFP: [E_local, 2I/16, ceil(H/512), 64, 4]; QoQ: meta [E_local, 2I/16, H/128, 16] */
   const void* w2_values;  /* [E_local, H/16, I/128, 64, 16] */
-  const void* w2_scales;  /* [E_local, H/16, ceil(I/512), 64, 4] */
+  const void* w2_scales;  /* MXFP: [E_local, H/16, ceil(I/512), 64, 4]; QoQ: meta [E_local, H/16, I/128, 16] */
   int32_t* recv_stats;    /* [E_local] cumulative_local_expert_recv_stats, may be NULL */
   void* y;                /* bf16 [num_tokens, hidden] */
   void* buffer;
@@ -136,6 +147,8 @@ typedef struct DgmMoeArgs {
                              deep_gemm/mega/fused.py:97); NULL = off. Workgroups beyond
                              phase_stamp_rows record nothing. */
   int32_t phase_stamp_rows;
+  const float* w1_row_scales; /* QoQ: s1 [E_local, 2I] (dgm_transform_qoq_weights order); else unused */
+  const float* w2_row_scales; /* QoQ: s1 [E_local, H]; else unused */
 } DgmMoeArgs;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
@@ -158,6 +171,8 @@ int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const voi
 /* Same with E2M1 x E2M1 operands and the scale taken from byte `sel` (0..3) of sa / sb. */
 int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void* sa, const void* sb, void* out,
                              int sel, hipStream_t stream);
+/* One int8 op (V_MFMA_I32_16X16X64_I8): a, b 64 x 16 bytes, out 64 x 4 int32. */
+int dgm_probe_mfma_i8(const void* a, const void* b, void* out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

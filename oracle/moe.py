@@ -130,6 +130,11 @@ def quant_act(x_f32, act_format):
         q, sf = packers.per_token_cast_to_fp8_ue8m0(x_f32, 32)
         sfb = ((sf.view(np.uint32) >> 23) & 0xFF).astype(np.uint8)
         return q, sfb, packers.dequant_fp8_rows(q, sf, 32)
+    if act_format == "qoq":
+        # per_token_cast_to_int8 (deep_gemm/quantization_qoq_fused.py:78-91); x_reference of
+        # tests/test_four_api_correctness.py:243-246: int8 * the token's scale
+        q, sf = packers.per_token_cast_to_int8(x_f32)
+        return q, sf, (q.astype(np.float32) * sf[:, None]).astype(np.float32)
     raise ValueError(act_format)
 
 
@@ -145,7 +150,25 @@ def requant_mid(a, act_format):
     if act_format == "mxfp8":
         sf = np.exp2(ceil_log2_f32(amax / np.float32(448.0))).astype(np.float32)
         return (e4m3_decode(e4m3_encode(g / sf)) * sf).reshape(a.shape).astype(np.float32)
+    if act_format == "qoq":
+        return requant_mid_qoq(a)[2]
     raise ValueError(act_format)
+
+
+FLT_TINY = np.float32(np.finfo(np.float32).tiny)
+
+
+def requant_mid_qoq(a):
+    """QoQ intermediate requant (tests/test_four_api_correctness.py:54-60, qoq branch): per 64
+    features, scale = max(amax / 127, tiny), q = clamp(rne(a / scale), +-127).
+    Returns (int8 codes, scales [.., n/64], dequantised)."""
+    a = as_f32(a)
+    g = a.reshape(*a.shape[:-1], -1, 64)
+    amax = np.abs(g).max(axis=-1, keepdims=True)
+    sc = np.maximum(amax / np.float32(127.0), FLT_TINY).astype(np.float32)
+    q = np.clip(np.rint(g / sc), -127, 127).astype(np.float32)
+    return (q.astype(np.int8).reshape(a.shape), sc[..., 0],
+            (q * sc).reshape(a.shape).astype(np.float32))
 
 
 def silu(x):
@@ -173,7 +196,7 @@ class LazyDequant:
 
 # ----------------------------------------------------------------------------- layer
 def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=10.0,
-                bf16_gate_up=True):
+                bf16_gate_up=True, route_bf16=False):
     """Expert part of the layer on dequantised inputs.
 
     x_dq [M, H] f32 (dequantised activations), topk_idx [M, k], topk_w [M, k],
@@ -200,10 +223,26 @@ def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=
         act = ((silu(gate) * up).astype(np.float32) * topk_w[t_ids, s_ids][:, None]).astype(np.float32)
         act = requant_mid(act, act_format)
         out = (act @ w2e.T).astype(np.float32)
+        if route_bf16:
+            out = round_bf16(out)
         for n, (t, s) in enumerate(zip(t_ids, s_ids)):
             routes[int(t) * topk + int(s)] = out[n]
             y[t] = (y[t] + out[n]).astype(np.float32)
     return y, routes
+
+
+def moe_forward_qoq(x_dq, topk_idx, topk_w, W1, W2, expert_begin, clamp=10.0):
+    """QoQ W4A8 layer of tests/test_four_api_correctness.py:421-446 on dequantised weights
+    (dequantize_qoq) and activations: fp32 gate/up (no bf16 rounding), clamp, SiLU * up * w,
+    per-64 int8 requant, fp32 down projection rounded to bf16 per route, fp32 sum."""
+    return moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, "qoq", clamp, bf16_gate_up=False,
+                       route_bf16=True)
+
+
+def qoq_group_acc(codes, z, x8):
+    """The W4A8 kernel's int32 accumulator of one K128 group (exact): sum_k (code - z) * x8.
+    codes [N, 128] (0..15), z [N], x8 [T, 128] int8 -> int64 [N, T]."""
+    return (codes.astype(np.int64) - z.astype(np.int64)[:, None]) @ x8.astype(np.int64).T
 
 
 def layer_forward(hidden_bf16_f32, router_w_bf16_f32, W1, W2, expert_begin, act_format,

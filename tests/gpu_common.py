@@ -43,6 +43,31 @@ def decode_native(vals, scales):
     return v.reshape(E, NB * 16, KT * 128).astype(np.float32)
 
 
+def decode_native_qoq(vals, meta, s1):
+    """QoQ native layout -> f32 [E, N, K] in native row order: (code - z) * s2 * s1.
+    vals [E, NB, KT, 64, 16], meta [E, NB, KT, 16] (byte r = z | s2 << 4), s1 [E, N]."""
+    vals = np.asarray(vals).astype(np.int64)
+    meta = np.asarray(meta).astype(np.int64)
+    E, NB, KT, L, B = vals.shape
+    d = vals.reshape(E, NB, KT, 64, 4, 4)                    # dword q of the lane, byte b
+    lo, hi = d & 0xF, d >> 4
+    # op h = q // 2: dword 2h byte b -> K j = b (lo), 4 + b (hi); dword 2h+1 -> 8 + b, 12 + b
+    code = np.zeros((E, NB, KT, 64, 2, 16), np.int64)
+    for h in range(2):
+        code[..., h, 0:4] = lo[..., 2 * h, :]
+        code[..., h, 4:8] = hi[..., 2 * h, :]
+        code[..., h, 8:12] = lo[..., 2 * h + 1, :]
+        code[..., h, 12:16] = hi[..., 2 * h + 1, :]
+    # lane l: row l % 16, op h, K = 64 h + 16 (l // 16) + j
+    c = code.reshape(E, NB, KT, 4, 16, 2, 16).transpose(0, 1, 4, 2, 5, 3, 6)  # E NB r KT h g j
+    c = c.reshape(E, NB, 16, KT, 128)
+    z = (meta & 15).transpose(0, 1, 3, 2)                       # E NB r KT
+    s2 = (meta >> 4).transpose(0, 1, 3, 2)
+    w = (c - z[..., None]) * s2[..., None]
+    w = w.reshape(E, NB * 16, KT * 128).astype(np.float32)
+    return (w * np.asarray(s1, dtype=np.float32)[..., None]).astype(np.float32)
+
+
 def interleave16(w):
     """Native L1 row order: block pair p = (gate rows 16p.., up rows I + 16p..)."""
     E, N, K = w.shape

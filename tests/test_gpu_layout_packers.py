@@ -162,3 +162,63 @@ def test_transform_dequant_invariant():
     (u1, t1, _), (u2, t2, _) = dgm.transform_mxfp4_weights_for_mega_moe_fused(
         (q1[0], q1[1]), (torch.from_numpy(lf).cuda(), q2[1]), src_order="low_first")
     np.testing.assert_array_equal(u2.cpu().numpy(), v2.cpu().numpy())
+
+
+def _i8_kmap(layout, l):
+    g = l // 16
+    if layout == "contiguous":                 # lane bytes j -> K = 16 g + j
+        return np.arange(16 * g, 16 * g + 16)
+    # split halves: bytes 0-7 -> K = 8 g .. +8, bytes 8-15 -> K = 32 + 8 g .. +8
+    return np.concatenate([np.arange(8 * g, 8 * g + 8), np.arange(32 + 8 * g, 40 + 8 * g)])
+
+
+def test_mfma_i8_lane_layout():
+    """V_MFMA_I32_16X16X64_I8 (the W4A8 path): lane l supplies A row l%16 / B column l%16,
+    16 int8 K values; result register i of lane l is D[4*(l/16)+i][l%16], exact int32. The
+    K order of a lane's 16 bytes is the one the W4A8 kernels assume (``I8_KMAP``)."""
+    need_gpu()
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    rng = np.random.default_rng(21)
+    a = rng.integers(-128, 128, (64, 16), dtype=np.int64).astype(np.int8)
+    b = rng.integers(-128, 128, (64, 16), dtype=np.int64).astype(np.int8)
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    out = torch.zeros(64 * 4, dtype=torch.int32, device="cuda")
+    _lib.check(_lib.load().dgm_probe_mfma_i8(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(out), _lib.stream()))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(64, 4)
+    res = {}
+    for layout in ("contiguous", "split"):
+        A = np.zeros((16, 64), np.int64)
+        B = np.zeros((64, 16), np.int64)
+        for l in range(64):
+            A[l % 16, _i8_kmap(layout, l)] = a[l]
+            B[_i8_kmap(layout, l), l % 16] = b[l]
+        D = A @ B
+        exp = np.array([[D[4 * (l // 16) + i, l % 16] for i in range(4)] for l in range(64)])
+        res[layout] = bool((exp == got).all())
+    print(res)
+    assert res[I8_KMAP], res
+
+
+I8_KMAP = "contiguous"
+
+
+def test_transform_qoq_invariant():
+    """QoQ: dequant(transform(q)) == interleave(dequant(q)) for L1 (interleaved) and L2, bit
+    for bit ((code - z) * s2 * s1 is exact in fp32)."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_qoq_fused as qq
+    from tests.gpu_common import decode_native_qoq
+    rng = np.random.default_rng(31)
+    w1 = randn_bf16(rng, (2, 64, 384), 0.05)
+    w2 = randn_bf16(rng, (2, 32, 256), 0.05)
+    q1 = qq.quantize_to_qoq(bf16_cpu(w1).cuda())
+    q2 = qq.quantize_to_qoq(bf16_cpu(w2).cuda())
+    (v1, m1, r1), (v2, m2, r2) = dgm.transform_qoq_weights_for_mega_moe_fused(q1, q2)
+    torch.cuda.synchronize()
+    d1 = pk.dequantize_qoq(*[t.cpu().numpy() for t in q1])
+    d2 = pk.dequantize_qoq(*[t.cpu().numpy() for t in q2])
+    np.testing.assert_array_equal(decode_native_qoq(v1.cpu().numpy(), m1.cpu().numpy(), r1.cpu().numpy()),
+                                  interleave16(d1))
+    np.testing.assert_array_equal(decode_native_qoq(v2.cpu().numpy(), m2.cpu().numpy(), r2.cpu().numpy()), d2)

@@ -1,0 +1,199 @@
+"""GPU parity of the QoQ W4A8 layer (qoq_mega_moe_fused) against the oracle.
+
+Bit-exact: the per-token int8 activation codes and scales of the frontend, the pool.
+Integer path: the intermediate int8 codes and per-64 scales the kernel hands from L1 to L2
+are checked against an exact-integer restatement of L1 (int64 group sums
+sum_k (code - z) * s2 * x8, then float(Q) * s1 * sx): scales within 1e-5 relative error,
+codes equal except for rare +-1 flips where SiLU's hardware exp2 / reciprocal or the fp32
+product order moves a value across a rounding boundary.
+Tolerance (the north star's bar): per-row cos >= 0.9999 and rel-RMSE <= 0.5 % of the bf16
+output against the fp32 oracle of the reference's QoQ test (tests/test_four_api_correctness.py:
+421-446: dequantised weights and activations, fp32 gate / up, per-64 int8 requant, per-route
+bf16)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import packers as pk
+from oracle import moe
+from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.9999
+REL_RMSE_MAX = 0.005
+
+
+class LazyQoQ:
+    """Per-expert dequantisation of quantize_to_qoq outputs (``W[e]`` -> f32 [N, K])."""
+
+    def __init__(self, q):
+        self.p, self.s2, self.z, self.s1 = q
+        E, N, Kh = self.p.shape
+        self.shape = (E, N, 2 * Kh)
+
+    def __getitem__(self, e):
+        return pk.dequantize_qoq(self.p[e:e + 1], self.s2[e:e + 1], self.z[e:e + 1], self.s1[e:e + 1])[0]
+
+
+def make_qoq_weights(E, H, I, seed, scale=0.02):
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_qoq_fused as qq
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    w1 = (torch.randn((E, 2 * I, H), generator=g, device="cuda", dtype=torch.float32) * scale).to(torch.bfloat16)
+    q1 = qq.quantize_to_qoq(w1)
+    del w1
+    w2 = (torch.randn((E, H, I), generator=g, device="cuda", dtype=torch.float32) * scale).to(torch.bfloat16)
+    q2 = qq.quantize_to_qoq(w2)
+    del w2
+    t = dgm.transform_qoq_weights_for_mega_moe_fused(q1, q2)
+    h1 = tuple(a.cpu().numpy() for a in q1)
+    h2 = tuple(a.cpu().numpy() for a in q2)
+    return t, h1, h2
+
+
+def run_qoq(M, E, E_local, expert_begin, H, I, topk, seed, force_balanced=False, zero_rows=(),
+            weights=None, select_in_mega=False):
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    print(f"qoq layer M={M} E={E} E_local={E_local} H={H} I={I} topk={topk} seed={seed} "
+          f"balanced={force_balanced} select_in_mega={select_in_mega}", flush=True)
+    rng = np.random.default_rng(seed)
+    x = randn_bf16(rng, (M, H))
+    for r in zero_rows:
+        x[r] = 0.0
+    rw = randn_bf16(rng, (E, H), 0.02)
+    if weights is None:
+        weights = make_qoq_weights(E_local, H, I, seed + 1)
+    (t1, t2), h1, h2 = weights
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="qoq",
+                                                 ep_size=E // E_local, ep_rank=expert_begin // E_local)
+    xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
+    stats = torch.zeros(E_local, dtype=torch.int32, device="cuda")
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    dgm.fable_router_quant_topk_frontend(xs, rws, buf, force_balanced=force_balanced, select_in_mega=select_in_mega)
+    dgm.qoq_mega_moe_fused(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats)
+    torch.cuda.synchronize()
+    # ---- oracle
+    logits = moe.router_logits_f32(x, rw)
+    idx, w, _ = moe.topk_softmax(logits, topk)
+    if force_balanced:
+        idx, w = moe.balanced_routing(M, E, topk)
+    for r in zero_rows:
+        idx[r] = -1
+        w[r] = 0.0
+    codes, sf, x_dq = moe.quant_act(x, "qoq")
+    ref, _ = moe.moe_forward_qoq(x_dq, idx, w, LazyQoQ(h1), LazyQoQ(h2), expert_begin)
+    return dict(buf=buf, y=y.float().cpu().numpy(), ref=ref, idx=idx, w=w, codes=codes, sf=sf,
+                stats=stats.cpu().numpy(), h1=h1, E_local=E_local, expert_begin=expert_begin, I=I, topk=topk)
+
+
+def check_frontend(r, M):
+    b = r["buf"]
+    np.testing.assert_array_equal(b.topk_idx[:M].cpu().numpy(), r["idx"])
+    np.testing.assert_array_equal(b.x[:M].cpu().numpy(), r["codes"])
+    sf = b.x_sf[:M].cpu().numpy()
+    np.testing.assert_array_equal(sf.view(np.uint32), np.repeat(r["sf"][:, None], sf.shape[1], 1).view(np.uint32))
+
+
+def check_pool(r):
+    counts, active, offsets, routes = r["buf"].pool_table()
+    rc, ra, ro, rr = moe.dispatch(r["idx"], r["expert_begin"], r["E_local"])
+    np.testing.assert_array_equal(counts.numpy(), rc)
+    np.testing.assert_array_equal(routes.numpy(), rr)
+    np.testing.assert_array_equal(r["stats"], rc)
+    return ra, ro, rr
+
+
+def check_mid(r, max_flip_frac=0.01):
+    """Intermediate codes / scales of every route against the exact-integer L1 restatement."""
+    ra, ro, rr = check_pool(r)
+    b, I, topk = r["buf"], r["I"], r["topk"]
+    p, s2, z, s1 = r["h1"]
+    codes_w = pk.unpack_marlin(p)                                      # [E, 2I, H] 0..15
+    total = int(ro[-1])
+    got_q = b.l2_acts[:total].cpu().numpy().astype(np.int64)
+    got_s = b.l2_acts_sf[:total].cpu().numpy()
+    x8 = r["codes"].astype(np.int64)
+    flips = 0
+    for a, e in enumerate(ra):
+        rows = rr[ro[a]:ro[a + 1]]
+        t = rows // topk
+        H = codes_w.shape[2]
+        G = H // 128
+        c = codes_w[e].reshape(2 * I, G, 128).astype(np.int64)
+        acc = np.zeros((2 * I, len(rows)), np.int64)
+        for gi in range(G):
+            acc += s2[e][:, gi, None].astype(np.int64) * moe.qoq_group_acc(c[:, gi], z[e][:, gi], x8[t, gi * 128:(gi + 1) * 128])
+        h = (acc.astype(np.float32) * s1[e][:, None]).astype(np.float32) * r["sf"][t][None, :]
+        gate = np.minimum(h[:I].T, np.float32(10.0))
+        up = np.clip(h[I:].T, -10.0, 10.0).astype(np.float32)
+        act = (moe.silu(gate) * up).astype(np.float32) * r["w"].reshape(-1)[rows][:, None]
+        q, sc, _ = moe.requant_mid_qoq(act.astype(np.float32))
+        gs = got_s[ro[a]:ro[a + 1]]
+        np.testing.assert_allclose(gs, sc, rtol=1e-5, atol=0)
+        d = got_q[ro[a]:ro[a + 1]] - q.astype(np.int64)
+        assert np.abs(d).max() <= 1, (e, np.abs(d).max())
+        flips += int((d != 0).sum())
+    n = total * I
+    assert flips <= max_flip_frac * n, (flips, n)
+    return flips, n
+
+
+def check_y(r, zero_rows=()):
+    assert r["buf"].kernel_error() == 0
+    for zr in zero_rows:
+        assert (r["y"][zr] == 0).all()
+    keep = [i for i in range(r["y"].shape[0]) if i not in zero_rows]
+    m = moe.metrics(r["y"][keep], r["ref"][keep])
+    assert m["cos_min"] >= COS_MIN and m["rel_rmse"] <= REL_RMSE_MAX, m
+    return m
+
+
+def test_qoq_small_layer():
+    need_gpu()
+    r = run_qoq(6, 16, 16, 0, 512, 256, 4, seed=700)
+    check_frontend(r, 6)
+    print("mid flips", check_mid(r))
+    print(check_y(r))
+
+
+def test_qoq_config0_shape():
+    """BASELINE config 0 shape (E=48, H=3072, I=1280, top-8, M=2) on the QoQ path."""
+    need_gpu()
+    r = run_qoq(2, 48, 48, 0, 3072, 1280, 8, seed=710)
+    check_frontend(r, 2)
+    print("mid flips", check_mid(r))
+    print(check_y(r))
+
+
+def test_qoq_ep_share_balanced():
+    """384-way router, forced-balanced, one EP rank's 48 experts, M=16 (config 3's layout)."""
+    need_gpu()
+    r = run_qoq(16, 384, 48, 48, 3072, 1280, 8, seed=720, force_balanced=True)
+    check_frontend(r, 16)
+    print("mid flips", check_mid(r))
+    print(check_y(r))
+
+
+def test_qoq_zero_rows_multi_slab_select_in_mega():
+    """Zero rows unrouted (y == 0), > 16 routes per expert (several slabs), top-k selected in
+    the fused kernel's prologue."""
+    need_gpu()
+    r = run_qoq(40, 8, 8, 0, 1024, 512, 4, seed=730, zero_rows=(3, 17), select_in_mega=True)
+    check_frontend(r, 40)
+    print("mid flips", check_mid(r))
+    print(check_y(r, zero_rows=(3, 17)))
+
+
+def test_qoq_buffer_format_guard():
+    """The MXFP entry points refuse a qoq buffer and the reverse; the QoQ split API is absent."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    b = dgm.get_fused_symm_buffer_for_mega_moe(None, 16, 4, 4, 512, 256, act_format="qoq")
+    y = torch.empty((4, 512), dtype=torch.bfloat16, device="cuda")
+    dummy = (torch.empty(1, device="cuda"),) * 3
+    with pytest.raises(ValueError):
+        dgm.mxfp4_mega_moe_fused(y, dummy, dummy, b)
+    with pytest.raises(NotImplementedError):
+        dgm.qoq_mega_moe_split(y, dummy, dummy, b)
