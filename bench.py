@@ -4,7 +4,8 @@ Headline workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 lay
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
 layer forward: router + top-8 + activation cast, then the fused kernel: dispatch, L1, L2,
 combine). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
-one seeded unbalanced-routing run at M=16. Before every timed step >= 1 GiB is written and
+the QoQ W4A8 layer (int8 activations, QoQ 4-bit weights), and one seeded unbalanced-routing
+run at M=16. Before every timed step >= 1 GiB is written and
 then 1 GiB of other data is read, so neither the 256 MB MALL nor the L2s hold weights (and
 no dirty lines are left to drain inside the timed region); per step, HIP events on the
 layer's stream bracket the frontend and the fused kernel.
@@ -26,6 +27,9 @@ sys.path.insert(0, HERE)
 
 E, H, I, TOPK = 384, 3072, 1280, 8
 MXFP4_EXPERT_BYTES = 6266880          # W1 + W2 values + E8M0 scales of one expert
+# QoQ W4A8: 4-bit codes (5,898,240 B) + one meta byte (z | s2 << 4) per row and K128 group
+# (2I * H/128 + H * I/128 = 92,160 B) + fp32 row scales s1 ((2I + H) * 4 = 22,528 B)
+QOQ_EXPERT_BYTES = 6012928
 HBM_PEAK_GBS = 8000.0
 
 
@@ -67,10 +71,40 @@ def build_weights(torch, seed, n_experts, chunk=32):
     return t, (p1, s1, p2, s2)
 
 
+def build_qoq_weights(torch, seed, n_experts, chunk=32):
+    """The same layer's weights in the QoQ W4A8 format (quantize_to_qoq on the GPU, then the
+    fused layout)."""
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_qoq_fused as qq
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    dev = "cuda"
+
+    def alloc(N, K):
+        return (torch.empty((n_experts, N, K // 2), dtype=torch.uint8, device=dev),
+                torch.empty((n_experts, N, K // 128), dtype=torch.uint8, device=dev),
+                torch.empty((n_experts, N, K // 128), dtype=torch.uint8, device=dev),
+                torch.empty((n_experts, N), dtype=torch.float32, device=dev))
+    q1, q2 = alloc(2 * I, H), alloc(H, I)
+    for e0 in range(0, n_experts, chunk):
+        e1 = min(n_experts, e0 + chunk)
+        for q, (N, K) in ((q1, (2 * I, H)), (q2, (H, I))):
+            w = (torch.randn((e1 - e0, N, K), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+            for dst, src in zip(q, qq.quantize_to_qoq(w)):
+                dst[e0:e1] = src
+            del w
+    t = dgm.transform_qoq_weights_for_mega_moe_fused(q1, q2)
+    del q1, q2
+    torch.cuda.synchronize()
+    return t
+
+
 def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True):
     """Times `steps` layer forwards. Per step three HIP events on the layer's stream: before the
     frontend, between frontend and the fused MoE kernel, after it."""
     (t1, t2) = weights
+    fused = dgm.qoq_mega_moe_fused if act == "qoq" else dgm.mxfp4_mega_moe_fused
+    expert_bytes = QOQ_EXPERT_BYTES if act == "qoq" else MXFP4_EXPERT_BYTES
     buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -92,7 +126,7 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
         if e: e[0].record(stream)
         dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=force_balanced, select_in_mega=True)
         if e: e[1].record(stream)
-        dgm.mxfp4_mega_moe_fused(y, t1, t2, buf)
+        fused(y, t1, t2, buf)
         if e: e[2].record(stream)
 
     for _ in range(warmup):
@@ -113,7 +147,7 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     ok = bool(torch.isfinite(y.float()).all()) and buf.kernel_error() == 0
     return dict(us_median=float(np.median(us)), us_min=float(us.min()), fe_us=float(np.median(us_fe)),
                 moe_us=float(np.median(us_moe)), moe_us_min=float(us_moe.min()), n_active=n_active,
-                weight_bytes=n_active * MXFP4_EXPERT_BYTES, finite=ok, wall_s=wall, y=y)
+                weight_bytes=n_active * expert_bytes, finite=ok, wall_s=wall, y=y)
 
 
 def copy_calibration(torch, mib, reps=3):
@@ -185,6 +219,7 @@ def main():
     ap.add_argument("--act", default="mxfp8", choices=["mxfp8", "mxfp4"], help="activation format of the headline line")
     ap.add_argument("--sweep", default="2,4,8,16", help="M values of the sweep (both activation formats)")
     ap.add_argument("--sweep-steps", type=int, default=10)
+    ap.add_argument("--no-qoq", action="store_true", help="skip the QoQ W4A8 sweep")
     ap.add_argument("--no-unbalanced", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -218,6 +253,15 @@ def main():
             r = time_layer(torch, dgm, M, weights, router_w, act, args.sweep_steps, args.warmup, 500 + M)
             sweep[act][M] = entry(r)
             log(f"M={M} {act}: {sweep[act][M]}")
+    if not args.no_qoq and [v for v in args.sweep.split(",") if v]:
+        log("building E384 QoQ weights ...")
+        qw = build_qoq_weights(torch, 4321, E)
+        sweep["qoq"] = {}
+        for M in [int(v) for v in args.sweep.split(",") if v]:
+            r = time_layer(torch, dgm, M, qw, router_w, "qoq", args.sweep_steps, args.warmup, 500 + M)
+            sweep["qoq"][M] = entry(r)
+            log(f"M={M} qoq: {sweep['qoq'][M]}")
+        del qw
     if not args.no_unbalanced:
         r = time_layer(torch, dgm, 16, weights, router_w, "mxfp8", args.sweep_steps, args.warmup, 777,
                        force_balanced=False)

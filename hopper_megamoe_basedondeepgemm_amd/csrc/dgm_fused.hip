@@ -121,6 +121,13 @@ DGM_DEV uint32_t qoq_meta(const uint32_t* md, int kq) {
   return (uint32_t)__builtin_amdgcn_ds_bpermute(((4 * U + kq) & 63) * 4, (int)md[U >> 4]);
 }
 DGM_DEV v4i lo4(v8i v) { return __builtin_shufflevector(v, v, 0, 1, 2, 3); }
+// acc += a * b on the low 24 bits of a and b (full-rate VALU). Written out because the
+// compiler, seeing only the low 24 bits of a product demanded, rewrites a 24-bit multiply
+// into a quarter-rate 32-bit one. The operands are VALU results and the destination is the
+// accumulator's own register (never a matrix-core operand), so no matrix-core hazard applies.
+DGM_DEV void mad_i24_acc(int& acc, int a, int b) {
+  asm("v_mad_i32_i24 %0, %1, %2, %0" : "+v"(acc) : "v"(a), "v"(b));
+}
 // Compiler-only ordering point: the matrix-core ops that use `b` come after the VALU work that
 // produced `q` (otherwise the scheduler issues every op of a loop first and keeps all their
 // results live until the end)
@@ -151,11 +158,14 @@ struct FusedSmem {
     U4 bst[KTM][64][BV];               // B slab in matrix-core fragment order
   };
   uint32_t bsc[(KTM + 3) / 4][64];     // its E8M0 scales, 4 K-tiles per dword
-  // QoQ slab extras: per column and 64-K chunk the sum of the column's int8 values (for the
-  // zero-point term), and per chunk and column the activation scale (chunk 0 only for the
-  // per-token scale of the input activations)
-  alignas(16) int xsum[ACT == DGM_ACT_QOQ ? 16 : 1][ACT == DGM_ACT_QOQ ? 2 * KTM : 1];
-  alignas(16) float csc[ACT == DGM_ACT_QOQ ? 16 : 1][ACT == DGM_ACT_QOQ ? 2 * KTM : 1];
+  // QoQ slab extras. Input rows (L1): per column and K-tile the sum of the column's int8
+  // values (for the zero-point term) and per column the token's scale. Intermediate rows (L2):
+  // per column and K-tile (chunks h = 0, 1 of 64 K with scales sm_h and value sums X_h) the
+  // promote coefficients {sm_0, sm_1 / 16, 8 X_1 sm_1, -(X_0 sm_0 + X_1 sm_1)}.
+  static constexpr int QX = ACT == DGM_ACT_QOQ ? 16 : 1;
+  alignas(16) int xsum[QX][ACT == DGM_ACT_QOQ ? KT1 : 1];
+  float xsc[QX];
+  alignas(16) float4 qc[QX][ACT == DGM_ACT_QOQ ? KT2 : 1];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
@@ -285,7 +295,8 @@ struct SlabRegs {
   uint64_t h[FR][4];             // coherent fragments: 64-bit halves (K bytes 0-15, 64-79)
   uint32_t sb[4];                // scale dwords of K-tiles 4g .. 4g+3 (byte l/16 is this lane's)
   uint32_t ok;                   // bit j: fragment j holds a real row; bit 8 + j: scale byte j
-  float fsc;                     // QoQ: an activation scale (see slab_load)
+  float fsc;                     // QoQ input rows: the token's scale (threads 0-15)
+  uint64_t sc2[FR];              // QoQ intermediate rows: fragment j's two chunk scales (lanes 0-15)
   float w;
 };
 
@@ -320,16 +331,25 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
   constexpr int KG = (KT + 3) / 4;
   static_assert(KG * 64 <= FT, "one scale word per thread");
   if constexpr (ACT == DGM_ACT_QOQ) {
-    // activations: one fp32 scale per token (row pitch KT * 4 bytes: the reference's
-    // [M, K/128] copies), thread c < 16; intermediate rows (COHERENT): one per 64-K chunk (row
-    // pitch KT * 8 bytes), thread 16 ch + c
-    static_assert(!COHERENT || 32 * KT <= FT, "one chunk scale per thread");
-    const int c = tid & 15, ch = tid >> 4;
-    const bool have = c < n && (COHERENT ? ch < 2 * KT : ch == 0);
-    const size_t rr = have ? (size_t)row_of(c) : 0;
-    const float* q = reinterpret_cast<const float*>(ssrc + rr * (COHERENT ? KT * 8 : KT * 4)) + (have ? ch : 0);
-    r.fsc = COHERENT ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *q;
-    ok |= have ? 1u << 8 : 0u;
+    if (COHERENT) {
+      // intermediate rows: fp32 scale per 64-K chunk (row pitch KT * 8 bytes); lane l < 16 of
+      // fragment j (K-tile kt, column l) loads the two chunk scales of its tile
+#pragma unroll
+      for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+        const int f = tid + j * FT;
+        const bool have = (ok >> j) & 1u && (f & 63) < 16;
+        const size_t rr = have ? (size_t)row_of(f & 15) : 0;
+        r.sc2[j] = ld_agent64(ssrc + rr * (KT * 8) + (have ? (f >> 6) * 8 : 0));
+      }
+    } else {
+      // input rows: one fp32 scale per token (row pitch KT * 4 bytes: the reference's
+      // [M, K/128] copies), thread c < 16
+      const int c = tid & 15;
+      const bool have = tid < 16 && c < n;
+      const size_t rr = have ? (size_t)row_of(c) : 0;
+      r.fsc = *reinterpret_cast<const float*>(ssrc + rr * (KT * 4));
+      ok |= have ? 1u << 8 : 0u;
+    }
   } else {
     const int g = tid >> 6, l = tid & 63, c = l & 15;
     const bool have = tid < KG * 64 && c < n;
@@ -396,12 +416,18 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
         s1 += __shfl_xor(s1, 16);
         s1 += __shfl_xor(s1, 32);
         if (l < 16) {
-          s.xsum[l][2 * kt] = s0;
-          s.xsum[l][2 * kt + 1] = s1;
+          if (COHERENT) {        // intermediate rows (L2): the K-tile's promote coefficients
+            const float sm0 = have ? __uint_as_float((uint32_t)r.sc2[j]) : 0.f;
+            const float sm1 = have ? __uint_as_float((uint32_t)(r.sc2[j] >> 32)) : 0.f;
+            const float x0 = (float)s0, x1 = (float)s1;
+            s.qc[l][kt] = make_float4(sm0, sm1 * 0.0625f, 8.f * x1 * sm1, -fmaf(x1, sm1, x0 * sm0));
+          } else {               // input rows (L1): per K-tile
+            s.xsum[l][kt] = s0 + s1;
+          }
         }
       }
     }
-    if (COHERENT ? tid < 32 * KT : tid < 16) s.csc[tid & 15][tid >> 4] = (r.ok >> 8) & 1u ? r.fsc : 0.f;
+    if (!COHERENT && tid < 16) s.xsc[tid] = (r.ok >> 8) & 1u ? r.fsc : 0.f;
   } else if (tid < KG * 64) {
     uint32_t w = 0;
 #pragma unroll
@@ -626,7 +652,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (has_next && nq != q0) load_scales(nq, sn);
       if (restage) load_slab(pre, na, ns0);
       const float wt_r = s.slab_w[c];
-      const float sx = ACT == DGM_ACT_QOQ ? s.csc[c][0] : 1.f;     // QoQ: the token's activation scale
+      const float sx = ACT == DGM_ACT_QOQ ? s.xsc[c] : 1.f;       // QoQ: the token's activation scale
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -639,16 +665,20 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         // per K-tile: two int8 ops on the raw 4-bit codes (exact int32 sums of code * x), then,
         // one tile later (off the matrix-core result's latency), the zero-point correction
         // P = acc - z * sum(x) and the group scale: Q += s2 * P (exact: |Q| < 2^31)
+        // (the promote's LDS inputs of a tile are read two ops ahead of their use)
         v4i qa = {0, 0, 0, 0}, prev = {0, 0, 0, 0};
-        auto promote = [&](auto uc, v4i a) __attribute__((always_inline)) {
-          constexpr int u = decltype(uc)::value;
-          const int2 xx = *reinterpret_cast<const int2*>(&s.xsum[c][2 * u]);
-          const int X = xx.x + xx.y;
-          const uint32_t md = qoq_meta<u>(sd, kq);
+        uint32_t md_c = qoq_meta<0>(sd, kq), md_n = 0;
+        int x_c = s.xsum[c][0], x_n = 0;
+        auto promote = [&](v4i a, uint32_t md, int X) __attribute__((always_inline)) {
+          const int nX = -X;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
+            // 24-bit multiplies (full rate; a 32-bit multiply is quarter rate): z, s2 < 16,
+            // |X| <= 128 * 127, |a - z X| <= 128 * 15 * 127 < 2^23
             const int z = (int)((md >> (8 * i)) & 15u), s2 = (int)((md >> (8 * i + 4)) & 15u);
-            qa[i] += (a[i] - z * X) * s2;
+            int q = qa[i];
+            mad_i24_acc(q, a[i] + __mul24(z, nX), s2);
+            qa[i] = q;
           }
         };
         static_for<KT1>([&](auto tc) {
@@ -662,10 +692,16 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           at = mfma_i8_16x16x64(qoq_codes(w.z, w.w), hi4(bop), at);
           if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, at);
           else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, at);
-          if constexpr (t > 0) promote(std::integral_constant<int, t - 1>{}, prev);
+          if constexpr (t > 0) promote(prev, md_n, x_n);         // tile t - 1
+          md_n = md_c;
+          x_n = x_c;
+          if constexpr (t + 1 < KT1) {
+            md_c = qoq_meta<t + 1>(sd, kq);
+            x_c = s.xsum[c][t + 1];
+          }
           prev = at;
         });
-        promote(std::integral_constant<int, KT1 - 1>{}, prev);
+        promote(prev, md_n, x_n);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = (float)qa[i] * __uint_as_float(sd[MR1 + i]) * sx;
       } else {
@@ -943,20 +979,26 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       };
       v8i bq0 = bfrag(0), bq1 = bfrag(1 % KT2);
       if constexpr (ACT == DGM_ACT_QOQ) {
-        // per K-tile two int8 ops, one per 64-K chunk (the intermediate's scale changes every
-        // 64 features); one tile later: f += s2 * sum_h float(acc_h - z * sum(x_h)) * scale_h
+        // Per K-tile two int8 ops, one per 64-K chunk (the intermediate's scale changes every
+        // 64 features). The down-projection codes are stored chunk-split: low nibbles = chunk 0,
+        // high nibbles = chunk 1 XOR 8, so op 0 takes (d & 0x0F0F0F0F) = code and op 1 takes
+        // (d & 0xF0F0F0F0) = 16 code - 128 (as int8) with one mask each. With X_h the chunk's
+        // value sums and sm_h its scales (per column), one tile later:
+        //   f += s2 * (sm_0 M_0 + sm_1 / 16 M_1 + 8 X_1 sm_1 - z (X_0 sm_0 + X_1 sm_1))
+        // (the coefficients per column and tile come from LDS, read two ops ahead of use)
         v4i p0 = {0, 0, 0, 0}, p1 = {0, 0, 0, 0};
-        auto promote = [&](auto uc, v4i a0, v4i a1) __attribute__((always_inline)) {
-          constexpr int u = decltype(uc)::value;
-          constexpr int jb = u / KT2, k = u % KT2;
-          const int2 xx = *reinterpret_cast<const int2*>(&s.xsum[c][2 * k]);
-          const float2 sm = *reinterpret_cast<const float2*>(&s.csc[c][2 * k]);
-          const uint32_t md = qoq_meta<u>(sd, kq);
+        uint32_t md_c = qoq_meta<0>(sd, kq), md_n = 0;
+        float4 qc_c = s.qc[c][0], qc_n = make_float4(0.f, 0.f, 0.f, 0.f);
+        auto promote = [&](auto jc, v4i m0, v4i m1, uint32_t md, float4 q) __attribute__((always_inline)) {
+          constexpr int jb = decltype(jc)::value;
+          uint32_t zb = md & 0x0F0F0F0Fu, sb = (md >> 4) & 0x0F0F0F0Fu;
+          asm("" : "+v"(zb), "+v"(sb));     // (keeps the byte-wise int -> float conversions)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int z = (int)((md >> (8 * i)) & 15u);
-            const float s2 = (float)((md >> (8 * i + 4)) & 15u);
-            const float v = fmaf((float)(a1[i] - z * xx.y), sm.y, (float)(a0[i] - z * xx.x) * sm.x);
+            const float z = (float)((zb >> (8 * i)) & 0xffu), s2 = (float)((sb >> (8 * i)) & 0xffu);
+            float v = fmaf(z, q.w, q.z);
+            v = fmaf((float)m1[i], q.y, v);
+            v = fmaf((float)m0[i], q.x, v);
             acc[jb][i] = fmaf(s2, v, acc[jb][i]);
           }
         };
@@ -968,15 +1010,25 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if constexpr (t + 2 < TI2) bq1 = bfrag((t + 2) % KT2);
           if constexpr (t >= 2) after_values(bop, acc[(t - 2) / KT2]);   // (tile t - 2 promoted)
           const U4 w = wr[k];
-          const v4i a0 = mfma_i8_16x16x64(qoq_codes(w.x, w.y), lo4(bop), v4i{0, 0, 0, 0});
-          const v4i a1 = mfma_i8_16x16x64(qoq_codes(w.z, w.w), hi4(bop), v4i{0, 0, 0, 0});
+          const v4i c0 = {(int)(w.x & 0x0F0F0F0Fu), (int)(w.y & 0x0F0F0F0Fu), (int)(w.z & 0x0F0F0F0Fu),
+                          (int)(w.w & 0x0F0F0F0Fu)};
+          const v4i c1 = {(int)(w.x & 0xF0F0F0F0u), (int)(w.y & 0xF0F0F0F0u), (int)(w.z & 0xF0F0F0F0u),
+                          (int)(w.w & 0xF0F0F0F0u)};
+          const v4i a0 = mfma_i8_16x16x64(c0, lo4(bop), v4i{0, 0, 0, 0});
+          const v4i a1 = mfma_i8_16x16x64(c1, hi4(bop), v4i{0, 0, 0, 0});
           if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, a1);
           else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, a1);
-          if constexpr (t > 0) promote(std::integral_constant<int, t - 1>{}, p0, p1);
+          if constexpr (t > 0) promote(std::integral_constant<int, (t - 1) / KT2>{}, p0, p1, md_n, qc_n);
+          md_n = md_c;
+          qc_n = qc_c;
+          if constexpr (t + 1 < TI2) {
+            md_c = qoq_meta<t + 1>(sd, kq);
+            qc_c = s.qc[c][(t + 1) % KT2];
+          }
           p0 = a0;
           p1 = a1;
         });
-        promote(std::integral_constant<int, TI2 - 1>{}, p0, p1);
+        promote(std::integral_constant<int, (TI2 - 1) / KT2>{}, p0, p1, md_n, qc_n);
 #pragma unroll
         for (int j = 0; j < RB2; ++j) {
           acc[j][0] *= __uint_as_float(s1r[j].x);

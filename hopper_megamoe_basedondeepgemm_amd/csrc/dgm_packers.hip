@@ -299,9 +299,12 @@ __global__ void k_transform_fp4(const uint8_t* __restrict__ src, const uint8_t* 
 
 // QoQ (W4A8) weights -> the fused kernel's layout (one thread per (expert, 16-row block,
 // K-tile, lane)). Values [E][N/16][K/128][64][16 B]: lane l = row l%16; its 16 bytes hold the
-// two K=64 int8 operands (op h: K = 64 h + 16 (l/16) + j, j = 0..15) as nibbles: dword 2h
-// byte b = n[b] | n[4+b] << 4, dword 2h+1 byte b = n[8+b] | n[12+b] << 4, so the 16 int8
-// codes come out as (d & 0x0F0F0F0F, (d >> 4) & 0x0F0F0F0F) per dword. Meta [E][N/16][K/128]
+// two K=64 int8 operands (op h: codes n[h][j] of K = 64 h + 16 (l/16) + j, j = 0..15) as
+// nibbles. L1 (l1_interleave = 1), paired: dword 2h byte b = n[h][b] | n[h][4+b] << 4, dword
+// 2h+1 byte b = n[h][8+b] | n[h][12+b] << 4, so op h's codes come out as (d & 0x0F0F0F0F,
+// (d >> 4) & 0x0F0F0F0F) of its two dwords. L2 (l1_interleave = 0), chunk-split: dword q byte
+// b = n[0][4q+b] | (n[1][4q+b] ^ 8) << 4, so op 0 is (d & 0x0F0F0F0F) and op 1 is
+// (d & 0xF0F0F0F0) = 16 code - 128 as int8, one mask per dword. Meta [E][N/16][K/128]
 // [16 B]: byte r = z | s2 << 4 of row r (both are 4-bit by construction: z 0..15, s2 1..15),
 // so dword kq holds the four rows 4 kq .. +3 that lane group kq accumulates. s1 [E][N] in the
 // same row order. l1_interleave as for the MXFP4 transform.
@@ -323,28 +326,36 @@ __global__ void k_transform_qoq(const uint8_t* __restrict__ src, const uint8_t* 
   if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
   else src_row = 16 * q + r;
   const uint8_t* row = src + ((int64_t)e * N + src_row) * (K / 2);
-  uint32_t o[4];
+  uint32_t n[2][16];       // codes of K = 128 kt + 64 h + 16 g + j
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    // K = 128 kt + 64 h + 16 g .. +16: two Marlin chunks of 8 (byte b = K[b] << 4 | K[b+4])
+    // two Marlin chunks of 8 (byte b = K[b] << 4 | K[b+4])
     const uint8_t* c = row + (128 * kt + 64 * h + 16 * g) / 2;
-    uint32_t n[16];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const uint32_t byte = c[4 * ch + b];
-        n[8 * ch + b] = byte >> 4;
-        n[8 * ch + b + 4] = byte & 0xfu;
+        n[h][8 * ch + b] = byte >> 4;
+        n[h][8 * ch + b + 4] = byte & 0xfu;
       }
-    uint32_t d0 = 0, d1 = 0;
+  }
+  uint32_t o[4] = {0u, 0u, 0u, 0u};
+  if (l1_interleave) {
+    // paired: dword 2h byte b = n[h][b] | n[h][4+b] << 4, dword 2h+1 byte b = n[h][8+b] | n[h][12+b] << 4
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      d0 |= (n[b] | (n[4 + b] << 4)) << (8 * b);
-      d1 |= (n[8 + b] | (n[12 + b] << 4)) << (8 * b);
-    }
-    o[2 * h] = d0;
-    o[2 * h + 1] = d1;
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        o[2 * h] |= (n[h][b] | (n[h][4 + b] << 4)) << (8 * b);
+        o[2 * h + 1] |= (n[h][8 + b] | (n[h][12 + b] << 4)) << (8 * b);
+      }
+  } else {
+    // chunk-split: dword q byte b = n[0][4q+b] | (n[1][4q+b] ^ 8) << 4
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) o[q] |= (n[0][4 * q + b] | ((n[1][4 * q + b] ^ 8u) << 4)) << (8 * b);
   }
   const int64_t tile = ((int64_t)e * NB + q) * KT + kt;
   *reinterpret_cast<U4*>(dst + tile * 1024 + lane * 16) = U4{o[0], o[1], o[2], o[3]};

@@ -83,7 +83,9 @@ int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E,
 
 /* Replaces deep_gemm/mega/fused.py:71 transform_qoq_weights_for_mega_moe_fused (one matrix per
  * call). packed [E, N, K/2] (Marlin), s2 / z u8 [E, N, K/128], s1 f32 [E, N] ->
- * dst_values [E, N/16, K/128, 64, 16] (int8 matrix-core fragment order, 4-bit codes),
+ * dst_values [E, N/16, K/128, 64, 16] (int8 matrix-core fragment order, 4-bit codes; the L1
+ * layout (l1_interleave = 1) pairs the nibbles of one 64-K operand, the L2 layout splits them
+ * by 64-K chunk with the high one offset by 8),
  * dst_meta [E, N/16, K/128, 16] (byte r = z | s2 << 4 of row r; z and s2 must be < 16), dst_s1 f32 [E, N] (row order of
  * dst_values; l1_interleave pairs gate / up 16-row blocks). */
 int dgm_transform_qoq_weights(const void* packed, const void* s2, const void* z, const void* s1, int E, int N,

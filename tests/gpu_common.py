@@ -43,21 +43,27 @@ def decode_native(vals, scales):
     return v.reshape(E, NB * 16, KT * 128).astype(np.float32)
 
 
-def decode_native_qoq(vals, meta, s1):
+def decode_native_qoq(vals, meta, s1, l1=True):
     """QoQ native layout -> f32 [E, N, K] in native row order: (code - z) * s2 * s1.
-    vals [E, NB, KT, 64, 16], meta [E, NB, KT, 16] (byte r = z | s2 << 4), s1 [E, N]."""
+    vals [E, NB, KT, 64, 16], meta [E, NB, KT, 16] (byte r = z | s2 << 4), s1 [E, N].
+    l1: the paired-nibble L1 layout, else the chunk-split L2 layout (high nibble ^ 8)."""
     vals = np.asarray(vals).astype(np.int64)
     meta = np.asarray(meta).astype(np.int64)
     E, NB, KT, L, B = vals.shape
     d = vals.reshape(E, NB, KT, 64, 4, 4)                    # dword q of the lane, byte b
     lo, hi = d & 0xF, d >> 4
-    # op h = q // 2: dword 2h byte b -> K j = b (lo), 4 + b (hi); dword 2h+1 -> 8 + b, 12 + b
     code = np.zeros((E, NB, KT, 64, 2, 16), np.int64)
-    for h in range(2):
-        code[..., h, 0:4] = lo[..., 2 * h, :]
-        code[..., h, 4:8] = hi[..., 2 * h, :]
-        code[..., h, 8:12] = lo[..., 2 * h + 1, :]
-        code[..., h, 12:16] = hi[..., 2 * h + 1, :]
+    if l1:
+        # op h: dword 2h byte b -> K j = b (lo), 4 + b (hi); dword 2h+1 -> 8 + b, 12 + b
+        for h in range(2):
+            code[..., h, 0:4] = lo[..., 2 * h, :]
+            code[..., h, 4:8] = hi[..., 2 * h, :]
+            code[..., h, 8:12] = lo[..., 2 * h + 1, :]
+            code[..., h, 12:16] = hi[..., 2 * h + 1, :]
+    else:
+        # dword q byte b: lo -> op 0 K j = 4q + b, hi ^ 8 -> op 1 K j = 4q + b
+        code[..., 0, :] = lo.reshape(E, NB, KT, 64, 16)
+        code[..., 1, :] = (hi ^ 8).reshape(E, NB, KT, 64, 16)
     # lane l: row l % 16, op h, K = 64 h + 16 (l // 16) + j
     c = code.reshape(E, NB, KT, 4, 16, 2, 16).transpose(0, 1, 4, 2, 5, 3, 6)  # E NB r KT h g j
     c = c.reshape(E, NB, 16, KT, 128)
