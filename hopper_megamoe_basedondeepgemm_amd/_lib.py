@@ -11,7 +11,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdgm_megamoe.so")
 
-ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1, "qoq": 2}
+ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1, "qoq": 2, "nvfp4": 3}
 FE_FORCE_BALANCED = 1
 FE_ZERO_ROW_UNROUTED = 2
 FE_SELECT_IN_MEGA = 4
@@ -23,8 +23,8 @@ EXPORTS = [
     "dgm_megamoe_split_launch",
     "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_probe_mfma_scale",
     "dgm_probe_mfma_scale_sel",
-    "dgm_probe_mfma_i8",
-    "dgm_transform_qoq_weights",
+    "dgm_probe_mfma_i8", "dgm_probe_mfma_f16", "dgm_probe_cvt_fp4",
+    "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights",
 ]
 
 
@@ -50,7 +50,8 @@ class MoeArgs(ctypes.Structure):
                 ("recv_stats", ctypes.c_void_p), ("y", ctypes.c_void_p), ("buffer", ctypes.c_void_p),
                 ("layout", ctypes.POINTER(BufferLayout)), ("phase_stamps", ctypes.c_void_p),
                 ("phase_stamp_rows", ctypes.c_int32), ("w1_row_scales", ctypes.c_void_p),
-                ("w2_row_scales", ctypes.c_void_p)]
+                ("w2_row_scales", ctypes.c_void_p), ("l1_global_scales", ctypes.c_void_p),
+                ("l2_global_scales", ctypes.c_void_p)]
 
 
 _lib = None
@@ -85,7 +86,10 @@ def load():
         "dgm_probe_mfma_scale": ([vp, vp, vp, vp, vp, i32, i32, vp], i32),
         "dgm_probe_mfma_scale_sel": ([vp, vp, vp, vp, vp, i32, vp], i32),
         "dgm_probe_mfma_i8": ([vp, vp, vp, vp], i32),
+        "dgm_probe_mfma_f16": ([vp, vp, vp, vp], i32),
+        "dgm_probe_cvt_fp4": ([vp, vp, vp, vp, i32, vp], i32),
         "dgm_transform_qoq_weights": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
+        "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -109,6 +109,36 @@ DGM_DEV U4 ld_stream_after(const uint8_t* base, int off, v4i acc) {
   asm("" : "+v"(off) : "v"(acc[0]));
   return ld_stream(base + off);
 }
+DGM_DEV uint32_t ld_stream32(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+DGM_DEV uint32_t ld_stream32_after(const uint8_t* base, int off, v4f acc) {
+  asm("" : "+v"(off) : "v"(acc[0]));
+  return ld_stream32(base + off);
+}
+// NVFP4 weight operand of op j: the lane's eight E2M1 codes (dword w) -> f16, times the
+// E4M3 block scale sv (exact in f16)
+DGM_DEV v8h nvfp4_operand(uint32_t w, _Float16 sv) {
+  const v2h ss = {sv, sv};
+  const v2h h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * ss;
+  const v2h h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * ss;
+  const v2h h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * ss;
+  const v2h h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * ss;
+  return __builtin_shufflevector(__builtin_shufflevector(h0, h1, 0, 1, 2, 3), __builtin_shufflevector(h2, h3, 0, 1, 2, 3),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
+DGM_DEV v8h as_v8h(U4 u) { return __builtin_bit_cast(v8h, u); }
+// one NVFP4 K-tile (four f16 ops): weight codes w, the lane's scale dword sw (byte j = op j's
+// block scale), B operands b[4]
+DGM_DEV v4f nvfp4_tile(U4 w, uint32_t sw, const U4 (&b)[4], v4f acc) {
+  const v2h s01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sw, 1.0f, false);
+  const v2h s23 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sw, 1.0f, true);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nvfp4_operand(w.x, s01.x), as_v8h(b[0]), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nvfp4_operand(w.y, s01.y), as_v8h(b[1]), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nvfp4_operand(w.z, s23.x), as_v8h(b[2]), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nvfp4_operand(w.w, s23.y), as_v8h(b[3]), acc, 0, 0, 0);
+  return acc;
+}
 DGM_DEV void st_agent32(void* p, uint32_t v) {
   __hip_atomic_store((uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -140,7 +170,9 @@ constexpr int NW = FT / 64;
 
 template <int KT1, int KT2, int ACT>
 struct FusedSmem {
-  static constexpr int BV = ACT == DGM_ACT_MXFP4 ? 1 : 2;          // U4 per lane per K-tile
+  // U4 per lane per K-tile: E2M1 (32 codes), E4M3 / int8 (two 16-byte halves), NVFP4 as f16
+  // (four ops of eight halves)
+  static constexpr int BV = ACT == DGM_ACT_MXFP4 ? 1 : ACT == DGM_ACT_NVFP4 ? 4 : 2;
   static constexpr int KTM = KT1 > KT2 ? KT1 : KT2;
   int exp_of_route[FUSED_MAX_ROUTES];
   float route_w[FUSED_MAX_ROUTES];     // routing weight of each route
@@ -166,6 +198,8 @@ struct FusedSmem {
   alignas(16) int xsum[QX][ACT == DGM_ACT_QOQ ? KT1 : 1];
   float xsc[QX];
   alignas(16) float4 qc[QX][ACT == DGM_ACT_QOQ ? KT2 : 1];
+  // NVFP4: per local expert the L1 / L2 output scales (1 when not given)
+  float gsl[2][ACT == DGM_ACT_NVFP4 ? FUSED_MAX_LOCAL : 1];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
@@ -297,6 +331,7 @@ struct SlabRegs {
   uint32_t ok;                   // bit j: fragment j holds a real row; bit 8 + j: scale byte j
   float fsc;                     // QoQ input rows: the token's scale (threads 0-15)
   uint64_t sc2[FR];              // QoQ intermediate rows: fragment j's two chunk scales (lanes 0-15)
+  uint32_t s16[FR];              // NVFP4: the dword holding fragment j's two 16-block scales
   float w;
 };
 
@@ -313,24 +348,34 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
     ok |= have ? 1u << j : 0u;
     const int kt = have ? f >> 6 : 0;
     const size_t rr = have ? (size_t)row_of(c) : 0;
-    // E2M1: 16 bytes at K = 32 g; E4M3: K = 16 g .. +16 and K = 64 + 16 g .. +16 (g = l / 16)
-    const uint8_t* q = ACT == DGM_ACT_MXFP4 ? src + rr * row_bytes + kt * 64 + (l >> 4) * 16
-                                            : src + rr * row_bytes + kt * 128 + (l >> 4) * 16;
+    // E2M1 (MXFP4, NVFP4): 16 bytes at K = 32 g; E4M3 / int8: K = 16 g .. +16 and
+    // K = 64 + 16 g .. +16 (g = l / 16)
+    constexpr bool FP4 = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_NVFP4;
+    const uint8_t* q = FP4 ? src + rr * row_bytes + kt * 64 + (l >> 4) * 16
+                           : src + rr * row_bytes + kt * 128 + (l >> 4) * 16;
     if (COHERENT) {
       r.h[j][0] = ld_agent64(q);
       r.h[j][1] = ld_agent64(q + 8);
-      if (ACT != DGM_ACT_MXFP4) {
+      if (!FP4) {
         r.h[j][2] = ld_agent64(q + 64);
         r.h[j][3] = ld_agent64(q + 72);
       }
     } else {
       r.v0[j] = *reinterpret_cast<const v4u*>(q);
-      if (ACT != DGM_ACT_MXFP4) r.v1[j] = *reinterpret_cast<const v4u*>(q + 64);
+      if (!FP4) r.v1[j] = *reinterpret_cast<const v4u*>(q + 64);
+    }
+    if constexpr (ACT == DGM_ACT_NVFP4) {
+      // the two E4M3 scales of the fragment (16-blocks 8 kt + 2 g, +1; row pitch KT * 8 bytes),
+      // as the aligned dword holding them
+      const uint32_t* sq = reinterpret_cast<const uint32_t*>(ssrc + rr * (KT * 8) + ((8 * kt + 2 * (l >> 4)) & ~3));
+      r.s16[j] = COHERENT ? __hip_atomic_load(sq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *sq;
     }
   }
   constexpr int KG = (KT + 3) / 4;
   static_assert(KG * 64 <= FT, "one scale word per thread");
-  if constexpr (ACT == DGM_ACT_QOQ) {
+  if constexpr (ACT == DGM_ACT_NVFP4) {
+    // (scales loaded with the fragments)
+  } else if constexpr (ACT == DGM_ACT_QOQ) {
     if (COHERENT) {
       // intermediate rows: fp32 scale per 64-K chunk (row pitch KT * 8 bytes); lane l < 16 of
       // fragment j (K-tile kt, column l) loads the two chunk scales of its tile
@@ -374,6 +419,45 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
   const v4u z = {0u, 0u, 0u, 0u};
+  if constexpr (ACT == DGM_ACT_NVFP4) {
+    // fragment (K-tile kt, column c, 32-K chunk g') -> f16 operand of op g' for the four lane
+    // groups q (K = 32 g' + 8 q .. +8): E2M1 -> f16 exactly, times the E4M3 block scale (the
+    // products are exact in f16)
+#pragma unroll
+    for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+      const int f = tid + j * FT;
+      if (f < KT * 64) {
+        const bool have = (r.ok >> j) & 1u;
+        const int kt = f >> 6, l = f & 63, c = l & 15, gq = l >> 4;
+        uint32_t w[4];
+        if (COHERENT) {
+          w[0] = (uint32_t)r.h[j][0];
+          w[1] = (uint32_t)(r.h[j][0] >> 32);
+          w[2] = (uint32_t)r.h[j][1];
+          w[3] = (uint32_t)(r.h[j][1] >> 32);
+        } else {
+          w[0] = r.v0[j].x;
+          w[1] = r.v0[j].y;
+          w[2] = r.v0[j].z;
+          w[3] = r.v0[j].w;
+        }
+        const uint32_t sc2 = r.s16[j] >> ((gq & 1) * 16);      // byte 0: block 2 g', byte 1: 2 g' + 1
+        const v2h s01 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(sc2, 1.0f, false);
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const _Float16 sv = qd < 2 ? s01.x : s01.y;
+          const v2h ss = {sv, sv};
+          const v2h h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[qd], 1.0f, 0) * ss;
+          const v2h h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[qd], 1.0f, 1) * ss;
+          const v2h h2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[qd], 1.0f, 2) * ss;
+          const v2h h3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w[qd], 1.0f, 3) * ss;
+          const v4u o = {__builtin_bit_cast(uint32_t, h0), __builtin_bit_cast(uint32_t, h1),
+                         __builtin_bit_cast(uint32_t, h2), __builtin_bit_cast(uint32_t, h3)};
+          *reinterpret_cast<v4u*>(&s.bst[kt][(qd << 4) | c][gq]) = have ? o : z;
+        }
+      }
+    }
+  } else {
 #pragma unroll
   for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
     const int f = tid + j * FT;
@@ -391,8 +475,11 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
       }
     }
   }
+  }
   constexpr int KG = (KT + 3) / 4;
-  if constexpr (ACT == DGM_ACT_QOQ) {
+  if constexpr (ACT == DGM_ACT_NVFP4) {
+    // (no scale plane: the scales are folded into the f16 operands)
+  } else if constexpr (ACT == DGM_ACT_QOQ) {
 #pragma unroll
     for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
       const int f = tid + j * FT;
@@ -452,8 +539,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   constexpr int KH = KT1 / 2;                               // L1 K-tiles per wave (K halves)
   constexpr int KG1 = (KT1 + 3) / 4, KG2 = (KT2 + 3) / 4;
   constexpr int H = KT1 * 128, I = KT2 * 128;
-  constexpr int XB = ACT == DGM_ACT_MXFP4 ? H / 2 : H;     // activation row bytes
-  constexpr int MB = ACT == DGM_ACT_MXFP4 ? I / 2 : I;     // intermediate row bytes
+  constexpr bool FP4A = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_NVFP4;   // E2M1 activations
+  constexpr int XB = FP4A ? H / 2 : H;     // activation row bytes
+  constexpr int MB = FP4A ? I / 2 : I;     // intermediate row bytes
   constexpr int QN1 = I / 64, NB1 = I / 8, NB2 = H / 16, NBL2 = H / (16 * NW);
   static_assert(I % 64 == 0, "L1 units are 64 intermediate features");
   const int tid = threadIdx.x, lane = tid & 63;
@@ -509,6 +597,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
   }
   for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;   // (shares LDS with the logits staging)
+  if constexpr (ACT == DGM_ACT_NVFP4) {
+    for (int e = tid; e < p.E_local; e += FT) {
+      s.gsl[0][e] = p.gs1 ? p.gs1[e] : 1.f;
+      s.gsl[1][e] = p.gs2 ? p.gs2[e] : 1.f;
+    }
+  }
   __syncthreads();
   for (int r = tid; r < R; r += FT) {
     int e = s.exp_of_route[r];
@@ -587,7 +681,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block; QoQ:
     // its meta dwords (4 per K-tile, spread over the lanes) and the s1 of the lane's 4 rows
     constexpr int MR1 = (4 * KT1 + 63) / 64;
-    constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : KG1;
+    constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : ACT == DGM_ACT_NVFP4 ? 1 : KG1;
     auto load_scales = [w1s, w1r, lane, pp, gu](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
       const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
       if constexpr (ACT == DGM_ACT_QOQ) {
@@ -600,10 +694,19 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         sw[MR1 + 1] = r.y;
         sw[MR1 + 2] = r.z;
         sw[MR1 + 3] = r.w;
+      } else if constexpr (ACT == DGM_ACT_NVFP4) {
+        sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
 #pragma unroll
         for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
       }
+    };
+    // NVFP4: the lane's scale dword of each tile (128 B of E4M3 scales per 16 x 128 tile), in a
+    // ring beside the tile ring
+    const int slane = (((lane >> 5) << 4) | (lane & 15)) * 4;
+    auto stile_base = [w1s, slane, pp, gu](int u) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+      return reinterpret_cast<const uint8_t*>(w1s) + blk * KT1 * 128 + slane;
     };
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
@@ -625,6 +728,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
     U4 wr[KR];
+    uint32_t sr[ACT == DGM_ACT_NVFP4 ? KR : 1];
     uint32_t sd[SW1], sn[SW1];
     SlabRegs<KT1, ACT, false> pre;
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
@@ -633,6 +737,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* b = tile_base(q0);
 #pragma unroll
       for (int k = 0; k < KR; ++k) wr[k] = ld_stream(b + k * 1024);
+      if constexpr (ACT == DGM_ACT_NVFP4) {
+        const uint8_t* sb = stile_base(q0);
+#pragma unroll
+        for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
+      }
       load_scales(q0, sd);
       slab_store(s, pre);
       staged = (q0 / QN1) << 16;
@@ -649,6 +758,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const bool restage = has_next && nkey != staged;
       const uint8_t* cb = tile_base(q0);
       const uint8_t* nb = !has_next ? w1v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
+      const uint8_t* csb = ACT == DGM_ACT_NVFP4 ? stile_base(q0) : nullptr;
+      const uint8_t* nsb = ACT != DGM_ACT_NVFP4 ? nullptr
+                           : !has_next ? reinterpret_cast<const uint8_t*>(w1s) + slane : nq == q0 ? csb : stile_base(nq);
       if (has_next && nq != q0) load_scales(nq, sn);
       if (restage) load_slab(pre, na, ns0);
       const float wt_r = s.slab_w[c];
@@ -704,6 +816,30 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         promote(prev, md_n, x_n);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = (float)qa[i] * __uint_as_float(sd[MR1 + i]) * sx;
+      } else if constexpr (ACT == DGM_ACT_NVFP4) {
+        // four f16 ops per tile: weights E2M1 x E4M3 -> f16 in registers, activations already
+        // f16 in LDS (read one tile ahead); scale dwords stream in their own ring
+        U4 bn[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bn[j] = s.bst[0][lane][j];
+        static_for<KT1>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          U4 bc[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bc[j] = bn[j];
+          if constexpr (t + 1 < KT1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bn[j] = s.bst[t + 1][lane][j];
+          }
+          acc = nvfp4_tile(wr[t % KR], sr[t % KR], bc, acc);
+          if constexpr (t + KR < KT1) {
+            wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
+            sr[t % KR] = ld_stream32_after(csb, (t + KR) * 128, acc);
+          } else {
+            wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
+            sr[t % KR] = ld_stream32_after(nsb, (t + KR - KT1) * 128, acc);
+          }
+        });
       } else {
         uint32_t bs = s.bsc[0][lane];
         static_for<KT1>([&](auto tc) {
@@ -718,10 +854,16 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
         });
       }
-      // all but this loop's KR youngest tile loads are done: the previous item's stores too
-      wait_vm_le<KR>();
+      // all but this loop's KR youngest tile loads (and scale loads) are done: the previous
+      // item's stores too
+      wait_vm_le<ACT == DGM_ACT_NVFP4 ? 2 * KR : KR>();
       const long long t_e0 = st ? wall_clock() : 0;
       if (st) l1_load_ticks += t_e0 - t_k0;
+      if constexpr (ACT == DGM_ACT_NVFP4) {
+        const float gsc = s.gsl[0][s.act[a]];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= gsc;
+      }
       if (gu == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
@@ -767,8 +909,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       __syncthreads();                                   // (2) amax visible, next slab staged
       if (gu == 0) {
-        const float am = ACT == DGM_ACT_QOQ ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
-                                            : fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
+        // requant group: QoQ 64 features (the unit), NVFP4 16 (this pair), MXFP 32 (two pairs)
+        const float am = ACT == DGM_ACT_QOQ     ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
+                         : ACT == DGM_ACT_NVFP4 ? s.amax[pp][c]
+                                                : fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
         const int row = r0 + s0 + c;
         // lane group kq holds features 16 pr + 4 kq .. +3 of column c
         if (ACT == DGM_ACT_QOQ) {
@@ -786,6 +930,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if (valid && lane < 32) {
             st_agent64(p.mid + (size_t)row * MB + 16 * pr + (lane < 16 ? 0 : 8), w64);
             if (pp == 0 && lane < 16) st_agent32(p.mid_sf + (size_t)row * (I / 16) + 4 * q, __float_as_uint(sc));
+          }
+        } else if (ACT == DGM_ACT_NVFP4) {
+          // E2M1 per 16 features: sf = E4M3 (round to nearest even) of max(amax, 1e-30) / 6,
+          // ties-down E2M1 of act / sf (sm100_b200/test_mega_moe.py:68-80, requant_fp4)
+          const uint32_t code = e4m3_encode(fmaxf(am, 1e-30f) / 6.0f);
+          const float sc = __builtin_amdgcn_cvt_f32_fp8((int)code, 0);
+          uint32_t w = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w |= e2m1_ties_down(act[i] / sc) << (4 * i);
+          const uint64_t w64 = (uint64_t)(w & 0xffffu) | ((uint64_t)(__shfl(w, c + 16) & 0xffffu) << 16) |
+                               ((uint64_t)(__shfl(w, c + 32) & 0xffffu) << 32) |
+                               ((uint64_t)(__shfl(w, c + 48) & 0xffffu) << 48);
+          if (valid && lane < 16) {
+            st_agent64(p.mid + (size_t)row * MB + 8 * pr, w64);
+            st_agent8(p.mid_sf + (size_t)row * (I / 16) + pr, (uint8_t)code);
           }
         } else if (ACT == DGM_ACT_MXFP4) {
           const uint32_t code = ceil_ue8m0_code(fmaxf(am, 1e-30f) / 6.0f);
@@ -861,18 +1020,25 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // per-item scale registers (the wave's RB2 contiguous 16-row blocks), loaded one item
     // ahead: MXFP: E8M0 scale dwords; QoQ: meta dwords (4 per K-tile)
     constexpr int MR2 = (4 * TI2 + 63) / 64;
-    constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : RB2 * KG2;
+    constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : ACT == DGM_ACT_NVFP4 ? 1 : RB2 * KG2;
     auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
       if constexpr (ACT == DGM_ACT_QOQ) {
         const uint32_t* mb = w2s + blk_of(v) * KT2 * 4;
 #pragma unroll
         for (int j = 0; j < MR2; ++j)
           sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * TI2 ? 64 * j + lane : 4 * TI2 - 1));
+      } else if constexpr (ACT == DGM_ACT_NVFP4) {
+        sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
         const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
 #pragma unroll
         for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
       }
+    };
+    // NVFP4: the lane's scale dword of each tile, in a ring beside the tile ring
+    const int slane = (((lane >> 5) << 4) | (lane & 15)) * 4;
+    auto stile_base = [w2s, slane, blk_of](int v) __attribute__((always_inline)) {
+      return reinterpret_cast<const uint8_t*>(w2s) + blk_of(v) * KT2 * 128 + slane;
     };
     const uint8_t* midv = p.mid;
     const uint8_t* mids = p.mid_sf;
@@ -904,6 +1070,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
     U4 wr[KT2];
+    uint32_t sr[ACT == DGM_ACT_NVFP4 ? KT2 : 1];
     uint32_t sd[SW2], sn[SW2];
     SlabRegs<KT2, ACT, true> pre;
     int ready = -1;           // an active expert whose L1 arrival is known complete
@@ -913,6 +1080,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* b = tile_base(q0);
 #pragma unroll
       for (int k = 0; k < KT2; ++k) wr[k] = ld_stream(b + k * 1024);
+      if constexpr (ACT == DGM_ACT_NVFP4) {
+        const uint8_t* sb = stile_base(q0);
+#pragma unroll
+        for (int k = 0; k < KT2; ++k) sr[k] = ld_stream32(sb + k * 128);
+      }
       load_scales(q0, sd);
     }
     while (q0 < U2) {
@@ -931,7 +1103,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if (tid == 0 && !seen) st[3] = wall_clock();
           seen = true;
         }
-        if constexpr (ACT == DGM_ACT_QOQ) {
+        if constexpr (ACT == DGM_ACT_QOQ || ACT == DGM_ACT_NVFP4) {
           load_slab(pre, a, s0);            // (pre holds nothing between items)
           slab_store(s, pre);
         } else {
@@ -960,6 +1132,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       const uint8_t* cb = tile_base(q0);
       const uint8_t* nb = !has_next ? w2v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
+      const uint8_t* csb = ACT == DGM_ACT_NVFP4 ? stile_base(q0) : nullptr;
+      const uint8_t* nsb = ACT != DGM_ACT_NVFP4 ? nullptr
+                           : !has_next ? reinterpret_cast<const uint8_t*>(w2s) + slane : nq == q0 ? csb : stile_base(nq);
       if (has_next && nq != q0) load_scales(nq, sn);
       // QoQ: the row scales s1 of the lane's 4 rows of each block, only used after the K loop
       // (so loaded for this item, here)
@@ -1036,6 +1211,34 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           acc[j][2] *= __uint_as_float(s1r[j].z);
           acc[j][3] *= __uint_as_float(s1r[j].w);
         }
+      } else if constexpr (ACT == DGM_ACT_NVFP4) {
+        U4 bn[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bn[j] = s.bst[0][lane][j];
+        static_for<TI2>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          constexpr int j = t / KT2, k = t % KT2;
+          U4 bc[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) bc[i] = bn[i];
+          if constexpr (t + 1 < TI2) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bn[i] = s.bst[(t + 1) % KT2][lane][i];
+          }
+          acc[j] = nvfp4_tile(wr[k], sr[k], bc, acc[j]);
+          if constexpr (t + KT2 < TI2) {
+            wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+            sr[k] = ld_stream32_after(csb, (t + KT2) * 128, acc[j]);
+          } else {
+            wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
+            sr[k] = ld_stream32_after(nsb, (t + KT2 - TI2) * 128, acc[j]);
+          }
+        });
+        const float gsc = s.gsl[1][s.act[a]];
+#pragma unroll
+        for (int j = 0; j < RB2; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[j][i] *= gsc;
       } else {
         uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
         static_for<TI2>([&](auto tc) {
@@ -1055,8 +1258,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
         });
       }
-      // all but this loop's KT2 youngest tile loads are done: the previous item's stores too
-      wait_vm_le<KT2>();
+      // all but this loop's KT2 youngest tile loads (and scale loads) are done: the previous
+      // item's stores too
+      wait_vm_le<ACT == DGM_ACT_NVFP4 ? 2 * KT2 : KT2>();
       if (s0 + c < n) {
         float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
 #pragma unroll
@@ -1153,7 +1357,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[5] = wall_clock();
 }
 
-struct GridCache { int blocks[3][3][2] = {}; };
+struct GridCache { int blocks[3][4][2] = {}; };
 GridCache g_grid;
 
 template <int KT1, int KT2, int ACT>
@@ -1185,7 +1389,8 @@ int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, 
     constexpr int KA = H_ / 128, KB = I_ / 128;                                               \
     return act == DGM_ACT_MXFP4   ? launch_fused_t<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream) \
            : act == DGM_ACT_MXFP8 ? launch_fused_t<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream) \
-                                  : launch_fused_t<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream);   \
+           : act == DGM_ACT_QOQ   ? launch_fused_t<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream)   \
+                                  : launch_fused_t<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream); \
   }
   DGM_FUSED_SHAPE(3072, 1280, 0)
   DGM_FUSED_SHAPE(512, 256, 1)

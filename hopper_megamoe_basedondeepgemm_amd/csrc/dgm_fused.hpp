@@ -27,6 +27,8 @@ struct FusedParams {
   const uint32_t* w2s;
   const float* w1r;         // QoQ: per-row weight scales s1 [E_local, N] (null for MXFP4)
   const float* w2r;
+  const float* gs1;         // NVFP4: optional per-expert scales of the L1 / L2 outputs (null = 1)
+  const float* gs2;
   const uint8_t* x;
   const uint8_t* xsf;
   int64_t* topk_idx;        // read, or written by workgroup 0 when select != 0

@@ -148,6 +148,30 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
     }
     return;
   }
+  if (act_format == DGM_ACT_NVFP4) {
+    // ---- NVFP4 activation cast (sm100 W4A4 rule): per 16 elements, 4 lanes of 4; sf = E4M3
+    // RNE of max(amax, 1e-30) / 6, codes = ties-down E2M1 of x / sf, low nibble first
+    const int64_t groups16 = (int64_t)M * (H / 16);
+    const int64_t nl = (int64_t)gridDim.x * gridDim.y * 256;
+    for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid; i < groups16 * 4; i += nl) {
+      const int64_t g = i >> 2;
+      const int part = (int)(i & 3);
+      const uint2 raw = *reinterpret_cast<const uint2*>(x + g * 16 + 4 * part);
+      const float v[4] = {__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                          __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+      float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      amax = fmaxf(amax, __shfl_xor(amax, 1));
+      amax = fmaxf(amax, __shfl_xor(amax, 2));
+      const uint32_t code = e4m3_encode(fmaxf(amax, 1e-30f) / 6.0f);
+      const float sc = __builtin_amdgcn_cvt_f32_fp8((int)code, 0);
+      uint32_t o = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o |= e2m1_ties_down(v[k] / sc) << (4 * k);
+      reinterpret_cast<uint16_t*>(q)[g * 4 + part] = (uint16_t)o;
+      if (part == 0) sf[g] = (uint8_t)code;
+    }
+    return;
+  }
   // ---- activation cast: 8 lanes per group
   const int64_t groups = (int64_t)M * (H / 32);
   const int64_t nlanes = (int64_t)gridDim.x * gridDim.y * 256;
@@ -569,19 +593,21 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts in (0, 1024]");
   DGM_CHECK_ARG(num_local_experts > 0 && num_local_experts <= num_experts, "num_local_experts");
   DGM_CHECK_ARG(hidden % 512 == 0 && intermediate % 128 == 0, "hidden % 512, intermediate % 128");
-  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8 || act_format == DGM_ACT_QOQ,
-                "act_format");
+  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_NVFP4, "act_format");
   DGM_CHECK_ARG((int64_t)max_tokens * topk <= MAX_ROUTES_DISPATCH, "max_tokens * topk <= 4096");
-  const size_t xb = act_format == DGM_ACT_MXFP4 ? hidden / 2 : hidden;
-  const size_t mb = act_format == DGM_ACT_MXFP4 ? intermediate / 2 : intermediate;
+  const bool fp4 = act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_NVFP4;
+  const size_t xb = fp4 ? hidden / 2 : hidden;
+  const size_t mb = fp4 ? intermediate / 2 : intermediate;
   // scales: E8M0 bytes per 32 (MXFP); QoQ: fp32 per token repeated over H / 128 slots (the
-  // same H / 32 bytes) and fp32 per 64 intermediate features (I / 16 bytes)
-  const size_t msfb = act_format == DGM_ACT_QOQ ? intermediate / 16 : intermediate / 32;
+  // same H / 32 bytes) and fp32 per 64 intermediate features (I / 16 bytes); NVFP4: E4M3
+  // bytes per 16
+  const size_t xsfb = act_format == DGM_ACT_NVFP4 ? hidden / 16 : hidden / 32;
+  const size_t msfb = act_format == DGM_ACT_QOQ || act_format == DGM_ACT_NVFP4 ? intermediate / 16 : intermediate / 32;
   const int R = max_tokens * topk;
   size_t off = 0;
   memset(out, 0, sizeof(*out));
   out->x = off; off += dgm_align256((size_t)max_tokens * xb);
-  out->x_sf = off; off += dgm_align256((size_t)max_tokens * (hidden / 32));
+  out->x_sf = off; off += dgm_align256((size_t)max_tokens * xsfb);
   out->topk_idx = off; off += dgm_align256((size_t)R * 8);
   out->topk_weights = off; off += dgm_align256((size_t)R * 4);
   out->logits = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
@@ -607,8 +633,7 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
   DGM_CHECK_ARG(num_experts <= 1024, "num_experts <= 1024");
   DGM_CHECK_ARG(hidden % 512 == 0, "hidden % 512 == 0");
   DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
-  DGM_CHECK_ARG(act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_MXFP8 || act_format == DGM_ACT_QOQ,
-                "act_format");
+  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_NVFP4, "act_format");
   DGM_CHECK_ARG(((uintptr_t)hidden_bf16 & 15) == 0 && ((uintptr_t)router_weight_bf16 & 15) == 0, "16-byte alignment");
   if (num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)buffer;
@@ -657,8 +682,7 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(A->num_local_experts > 0 && A->num_local_experts <= MAX_LOCAL_EXPERTS, "num_local_experts");
   DGM_CHECK_ARG(A->expert_begin >= 0 && A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
-  DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8 || A->act_format == DGM_ACT_QOQ,
-                "act_format");
+  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4, "act_format");
   DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ || (A->w1_row_scales && A->w2_row_scales),
                 "QoQ needs the row scales s1 of both matrices");
   DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
@@ -681,6 +705,8 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.w2s = (const uint32_t*)A->w2_scales;
     p.w1r = A->act_format == DGM_ACT_QOQ ? (const float*)A->w1_row_scales : nullptr;
     p.w2r = A->act_format == DGM_ACT_QOQ ? (const float*)A->w2_row_scales : nullptr;
+    p.gs1 = A->act_format == DGM_ACT_NVFP4 ? A->l1_global_scales : nullptr;
+    p.gs2 = A->act_format == DGM_ACT_NVFP4 ? A->l2_global_scales : nullptr;
     p.x = buf + L->x;
     p.xsf = buf + L->x_sf;
     p.topk_idx = (int64_t*)(buf + L->topk_idx);
@@ -709,15 +735,15 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
-  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ,
-                "QoQ layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
+                "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
   return dgm_megamoe_split_launch(A, stream);
 }
 
 int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
   DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8,
-                "split path: act_format must be MXFP4 or MXFP8 (the QoQ layer is fused only)");
+                "split path: act_format must be MXFP4 or MXFP8 (the QoQ and NVFP4 layers are fused only)");
   const DgmBufferLayout* L = A->layout;
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   if (A->num_tokens == 0) return 0;

@@ -297,6 +297,56 @@ __global__ void k_transform_fp4(const uint8_t* __restrict__ src, const uint8_t* 
   sdst[((((int64_t)e * NB + q) * KG + kt / 4) * 64 + lane) * 4 + (kt & 3)] = sc;
 }
 
+// NVFP4 weights -> the fused kernel's layout for the f16 matrix core (one thread per (expert,
+// 16-row block, K-tile, lane)). Source: packed [E][N][K/2] (Marlin or low-first order), scales
+// [E][N][K/16] E4M3 bytes. Values [E][N/16][K/128][64 lanes][16 B]: lane l = row l%16; dword j
+// holds op j's eight codes K = 128 kt + 32 j + 8 (l/16) .. +8, byte b = K[2b] | K[2b+1] << 4.
+// Scales [E][N/16][K/128][2][16][4 B]: dword (p, r) byte j = the scale of row r, 16-block
+// 8 kt + 2 j + p, so lane l reads dword (l/32, l%16) for the four blocks its ops touch.
+__global__ void k_transform_nvfp4(const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
+                                  int E, int N, int K, int src_order, int l1_interleave,
+                                  uint8_t* __restrict__ dst, uint8_t* __restrict__ sdst) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int KT = K / 128, NB = N / 16;
+  const int64_t total = (int64_t)E * NB * KT * 64;
+  if (tid >= total) return;
+  const int lane = (int)(tid & 63);
+  int64_t t = tid >> 6;
+  const int kt = (int)(t % KT); t /= KT;
+  const int q = (int)(t % NB);
+  const int e = (int)(t / NB);
+  const int r = lane & 15, g = lane >> 4;
+  int src_row;
+  if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
+  else src_row = 16 * q + r;
+  const uint8_t* row = src + ((int64_t)e * N + src_row) * (K / 2) + kt * 64;
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(row + 16 * j + 4 * g);   // K 32 j + 8 g .. +8
+    if (src_order == 0) {        // Marlin: byte b = K[b] << 4 | K[b+4]
+      uint32_t n[8];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (w >> (8 * b)) & 0xffu;
+        n[b] = byte >> 4;
+        n[b + 4] = byte & 0xfu;
+      }
+      o[j] = lowfirst8(n);
+    } else {
+      o[j] = w;
+    }
+  }
+  const int64_t tile = ((int64_t)e * NB + q) * KT + kt;
+  *reinterpret_cast<U4*>(dst + tile * 1024 + lane * 16) = U4{o[0], o[1], o[2], o[3]};
+  if ((g & 1) == 0) {
+    const int p = g >> 1;
+    const uint8_t* sr = ssrc + ((int64_t)e * N + src_row) * (K / 16) + 8 * kt + p;
+    const uint32_t sd = (uint32_t)sr[0] | ((uint32_t)sr[2] << 8) | ((uint32_t)sr[4] << 16) | ((uint32_t)sr[6] << 24);
+    *reinterpret_cast<uint32_t*>(sdst + tile * 128 + (16 * p + r) * 4) = sd;
+  }
+}
+
 // QoQ (W4A8) weights -> the fused kernel's layout (one thread per (expert, 16-row block,
 // K-tile, lane)). Values [E][N/16][K/128][64][16 B]: lane l = row l%16; its 16 bytes hold the
 // two K=64 int8 operands (op h: codes n[h][j] of K = 64 h + 16 (l/16) + j, j = 0..15) as
@@ -476,6 +526,20 @@ int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E,
   if (pad_total > 0)
     hipLaunchKernelGGL(k_fill_scale_pad, dim3(grid_for(pad_total, 256)), dim3(256), 0, stream,
                        (uint8_t*)dst_scales, (int64_t)E * NB, KT, KG);
+  return dgm_last_launch_status();
+}
+
+int dgm_transform_nvfp4_weights(const void* packed, const void* scale_e4m3, int E, int N, int K, int src_order,
+                                int l1_interleave, void* dst_values, void* dst_scales, hipStream_t stream) {
+  DGM_CHECK_ARG(packed && scale_e4m3 && dst_values && dst_scales, "null pointer");
+  DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 32 == 0 && K % 128 == 0, "N % 32, K % 128");
+  DGM_CHECK_ARG(src_order == 0 || src_order == 1, "src_order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(((uintptr_t)packed & 3) == 0 && ((uintptr_t)dst_values & 15) == 0 && ((uintptr_t)dst_scales & 3) == 0,
+                "alignment");
+  const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
+  hipLaunchKernelGGL(k_transform_nvfp4, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)packed,
+                     (const uint8_t*)scale_e4m3, E, N, K, src_order, l1_interleave, (uint8_t*)dst_values,
+                     (uint8_t*)dst_scales);
   return dgm_last_launch_status();
 }
 

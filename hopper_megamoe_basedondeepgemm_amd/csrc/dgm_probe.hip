@@ -67,3 +67,44 @@ extern "C" int dgm_probe_mfma_i8(const void* a, const void* b, void* out, hipStr
   hipLaunchKernelGGL(k_probe_i8, dim3(1), dim3(64), 0, stream, (const v4i*)a, (const v4i*)b, (v4i*)out);
   return dgm_last_launch_status();
 }
+
+// One f16 matrix-core op (V_MFMA_F32_16X16X32_F16) on caller-provided lane fragments (a, b:
+// 64 x 8 halves; out: 64 x 4 fp32), to pin the lane layout of the NVFP4 path.
+__global__ void k_probe_f16(const v8h* a, const v8h* b, v4f* out) {
+  const int l = threadIdx.x;
+  v4f c = {0.f, 0.f, 0.f, 0.f};
+  out[l] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[l], b[l], c, 0, 0, 0);
+}
+
+extern "C" int dgm_probe_mfma_f16(const void* a, const void* b, void* out, hipStream_t stream) {
+  DGM_CHECK_ARG(a && b && out, "null pointer");
+  hipLaunchKernelGGL(k_probe_f16, dim3(1), dim3(64), 0, stream, (const v8h*)a, (const v8h*)b, (v4f*)out);
+  return dgm_last_launch_status();
+}
+
+// The conversions of the NVFP4 path: for each i < n, out_h[4 i + j] = the two f16 of
+// V_CVT_SCALEF32_PK_F16_FP4 on byte j of src[i] with the fp32 scale[i]; out_f[4 i + j] =
+// V_CVT_F32_FP8 of byte j of src[i] (E4M3).
+__global__ void k_probe_cvt(const uint32_t* src, const float* scale, uint32_t* out_h, float* out_f, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t v = src[i];
+  const float sc = scale[i];
+  out_h[4 * i + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 0));
+  out_h[4 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 1));
+  out_h[4 * i + 2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 2));
+  out_h[4 * i + 3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, sc, 3));
+  out_f[4 * i + 0] = __builtin_amdgcn_cvt_f32_fp8((int)v, 0);
+  out_f[4 * i + 1] = __builtin_amdgcn_cvt_f32_fp8((int)v, 1);
+  out_f[4 * i + 2] = __builtin_amdgcn_cvt_f32_fp8((int)v, 2);
+  out_f[4 * i + 3] = __builtin_amdgcn_cvt_f32_fp8((int)v, 3);
+}
+
+extern "C" int dgm_probe_cvt_fp4(const void* src, const void* scale, void* out_h, void* out_f, int n,
+                                 hipStream_t stream) {
+  DGM_CHECK_ARG(src && scale && out_h && out_f && n >= 0, "null pointer or n < 0");
+  if (n == 0) return 0;
+  hipLaunchKernelGGL(k_probe_cvt, dim3((n + 255) / 256), dim3(256), 0, stream, (const uint32_t*)src,
+                     (const float*)scale, (uint32_t*)out_h, (float*)out_f, n);
+  return dgm_last_launch_status();
+}

@@ -27,8 +27,9 @@ class FusedSymmBuffer:
     l1_acts_sf (aliases of x / x_sf: routed rows are read in place), l2_acts / l2_acts_sf
     (L1 -> L2 activations in pool order), combine_partials (fp32 [tokens, topk, H] route
     outputs), logits (fp32 router logits) and pool (dispatch table, int32).
-    act_format "mxfp4" / "mxfp8": uint8 codes with E8M0 scale bytes per 32; "qoq": int8 codes,
-    x_sf fp32 [tokens, H/128] (one scale per token, repeated), l2_acts_sf fp32 [routes, I/64]."""
+    act_format "mxfp4" / "mxfp8": uint8 codes with E8M0 scale bytes per 32; "nvfp4": E2M1 codes
+    (low nibble first) with E4M3 scale bytes per 16; "qoq": int8 codes, x_sf fp32 [tokens, H/128]
+    (one scale per token, repeated), l2_acts_sf fp32 [routes, I/64]."""
 
     def __init__(self, group, num_experts, max_tokens, topk, hidden, intermediate,
                  act_format="mxfp4", ep_size=None, ep_rank=None, device=None):
@@ -64,9 +65,10 @@ class FusedSymmBuffer:
         if qoq:   # int8 codes, fp32 scale per token repeated over the H / 128 slots
             self.x = view(L.x, max_tokens * xb, torch.int8, (max_tokens, xb))
             self.x_sf = view(L.x_sf, max_tokens * (hidden // 128), torch.float32, (max_tokens, hidden // 128))
-        else:     # codes, E8M0 scale bytes per 32
+        else:     # codes, E8M0 scale bytes per 32 (NVFP4: E4M3 per 16)
+            sfv = 16 if act_format == "nvfp4" else 32
             self.x = view(L.x, max_tokens * xb, torch.uint8, (max_tokens, xb))
-            self.x_sf = view(L.x_sf, max_tokens * (hidden // 32), torch.uint8, (max_tokens, hidden // 32))
+            self.x_sf = view(L.x_sf, max_tokens * (hidden // sfv), torch.uint8, (max_tokens, hidden // sfv))
         self.topk_idx = view(L.topk_idx, R, torch.int64, (max_tokens, topk))
         self.topk_weights = view(L.topk_weights, R, torch.float32, (max_tokens, topk))
         self.logits = view(L.logits, max_tokens * num_experts, torch.float32, (max_tokens, num_experts))
@@ -76,7 +78,7 @@ class FusedSymmBuffer:
             self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 64), torch.float32, (R, intermediate // 64))
         else:
             self.l2_acts = view(L.mid, R * mb, torch.uint8, (R, mb))
-            self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 32), torch.uint8, (R, intermediate // 32))
+            self.l2_acts_sf = view(L.mid_sf, R * (intermediate // sfv), torch.uint8, (R, intermediate // sfv))
         self.combine_partials = view(L.partials, R * hidden, torch.float32, (max_tokens, topk, hidden))
         self.l1_acts, self.l1_acts_sf = self.x, self.x_sf
         self.handle = types.SimpleNamespace(buffer_ptrs=[b.data_ptr()])
@@ -176,6 +178,32 @@ def transform_qoq_weights_for_mega_moe_fused(l1, l2):
     return _transform_qoq_one(l1, True), _transform_qoq_one(l2, False)
 
 
+def _transform_nvfp4_one(packed, scale, l1_interleave, src_order):
+    _lib.require_gpu(packed, scale)
+    assert packed.dtype == torch.uint8 and scale.dtype == torch.uint8 and packed.dim() == 3
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert tuple(scale.shape) == (E, N, K // 16), (scale.shape, packed.shape)
+    assert N % 32 == 0 and K % 128 == 0, (N, K)
+    vals = torch.empty((E, N // 16, K // 128, 64, 16), dtype=torch.uint8, device=packed.device)
+    sc = torch.empty((E, N // 16, K // 128, 2, 16, 4), dtype=torch.uint8, device=packed.device)
+    order = {"marlin": 0, "low_first": 1}[src_order]
+    _lib.check(_lib.load().dgm_transform_nvfp4_weights(_lib.ptr(packed.contiguous()), _lib.ptr(scale.contiguous()),
+                                                       E, N, K, order, int(l1_interleave), _lib.ptr(vals),
+                                                       _lib.ptr(sc), _lib.stream()))
+    return vals, sc
+
+
+def transform_nvfp4_weights_for_mega_moe_fused(l1, l2, src_order="marlin"):
+    """NVFP4 W4A4 weights (``(packed [E, N, K/2], E4M3 scales [E, N, K/16])`` per matrix, from
+    ``quantize_to_nvfp4`` (Marlin order) or the W4A4 row cast (``src_order="low_first"``,
+    sm100_b200/test_mega_moe.py:68-93)) -> the fused kernel's layout for the f16 matrix core
+    (the role of sm100_b200/mega___init__.py:102 ``transform_weights_for_mega_moe`` and
+    deep_gemm/mega/__init__.py:174 ``transform_nvfp4_weights_for_mega_moe_sm90``). L1 gate/up
+    blocks are interleaved. Returns ``((w1_values, w1_scales), (w2_values, w2_scales))``."""
+    return _transform_nvfp4_one(*l1, True, src_order), _transform_nvfp4_one(*l2, False, src_order)
+
+
 def transform_weights_for_mega_moe(l1, l2):
     """sm100_b200 style inputs (low-nibble-first packing from per_token_cast_to_fp4)."""
     return transform_mxfp4_weights_for_mega_moe_fused(l1, l2, src_order="low_first")
@@ -227,13 +255,24 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
 
 
 # ----------------------------------------------------------------------------- fused layer
+_ENTRY_FOR = {"qoq": "qoq_mega_moe_fused", "nvfp4": "fp4_fp4_mega_moe / nvfp4_mega_moe"}
+
+
 def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
-           fast_math=True, qoq=False):
-    if qoq != (b.act_format == "qoq"):
+           fast_math=True, fmt=None, global_scales=(None, None)):
+    fmt = fmt or ("mxfp8" if b.act_format in ("mxfp8", "fp8") else "mxfp4")
+    kind = lambda f: f if f in ("qoq", "nvfp4") else "mxfp"
+    if kind(fmt) != kind(b.act_format):
         raise ValueError(f"buffer was sized for {b.act_format!r}: use "
-                         f"{'qoq' if b.act_format == 'qoq' else 'mxfp4'}_mega_moe_*")
-    w1, sf1, rs1 = l1
-    w2, sf2, rs2 = l2
+                         f"{_ENTRY_FOR.get(b.act_format, 'mxfp4_mega_moe_fused / _split')}")
+    qoq = b.act_format == "qoq"
+    nv = b.act_format == "nvfp4"
+    if nv:
+        (w1, sf1), (w2, sf2) = l1, l2
+        rs1 = rs2 = None
+    else:
+        w1, sf1, rs1 = l1
+        w2, sf2, rs2 = l2
     _lib.require_gpu(y, w1, sf1, w2, sf2, stats)
     assert y.dtype == torch.bfloat16 and y.is_contiguous() and y.size(1) == b.hidden
     m = y.size(0) if num_tokens is None else num_tokens
@@ -242,7 +281,14 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
     kg = lambda k: (k // 128 + 3) // 4
     assert tuple(w1.shape) == (E_l, 2 * I // 16, H // 128, 64, 16) and w1.dtype == torch.uint8, w1.shape
     assert tuple(w2.shape) == (E_l, H // 16, I // 128, 64, 16) and w2.dtype == torch.uint8, w2.shape
-    if qoq:   # meta [E, N/16, K/128, 16] (z | s2 << 4 per row), row scales s1 [E, N]
+    if nv:    # E4M3 scales [E, N/16, K/128, 2, 16, 4]
+        assert tuple(sf1.shape) == (E_l, 2 * I // 16, H // 128, 2, 16, 4) and sf1.dtype == torch.uint8, sf1.shape
+        assert tuple(sf2.shape) == (E_l, H // 16, I // 128, 2, 16, 4) and sf2.dtype == torch.uint8, sf2.shape
+        for g in global_scales:
+            if g is not None:
+                _lib.require_gpu(g)
+                assert g.dtype == torch.float32 and g.numel() == E_l and g.is_contiguous()
+    elif qoq:   # meta [E, N/16, K/128, 16] (z | s2 << 4 per row), row scales s1 [E, N]
         _lib.require_gpu(rs1, rs2)
         assert tuple(sf1.shape) == (E_l, 2 * I // 16, H // 128, 16) and sf1.dtype == torch.uint8, sf1.shape
         assert tuple(sf2.shape) == (E_l, H // 16, I // 128, 16) and sf2.dtype == torch.uint8, sf2.shape
@@ -267,7 +313,9 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
                         phase_stamps=phase_stamps.data_ptr() if phase_stamps is not None else None,
                         phase_stamp_rows=phase_stamps.numel() // 8 if phase_stamps is not None else 0,
                         w1_row_scales=rs1.data_ptr() if qoq else None,
-                        w2_row_scales=rs2.data_ptr() if qoq else None)
+                        w2_row_scales=rs2.data_ptr() if qoq else None,
+                        l1_global_scales=global_scales[0].data_ptr() if global_scales[0] is not None else None,
+                        l2_global_scales=global_scales[1].data_ptr() if global_scales[1] is not None else None)
     if phase_stamps is not None:
         assert phase_stamps.dtype == torch.int64 and phase_stamps.is_cuda and phase_stamps.is_contiguous()
     fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
@@ -295,7 +343,40 @@ def qoq_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, ac
     integer scale and per-row fp32 scale, exact int32 group sums; fp32 gate / up, SiLU * up *
     routing weight, int8 requant per 64 features, L2, fp32 combine -> bf16 ``y``."""
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
-           fast_math=fast_math, qoq=True)
+           fast_math=fast_math, fmt="qoq")
+
+
+def fp4_fp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats=None,
+                     recipe=None, activation="swiglu", activation_clamp=None, fast_math=True):
+    """sm100_b200/mega___init__.py:244 W4A4 entry: packed E2M1 activations and weights. On an
+    ``act_format="nvfp4"`` buffer (E4M3 scale per 16; weights from
+    ``transform_nvfp4_weights_for_mega_moe_fused``) it runs the NVFP4 layer; on an "mxfp4"
+    buffer the MXFP4 layer (weights from ``transform_mxfp4_weights_for_mega_moe_fused``).
+    ``activation_clamp=None`` = no clamp."""
+    b = sym_buffer
+    assert b.act_format in ("mxfp4", "nvfp4"), "buffer must be created with act_format mxfp4/nvfp4"
+    vec = 16 if b.act_format == "nvfp4" else 32
+    assert recipe is None or tuple(recipe)[2] == vec, recipe
+    assert activation == "swiglu", activation
+    _fused(y, l1_weights, l2_weights, b, cumulative_local_expert_recv_stats, activation_clamp,
+           fast_math=fast_math, fmt=b.act_format)
+
+
+def nvfp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats=None,
+                   l1_global_scales=None, l2_global_scales=None, recipe=(128, 128, 128), activation="swiglu",
+                   activation_clamp=None, fast_math=True, kernel_family="auto", family_threshold=256):
+    """deep_gemm/mega/__init__.py:277 NVFP4 entry with per-expert fp32 global scales
+    (``l1_global_scales`` / ``l2_global_scales`` [E_local], multiplied into the L1 / L2
+    outputs), here on an ``act_format="nvfp4"`` buffer (W4A4). ``recipe``, ``kernel_family`` and
+    ``family_threshold`` select SM90 kernel families there and have no effect here."""
+    assert sym_buffer.act_format == "nvfp4", "buffer must be created with act_format='nvfp4'"
+    assert activation == "swiglu", activation
+    if kernel_family not in ("auto", "split", "fused"):
+        raise ValueError("kernel_family must be one of 'auto', 'fused', or 'split'")
+    if family_threshold <= 0:
+        raise ValueError("family_threshold must be positive")
+    _fused(y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats, activation_clamp,
+           fast_math=fast_math, fmt="nvfp4", global_scales=(l1_global_scales, l2_global_scales))
 
 
 def qoq_mega_moe_split(*_, **__):
@@ -323,6 +404,7 @@ def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
     is selected in the fused kernel's prologue when the token count allows)."""
     fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
                                      token_offset=token_offset, select_in_mega=True)
-    # (a qoq buffer runs the QoQ layer: the reference's DG_W4A8_INT=1 route)
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, qoq=b.act_format == "qoq")
+    # (a qoq buffer runs the QoQ layer: the reference's DG_W4A8_INT=1 route; an nvfp4 buffer the
+    # W4A4 NVFP4 layer)
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, fmt=b.act_format)
     return y

@@ -24,6 +24,7 @@ extern "C" {
 /* activation formats (the "act_format" of sm100_b200/test_mega_moe.py:57) */
 #define DGM_ACT_MXFP4 0 /* E2M1 + UE8M0 per 32 (W4A4)          */
 #define DGM_ACT_MXFP8 1 /* E4M3 + UE8M0 per 32 (W-MXFP4 x A-FP8) */
+#define DGM_ACT_NVFP4 3 /* W4A4 NVFP4: E2M1 + E4M3 scale per 16 (activations and weights) */
 #define DGM_ACT_QOQ 2   /* QoQ W4A8: int8 activations with one fp32 scale per token, QoQ weights
                            (deep_gemm/quantization_qoq_fused.py:1-11) */
 
@@ -80,6 +81,14 @@ int dgm_cast_int8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_i8, 
 int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E, int N, int K,
                               int src_order, int l1_interleave, void* dst_values,
                               void* dst_scales, hipStream_t stream);
+
+/* Replaces the weight preparation of the W4A4 NVFP4 path (sm100_b200/mega___init__.py:102-111
+ * transform_weights_for_mega_moe, deep_gemm/mega/__init__.py:174 transform_nvfp4_weights_for_mega_moe_sm90),
+ * one matrix per call: packed [E, N, K/2] (src_order 0 = Marlin, 1 = low-nibble-first) and E4M3
+ * scales [E, N, K/16] -> dst_values [E, N/16, K/128, 64, 16] (f16 matrix-core fragment order)
+ * and dst_scales [E, N/16, K/128, 2, 16, 4] (per lane the four 16-block scales of its ops). */
+int dgm_transform_nvfp4_weights(const void* packed, const void* scale_e4m3, int E, int N, int K, int src_order,
+                                int l1_interleave, void* dst_values, void* dst_scales, hipStream_t stream);
 
 /* Replaces deep_gemm/mega/fused.py:71 transform_qoq_weights_for_mega_moe_fused (one matrix per
  * call). packed [E, N, K/2] (Marlin), s2 / z u8 [E, N, K/128], s1 f32 [E, N] ->
@@ -138,9 +147,11 @@ typedef struct DgmMoeArgs {
   int32_t fe_flags;       /* with select_in_mega: the frontend's DGM_FE_* flags */
   int32_t token_offset;   /* with select_in_mega: global id of row 0 */
   const void* w1_values;  /* [E_local, 2I/16, H/128, 64, 16] */
-  const void* w1_scales;  /* MXFP: [E_local, 2I/16, ceil(H/512), 64, 4]; QoQ: meta [E_local, 2I/16, H/128, 16] */
+  const void* w1_scales;  /* MXFP: [E_local, 2I/16, ceil(H/512), 64, 4]; QoQ: meta [E_local, 2I/16, H/128, 16];
+                             NVFP4: [E_local, 2I/16, H/128, 2, 16, 4] */
   const void* w2_values;  /* [E_local, H/16, I/128, 64, 16] */
-  const void* w2_scales;  /* MXFP: [E_local, H/16, ceil(I/512), 64, 4]; QoQ: meta [E_local, H/16, I/128, 16] */
+  const void* w2_scales;  /* MXFP: [E_local, H/16, ceil(I/512), 64, 4]; QoQ: meta [E_local, H/16, I/128, 16];
+                             NVFP4: [E_local, H/16, I/128, 2, 16, 4] */
   int32_t* recv_stats;    /* [E_local] cumulative_local_expert_recv_stats, may be NULL */
   void* y;                /* bf16 [num_tokens, hidden] */
   void* buffer;
@@ -151,6 +162,9 @@ typedef struct DgmMoeArgs {
   int32_t phase_stamp_rows;
   const float* w1_row_scales; /* QoQ: s1 [E_local, 2I] (dgm_transform_qoq_weights order); else unused */
   const float* w2_row_scales; /* QoQ: s1 [E_local, H]; else unused */
+  const float* l1_global_scales; /* NVFP4: optional fp32 [E_local] per-expert scale of the L1 output
+                                    (deep_gemm/mega/__init__.py:277 nvfp4_mega_moe); NULL = 1 */
+  const float* l2_global_scales; /* NVFP4: the same for the L2 output */
 } DgmMoeArgs;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
@@ -175,6 +189,11 @@ int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void* sa, const
                              int sel, hipStream_t stream);
 /* One int8 op (V_MFMA_I32_16X16X64_I8): a, b 64 x 16 bytes, out 64 x 4 int32. */
 int dgm_probe_mfma_i8(const void* a, const void* b, void* out, hipStream_t stream);
+/* Same for V_MFMA_F32_16X16X32_F16 (a, b: 64 x 8 halves; out: 64 x 4 fp32), and the NVFP4 path's
+ * conversions: for i < n, out_h[4i+j] = V_CVT_SCALEF32_PK_F16_FP4(byte j of src[i], scale[i])
+ * (two f16), out_f[4i+j] = V_CVT_F32_FP8(byte j of src[i]) (E4M3). */
+int dgm_probe_mfma_f16(const void* a, const void* b, void* out, hipStream_t stream);
+int dgm_probe_cvt_fp4(const void* src, const void* scale, void* out_h, void* out_f, int n, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -130,6 +130,10 @@ def quant_act(x_f32, act_format):
         q, sf = packers.per_token_cast_to_fp8_ue8m0(x_f32, 32)
         sfb = ((sf.view(np.uint32) >> 23) & 0xFF).astype(np.uint8)
         return q, sfb, packers.dequant_fp8_rows(q, sf, 32)
+    if act_format == "nvfp4":
+        # W4A4 NVFP4 row cast (sm100_b200/test_mega_moe.py:68-93, act_format 'nvfp4')
+        p, sf, sfb = packers.cast_to_nvfp4_rows(x_f32)
+        return p, sfb, packers.dequant_fp4_rows(p, sf, 16)
     if act_format == "qoq":
         # per_token_cast_to_int8 (deep_gemm/quantization_qoq_fused.py:78-91); x_reference of
         # tests/test_four_api_correctness.py:243-246: int8 * the token's scale
@@ -152,7 +156,22 @@ def requant_mid(a, act_format):
         return (e4m3_decode(e4m3_encode(g / sf)) * sf).reshape(a.shape).astype(np.float32)
     if act_format == "qoq":
         return requant_mid_qoq(a)[2]
+    if act_format == "nvfp4":
+        return requant_mid_nvfp4(a)
     raise ValueError(act_format)
+
+
+def requant_mid_nvfp4(a):
+    """W4A4 NVFP4 intermediate requant (sm100_b200/test_mega_moe.py:431-438 ``requant_fp4`` with
+    the NVFP4 rule of :68-72): per 16, sf = E4M3(max(amax, 1e-30) / 6) (round to nearest even),
+    ties-down E2M1 of a / sf; returns the dequantised values."""
+    a = as_f32(a)
+    g = a.reshape(*a.shape[:-1], -1, 16)
+    amax = np.maximum(np.abs(g).max(axis=-1, keepdims=True), np.float32(1e-30))
+    sf = e4m3_decode(e4m3_encode(amax / np.float32(6.0)))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        codes = e2m1_code_ties_down(g / sf)
+    return (e2m1_decode(codes) * sf).reshape(a.shape).astype(np.float32)
 
 
 FLT_TINY = np.float32(np.finfo(np.float32).tiny)
@@ -196,7 +215,7 @@ class LazyDequant:
 
 # ----------------------------------------------------------------------------- layer
 def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=10.0,
-                bf16_gate_up=True, route_bf16=False):
+                bf16_gate_up=True, route_bf16=False, gs1=None, gs2=None):
     """Expert part of the layer on dequantised inputs.
 
     x_dq [M, H] f32 (dequantised activations), topk_idx [M, k], topk_w [M, k],
@@ -215,6 +234,8 @@ def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=
             continue
         w1e, w2e = W1[e], W2[e]
         h = (x_dq[t_ids] @ w1e.T).astype(np.float32)
+        if gs1 is not None:    # per-expert output scale (deep_gemm/mega/__init__.py:277 global scales)
+            h = (h * np.float32(gs1[e])).astype(np.float32)
         gate, up = h[:, :I], h[:, I:]
         if bf16_gate_up:
             gate, up = round_bf16(gate), round_bf16(up)
@@ -223,6 +244,8 @@ def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=
         act = ((silu(gate) * up).astype(np.float32) * topk_w[t_ids, s_ids][:, None]).astype(np.float32)
         act = requant_mid(act, act_format)
         out = (act @ w2e.T).astype(np.float32)
+        if gs2 is not None:
+            out = (out * np.float32(gs2[e])).astype(np.float32)
         if route_bf16:
             out = round_bf16(out)
         for n, (t, s) in enumerate(zip(t_ids, s_ids)):

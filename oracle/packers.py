@@ -185,7 +185,8 @@ def cast_to_nvfp4_rows(x):
     amax = np.maximum(np.abs(g).max(axis=-1), np.float32(1e-30))
     sfb = e4m3_encode(amax / FP4_MAX)
     sf = e4m3_decode(sfb)
-    codes = e2m1_code_ties_down(g / sf[..., None]).reshape(*outer, K)
+    with np.errstate(divide="ignore", invalid="ignore"):     # sf 0: x / 0 -> code 7 or 0
+        codes = e2m1_code_ties_down(g / sf[..., None]).reshape(*outer, K)
     return pack_low_first(codes), sf, sfb
 
 

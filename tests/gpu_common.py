@@ -86,3 +86,23 @@ def interleave16(w):
 def layer_metrics(y, ref):
     from oracle.moe import metrics
     return metrics(y, ref)
+
+
+def decode_native_nvfp4(vals, scales):
+    """NVFP4 native layout -> f32 [E, N, K] in native row order: E2M1(code) * E4M3(scale).
+    vals [E, NB, KT, 64, 16] (lane l = row l%16, dword j = K 32 j + 8 (l/16) .. +8, low nibble
+    first), scales [E, NB, KT, 2, 16, 4] (dword (p, r) byte j = block 2 j + p of row r)."""
+    vals = np.asarray(vals)
+    scales = np.asarray(scales)
+    E, NB, KT, L, B = vals.shape
+    lo, hi = vals & 0xF, vals >> 4
+    nib = np.stack([lo, hi], axis=-1).reshape(E, NB, KT, 4, 16, 4, 8)     # g, r, j, k
+    v = nu.e2m1_decode(nib)
+    # scale of (g, r, j): scales[..., g // 2, r, j]
+    sc = np.zeros((E, NB, KT, 4, 16, 4), np.float32)
+    for g in range(4):
+        sc[:, :, :, g] = nu.e4m3_decode(scales[:, :, :, g // 2])
+    v = v * sc[..., None]
+    # K within the tile = 32 j + 8 g + k; rows r
+    v = v.transpose(0, 1, 4, 2, 5, 3, 6)                                  # E NB r KT j g k
+    return v.reshape(E, NB * 16, KT * 128).astype(np.float32)

@@ -223,3 +223,67 @@ def test_transform_qoq_invariant():
                                   interleave16(d1))
     np.testing.assert_array_equal(decode_native_qoq(v2.cpu().numpy(), m2.cpu().numpy(), r2.cpu().numpy(), l1=False),
                                   d2)
+
+
+def test_mfma_f16_lane_layout():
+    """V_MFMA_F32_16X16X32_F16 (the NVFP4 path): lane l supplies A row l%16 / B column l%16 with
+    8 halves of K = 8 (l/16) .. +8; result register i of lane l is D[4 (l/16) + i][l%16]. Inputs
+    are small integers, so the fp32 sums are exact."""
+    need_gpu()
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    rng = np.random.default_rng(23)
+    a = rng.integers(-8, 9, (64, 8)).astype(np.float16)
+    b = rng.integers(-8, 9, (64, 8)).astype(np.float16)
+    ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+    out = torch.zeros(64 * 4, dtype=torch.float32, device="cuda")
+    _lib.check(_lib.load().dgm_probe_mfma_f16(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(out), _lib.stream()))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(64, 4)
+    A = np.zeros((16, 32))
+    B = np.zeros((32, 16))
+    for l in range(64):
+        A[l % 16, 8 * (l // 16):8 * (l // 16) + 8] = a[l]
+        B[8 * (l // 16):8 * (l // 16) + 8, l % 16] = b[l]
+    D = A @ B
+    exp = np.array([[D[4 * (l // 16) + i, l % 16] for i in range(4)] for l in range(64)])
+    np.testing.assert_array_equal(got, exp)
+
+
+def test_cvt_fp4_f16_and_fp8():
+    """V_CVT_SCALEF32_PK_F16_FP4 on every byte with scales that are UE4M3 values (normal and
+    subnormal, non-power-of-two mantissas): low nibble -> first half, high nibble -> second,
+    value = E2M1(code) * scale exactly (the product fits f16). V_CVT_F32_FP8 = the E4M3 value of
+    every byte except NaN."""
+    need_gpu()
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    from oracle import numerics as nu
+    codes = np.arange(256, dtype=np.uint32)
+    sc_codes = np.array([0x38, 0x39, 0x3F, 0x01, 0x05, 0x07, 0x08, 0x0B, 0x7E, 0x55, 0x2A], np.uint8)
+    scales = nu.e4m3_decode(sc_codes).astype(np.float32)
+    src = np.repeat(codes * 0x01010101, len(scales)).astype(np.uint32)
+    sc = np.tile(scales, len(codes)).astype(np.float32)
+    n = src.size
+    ts, tsc = torch.from_numpy(src.view(np.int32)).cuda(), torch.from_numpy(sc).cuda()
+    oh = torch.zeros(4 * n, dtype=torch.int32, device="cuda")
+    of = torch.zeros(4 * n, dtype=torch.float32, device="cuda")
+    _lib.check(_lib.load().dgm_probe_cvt_fp4(_lib.ptr(ts), _lib.ptr(tsc), _lib.ptr(oh), _lib.ptr(of), n,
+                                             _lib.stream()))
+    torch.cuda.synchronize()
+    h = oh.cpu().numpy().view(np.uint32).reshape(n, 4)
+    lo = (h & 0xFFFF).astype(np.uint16).view(np.float16).astype(np.float32)
+    hi = (h >> 16).astype(np.uint16).view(np.float16).astype(np.float32)
+    byte = (src & 0xFF)
+    exp_lo = nu.e2m1_decode(byte & 0xF) * sc
+    exp_hi = nu.e2m1_decode(byte >> 4) * sc
+    ok_scaled = bool((lo[:, 0] == exp_lo).all() and (hi[:, 0] == exp_hi).all())
+    pow2 = np.exp2(np.floor(np.log2(sc))).astype(np.float32)
+    ok_exp = bool((lo[:, 0] == nu.e2m1_decode(byte & 0xF) * pow2).all() and
+                  (hi[:, 0] == nu.e2m1_decode(byte >> 4) * pow2).all())
+    bad = np.nonzero(lo[:, 0] != exp_lo)[0][:8]
+    print("full-float scale:", ok_scaled, "exponent only:", ok_exp, "examples:",
+          [(int(byte[i]), float(sc[i]), float(lo[i, 0]), float(exp_lo[i])) for i in bad])
+    assert ok_scaled or ok_exp
+    f = of.cpu().numpy().reshape(n, 4)[:, 0]
+    ref = nu.e4m3_decode(byte.astype(np.uint8))
+    keep = ~np.isnan(ref)
+    np.testing.assert_array_equal(f[keep], ref[keep])
