@@ -4,8 +4,9 @@ Headline workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 lay
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
 layer forward: router + top-8 + activation cast, then the fused kernel: dispatch, L1, L2,
 combine). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
-the QoQ W4A8 layer (int8 activations, QoQ 4-bit weights), and one seeded unbalanced-routing
-run at M=16. Before every timed step >= 1 GiB is written and
+the QoQ W4A8 layer (int8 activations, QoQ 4-bit weights), the NVFP4 W4A4 layer at M = 16, 64,
+128 with seeded unbalanced routing (config 4), and one seeded unbalanced-routing A-MXFP8 run at
+M=16. Before every timed step >= 1 GiB is written and
 then 1 GiB of other data is read, so neither the 256 MB MALL nor the L2s hold weights (and
 no dirty lines are left to drain inside the timed region); per step, HIP events on the
 layer's stream bracket the frontend and the fused kernel.
@@ -30,6 +31,8 @@ MXFP4_EXPERT_BYTES = 6266880          # W1 + W2 values + E8M0 scales of one expe
 # QoQ W4A8: 4-bit codes (5,898,240 B) + one meta byte (z | s2 << 4) per row and K128 group
 # (2I * H/128 + H * I/128 = 92,160 B) + fp32 row scales s1 ((2I + H) * 4 = 22,528 B)
 QOQ_EXPERT_BYTES = 6012928
+# NVFP4 W4A4: E2M1 values (5,898,240 B) + one E4M3 scale per 16 (737,280 B)
+NVFP4_EXPERT_BYTES = 6635520
 HBM_PEAK_GBS = 8000.0
 
 
@@ -99,12 +102,35 @@ def build_qoq_weights(torch, seed, n_experts, chunk=32):
     return t
 
 
+def build_nvfp4_weights(torch, seed, n_experts, chunk=32):
+    """The layer's weights in the NVFP4 W4A4 format (quantize_to_nvfp4 on the GPU, then the
+    fused layout)."""
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_nvfp4 as qn
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    q = []
+    for N, K in ((2 * I, H), (H, I)):
+        p = torch.empty((n_experts, N, K // 2), dtype=torch.uint8, device="cuda")
+        sc = torch.empty((n_experts, N, K // 16), dtype=torch.uint8, device="cuda")
+        for e0 in range(0, n_experts, chunk):
+            e1 = min(n_experts, e0 + chunk)
+            w = (torch.randn((e1 - e0, N, K), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+            p[e0:e1], sc[e0:e1] = qn.quantize_to_nvfp4(w)
+            del w
+        q.append((p, sc))
+    t = dgm.transform_nvfp4_weights_for_mega_moe_fused(q[0], q[1])
+    del q
+    torch.cuda.synchronize()
+    return t
+
+
 def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True):
     """Times `steps` layer forwards. Per step three HIP events on the layer's stream: before the
     frontend, between frontend and the fused MoE kernel, after it."""
     (t1, t2) = weights
-    fused = dgm.qoq_mega_moe_fused if act == "qoq" else dgm.mxfp4_mega_moe_fused
-    expert_bytes = QOQ_EXPERT_BYTES if act == "qoq" else MXFP4_EXPERT_BYTES
+    fused = {"qoq": dgm.qoq_mega_moe_fused, "nvfp4": dgm.fp4_fp4_mega_moe}.get(act, dgm.mxfp4_mega_moe_fused)
+    expert_bytes = {"qoq": QOQ_EXPERT_BYTES, "nvfp4": NVFP4_EXPERT_BYTES}.get(act, MXFP4_EXPERT_BYTES)
     buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -220,6 +246,8 @@ def main():
     ap.add_argument("--sweep", default="2,4,8,16", help="M values of the sweep (both activation formats)")
     ap.add_argument("--sweep-steps", type=int, default=10)
     ap.add_argument("--no-qoq", action="store_true", help="skip the QoQ W4A8 sweep")
+    ap.add_argument("--nvfp4-sweep", default="16,64,128",
+                    help="M values of the NVFP4 W4A4 sweep (seeded unbalanced routing); empty = skip")
     ap.add_argument("--no-unbalanced", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -262,6 +290,17 @@ def main():
             sweep["qoq"][M] = entry(r)
             log(f"M={M} qoq: {sweep['qoq'][M]}")
         del qw
+    nv_ms = [int(v) for v in args.nvfp4_sweep.split(",") if v]
+    if nv_ms:
+        log("building E384 NVFP4 weights ...")
+        nw = build_nvfp4_weights(torch, 5678, E)
+        sweep["nvfp4_unbalanced"] = {}
+        for M in nv_ms:
+            r = time_layer(torch, dgm, M, nw, router_w, "nvfp4", args.sweep_steps, args.warmup, 900 + M,
+                           force_balanced=False)
+            sweep["nvfp4_unbalanced"][M] = entry(r)
+            log(f"M={M} nvfp4 unbalanced: {sweep['nvfp4_unbalanced'][M]}")
+        del nw
     if not args.no_unbalanced:
         r = time_layer(torch, dgm, 16, weights, router_w, "mxfp8", args.sweep_steps, args.warmup, 777,
                        force_balanced=False)
