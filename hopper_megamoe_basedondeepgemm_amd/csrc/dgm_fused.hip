@@ -180,6 +180,7 @@ struct FusedSmem {
   int act[FUSED_MAX_LOCAL];
   int aoff[FUSED_MAX_LOCAL + 1];
   int nslot[FUSED_MAX_TOKENS];
+  int tflag[FUSED_MAX_TOKENS];         // select_in_mega: the frontend's per-token flags
   int wsum[NW][2];
   int meta[4];
   union {
@@ -250,6 +251,73 @@ DGM_DEV void scan_experts(S& s, int n) {
     s.aoff[ta] = tc;
   }
   __syncthreads();
+}
+
+// The pool table of R <= 64 * KPL routes by one wave: a bitonic sort of the keys
+// (local expert << 16 | route id; routes of other ranks sort last) over 64 lanes x KPL
+// registers (element i = lane + 64 j) gives the canonical pool order (expert asc, route asc =
+// token asc, slot asc) directly; expert boundaries give the active list, offsets and counts.
+// Writes s.routes, s.act, s.aoff, s.meta[0..1], s.cnt (of active experts; the rest must be
+// zero) and s.nslot (must be zero).
+template <int KPL, class S>
+DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane) {
+  constexpr int N = 64 * KPL;
+  uint32_t key[KPL];
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int i = lane + 64 * j;
+    const int e = i < R ? s.exp_of_route[i] : -1;
+    key[j] = ((e < 0 ? 0xffffu : (uint32_t)e) << 16) | (uint32_t)i;
+  }
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int d = size >> 1; d > 0; d >>= 1) {
+      uint32_t nk[KPL];
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int i = lane + 64 * j;
+        const uint32_t other = d < 64 ? (uint32_t)__shfl_xor((int)key[j], d) : key[j ^ (d >> 6)];
+        const bool up = (i & size) == 0, lower = (i & d) == 0;
+        const uint32_t lo = key[j] < other ? key[j] : other, hi = key[j] < other ? other : key[j];
+        nk[j] = lower == up ? lo : hi;
+      }
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) key[j] = nk[j];
+    }
+  }
+  int base = 0, total = 0;
+  uint32_t last_prev = 0xffffffffu;     // key of element 64 j - 1
+#pragma unroll
+  for (int j = 0; j < KPL; ++j) {
+    const int i = lane + 64 * j;
+    const uint32_t e = key[j] >> 16;
+    const bool valid = e != 0xffffu;
+    const uint32_t up1 = (uint32_t)__shfl_up((int)key[j], 1);
+    const uint32_t prev = lane == 0 ? last_prev : up1;
+    const bool first = valid && (i == 0 || (prev >> 16) != e);
+    const uint64_t fb = __ballot(first), vb = __ballot(valid);
+    const int a = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(fb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)fb, 0u));
+    if (valid) {
+      const int r = (int)(key[j] & 0xffffu);
+      s.routes[i] = r;
+      atomicAdd(&s.nslot[r / topk], 1);
+    }
+    if (first) {
+      s.act[a] = (int)e;
+      s.aoff[a] = i;
+    }
+    base += __popcll(fb);
+    total += __popcll(vb);
+    last_prev = (uint32_t)__shfl((int)key[j], 63);
+  }
+  if (lane == 0) {
+    s.aoff[base] = total;
+    s.meta[0] = base;
+    s.meta[1] = total;
+  }
+  // per active expert: count = next offset - offset (the wave's LDS stores above come first)
+  for (int a = lane; a < base; a += 64) s.cnt[s.act[a]] = s.aoff[a + 1] - s.aoff[a];
 }
 
 DGM_DEV bool spin_until(const int* p, int target, int limit, int* err) {
@@ -566,6 +634,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     for (int t0 = 0; t0 < p.M; t0 += TC) {
       const int tn = p.M - t0 < TC ? p.M - t0 : TC;
       for (int i = tid; i < tn * p.E; i += FT) lg[i] = p.logits[(size_t)t0 * p.E + i];
+      if (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED)
+        for (int i = tid; i < tn; i += FT) s.tflag[t0 + i] = p.token_flags[t0 + i];
       __syncthreads();
       for (int tt = wv; tt < tn; tt += NW) {
         const int t = t0 + tt;
@@ -573,7 +643,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         float wt;
         const float* row = lg + tt * p.E;
         select_topk_wave([row](int e) { return row[e]; }, p.E, p.topk, (p.fe_flags & DGM_FE_FORCE_BALANCED) != 0,
-                         p.token_offset + t, (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) && (p.token_flags[t] & 1),
+                         p.token_offset + t, (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) && (s.tflag[t] & 1),
                          lane, idx, wt);
         if (lane < p.topk) {
           const int r = t * p.topk + lane;
@@ -604,20 +674,30 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
   }
   __syncthreads();
-  for (int r = tid; r < R; r += FT) {
-    int e = s.exp_of_route[r];
-    if (e >= 0) { atomicAdd(&s.cnt[e], 1); atomicAdd(&s.nslot[r / p.topk], 1); }
+  if (R <= 256) {
+    // one wave sorts the routes (the other waves wait at the barrier)
+    if (wv == 0) {
+      if (R <= 64) wave_dispatch<1>(s, R, p.topk, lane);
+      else if (R <= 128) wave_dispatch<2>(s, R, p.topk, lane);
+      else wave_dispatch<4>(s, R, p.topk, lane);
+    }
+    __syncthreads();
+  } else {
+    for (int r = tid; r < R; r += FT) {
+      int e = s.exp_of_route[r];
+      if (e >= 0) { atomicAdd(&s.cnt[e], 1); atomicAdd(&s.nslot[r / p.topk], 1); }
+    }
+    __syncthreads();
+    scan_experts(s, p.E_local);
+    for (int r = tid; r < R; r += FT) {
+      int e = s.exp_of_route[r];
+      if (e < 0) continue;
+      int rank = 0;
+      for (int q = 0; q < r; ++q) rank += s.exp_of_route[q] == e ? 1 : 0;
+      s.routes[s.eoff[e] + rank] = r;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  scan_experts(s, p.E_local);
-  for (int r = tid; r < R; r += FT) {
-    int e = s.exp_of_route[r];
-    if (e < 0) continue;
-    int rank = 0;
-    for (int q = 0; q < r; ++q) rank += s.exp_of_route[q] == e ? 1 : 0;
-    s.routes[s.eoff[e] + rank] = r;
-  }
-  __syncthreads();
   const int n_active = s.meta[0];
   if (st && tid == 0) st[1] = wall_clock();
   if (blockIdx.x == 0) {
