@@ -51,7 +51,8 @@ class MoeArgs(ctypes.Structure):
                 ("layout", ctypes.POINTER(BufferLayout)), ("phase_stamps", ctypes.c_void_p),
                 ("phase_stamp_rows", ctypes.c_int32), ("w1_row_scales", ctypes.c_void_p),
                 ("w2_row_scales", ctypes.c_void_p), ("l1_global_scales", ctypes.c_void_p),
-                ("l2_global_scales", ctypes.c_void_p)]
+                ("l2_global_scales", ctypes.c_void_p), ("fe_in_mega", ctypes.c_int32),
+                ("hidden_states", ctypes.c_void_p), ("router_weight", ctypes.c_void_p)]
 
 
 _lib = None

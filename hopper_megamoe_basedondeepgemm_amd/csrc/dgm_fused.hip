@@ -40,6 +40,7 @@
 #include "dgm_common.hpp"
 #include "dgm_abi_internal.hpp"
 #include "dgm_fused.hpp"
+#include "dgm_frontend.hpp"
 
 using namespace dgm;
 
@@ -253,12 +254,14 @@ DGM_DEV void scan_experts(S& s, int n) {
   __syncthreads();
 }
 
-// The pool table of R <= 64 * KPL routes by one wave: a bitonic sort of the keys
-// (local expert << 16 | route id; routes of other ranks sort last) over 64 lanes x KPL
-// registers (element i = lane + 64 j) gives the canonical pool order (expert asc, route asc =
-// token asc, slot asc) directly; expert boundaries give the active list, offsets and counts.
-// Writes s.routes, s.act, s.aoff, s.meta[0..1], s.cnt (of active experts; the rest must be
-// zero) and s.nslot (must be zero).
+// The pool table of R <= 64 * KPL routes by one wave. Keys = local expert << 16 | route id
+// (routes of other ranks sort last) over 64 lanes x KPL registers (element i = lane + 64 j);
+// sorted, they are the canonical pool order (expert asc, route asc = token asc, slot asc), and
+// expert boundaries give the active list, offsets and counts. KPL <= 2: each key's rank is
+// counted against every key (broadcast by readlane), then keys are scattered to their ranks
+// and read back in order; KPL = 4: an in-register bitonic sort. Writes s.routes, s.act,
+// s.aoff, s.meta[0..1], s.cnt (of active experts; the rest must be zero) and s.nslot (must
+// be zero).
 template <int KPL, class S>
 DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane) {
   constexpr int N = 64 * KPL;
@@ -269,6 +272,23 @@ DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane) {
     const int e = i < R ? s.exp_of_route[i] : -1;
     key[j] = ((e < 0 ? 0xffffu : (uint32_t)e) << 16) | (uint32_t)i;
   }
+  if constexpr (KPL <= 2) {
+    int rank[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) rank[j] = 0;
+#pragma unroll
+    for (int jj = 0; jj < KPL; ++jj)
+      for (int q = 0; q < 64; ++q) {
+        const uint32_t kq = (uint32_t)__builtin_amdgcn_readlane((int)key[jj], q);
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) rank[j] += kq < key[j] ? 1 : 0;
+      }
+    // (the route-table slots double as the sort buffer: keys of the routes are unique)
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) s.routes[rank[j]] = (int)key[j];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) key[j] = (uint32_t)s.routes[lane + 64 * j];
+  } else {
 #pragma unroll
   for (int size = 2; size <= N; size <<= 1) {
 #pragma unroll
@@ -285,6 +305,7 @@ DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane) {
 #pragma unroll
       for (int j = 0; j < KPL; ++j) key[j] = nk[j];
     }
+  }
   }
   int base = 0, total = 0;
   uint32_t last_prev = 0xffffffffu;     // key of element 64 j - 1
@@ -390,7 +411,7 @@ DGM_DEV void stage_slab(S& s, const uint8_t* __restrict__ src, const uint8_t* __
 // only combined or masked at the store: doing either earlier would wait for every older load.
 // Every lane loads (from row 0 when it has no row), so no loaded value crosses a divergent
 // branch.
-template <int KT, int ACT, bool COHERENT>
+template <int KT, int ACT, bool COHERENT, bool MIDL = COHERENT>
 struct SlabRegs {
   static constexpr int FR = (KT * 64 + FT - 1) / FT;
   v4u v0[FR], v1[FR];            // non-coherent fragments
@@ -403,13 +424,15 @@ struct SlabRegs {
   float w;
 };
 
-template <int KT, int ACT, bool COHERENT, class RowOf, class WeightOf>
-DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
+// COHERENT: agent-scope loads (rows written by other workgroups of this launch); MIDL: the
+// intermediate rows' layout (QoQ: per-chunk scales) rather than the input activations'.
+template <int KT, int ACT, bool COHERENT, bool MIDL, class RowOf, class WeightOf>
+DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT, MIDL>& r, const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
                        int row_bytes, int n, RowOf row_of, WeightOf weight_of) {
   const int tid = threadIdx.x;
   uint32_t ok = 0;
 #pragma unroll
-  for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+  for (int j = 0; j < SlabRegs<KT, ACT, COHERENT, MIDL>::FR; ++j) {
     const int f = tid + j * FT;
     const int l = f & 63, c = l & 15;
     const bool have = f < KT * 64 && c < n;
@@ -444,11 +467,11 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
   if constexpr (ACT == DGM_ACT_NVFP4) {
     // (scales loaded with the fragments)
   } else if constexpr (ACT == DGM_ACT_QOQ) {
-    if (COHERENT) {
+    if (MIDL) {
       // intermediate rows: fp32 scale per 64-K chunk (row pitch KT * 8 bytes); lane l < 16 of
       // fragment j (K-tile kt, column l) loads the two chunk scales of its tile
 #pragma unroll
-      for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+      for (int j = 0; j < SlabRegs<KT, ACT, COHERENT, MIDL>::FR; ++j) {
         const int f = tid + j * FT;
         const bool have = (ok >> j) & 1u && (f & 63) < 16;
         const size_t rr = have ? (size_t)row_of(f & 15) : 0;
@@ -460,7 +483,8 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
       const int c = tid & 15;
       const bool have = tid < 16 && c < n;
       const size_t rr = have ? (size_t)row_of(c) : 0;
-      r.fsc = *reinterpret_cast<const float*>(ssrc + rr * (KT * 4));
+      const float* fq = reinterpret_cast<const float*>(ssrc + rr * (KT * 4));
+      r.fsc = COHERENT ? __hip_atomic_load(fq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *fq;
       ok |= have ? 1u << 8 : 0u;
     }
   } else {
@@ -480,8 +504,8 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT>& r, const uint8_t* __restrict
   r.w = tid < n && tid < 16 ? weight_of(tid) : 0.f;
 }
 
-template <int KT, int ACT, bool COHERENT, class S>
-DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
+template <int KT, int ACT, bool COHERENT, bool MIDL, class S>
+DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT, MIDL>& r) {
   // (the thread index is made opaque so that the LDS addresses below are recomputed here
   // rather than hoisted out of the work loop and kept live, or spilled, across it)
   int tid = threadIdx.x;
@@ -492,7 +516,7 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
     // groups q (K = 32 g' + 8 q .. +8): E2M1 -> f16 exactly, times the E4M3 block scale (the
     // products are exact in f16)
 #pragma unroll
-    for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+    for (int j = 0; j < SlabRegs<KT, ACT, COHERENT, MIDL>::FR; ++j) {
       const int f = tid + j * FT;
       if (f < KT * 64) {
         const bool have = (r.ok >> j) & 1u;
@@ -527,7 +551,7 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
     }
   } else {
 #pragma unroll
-  for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+  for (int j = 0; j < SlabRegs<KT, ACT, COHERENT, MIDL>::FR; ++j) {
     const int f = tid + j * FT;
     if (f < KT * 64) {
       const bool have = (r.ok >> j) & 1u;
@@ -549,7 +573,7 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
     // (no scale plane: the scales are folded into the f16 operands)
   } else if constexpr (ACT == DGM_ACT_QOQ) {
 #pragma unroll
-    for (int j = 0; j < SlabRegs<KT, ACT, COHERENT>::FR; ++j) {
+    for (int j = 0; j < SlabRegs<KT, ACT, COHERENT, MIDL>::FR; ++j) {
       const int f = tid + j * FT;
       if (f < KT * 64) {
         const bool have = (r.ok >> j) & 1u;
@@ -571,7 +595,7 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
         s1 += __shfl_xor(s1, 16);
         s1 += __shfl_xor(s1, 32);
         if (l < 16) {
-          if (COHERENT) {        // intermediate rows (L2): the K-tile's promote coefficients
+          if (MIDL) {            // intermediate rows (L2): the K-tile's promote coefficients
             const float sm0 = have ? __uint_as_float((uint32_t)r.sc2[j]) : 0.f;
             const float sm1 = have ? __uint_as_float((uint32_t)(r.sc2[j] >> 32)) : 0.f;
             const float x0 = (float)s0, x1 = (float)s1;
@@ -582,7 +606,7 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT>& r) {
         }
       }
     }
-    if (!COHERENT && tid < 16) s.xsc[tid] = (r.ok >> 8) & 1u ? r.fsc : 0.f;
+    if (!MIDL && tid < 16) s.xsc[tid] = (r.ok >> 8) & 1u ? r.fsc : 0.f;
   } else if (tid < KG * 64) {
     uint32_t w = 0;
 #pragma unroll
@@ -623,6 +647,39 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   long long wait_ticks = 0, l1_load_ticks = 0, l1_sig_ticks = 0;
   if (st && tid == 0) st[0] = wall_clock();
 
+  // ---------------------------------------------------------------- in-kernel frontend
+  // (fe_in) router logits, zero-row flags and the activation cast, spread over the grid, with
+  // write-through stores; then every workgroup waits until all have arrived (the grid is what
+  // the device keeps resident, so all workgroups run at once)
+  if (p.fe_in) {
+    constexpr int J = H / 512;
+    static_assert(H % 512 == 0, "in-kernel frontend: hidden % 512");
+    const int ngrp = (p.M + 3) / 4, npairs = p.E * ngrp;
+    for (int pi = (int)blockIdx.x * NW + wv; pi < npairs; pi += (int)gridDim.x * NW) {
+      const int e = pi % p.E, tg = pi / p.E;
+      router_wave<J, true>(p.hidden, p.router_w, p.M, p.E, e, 4 * tg, lane, const_cast<float*>(p.logits),
+                           const_cast<int*>(p.token_flags), e == 0);
+    }
+    uint8_t* xq = const_cast<uint8_t*>(p.x);
+    uint8_t* xsf = const_cast<uint8_t*>(p.xsf);
+    const int64_t lane0 = (int64_t)blockIdx.x * FT + tid, nl = (int64_t)gridDim.x * FT;
+    if constexpr (ACT == DGM_ACT_QOQ) {
+      for (int t = (int)blockIdx.x * NW + wv; t < p.M; t += (int)gridDim.x * NW) cast_qoq_token<J, true>(p.hidden, t, lane, xq, xsf);
+    } else if constexpr (ACT == DGM_ACT_NVFP4) {
+      for (int64_t i = lane0; i < (int64_t)p.M * (H / 16) * 4; i += nl) cast_lane_nvfp4<true>(p.hidden, i, xq, xsf);
+    } else {
+      for (int64_t i = lane0; i < (int64_t)p.M * (H / 32) * 8; i += nl) cast_lane_mx<true>(p.hidden, ACT, i, xq, xsf);
+    }
+    wait_mem();                  // this wave's stores have completed
+    __syncthreads();
+    if (tid == 0) {
+      int* gc = p.counters + CNT_GRID;
+      __hip_atomic_fetch_add(gc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      spin_until(gc, (int)gridDim.x, p.spin_limit, err);
+    }
+    __syncthreads();
+  }
+
   // ---------------------------------------------------------------- dispatch (every WG)
   for (int t = tid; t < p.M; t += FT) s.nslot[t] = 0;
   if (p.select) {
@@ -633,9 +690,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const int TC = (int)(sizeof(s.bst) / 4) / p.E;
     for (int t0 = 0; t0 < p.M; t0 += TC) {
       const int tn = p.M - t0 < TC ? p.M - t0 : TC;
-      for (int i = tid; i < tn * p.E; i += FT) lg[i] = p.logits[(size_t)t0 * p.E + i];
+      // (agent-scope loads: the in-kernel frontend may have written them in this launch)
+      for (int i = tid; i < tn * p.E; i += FT) lg[i] = ld_agent_f32(p.logits + (size_t)t0 * p.E + i);
       if (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED)
-        for (int i = tid; i < tn; i += FT) s.tflag[t0 + i] = p.token_flags[t0 + i];
+        for (int i = tid; i < tn; i += FT)
+          s.tflag[t0 + i] = __hip_atomic_load(p.token_flags + t0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __syncthreads();
       for (int tt = wv; tt < tn; tt += NW) {
         const int t = t0 + tt;
@@ -790,9 +849,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     };
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
-    auto load_slab = [xv, xs, topk](SlabRegs<KT1, ACT, false>& r, int a, int s0) __attribute__((always_inline)) {
+    // (agent-scope loads: the rows may have been written by this launch's in-kernel frontend)
+    auto load_slab = [xv, xs, topk](SlabRegs<KT1, ACT, true, false>& r, int a, int s0) __attribute__((always_inline)) {
       const int* rts = s.routes + s.aoff[a] + s0;
-      slab_load<KT1, ACT, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
+      slab_load<KT1, ACT, true, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
                                  [rts, topk](int cc) { return rts[cc] / topk; },
                                  [rts](int cc) { return s.route_w[rts[cc]]; });
     };
@@ -810,7 +870,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     U4 wr[KR];
     uint32_t sr[ACT == DGM_ACT_NVFP4 ? KR : 1];
     uint32_t sd[SW1], sn[SW1];
-    SlabRegs<KT1, ACT, false> pre;
+    SlabRegs<KT1, ACT, true, false> pre;
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
     if (q0 < U1) {
       load_slab(pre, q0 / QN1, 0);      // (ahead of the tiles: the store below waits for it only)
@@ -1124,7 +1184,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const uint8_t* mids = p.mid_sf;
     auto load_slab = [midv, mids](SlabRegs<KT2, ACT, true>& r, int a, int s0) __attribute__((always_inline)) {
       const int rb = s.aoff[a] + s0;
-      slab_load<KT2, ACT, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
+      slab_load<KT2, ACT, true, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
                                 [](int) { return 0.f; });
     };
     // arrivals of item (unit v, slab s0): its routes' outputs for the unit's blocks are complete
@@ -1430,6 +1490,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     for (int a = tid; a < n_active; a += FT) __hip_atomic_store(&l1_done[a], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int i = tid; i < p.M * NBL2; i += FT) __hip_atomic_store(&comb[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < 2) __hip_atomic_store(p.counters + CNT_CLAIM + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 2) __hip_atomic_store(p.counters + CNT_GRID, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_mem();
     __syncthreads();
     if (tid == 0) __hip_atomic_store(exit_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

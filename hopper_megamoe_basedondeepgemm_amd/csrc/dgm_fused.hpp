@@ -12,6 +12,7 @@ constexpr int FUSED_MAX_NB64 = 64;       // hidden / 64 (hidden <= 4096); combin
 constexpr int CNT_EXIT = 0;              // workgroups finished (last one clears everything)
 constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
 constexpr int CNT_CLAIM = 2;             // next unclaimed L1 unit, then [3] next unclaimed L2 unit
+constexpr int CNT_GRID = 4;              // in-kernel frontend: workgroups past the frontend work
 constexpr int CNT_L1 = 64;               // [FUSED_MAX_LOCAL] L1 units done per active expert slot
 constexpr int CNT_TOTAL = CNT_L1 + FUSED_MAX_LOCAL + FUSED_MAX_TOKENS * FUSED_MAX_NB64;  // + combine counters
 constexpr int CNT_FE = CNT_TOTAL;        // frontend: arrival counters of 4-token chunks
@@ -46,6 +47,9 @@ struct FusedParams {
   int stamp_rows;
   int M, topk, expert_begin, E_local;
   int select, fe_flags, token_offset, E;   // select the top-k in the prologue (DGM_FE_* flags)
+  int fe_in;                // run the frontend (router + cast) in the kernel first: needs select
+  const uint16_t* hidden;   // fe_in: bf16 [M, H] hidden states and bf16 [E, H] router weights
+  const uint16_t* router_w;
   float clamp;
   int fast_math;
   int spin_limit;

@@ -19,6 +19,7 @@
 #include "dgm_common.hpp"
 #include "dgm_abi_internal.hpp"
 #include "dgm_fused.hpp"
+#include "dgm_frontend.hpp"
 
 using namespace dgm;
 
@@ -59,14 +60,10 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
 
 // ------------------------------------------------------------------ frontend
 // Router: wave w of workgroup (bx, by) computes the logits of expert 4 bx + w for tokens
-// 4 by .. +3. Lane l accumulates K = 512 j + 8 l + i (j, then i ascending) with fp32 FMAs of
-// exact bf16 products, then an xor butterfly (32..1) reduces the 64 lane sums: a fixed
-// order, so the fp32 logits are reproducible bit for bit. Workgroups with bx == 0 also record
-// each token's all-zero flag (token_flags bit 0) from the rows they hold.
-// Cast: 8 lanes per 32-element activation group, 4 elements per lane (MXFP4 rows with amax
-// floor 1e-30, MXFP8 rows with amax floor 1e-4: the rules of dgm_cast_fp4_rows /
-// dgm_cast_fp8_rows), spread over the whole grid after the router work; QoQ: one wave per
-// token (per-token int8, the rule of dgm_cast_int8_rows).
+// 4 by .. +3 (router_wave: fixed accumulation order, bit-reproducible fp32 logits);
+// workgroups with bx == 0 also record each token's all-zero flag. Cast, spread over the whole
+// grid after the router work: MXFP4 / MXFP8 8 lanes per 32-element group, NVFP4 4 lanes per
+// 16-element group, QoQ one wave per token (dgm_frontend.hpp).
 template <int J>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
@@ -74,134 +71,18 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
                                                   uint8_t* __restrict__ sf) {
   constexpr int H = J * 512;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // ---- router logits
-  const int e = blockIdx.x * 4 + wave;
-  const int t0 = blockIdx.y * 4;
-  {
-    U4 wv[J];
-    const int ee = e < E ? e : E - 1;
-#pragma unroll
-    for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const U4*>(w + (size_t)ee * H + 512 * j + 8 * lane);
-    U4 xv[4][J];
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      int t = t0 + tt < M ? t0 + tt : M - 1;
-#pragma unroll
-      for (int j = 0; j < J; ++j) xv[tt][j] = *reinterpret_cast<const U4*>(x + (size_t)t * H + 512 * j + 8 * lane);
-    }
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      float acc = 0.f;
-      uint32_t any = 0;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        uint32_t xa[4] = {xv[tt][j].x, xv[tt][j].y, xv[tt][j].z, xv[tt][j].w};
-        uint32_t wa[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          acc = fmaf(__uint_as_float(xa[qq] << 16), __uint_as_float(wa[qq] << 16), acc);
-          acc = fmaf(__uint_as_float(xa[qq] & 0xffff0000u), __uint_as_float(wa[qq] & 0xffff0000u), acc);
-          any |= xa[qq] & 0x7fff7fffu;
-        }
-      }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
-      const bool nonzero = __any(any != 0u);
-      if (lane == 0 && t0 + tt < M) {
-        if (e < E) logits[(size_t)(t0 + tt) * E + e] = acc;
-        if (blockIdx.x == 0 && wave == 0) token_flags[t0 + tt] = nonzero ? 0 : 1;
-      }
-    }
-  }
+  router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, token_flags,
+                        blockIdx.x == 0 && wave == 0);
+  const int64_t lane0 = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid;
+  const int64_t nl = (int64_t)gridDim.x * gridDim.y * 256;
   if (act_format == DGM_ACT_QOQ) {
-    // ---- QoQ activation cast (per_token_cast_to_int8): one wave per token, lane l holds
-    // elements 512 j + 8 l .. +7; sf = max(amax, 1e-30) / 127 (fp32), q = clamp(rne(x / sf),
-    // +-127); the scale is repeated over the row's H / 128 slots
     const int nwaves = gridDim.x * gridDim.y * 4;
-    for (int t = ((int)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave; t < M; t += nwaves) {
-      U4 xv[J];
-      float amax = 0.f;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        xv[j] = *reinterpret_cast<const U4*>(x + (size_t)t * H + 512 * j + 8 * lane);
-        const uint32_t d[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-          amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(d[k] << 16)), fabsf(__uint_as_float(d[k] & 0xffff0000u))));
-      }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-      const float scale = fmaxf(amax, 1e-30f) / 127.0f;
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const uint32_t d[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-        uint32_t o[2] = {0u, 0u};
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t bits = (k & 1) ? (d[k >> 1] & 0xffff0000u) : (d[k >> 1] << 16);
-          const float v = fminf(fmaxf(rintf(__uint_as_float(bits) / scale), -127.f), 127.f);
-          o[k >> 2] |= ((uint32_t)(int)v & 0xffu) << (8 * (k & 3));
-        }
-        *reinterpret_cast<uint2*>(q + (size_t)t * H + 512 * j + 8 * lane) = make_uint2(o[0], o[1]);
-      }
-      if (lane < H / 128) reinterpret_cast<float*>(sf)[(size_t)t * (H / 128) + lane] = scale;
-    }
-    return;
-  }
-  if (act_format == DGM_ACT_NVFP4) {
-    // ---- NVFP4 activation cast (sm100 W4A4 rule): per 16 elements, 4 lanes of 4; sf = E4M3
-    // RNE of max(amax, 1e-30) / 6, codes = ties-down E2M1 of x / sf, low nibble first
-    const int64_t groups16 = (int64_t)M * (H / 16);
-    const int64_t nl = (int64_t)gridDim.x * gridDim.y * 256;
-    for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid; i < groups16 * 4; i += nl) {
-      const int64_t g = i >> 2;
-      const int part = (int)(i & 3);
-      const uint2 raw = *reinterpret_cast<const uint2*>(x + g * 16 + 4 * part);
-      const float v[4] = {__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
-                          __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
-      float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-      amax = fmaxf(amax, __shfl_xor(amax, 1));
-      amax = fmaxf(amax, __shfl_xor(amax, 2));
-      const uint32_t code = e4m3_encode(fmaxf(amax, 1e-30f) / 6.0f);
-      const float sc = __builtin_amdgcn_cvt_f32_fp8((int)code, 0);
-      uint32_t o = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o |= e2m1_ties_down(v[k] / sc) << (4 * k);
-      reinterpret_cast<uint16_t*>(q)[g * 4 + part] = (uint16_t)o;
-      if (part == 0) sf[g] = (uint8_t)code;
-    }
-    return;
-  }
-  // ---- activation cast: 8 lanes per group
-  const int64_t groups = (int64_t)M * (H / 32);
-  const int64_t nlanes = (int64_t)gridDim.x * gridDim.y * 256;
-  for (int64_t i = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid; i < groups * 8; i += nlanes) {
-    const int64_t g = i >> 3;
-    const int part = (int)(i & 7);            // elements 4 part .. +3 of the group
-    const uint2 raw = *reinterpret_cast<const uint2*>(x + g * 32 + 4 * part);
-    float v[4] = {__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
-                  __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
-    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    amax = fmaxf(amax, __shfl_xor(amax, 1));
-    amax = fmaxf(amax, __shfl_xor(amax, 2));
-    amax = fmaxf(amax, __shfl_xor(amax, 4));
-    if (act_format == DGM_ACT_MXFP4) {
-      const uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-30f) / 6.0f);
-      const float sc = e8m0_value(code);
-      uint32_t o = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o |= e2m1_ties_down(v[k] / sc) << (4 * k);
-      reinterpret_cast<uint16_t*>(q)[g * 8 + part] = (uint16_t)o;
-      if (part == 0) sf[g] = (uint8_t)code;
-    } else {
-      const uint32_t code = ceil_ue8m0_code(fmaxf(amax, 1e-4f) / 448.0f);
-      const float inv = 1.0f / e8m0_value(code);
-      uint32_t o = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) o |= e4m3_encode(v[k] * inv) << (8 * k);
-      reinterpret_cast<uint32_t*>(q)[g * 8 + part] = o;
-      if (part == 0) sf[g] = (uint8_t)code;
-    }
+    for (int t = ((int)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave; t < M; t += nwaves)
+      cast_qoq_token<J, false>(x, t, lane, q, sf);
+  } else if (act_format == DGM_ACT_NVFP4) {
+    for (int64_t i = lane0; i < (int64_t)M * (H / 16) * 4; i += nl) cast_lane_nvfp4<false>(x, i, q, sf);
+  } else {
+    for (int64_t i = lane0; i < (int64_t)M * (H / 32) * 8; i += nl) cast_lane_mx<false>(x, act_format, i, q, sf);
   }
 }
 
@@ -691,9 +572,18 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   if (A->num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)A->buffer;
   const int routes_n = A->num_tokens * A->topk;
+  if (A->fe_in_mega) {
+    DGM_CHECK_ARG(A->hidden_states && A->router_weight, "fe_in_mega: null hidden_states / router_weight");
+    DGM_CHECK_ARG(((uintptr_t)A->hidden_states & 15) == 0 && ((uintptr_t)A->router_weight & 15) == 0, "16-byte alignment");
+    DGM_CHECK_ARG(A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS, "fe_in_mega: num_tokens <= 64");
+    DGM_CHECK_ARG(A->hidden % 512 == 0, "fe_in_mega: hidden % 512 == 0");
+    DGM_CHECK_ARG(A->topk <= A->num_experts && A->num_experts <= 1024, "fe_in_mega: topk, num_experts");
+    DGM_CHECK_ARG(!(A->fe_flags & DGM_FE_FORCE_BALANCED) || A->num_experts % A->topk == 0,
+                  "forced-balanced needs E % topk == 0");
+  }
   if (routes_n <= FUSED_MAX_ROUTES && A->num_local_experts <= FUSED_MAX_LOCAL &&
       A->num_tokens <= FUSED_MAX_TOKENS && A->hidden / 64 <= FUSED_MAX_NB64) {
-    const bool sel = A->select_in_mega && A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS;
+    const bool sel = (A->select_in_mega || A->fe_in_mega) && A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS;
     if (A->select_in_mega && !sel) {
       int st = materialize_topk(A, buf, L, stream);
       if (st) return st;
@@ -714,6 +604,9 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.logits = (const float*)(buf + L->logits);
     p.token_flags = (const int*)(buf + L->token_flags);
     p.select = sel ? 1 : 0;
+    p.fe_in = A->fe_in_mega ? 1 : 0;
+    p.hidden = (const uint16_t*)A->hidden_states;
+    p.router_w = (const uint16_t*)A->router_weight;
     p.fe_flags = A->fe_flags;
     p.token_offset = A->token_offset;
     p.E = A->num_experts;
@@ -737,6 +630,7 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   }
   DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
                 "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+  DGM_CHECK_ARG(!A->fe_in_mega, "fe_in_mega: the fused kernel's limits (tokens, routes, local experts) are exceeded");
   return dgm_megamoe_split_launch(A, stream);
 }
 

@@ -259,7 +259,7 @@ _ENTRY_FOR = {"qoq": "qoq_mega_moe_fused", "nvfp4": "fp4_fp4_mega_moe / nvfp4_me
 
 
 def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
-           fast_math=True, fmt=None, global_scales=(None, None)):
+           fast_math=True, fmt=None, global_scales=(None, None), fe=None):
     fmt = fmt or ("mxfp8" if b.act_format in ("mxfp8", "fp8") else "mxfp4")
     kind = lambda f: f if f in ("qoq", "nvfp4") else "mxfp"
     if kind(fmt) != kind(b.act_format):
@@ -301,6 +301,10 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
     if stats is not None:
         assert stats.dtype == torch.int32 and stats.numel() == E_l
     sel = getattr(b, "_fe_select", None)
+    if fe is not None:        # in-kernel frontend: (hidden, router_weight, flags, token_offset)
+        hidden, router_weight, fe_flags, fe_off = fe
+        sel = (fe_flags, fe_off)
+        b._fe_select = None
     args = _lib.MoeArgs(num_tokens=m, hidden=b.hidden, intermediate=b.intermediate_hidden,
                         num_experts=b.num_experts, expert_begin=b.expert_begin, num_local_experts=E_l,
                         topk=b.num_topk, act_format=b.act_code,
@@ -315,7 +319,10 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
                         w1_row_scales=rs1.data_ptr() if qoq else None,
                         w2_row_scales=rs2.data_ptr() if qoq else None,
                         l1_global_scales=global_scales[0].data_ptr() if global_scales[0] is not None else None,
-                        l2_global_scales=global_scales[1].data_ptr() if global_scales[1] is not None else None)
+                        l2_global_scales=global_scales[1].data_ptr() if global_scales[1] is not None else None,
+                        fe_in_mega=int(fe is not None),
+                        hidden_states=fe[0].data_ptr() if fe is not None else None,
+                        router_weight=fe[1].data_ptr() if fe is not None else None)
     if phase_stamps is not None:
         assert phase_stamps.dtype == torch.int64 and phase_stamps.is_cuda and phase_stamps.is_contiguous()
     fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
@@ -400,11 +407,28 @@ def mxfp4_mega_moe_split(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
                              cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
                              force_balanced=None, token_offset=0, **_):
-    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states (the top-k
-    is selected in the fused kernel's prologue when the token count allows)."""
-    fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
-                                     token_offset=token_offset, select_in_mega=True)
+    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states. Up to 64
+    tokens this is one launch: the fused kernel computes the router logits, zero-row flags and
+    the activation cast itself (spread over all workgroups), meets at a grid-wide arrival
+    counter, then selects the top-k and runs the layer; above that, the frontend launch and the
+    fused launch."""
     # (a qoq buffer runs the QoQ layer: the reference's DG_W4A8_INT=1 route; an nvfp4 buffer the
     # W4A4 NVFP4 layer)
+    m = hidden_states.size(0)
+    if m <= SELECT_IN_MEGA_MAX_TOKENS and b.hidden % 512 == 0:
+        # one launch: the fused kernel runs the frontend (router, zero-row flags, cast) itself
+        _lib.require_gpu(hidden_states, router_weight)
+        assert hidden_states.dtype == torch.bfloat16 and router_weight.dtype == torch.bfloat16
+        assert hidden_states.size(1) == b.hidden and tuple(router_weight.shape) == (b.num_experts, b.hidden)
+        if force_balanced is None:
+            force_balanced = os.environ.get("DG_FE_FORCE_BALANCED", "0") == "1"
+        zero_row = os.environ.get("DG_FE_ZERO_ROW_UNROUTED", "1") == "1"
+        flags = (_lib.FE_FORCE_BALANCED if force_balanced else 0) | (_lib.FE_ZERO_ROW_UNROUTED if zero_row else 0)
+        assert y.size(0) == m
+        _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, fmt=b.act_format,
+               fe=(hidden_states.contiguous(), router_weight.contiguous(), flags, int(token_offset)))
+        return y
+    fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
+                                     token_offset=token_offset, select_in_mega=True)
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, fmt=b.act_format)
     return y

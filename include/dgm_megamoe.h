@@ -165,6 +165,14 @@ typedef struct DgmMoeArgs {
   const float* l1_global_scales; /* NVFP4: optional fp32 [E_local] per-expert scale of the L1 output
                                     (deep_gemm/mega/__init__.py:277 nvfp4_mega_moe); NULL = 1 */
   const float* l2_global_scales; /* NVFP4: the same for the L2 output */
+  /* In-kernel frontend (deep_gemm/mega/__init__.py:451 mxfp4_mega_moe_from_bf16 as one launch):
+   * with fe_in_mega = 1 the kernel first computes the router logits, zero-row flags and the
+   * activation cast into the buffer (the work of dgm_router_topk_launch) of hidden_states, then selects
+   * the top-k itself (select_in_mega is implied; num_tokens <= 64). fe_flags / token_offset as
+   * for dgm_router_topk_launch. */
+  int32_t fe_in_mega;
+  const void* hidden_states; /* bf16 [num_tokens, hidden] */
+  const void* router_weight; /* bf16 [num_experts, hidden] */
 } DgmMoeArgs;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
