@@ -2,9 +2,8 @@
 
 Headline workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
-layer forward from bf16 hidden states: router + top-8 + activation cast, dispatch, L1, L2,
-combine; up to 64 tokens this is one launch of the fused kernel, which runs the frontend work
-itself, above that the frontend launch and the fused launch). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
+layer forward from bf16 hidden states: the frontend launch (router + activation cast), then the
+fused kernel: top-8 in its prologue, dispatch, L1, L2, combine). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
 the QoQ W4A8 layer (int8 activations, QoQ 4-bit weights), the NVFP4 W4A4 layer at M = 16, 64,
 128 with seeded unbalanced routing (config 4), and one seeded unbalanced-routing A-MXFP8 run at
 M=16. Before every timed step >= 1 GiB is written and
@@ -149,7 +148,7 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     stream = torch.cuda.current_stream()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
 
-    one = M <= 64        # one launch: the fused kernel runs the frontend itself (from_bf16)
+    one = False          # (the one-launch layer, DG_ONE_LAUNCH, measures about the same)
 
     def layer(e=None):
         if e: e[0].record(stream)
@@ -341,8 +340,7 @@ def main():
         "dtype": "mxfp4xmxfp8" if args.act == "mxfp8" else "mxfp4xmxfp4",
         "data": "synthetic: seeded randn bf16 weights packed to MXFP4 on the GPU, forced-balanced routing",
         "config": {"workload": f"E384 layer on one GPU (BASELINE config 2), W-MXFP4 x A-{args.act.upper()}, "
-                               f"M={args.m}, forced-balanced; value = the whole layer from bf16 hidden states (one "
-                               f"launch up to 64 tokens: in-kernel frontend + fused MoE)",
+                               f"M={args.m}, forced-balanced; value = frontend + fused MoE kernel",
                    "M": args.m, "experts": E, "hidden": H, "intermediate": I, "topk": TOPK,
                    "active_experts": main_r["n_active"], "frontend_us": round(main_r["fe_us"], 2),
                    "moe_kernel_us": round(moe_us, 2), "sweep": sweep, "mall_flush_bytes": 1 << 30},

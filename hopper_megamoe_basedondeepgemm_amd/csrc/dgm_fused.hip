@@ -654,28 +654,45 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (p.fe_in) {
     constexpr int J = H / 512;
     static_assert(H % 512 == 0, "in-kernel frontend: hidden % 512");
+    // router (expert, 4-token group) pairs wave-major from the first wave of every workgroup,
+    // cast waves from the last wave down, so both run side by side on all workgroups
+    const int G = (int)gridDim.x;
     const int ngrp = (p.M + 3) / 4, npairs = p.E * ngrp;
-    for (int pi = (int)blockIdx.x * NW + wv; pi < npairs; pi += (int)gridDim.x * NW) {
+    for (int pi = wv * G + (int)blockIdx.x; pi < npairs; pi += NW * G) {
       const int e = pi % p.E, tg = pi / p.E;
       router_wave<J, true>(p.hidden, p.router_w, p.M, p.E, e, 4 * tg, lane, const_cast<float*>(p.logits),
                            const_cast<int*>(p.token_flags), e == 0);
     }
     uint8_t* xq = const_cast<uint8_t*>(p.x);
     uint8_t* xsf = const_cast<uint8_t*>(p.xsf);
-    const int64_t lane0 = (int64_t)blockIdx.x * FT + tid, nl = (int64_t)gridDim.x * FT;
+    const int cw = (NW - 1 - wv) * G + (int)blockIdx.x;          // cast wave index
     if constexpr (ACT == DGM_ACT_QOQ) {
-      for (int t = (int)blockIdx.x * NW + wv; t < p.M; t += (int)gridDim.x * NW) cast_qoq_token<J, true>(p.hidden, t, lane, xq, xsf);
+      for (int t = cw; t < p.M; t += NW * G) cast_qoq_token<J, true>(p.hidden, t, lane, xq, xsf);
     } else if constexpr (ACT == DGM_ACT_NVFP4) {
-      for (int64_t i = lane0; i < (int64_t)p.M * (H / 16) * 4; i += nl) cast_lane_nvfp4<true>(p.hidden, i, xq, xsf);
+      for (int64_t i = (int64_t)cw * 64 + lane; i < (int64_t)p.M * (H / 16) * 4; i += (int64_t)NW * G * 64)
+        cast_lane_nvfp4<true>(p.hidden, i, xq, xsf);
     } else {
-      for (int64_t i = lane0; i < (int64_t)p.M * (H / 32) * 8; i += nl) cast_lane_mx<true>(p.hidden, ACT, i, xq, xsf);
+      for (int64_t i = (int64_t)cw * 64 + lane; i < (int64_t)p.M * (H / 32) * 8; i += (int64_t)NW * G * 64)
+        cast_lane_mx<true>(p.hidden, ACT, i, xq, xsf);
     }
     wait_mem();                  // this wave's stores have completed
     __syncthreads();
-    if (tid == 0) {
-      int* gc = p.counters + CNT_GRID;
-      __hip_atomic_fetch_add(gc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      spin_until(gc, (int)gridDim.x, p.spin_limit, err);
+    if (tid == 0)
+      __hip_atomic_fetch_add(p.counters + CNT_GRID + ((int)blockIdx.x % GRID_SLOTS) * GRID_STRIDE, 1,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (wv == 0) {               // lane k < GRID_SLOTS watches slot k (bounded)
+      const int k = lane % GRID_SLOTS;
+      const int expect = ((int)gridDim.x - k + GRID_SLOTS - 1) / GRID_SLOTS;
+      const int* gc = p.counters + CNT_GRID + k * GRID_STRIDE;
+      for (int it = 0;; ++it) {
+        const int v = __hip_atomic_load(gc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__all(v >= expect)) break;
+        if (it > p.spin_limit) {
+          if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
     }
     __syncthreads();
   }
@@ -1490,7 +1507,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     for (int a = tid; a < n_active; a += FT) __hip_atomic_store(&l1_done[a], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int i = tid; i < p.M * NBL2; i += FT) __hip_atomic_store(&comb[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < 2) __hip_atomic_store(p.counters + CNT_CLAIM + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid == 2) __hip_atomic_store(p.counters + CNT_GRID, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < GRID_SLOTS)
+      __hip_atomic_store(p.counters + CNT_GRID + tid * GRID_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_mem();
     __syncthreads();
     if (tid == 0) __hip_atomic_store(exit_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

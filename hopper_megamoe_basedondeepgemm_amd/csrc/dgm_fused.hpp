@@ -12,12 +12,14 @@ constexpr int FUSED_MAX_NB64 = 64;       // hidden / 64 (hidden <= 4096); combin
 constexpr int CNT_EXIT = 0;              // workgroups finished (last one clears everything)
 constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
 constexpr int CNT_CLAIM = 2;             // next unclaimed L1 unit, then [3] next unclaimed L2 unit
-constexpr int CNT_GRID = 4;              // in-kernel frontend: workgroups past the frontend work
 constexpr int CNT_L1 = 64;               // [FUSED_MAX_LOCAL] L1 units done per active expert slot
 constexpr int CNT_TOTAL = CNT_L1 + FUSED_MAX_LOCAL + FUSED_MAX_TOKENS * FUSED_MAX_NB64;  // + combine counters
-constexpr int CNT_FE = CNT_TOTAL;        // frontend: arrival counters of 4-token chunks
-constexpr int CNT_FE_CHUNKS = 1024;
-constexpr int CNT_ALL = CNT_FE + CNT_FE_CHUNKS;
+// in-kernel frontend: workgroups past the frontend work, counted on GRID_SLOTS counters (one
+// per 64-byte line; workgroup g arrives on slot g % GRID_SLOTS), so the arrivals do not all
+// serialize on one address
+constexpr int CNT_GRID = CNT_TOTAL;
+constexpr int GRID_SLOTS = 32, GRID_STRIDE = 16;
+constexpr int CNT_ALL = CNT_GRID + 1024;
 
 inline __host__ __device__ int a256i(int x) { return (x + 255) & ~255; }
 

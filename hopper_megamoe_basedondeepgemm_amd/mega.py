@@ -406,16 +406,20 @@ def mxfp4_mega_moe_split(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
                              cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
-                             force_balanced=None, token_offset=0, **_):
-    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states. Up to 64
-    tokens this is one launch: the fused kernel computes the router logits, zero-row flags and
-    the activation cast itself (spread over all workgroups), meets at a grid-wide arrival
-    counter, then selects the top-k and runs the layer; above that, the frontend launch and the
-    fused launch."""
+                             force_balanced=None, token_offset=0, phase_stamps=None, one_launch=None, **_):
+    """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states: the
+    frontend launch, then the fused launch (the top-k selected in its prologue up to 64 tokens).
+    ``one_launch`` (env DG_ONE_LAUNCH=1; up to 64 tokens): a single launch instead, in which the
+    fused kernel computes the router logits, zero-row flags and activation cast itself (spread
+    over all workgroups) and meets at a grid-wide arrival counter before its prologue; same
+    results bit for bit, about the same time on MI355X (the frontend's load latency moves
+    into the kernel)."""
     # (a qoq buffer runs the QoQ layer: the reference's DG_W4A8_INT=1 route; an nvfp4 buffer the
     # W4A4 NVFP4 layer)
     m = hidden_states.size(0)
-    if m <= SELECT_IN_MEGA_MAX_TOKENS and b.hidden % 512 == 0:
+    if one_launch is None:
+        one_launch = os.environ.get("DG_ONE_LAUNCH", "0") == "1"
+    if one_launch and m <= SELECT_IN_MEGA_MAX_TOKENS and b.hidden % 512 == 0:
         # one launch: the fused kernel runs the frontend (router, zero-row flags, cast) itself
         _lib.require_gpu(hidden_states, router_weight)
         assert hidden_states.dtype == torch.bfloat16 and router_weight.dtype == torch.bfloat16
@@ -426,9 +430,11 @@ def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
         flags = (_lib.FE_FORCE_BALANCED if force_balanced else 0) | (_lib.FE_ZERO_ROW_UNROUTED if zero_row else 0)
         assert y.size(0) == m
         _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, fmt=b.act_format,
-               fe=(hidden_states.contiguous(), router_weight.contiguous(), flags, int(token_offset)))
+               fe=(hidden_states.contiguous(), router_weight.contiguous(), flags, int(token_offset)),
+               phase_stamps=phase_stamps)
         return y
     fable_router_quant_topk_frontend(hidden_states, router_weight, b, force_balanced=force_balanced,
                                      token_offset=token_offset, select_in_mega=True)
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, fmt=b.act_format)
+    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, fmt=b.act_format,
+           phase_stamps=phase_stamps)
     return y

@@ -1,4 +1,4 @@
-"""The one-launch layer (``mxfp4_mega_moe_from_bf16`` up to 64 tokens: router, zero-row flags and
+"""The one-launch layer (``mxfp4_mega_moe_from_bf16(one_launch=True)``, up to 64 tokens: router, zero-row flags and
 activation cast inside the fused kernel, before its top-k prologue) against the two-launch path
 (``fable_router_quant_topk_frontend`` + the fused layer) on the same inputs: logits, flags,
 activation codes and scales, routing, pool and y must agree bit for bit (same device
@@ -64,7 +64,8 @@ def test_one_launch_matches_two_launch(fmt, balanced):
     for call in range(2):
         y1 = torch.full((M, H), 7.0, dtype=torch.bfloat16, device="cuda")
         clamp = 10.0
-        dgm.mxfp4_mega_moe_from_bf16(y1, xs, rws, t1, t2, b1, activation_clamp=clamp, force_balanced=balanced)
+        dgm.mxfp4_mega_moe_from_bf16(y1, xs, rws, t1, t2, b1, activation_clamp=clamp, force_balanced=balanced,
+                                     one_launch=True)
         torch.cuda.synchronize()
         assert b1.kernel_error() == 0
         got = snapshot(b1, M)
