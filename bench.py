@@ -195,17 +195,17 @@ def copy_calibration(torch, mib, reps=3):
     torch.cuda.synchronize()
 
 
-def cpu_baseline(packed, M=8, sample_routes=16, reps=5, seed=7):
+def cpu_baseline(packed, M=8, sample_routes=None, reps=10, seed=7):
     """The oracle (numpy fp32 restatement) on the host cores: router + top-8 + cast for the
-    M tokens, then `sample_routes` of the 8*M expert routes (forced-balanced: one route per
-    active expert), weights dequantised once before timing (as the reference's CPU path does).
-    The route time is scaled to one layer (8*M routes). Returns (us per layer, BLAS threads)."""
+    M tokens, then `sample_routes` (default: all) of the 8*M expert routes (forced-balanced: one
+    route per active expert), weights dequantised once before timing (as the reference's CPU path
+    does). The route time is scaled to one layer (8*M routes). Returns (us per layer, BLAS threads)."""
     from oracle import moe, numerics as nu
     rng = np.random.default_rng(seed)
     x = nu.round_bf16(rng.standard_normal((M, H)).astype(np.float32))
     rw = nu.round_bf16(rng.standard_normal((E, H)).astype(np.float32) * np.float32(0.02))
     idx, w = moe.balanced_routing(M, E, TOPK)
-    routes = [(t, s) for t in range(M) for s in range(TOPK)][:sample_routes]
+    routes = [(t, s) for t in range(M) for s in range(TOPK)][:sample_routes or M * TOPK]
     used = sorted({int(idx[t, s]) for t, s in routes})
     p1, s1, p2, s2 = [np.stack([t[e].cpu().numpy() for e in used]) for t in packed]
     W1 = moe.LazyDequant(p1, s1)
@@ -324,9 +324,9 @@ def main():
             t0 = time.perf_counter()
             us, threads = cpu_baseline(packed, M=args.m)
             cpu = dict(value=round(us, 1), unit="us/layer", cores=threads, kind="port",
-                       sample=f"oracle (numpy fp32) router+top8+cast for M={args.m}, then 16 of the {8 * args.m} "
-                              f"expert routes (weights pre-dequantised), median of 5, route time scaled to "
-                              f"{8 * args.m} routes; A-MXFP8; {time.perf_counter() - t0:.1f} s of host time")
+                       sample=f"oracle (numpy fp32): the whole M={args.m} layer (router + top-8 + cast, then "
+                              f"all {8 * args.m} expert routes with weights dequantised beforehand), median of 10; "
+                              f"A-MXFP8; {time.perf_counter() - t0:.1f} s of host time incl. the dequantisation")
             log(f"cpu baseline: {cpu}")
         except Exception as ex:  # reported, never fatal
             cpu = dict(value=None, unit="us/layer", cores=None, kind="port", sample=f"failed: {ex}")

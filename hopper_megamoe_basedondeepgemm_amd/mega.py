@@ -205,7 +205,15 @@ def transform_nvfp4_weights_for_mega_moe_fused(l1, l2, src_order="marlin"):
 
 
 def transform_weights_for_mega_moe(l1, l2):
-    """sm100_b200 style inputs (low-nibble-first packing from per_token_cast_to_fp4)."""
+    """sm100_b200/mega___init__.py:102 for its W4A4 layer: low-nibble-first packed weights
+    (per_token_cast_to_fp4 style) with one scale byte per 32 K (UE8M0: MXFP4 layout) or per 16 K
+    (E4M3: NVFP4 layout); the scale count per row picks the format."""
+    packed, sf = l1
+    per_row = sf.shape[-1] * sf.element_size()
+    k = 2 * packed.shape[-1]
+    if per_row == k // 16:
+        return transform_nvfp4_weights_for_mega_moe_fused(l1, l2, src_order="low_first")
+    assert per_row == k // 32, f"scales per row {per_row} fit neither K/32 nor K/16 (K={k})"
     return transform_mxfp4_weights_for_mega_moe_fused(l1, l2, src_order="low_first")
 
 

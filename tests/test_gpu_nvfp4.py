@@ -125,6 +125,23 @@ def test_transform_nvfp4_invariant():
     from oracle import numerics as nu
     d3 = pk.dequant_fp4_rows(p3, nu.e4m3_decode(sb3), 16)
     np.testing.assert_array_equal(decode_native_nvfp4(v3.cpu().numpy(), s3.cpu().numpy()), d3)
+    # the sm100 name picks the format from the scale count per row (K/16: NVFP4, K/32: MXFP4)
+    p1, _, sb1 = pk.cast_to_nvfp4_rows(w1)
+    lf1 = (torch.from_numpy(p1).cuda(), torch.from_numpy(sb1).cuda())
+    lf2 = (torch.from_numpy(p3).cuda(), torch.from_numpy(sb3).cuda())
+    got = dgm.transform_weights_for_mega_moe(lf1, lf2)
+    want = dgm.transform_nvfp4_weights_for_mega_moe_fused(lf1, lf2, src_order="low_first")
+    for g, w in zip(got, want):
+        for a, b in zip(g, w):
+            assert torch.equal(a, b)
+    m1 = pk.cast_to_fp4_rows(w1)
+    m2 = pk.cast_to_fp4_rows(w2)
+    mx1 = (torch.from_numpy(m1[0]).cuda(), torch.from_numpy(m1[2]).cuda())
+    mx2 = (torch.from_numpy(m2[0]).cuda(), torch.from_numpy(m2[2]).cuda())
+    got = dgm.transform_weights_for_mega_moe(mx1, mx2)
+    want = dgm.transform_mxfp4_weights_for_mega_moe_fused(mx1, mx2, src_order="low_first")
+    for g, w in zip(got, want):
+        assert torch.equal(g[0], w[0]) and torch.equal(g[1], w[1])
 
 
 def test_nvfp4_small_layer():
