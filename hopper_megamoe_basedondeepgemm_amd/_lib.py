@@ -24,7 +24,8 @@ EXPORTS = [
     "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_probe_mfma_scale",
     "dgm_probe_mfma_scale_sel",
     "dgm_probe_mfma_i8", "dgm_probe_mfma_f16", "dgm_probe_cvt_fp4",
-    "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights",
+    "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
+    "dgm_transform_qoq_int4_weights",
 ]
 
 
@@ -75,6 +76,8 @@ def load():
         "dgm_cast_fp8_rows": ([vp, i64, i64, vp, vp, vp], i32),
         "dgm_quantize_nvfp4": ([vp, i64, i64, vp, vp, vp], i32),
         "dgm_quantize_qoq": ([vp, i64, i64, vp, vp, vp, vp, vp], i32),
+        "dgm_quantize_qoq_int4": ([vp, i64, i64, vp, vp, vp], i32),
+        "dgm_transform_qoq_int4_weights": ([vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
         "dgm_cast_int8_rows": ([vp, i64, i64, vp, vp, vp], i32),
         "dgm_transform_fp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_fused_buffer_layout": ([i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(BufferLayout)], i32),

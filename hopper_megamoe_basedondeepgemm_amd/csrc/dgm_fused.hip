@@ -707,11 +707,31 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const int TC = (int)(sizeof(s.bst) / 4) / p.E;
     for (int t0 = 0; t0 < p.M; t0 += TC) {
       const int tn = p.M - t0 < TC ? p.M - t0 : TC;
-      // (agent-scope loads: the in-kernel frontend may have written them in this launch)
-      for (int i = tid; i < tn * p.E; i += FT) lg[i] = ld_agent_f32(p.logits + (size_t)t0 * p.E + i);
-      if (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED)
-        for (int i = tid; i < tn; i += FT)
-          s.tflag[t0 + i] = __hip_atomic_load(p.token_flags + t0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // Rounds of SB values per thread, all loaded before any is written, so that a round costs
+      // one memory round trip (a load-store loop would pay one per value). The in-kernel
+      // frontend's values (written in this launch) need agent-scope loads; the frontend
+      // kernel's are read through the cache.
+      const float* src = p.logits + (size_t)t0 * p.E;
+      const int nv = tn * p.E;
+      const int* tfs = p.token_flags + t0 + (tid < tn ? tid : 0);
+      constexpr int SB = 8;
+      for (int i0 = 0; i0 < nv; i0 += SB * FT) {
+        float v[SB];
+        int fl;
+        if (p.fe_in) {
+#pragma unroll
+          for (int j = 0; j < SB; ++j) v[j] = ld_agent_f32(src + min(i0 + j * FT + tid, nv - 1));
+          fl = __hip_atomic_load(tfs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+#pragma unroll
+          for (int j = 0; j < SB; ++j) v[j] = src[min(i0 + j * FT + tid, nv - 1)];
+          fl = *tfs;
+        }
+#pragma unroll
+        for (int j = 0; j < SB; ++j)
+          if (i0 + j * FT + tid < nv) lg[i0 + j * FT + tid] = v[j];
+        if (i0 == 0 && tid < tn) s.tflag[t0 + tid] = fl;
+      }
       __syncthreads();
       for (int tt = wv; tt < tn; tt += NW) {
         const int t = t0 + tt;
@@ -785,7 +805,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     if (tid == 0) { meta[0] = n_active; meta[1] = s.meta[1]; }
     for (int e = tid; e < p.E_local; e += FT) {
       gcnt[e] = s.cnt[e];
-      if (p.recv_stats) p.recv_stats[e] += s.cnt[e];
+      if (p.recv_stats && (p.phases & 1)) p.recv_stats[e] += s.cnt[e];
     }
     for (int a = tid; a <= n_active; a += FT) {
       goff[a] = s.aoff[a];
@@ -821,7 +841,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // intermediate stores have completed when the next item's K loop is done (memory ops
   // complete in order and that loop waited for younger tiles); the unit's arrival is
   // signalled then.
-  {
+  if (p.phases & 1) {
     constexpr int KR = KT1 % 12 == 0 ? 12 : KT1;   // ring depth: tiles in flight per wave
     static_assert(KT1 % KR == 0, "the ring depth divides the K-tile count");
     const int pp = wv & 3, gu = wv >> 2;
@@ -1161,7 +1181,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // arrival is already complete, else staged at the item's start after a bounded wait. Route
   // outputs (fp32) go to `partials`; one item later, when they have completed, each route
   // bumps the arrival counters of its (token, 128-row block)s (no return value).
-  {
+  if (p.phases & 2) {
     static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
     int* claim = p.counters + CNT_CLAIM + 1;
     const uint8_t* w2v = p.w2v;
@@ -1251,7 +1271,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
         if (a != ready) {
-          if (tid == 0) spin_until(&l1_done[a], QN1, p.spin_limit, err);
+          if (tid == 0 && (p.phases & 1)) spin_until(&l1_done[a], QN1, p.spin_limit, err);
           ready = a;
         }
         __syncthreads();
@@ -1279,7 +1299,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       bool pf = false;
       if (has_next && nkey != key) {
         if (tid == 0)
-          s.claimv[1] = na == ready || __hip_atomic_load(&l1_done[na], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
+          s.claimv[1] = !(p.phases & 1) || na == ready ||
+                        __hip_atomic_load(&l1_done[na], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
         __syncthreads();
         pf = __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0;
         if (pf) {
@@ -1469,7 +1490,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // (token t, 128-row block b) pairs, PG consecutive pairs per pass and workgroup: wait until
   // every local route of t has delivered block b, then sum the routes in slot order (fp32)
   // -> bf16 y. The waits are only on L2 items, which never wait on this phase.
-  {
+  if (p.phases & 2) {
     constexpr int CB = 16 * NW, PG = FT / CB;
     const int P = p.M * NBL2;
     for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {

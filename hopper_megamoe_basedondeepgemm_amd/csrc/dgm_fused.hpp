@@ -55,6 +55,10 @@ struct FusedParams {
   float clamp;
   int fast_math;
   int spin_limit;
+  // Phases run by this launch: bit 0 dispatch + L1 (intermediate rows to `mid`, recv stats),
+  // bit 1 L2 + combine. 3 = the whole layer; 1 then 2 = the split API's two launches (the
+  // second reads the top-k written by the first and does not wait for L1 arrivals).
+  int phases;
 };
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream);

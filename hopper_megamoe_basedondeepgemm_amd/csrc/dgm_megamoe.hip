@@ -456,6 +456,9 @@ void dgm_set_error(const char* msg) {
   g_err[sizeof(g_err) - 1] = 0;
 }
 
+static bool fused_fits(const DgmMoeArgs* A);
+static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stream);
+
 extern "C" {
 
 int dgm_version(void) { return 1; }
@@ -570,8 +573,6 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 32 == 0, "shape");
   DGM_CHECK_ARG(A->intermediate % 128 == 0, "intermediate % 128 == 0");
   if (A->num_tokens == 0) return 0;
-  uint8_t* buf = (uint8_t*)A->buffer;
-  const int routes_n = A->num_tokens * A->topk;
   if (A->fe_in_mega) {
     DGM_CHECK_ARG(A->hidden_states && A->router_weight, "fe_in_mega: null hidden_states / router_weight");
     DGM_CHECK_ARG(((uintptr_t)A->hidden_states & 15) == 0 && ((uintptr_t)A->router_weight & 15) == 0, "16-byte alignment");
@@ -581,10 +582,29 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     DGM_CHECK_ARG(!(A->fe_flags & DGM_FE_FORCE_BALANCED) || A->num_experts % A->topk == 0,
                   "forced-balanced needs E % topk == 0");
   }
-  if (routes_n <= FUSED_MAX_ROUTES && A->num_local_experts <= FUSED_MAX_LOCAL &&
-      A->num_tokens <= FUSED_MAX_TOKENS && A->hidden / 64 <= FUSED_MAX_NB64) {
-    const bool sel = (A->select_in_mega || A->fe_in_mega) && A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS;
-    if (A->select_in_mega && !sel) {
+  if (fused_fits(A)) return fused_launch_phases(A, 3, stream);
+  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
+                "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+  DGM_CHECK_ARG(!A->fe_in_mega, "fe_in_mega: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+  return dgm_megamoe_split_launch(A, stream);
+}
+
+}  // extern "C"
+
+// The persistent kernel's limits (route, token, expert and combine-block counts of its LDS tables)
+static bool fused_fits(const DgmMoeArgs* A) {
+  return A->num_tokens * A->topk <= FUSED_MAX_ROUTES && A->num_local_experts <= FUSED_MAX_LOCAL &&
+         A->num_tokens <= FUSED_MAX_TOKENS && A->hidden / 64 <= FUSED_MAX_NB64;
+}
+
+// One launch of the persistent kernel running `phases` (FusedParams::phases) of the layer.
+static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stream) {
+  const DgmBufferLayout* L = A->layout;
+  uint8_t* buf = (uint8_t*)A->buffer;
+  {
+    const bool sel = (A->select_in_mega || A->fe_in_mega) && A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS &&
+                     (phases & 1);
+    if (A->select_in_mega && !sel && (phases & 1)) {
       int st = materialize_topk(A, buf, L, stream);
       if (st) return st;
     }
@@ -626,18 +646,34 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     p.spin_limit = 1 << 22;
     p.stamps = (long long*)A->phase_stamps;
     p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;
+    p.phases = phases;
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
-  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
-                "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
-  DGM_CHECK_ARG(!A->fe_in_mega, "fe_in_mega: the fused kernel's limits (tokens, routes, local experts) are exceeded");
-  return dgm_megamoe_split_launch(A, stream);
 }
+
+extern "C" {
 
 int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
-  DGM_CHECK_ARG(A->act_format == DGM_ACT_MXFP4 || A->act_format == DGM_ACT_MXFP8,
-                "split path: act_format must be MXFP4 or MXFP8 (the QoQ and NVFP4 layers are fused only)");
+  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4, "act_format");
+  DGM_CHECK_ARG(!A->fe_in_mega, "split path: fe_in_mega is a fused-launch option");
+  if (A->act_format == DGM_ACT_QOQ || A->act_format == DGM_ACT_NVFP4) {
+    // two launches of the persistent kernel: dispatch + L1, then L2 + combine
+    DGM_CHECK_ARG(A->w1_values && A->w1_scales && A->w2_values && A->w2_scales, "null weights");
+    DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ || (A->w1_row_scales && A->w2_row_scales),
+                  "QoQ needs the row scales s1 of both matrices");
+    DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= A->layout->max_routes,
+                  "num_tokens exceeds the buffer");
+    DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
+    DGM_CHECK_ARG(A->num_local_experts > 0 && A->expert_begin >= 0 &&
+                  A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
+    DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 128 == 0, "shape");
+    if (A->num_tokens == 0) return 0;
+    DGM_CHECK_ARG(fused_fits(A), "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+    int st = fused_launch_phases(A, 1, stream);
+    if (st) return st;
+    return fused_launch_phases(A, 2, stream);
+  }
   const DgmBufferLayout* L = A->layout;
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   if (A->num_tokens == 0) return 0;

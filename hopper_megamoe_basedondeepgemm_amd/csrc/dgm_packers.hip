@@ -193,9 +193,11 @@ __global__ void k_quantize_nvfp4(const uint16_t* __restrict__ w, int64_t groups1
 
 // ------------------------------------------------------------------ QoQ W4A8 packer
 // One wave per weight row: row amax -> s1 (bf16), then lane-per-K128-group codes.
+// plane != null: the split path's int4 form (s2 clamped to 127 instead of 15, which |w8| <= 112
+// never reaches; s2 | z << 8 | bf16(s1) << 16 per (row, K128 group) instead of s2o / zo / s1o)
 __global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int K,
                                uint8_t* __restrict__ packed, uint8_t* __restrict__ s2o,
-                               uint8_t* __restrict__ zo, float* __restrict__ s1o) {
+                               uint8_t* __restrict__ zo, float* __restrict__ s1o, uint32_t* __restrict__ plane) {
   int lane = threadIdx.x & 63;
   int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -205,7 +207,7 @@ __global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
   float s1 = round_bf16(fmaxf(amax / 120.0f, 1e-30f));
-  if (lane == 0) s1o[row] = s1;
+  if (lane == 0 && !plane) s1o[row] = s1;
   int G = K / 128;
   for (int g = lane; g < G; g += 64) {
     const uint16_t* p = src + g * 128;
@@ -215,7 +217,7 @@ __global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int
       mn = fminf(mn, w8);
       mx = fmaxf(mx, w8);
     }
-    float s2 = fminf(fmaxf(ceilf((mx - mn) / 15.0f), 1.f), 15.f);
+    float s2 = fminf(fmaxf(ceilf((mx - mn) / 15.0f), 1.f), plane ? 127.f : 15.f);
     float z = fminf(fmaxf(rintf(-mn / s2), 0.f), 15.f);
     uint32_t* dst = reinterpret_cast<uint32_t*>(packed + row * (K / 2) + g * 64);
     for (int c8 = 0; c8 < 16; ++c8) {
@@ -226,8 +228,12 @@ __global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int
       }
       dst[c8] = marlin8(n);
     }
-    s2o[row * G + g] = (uint8_t)s2;
-    zo[row * G + g] = (uint8_t)z;
+    if (plane) {
+      plane[row * G + g] = (__float_as_uint(s1) & 0xFFFF0000u) | ((uint32_t)z << 8) | (uint32_t)s2;
+    } else {
+      s2o[row * G + g] = (uint8_t)s2;
+      zo[row * G + g] = (uint8_t)z;
+    }
   }
 }
 
@@ -358,8 +364,11 @@ __global__ void k_transform_nvfp4(const uint8_t* __restrict__ src, const uint8_t
 // [16 B]: byte r = z | s2 << 4 of row r (both are 4-bit by construction: z 0..15, s2 1..15),
 // so dword kq holds the four rows 4 kq .. +3 that lane group kq accumulates. s1 [E][N] in the
 // same row order. l1_interleave as for the MXFP4 transform.
+// plane != null: s2, z and s1 come from the int4 packer's coefficient plane (bytes 0, 1 and the
+// bf16 high half of each (row, K128 group) word) instead of s2 / z / s1
 __global__ void k_transform_qoq(const uint8_t* __restrict__ src, const uint8_t* __restrict__ s2,
-                                const uint8_t* __restrict__ z, const float* __restrict__ s1, int E, int N,
+                                const uint8_t* __restrict__ z, const float* __restrict__ s1,
+                                const uint32_t* __restrict__ plane, int E, int N,
                                 int K, int l1_interleave, uint8_t* __restrict__ dst, uint8_t* __restrict__ mdst,
                                 float* __restrict__ s1dst) {
   int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -411,8 +420,10 @@ __global__ void k_transform_qoq(const uint8_t* __restrict__ src, const uint8_t* 
   *reinterpret_cast<U4*>(dst + tile * 1024 + lane * 16) = U4{o[0], o[1], o[2], o[3]};
   if (g == 0) {
     const int64_t mi = ((int64_t)e * N + src_row) * KT + kt;
-    mdst[tile * 16 + r] = (uint8_t)((z[mi] & 15u) | (s2[mi] << 4));
-    if (kt == 0) s1dst[((int64_t)e * NB + q) * 16 + r] = s1[(int64_t)e * N + src_row];
+    const uint32_t zv = plane ? (plane[mi] >> 8) & 0xffu : z[mi], sv = plane ? plane[mi] & 0xffu : s2[mi];
+    mdst[tile * 16 + r] = (uint8_t)((zv & 15u) | (sv << 4));
+    if (kt == 0)
+      s1dst[((int64_t)e * NB + q) * 16 + r] = plane ? __uint_as_float(plane[mi] & 0xFFFF0000u) : s1[(int64_t)e * N + src_row];
   }
 }
 
@@ -494,7 +505,18 @@ int dgm_quantize_qoq(const void* w_bf16, int64_t rows, int64_t K, void* packed, 
   if (rows == 0) return 0;
   hipLaunchKernelGGL(k_quantize_qoq, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
                      (const uint16_t*)w_bf16, rows, (int)K, (uint8_t*)packed, (uint8_t*)s2,
-                     (uint8_t*)z, (float*)s1_f32);
+                     (uint8_t*)z, (float*)s1_f32, (uint32_t*)nullptr);
+  return dgm_last_launch_status();
+}
+
+int dgm_quantize_qoq_int4(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* plane_i32,
+                          hipStream_t stream) {
+  DGM_CHECK_ARG(w_bf16 && packed && plane_i32, "null pointer");
+  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 128 == 0, "K must be a positive multiple of 128");
+  if (rows == 0) return 0;
+  hipLaunchKernelGGL(k_quantize_qoq, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
+                     (const uint16_t*)w_bf16, rows, (int)K, (uint8_t*)packed, (uint8_t*)nullptr,
+                     (uint8_t*)nullptr, (float*)nullptr, (uint32_t*)plane_i32);
   return dgm_last_launch_status();
 }
 
@@ -551,8 +573,21 @@ int dgm_transform_qoq_weights(const void* packed, const void* s2, const void* z,
   DGM_CHECK_ARG(!l1_interleave || N % 32 == 0, "l1_interleave needs N % 32 == 0");
   const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
   hipLaunchKernelGGL(k_transform_qoq, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)packed,
-                     (const uint8_t*)s2, (const uint8_t*)z, (const float*)s1, E, N, K, l1_interleave,
-                     (uint8_t*)dst_values, (uint8_t*)dst_meta, (float*)dst_s1);
+                     (const uint8_t*)s2, (const uint8_t*)z, (const float*)s1, (const uint32_t*)nullptr, E, N, K,
+                     l1_interleave, (uint8_t*)dst_values, (uint8_t*)dst_meta, (float*)dst_s1);
+  return dgm_last_launch_status();
+}
+
+int dgm_transform_qoq_int4_weights(const void* packed, const void* plane_i32, int E, int N, int K, int l1_interleave,
+                                   void* dst_values, void* dst_meta, void* dst_s1, hipStream_t stream) {
+  DGM_CHECK_ARG(packed && plane_i32 && dst_values && dst_meta && dst_s1, "null pointer");
+  DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "E, N, K (N % 16, K % 128)");
+  DGM_CHECK_ARG(!l1_interleave || N % 32 == 0, "l1_interleave needs N % 32 == 0");
+  const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
+  hipLaunchKernelGGL(k_transform_qoq, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)packed,
+                     (const uint8_t*)nullptr, (const uint8_t*)nullptr, (const float*)nullptr,
+                     (const uint32_t*)plane_i32, E, N, K, l1_interleave, (uint8_t*)dst_values, (uint8_t*)dst_meta,
+                     (float*)dst_s1);
   return dgm_last_launch_status();
 }
 

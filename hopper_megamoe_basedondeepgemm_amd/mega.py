@@ -204,6 +204,34 @@ def transform_nvfp4_weights_for_mega_moe_fused(l1, l2, src_order="marlin"):
     return _transform_nvfp4_one(*l1, True, src_order), _transform_nvfp4_one(*l2, False, src_order)
 
 
+def _transform_qoq_int4_one(q, l1_interleave):
+    packed, plane = q
+    _lib.require_gpu(packed, plane)
+    assert packed.dtype == torch.uint8 and plane.dtype == torch.int32 and packed.dim() == 3
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert tuple(plane.shape) == (E, N, K // 128) and N % 16 == 0 and K % 128 == 0, (plane.shape, packed.shape)
+    # the fused layout keeps z and s2 as one nibble each (quantize_to_qoq_int4: z <= 15, s2 <= 15)
+    pl = plane.contiguous()
+    if int(torch.maximum(pl & 0xFF, (pl >> 8) & 0xFF).max().item()) > 15:
+        raise ValueError("QoQ plane out of range: z and s2 must be < 16")
+    vals = torch.empty((E, N // 16, K // 128, 64, 16), dtype=torch.uint8, device=packed.device)
+    meta = torch.empty((E, N // 16, K // 128, 16), dtype=torch.uint8, device=packed.device)
+    rs = torch.empty((E, N), dtype=torch.float32, device=packed.device)
+    _lib.check(_lib.load().dgm_transform_qoq_int4_weights(
+        _lib.ptr(packed.contiguous()), _lib.ptr(pl), E, N, K, int(l1_interleave), _lib.ptr(vals), _lib.ptr(meta),
+        _lib.ptr(rs), _lib.stream()))
+    return vals, meta, rs
+
+
+def transform_qoq_int4_weights_for_mega_moe_sm90(l1_weights, l2_weights, block_n: int = 128):
+    """deep_gemm/mega/__init__.py:308: ``quantize_to_qoq_int4`` pairs ``(packed [E, N, K/2],
+    plane int32 [E, N, K/128])`` -> the same layout as ``transform_qoq_weights_for_mega_moe_fused``
+    (values, meta, s1) per matrix. ``block_n`` picks an SM90 tile there and has no effect here."""
+    assert block_n in (128, 256)
+    return _transform_qoq_int4_one(l1_weights, True), _transform_qoq_int4_one(l2_weights, False)
+
+
 def transform_weights_for_mega_moe(l1, l2):
     """sm100_b200/mega___init__.py:102 for its W4A4 layer: low-nibble-first packed weights
     (per_token_cast_to_fp4 style) with one scale byte per 32 K (UE8M0: MXFP4 layout) or per 16 K
@@ -390,14 +418,48 @@ def nvfp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_exper
         raise ValueError("kernel_family must be one of 'auto', 'fused', or 'split'")
     if family_threshold <= 0:
         raise ValueError("family_threshold must be positive")
+    # 'split' (or 'auto' above family_threshold tokens): two launches, dispatch + L1 then L2 +
+    # combine, with the fused launch's results bit for bit
+    split = kernel_family == "split" or (kernel_family == "auto" and y.size(0) > family_threshold)
     _fused(y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats, activation_clamp,
-           fast_math=fast_math, fmt="nvfp4", global_scales=(l1_global_scales, l2_global_scales))
+           split=split, fast_math=fast_math, fmt="nvfp4", global_scales=(l1_global_scales, l2_global_scales))
 
 
-def qoq_mega_moe_split(*_, **__):
-    """deep_gemm/mega/__init__.py:584 (the sm90 legacy buffer and QoQ int4 layout). Not provided:
-    the QoQ layer runs as the fused kernel only (``qoq_mega_moe_fused``)."""
-    raise NotImplementedError("qoq_mega_moe_split: use qoq_mega_moe_fused on a qoq buffer")
+def _split_entry(fmts, y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats=None,
+                 l1_global_scales=None, l2_global_scales=None, recipe=None, activation="swiglu",
+                 activation_clamp=None, fast_math=True, attn_tp_size=1, attn_tp_group=None,
+                 broadcast_output=False, router_input=None, router_weight=None, router_logits=None,
+                 router_renormalize=True, tp_combine_output=None, hidden_input=None):
+    """The split API's argument list (deep_gemm/mega/__init__.py:340-433 mxfp4_mega_moe) on a
+    buffer of ``get_fused_symm_buffer_for_mega_moe``. ``router_input`` / ``router_weight``: the
+    frontend (router, top-k, activation cast) runs first on those. One GPU: attn_tp_size must be
+    1; ``router_logits``, ``tp_combine_output`` and ``hidden_input`` (the multi-rank and
+    attention-TP paths) are not provided."""
+    b = sym_buffer
+    if b.act_format not in fmts:
+        raise ValueError(f"buffer was sized for {b.act_format!r}; this entry point takes {fmts}")
+    assert activation == "swiglu", activation
+    assert (router_input is None) == (router_weight is None)
+    if attn_tp_size != 1 or tp_combine_output is not None or broadcast_output:
+        raise NotImplementedError("attention-TP layouts need more than one GPU")
+    if router_logits is not None or hidden_input is not None:
+        raise NotImplementedError("router_logits / hidden_input: run fable_router_quant_topk_frontend first")
+    if b.act_format != "nvfp4" and (l1_global_scales is not None or l2_global_scales is not None):
+        raise ValueError("per-expert global scales are an NVFP4 option")
+    if router_input is not None:
+        assert router_input.shape == (y.size(0), b.hidden)
+        fable_router_quant_topk_frontend(router_input, router_weight, b)
+    _fused(y, l1_weights, l2_weights, b, cumulative_local_expert_recv_stats, activation_clamp, split=True,
+           fast_math=fast_math, fmt=b.act_format, global_scales=(l1_global_scales, l2_global_scales))
+
+
+def qoq_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs):
+    """deep_gemm/mega/__init__.py:584: the QoQ W4A8 layer as two launches of the persistent
+    kernel (dispatch + L1 into the buffer's intermediate rows, then L2 + combine), on an
+    ``act_format="qoq"`` buffer; weights from ``transform_qoq_weights_for_mega_moe_fused`` or
+    ``transform_qoq_int4_weights_for_mega_moe_sm90``. Same results as ``qoq_mega_moe_fused``
+    bit for bit. Arguments as ``mxfp4_mega_moe`` (activation_clamp default None = no clamp)."""
+    _split_entry(("qoq",), y, l1_weights, l2_weights, sym_buffer, *args, **kwargs)
 
 
 def fused_workgroups(b):

@@ -101,6 +101,19 @@ int dgm_transform_qoq_weights(const void* packed, const void* s2, const void* z,
                               int K, int l1_interleave, void* dst_values, void* dst_meta, void* dst_s1,
                               hipStream_t stream);
 
+/* Replaces deep_gemm/quantization_mxfp4.py:323 quantize_to_qoq_int4 (the split path's QoQ packer):
+ * bf16 [rows, K] -> Marlin-packed codes [rows, K/2] and an int32 plane [rows, K/128] holding
+ * s2 | z << 8 | bf16(s1) << 16 per (row, K128 group). The codes, s2, z and s1 equal
+ * dgm_quantize_qoq's. */
+int dgm_quantize_qoq_int4(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* plane_i32,
+                          hipStream_t stream);
+
+/* Replaces deep_gemm/mega/__init__.py:308 transform_qoq_int4_weights_for_mega_moe_sm90 (one matrix
+ * per call): dgm_transform_qoq_weights with s2, z and s1 read from the int4 packer's plane
+ * (z and s2 must be < 16). */
+int dgm_transform_qoq_int4_weights(const void* packed, const void* plane_i32, int E, int N, int K, int l1_interleave,
+                                   void* dst_values, void* dst_meta, void* dst_s1, hipStream_t stream);
+
 /* ------------------------------------------------------------------ fused buffer
  * Replaces csrc/apis/mega_fused.hpp:31-76 get_symm_buffer_size_for_fused_mega_moe:
  * byte offsets of every view inside one device buffer (single GPU, no symmetric memory). */
@@ -178,8 +191,10 @@ typedef struct DgmMoeArgs {
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
 
 /* Replaces csrc/apis/mega.hpp:550 _C.mxfp4_mega_moe_split / deep_gemm/mega/__init__.py:579
- * mxfp4_mega_moe_split: the same layer as separate launches (dispatch, L1, L2, combine)
- * instead of one persistent kernel; identical numerics. */
+ * mxfp4_mega_moe_split and :584 qoq_mega_moe_split: the same layer as separate launches instead
+ * of one persistent kernel, identical numerics. MXFP4 / MXFP8: dispatch, L1, L2, combine
+ * kernels; QoQ / NVFP4: the persistent kernel twice, dispatch + L1 then L2 + combine (the
+ * fused kernel's limits on tokens, routes and local experts apply). fe_in_mega is rejected. */
 int dgm_megamoe_split_launch(const DgmMoeArgs* args, hipStream_t stream);
 
 /* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the

@@ -221,6 +221,50 @@ def dequantize_qoq(packed, s2, z, s1):
     return (wv.reshape(E, N, K) * as_f32(s1)[..., None]).astype(np.float32)
 
 
+def quantize_to_qoq_int4(w):
+    """``quantize_to_qoq_int4`` (deep_gemm/quantization_mxfp4.py:323-353), the split path's QoQ
+    packer: the same s1 / w8 / z / code chain as quantize_to_qoq except s2 = clamp(ceil((mx-mn)/15),
+    1, 127); Marlin-packed codes and an int32 plane per (row, K128 group) with bytes
+    [s2, z, s1 as bf16 (high half)]. Returns (packed [E,N,K/2], plane int32 [E,N,K/128])."""
+    w = as_f32(w)
+    E, N, K = w.shape
+    s1 = round_bf16(np.maximum(np.abs(w).max(axis=-1, keepdims=True) / np.float32(120.0), np.float32(1e-30)))
+    w8 = np.clip(np.rint(w / s1), -112, 112).astype(np.float32)
+    g = w8.reshape(E, N, K // 128, 128)
+    mn = g.min(axis=-1, keepdims=True)
+    mx = g.max(axis=-1, keepdims=True)
+    s2 = np.clip(np.ceil((mx - mn) / np.float32(15.0)), 1, 127).astype(np.float32)
+    z = np.clip(np.rint(-mn / s2), 0, 15).astype(np.float32)
+    code = np.clip(np.rint((g / s2 + z).astype(np.float32)), 0, 15).reshape(E, N, K)
+    s1w = (s1.astype(np.float32).view(np.uint32) & np.uint32(0xFFFF0000)).astype(np.uint32)
+    plane = (np.broadcast_to(s1w, (E, N, K // 128)) | (z[..., 0].astype(np.uint32) << 8)
+             | s2[..., 0].astype(np.uint32)).view(np.int32)
+    return pack_marlin(code.astype(np.uint8)), np.ascontiguousarray(plane)
+
+
+def dequantize_qoq_int4(packed, plane):
+    """``dequantize_qoq_int4`` (deep_gemm/quantization_mxfp4.py:365-383):
+    (code - z) * s2 * s1 with s2 = byte 0, z = byte 1, s1 = the plane's high half as fp32."""
+    codes = unpack_marlin(packed).astype(np.float32)
+    E, N, K = codes.shape
+    u = np.ascontiguousarray(plane).view(np.uint32)
+    s2 = (u & 0xFF).astype(np.float32)
+    z = ((u >> 8) & 0xFF).astype(np.float32)
+    s1 = (u & np.uint32(0xFFFF0000)).view(np.float32)
+    c = codes.reshape(E, N, K // 128, 128)
+    return ((c - z[..., None]) * s2[..., None] * s1[..., None]).reshape(E, N, K).astype(np.float32)
+
+
+def qoq_int4_to_fused(packed, plane):
+    """The int4 packer's output in quantize_to_qoq's form (packed, s2, z, s1): the same codes;
+    s2, z and the row's s1 read back from the plane (s1 is the same in every group of a row)."""
+    u = np.ascontiguousarray(plane).view(np.uint32)
+    s2 = (u & 0xFF).astype(np.uint8)
+    z = ((u >> 8) & 0xFF).astype(np.uint8)
+    s1 = (u[..., 0] & np.uint32(0xFFFF0000)).view(np.float32)
+    return packed, s2, z, s1
+
+
 def qoq_int_codes(packed, s2, z):
     """Integer weight (code - z) * s2 per element (exact, |.| <= 225)."""
     codes = unpack_marlin(packed).astype(np.int64)

@@ -1,7 +1,7 @@
 """Write the golden vectors under tests/golden/ from the reference's own Python packers.
 
 Run in the build container only (the reference tree is not present on GPU boxes):
-    python tests/golden/make_golden.py /root/reference
+    python tests/golden/make_golden.py /root/reference [fixture names to rewrite]
 
 What it does: loads the reference's torch-only packer files by path (no package __init__,
 no extension module), feeds them seeded inputs built here (bf16-representable values plus
@@ -62,7 +62,7 @@ def weight_inputs(rng, E, N, K, scale):
     return w
 
 
-def main(ref_root):
+def main(ref_root, only=()):
     mods = load_ref(ref_root)
     rng = np.random.default_rng(20261201)
     out = {}
@@ -93,6 +93,11 @@ def main(ref_root):
     wq = weight_inputs(rng, 2, 16, 256, 0.05)
     pq, s2, z, s1 = mods["quantization_qoq_fused"].quantize_to_qoq(torch.from_numpy(wq).to(torch.bfloat16))
     out["qoq"] = dict(w=wq, packed=pq.numpy(), s2=s2.numpy(), z=z.numpy(), s1=s1.numpy())
+    # the split path's QoQ int4 packer (int32 coefficient plane) on the same weights, and its
+    # reference dequantisation
+    pi4, plane = mods["quantization_mxfp4"].quantize_to_qoq_int4(torch.from_numpy(wq).to(torch.bfloat16))
+    deq = mods["quantization_mxfp4"].dequantize_qoq_int4(pi4, plane)
+    out["qoq_int4"] = dict(w=wq, packed=pi4.numpy(), plane=plane.numpy(), deq=deq.numpy())
     xa = bf16_round(rng.standard_normal((4, 512)).astype(np.float32))
     qb, sf = mods["quantization_qoq_fused"].per_token_cast_to_int8(torch.from_numpy(xa).to(torch.bfloat16))
     out["int8_act"] = dict(x=xa, q=qb.view(torch.int8).numpy(), sf=sf.numpy())
@@ -117,9 +122,12 @@ def main(ref_root):
     out["ue8m0"] = dict(x=ue, y=m.ceil_to_ue8m0(torch.from_numpy(ue)).numpy())
 
     for name, d in out.items():
+        if only and name not in only:
+            continue
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **d)
         print(name, {k: v.shape for k, v in d.items()})
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    # optional further arguments: the fixture names to (re)write, e.g. qoq_int4
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference", set(sys.argv[2:]))

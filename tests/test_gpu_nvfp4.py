@@ -177,3 +177,38 @@ def test_nvfp4_global_scales_zero_rows_select_in_mega():
     check_frontend(r, 40)
     check_pool(r)
     print(check_y(r, zero_rows=(5, 21)))
+
+
+def test_nvfp4_split_family_matches_fused():
+    """kernel_family="split" (dispatch + L1, then L2 + combine: two launches) and "auto" above
+    family_threshold give the fused launch's output, intermediate rows and recv stats bit for
+    bit, with per-expert global scales, zero rows and the top-k selected in the first launch."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    M, E, H, I, topk = 40, 8, 1024, 512, 4
+    print(f"nvfp4 split vs fused M={M} E={E} H={H} I={I}", flush=True)
+    rng = np.random.default_rng(840)
+    x = randn_bf16(rng, (M, H))
+    x[7] = 0.0
+    rw = randn_bf16(rng, (E, H), 0.02)
+    (t1, t2), _, _ = make_nvfp4_weights(E, H, I, 841)
+    gs1 = torch.from_numpy((rng.random(E) * 1.5 + 0.25).astype(np.float32)).cuda()
+    gs2 = torch.from_numpy((rng.random(E) * 1.5 + 0.25).astype(np.float32)).cuda()
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="nvfp4")
+    xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
+    R = M * topk
+    outs = []
+    for family, thr, sel in (("fused", 256, False), ("split", 256, False), ("auto", 16, True)):
+        y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        stats = torch.zeros(E, dtype=torch.int32, device="cuda")
+        dgm.fable_router_quant_topk_frontend(xs, rws, buf, select_in_mega=sel)
+        dgm.nvfp4_mega_moe(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0,
+                           l1_global_scales=gs1, l2_global_scales=gs2, kernel_family=family, family_threshold=thr)
+        torch.cuda.synchronize()
+        assert buf.kernel_error() == 0
+        outs.append((y.clone(), stats.clone(), buf.l2_acts[:R].clone(), buf.l2_acts_sf[:R].clone(),
+                     buf.topk_idx[:M].clone()))
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            assert torch.equal(a, b)
+    assert (outs[0][0][7] == 0).all()

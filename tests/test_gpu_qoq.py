@@ -187,7 +187,7 @@ def test_qoq_zero_rows_multi_slab_select_in_mega():
 
 
 def test_qoq_buffer_format_guard():
-    """The MXFP entry points refuse a qoq buffer and the reverse; the QoQ split API is absent."""
+    """The MXFP entry points refuse a qoq buffer and the QoQ entry points an MXFP buffer."""
     need_gpu()
     import hopper_megamoe_basedondeepgemm_amd as dgm
     b = dgm.get_fused_symm_buffer_for_mega_moe(None, 16, 4, 4, 512, 256, act_format="qoq")
@@ -195,5 +195,79 @@ def test_qoq_buffer_format_guard():
     dummy = (torch.empty(1, device="cuda"),) * 3
     with pytest.raises(ValueError):
         dgm.mxfp4_mega_moe_fused(y, dummy, dummy, b)
-    with pytest.raises(NotImplementedError):
-        dgm.qoq_mega_moe_split(y, dummy, dummy, b)
+    bm = dgm.get_fused_symm_buffer_for_mega_moe(None, 16, 4, 4, 512, 256, act_format="mxfp4")
+    with pytest.raises(ValueError):
+        dgm.qoq_mega_moe_split(y, dummy, dummy, bm)
+    with pytest.raises(ValueError):
+        dgm.qoq_mega_moe_fused(y, dummy, dummy, bm)
+
+
+def test_qoq_int4_packer_and_split_matches_fused():
+    """The split path: quantize_to_qoq_int4 (int32 coefficient plane) bit-exact against the
+    oracle; transform_qoq_int4_weights_for_mega_moe_sm90 equal to the fused packer's transform of
+    the same weights; qoq_mega_moe_split (dispatch + L1, then L2 + combine) equal to
+    qoq_mega_moe_fused bit for bit (y, intermediate codes and scales, recv stats), with the
+    frontend run from router_input / router_weight and with the top-k selected in the first
+    launch; y within tolerance of the oracle."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4 as qm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_qoq_fused as qq
+    M, E, H, I, topk = 40, 16, 512, 256, 4
+    print(f"qoq int4 packer + split vs fused M={M} E={E} H={H} I={I}", flush=True)
+    rng = np.random.default_rng(740)
+    w1 = randn_bf16(rng, (E, 2 * I, H), 0.02)
+    w2 = randn_bf16(rng, (E, H, I), 0.02)
+    w1d, w2d = bf16_cpu(w1).cuda(), bf16_cpu(w2).cuda()
+    i1, i2 = qm.quantize_to_qoq_int4(w1d), qm.quantize_to_qoq_int4(w2d)
+    for got, w in ((i1, w1), (i2, w2)):
+        rp, rpl = pk.quantize_to_qoq_int4(w)
+        np.testing.assert_array_equal(got[0].cpu().numpy(), rp)
+        np.testing.assert_array_equal(got[1].cpu().numpy(), rpl)
+    t4 = dgm.transform_qoq_int4_weights_for_mega_moe_sm90(i1, i2)
+    tf = dgm.transform_qoq_weights_for_mega_moe_fused(qq.quantize_to_qoq(w1d), qq.quantize_to_qoq(w2d))
+    for a, b in zip(t4, tf):
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)
+    x = randn_bf16(rng, (M, H))
+    x[9] = 0.0
+    rw = randn_bf16(rng, (E, H), 0.02)
+    xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="qoq")
+    R = M * topk
+    outs = []
+    for mode in ("fused", "split_router_input", "split_select_in_mega"):
+        y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        stats = torch.zeros(E, dtype=torch.int32, device="cuda")
+        if mode == "fused":
+            dgm.fable_router_quant_topk_frontend(xs, rws, buf)
+            dgm.qoq_mega_moe_fused(y, t4[0], t4[1], buf, cumulative_local_expert_recv_stats=stats)
+        elif mode == "split_router_input":
+            dgm.qoq_mega_moe_split(y, t4[0], t4[1], buf, stats, activation_clamp=10.0,
+                                   router_input=xs, router_weight=rws)
+        else:
+            dgm.fable_router_quant_topk_frontend(xs, rws, buf, select_in_mega=True)
+            dgm.qoq_mega_moe_split(y, t4[0], t4[1], buf, cumulative_local_expert_recv_stats=stats,
+                                   activation_clamp=10.0)
+        torch.cuda.synchronize()
+        assert buf.kernel_error() == 0
+        outs.append((y.clone(), stats.clone(), buf.l2_acts[:R].clone(), buf.l2_acts_sf[:R].clone(),
+                     buf.topk_idx[:M].clone()))
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            assert torch.equal(a, b)
+    # y against the oracle
+    logits = moe.router_logits_f32(x, rw)
+    idx, w, _ = moe.topk_softmax(logits, topk)
+    idx[9] = -1
+    w[9] = 0.0
+    _, _, x_dq = moe.quant_act(x, "qoq")
+    h1 = pk.qoq_int4_to_fused(*(a.cpu().numpy() for a in i1))
+    h2 = pk.qoq_int4_to_fused(*(a.cpu().numpy() for a in i2))
+    ref, _ = moe.moe_forward_qoq(x_dq, idx, w, LazyQoQ(h1), LazyQoQ(h2), 0)
+    yv = outs[0][0].float().cpu().numpy()
+    assert (yv[9] == 0).all()
+    keep = [i for i in range(M) if i != 9]
+    m = moe.metrics(yv[keep], ref[keep])
+    assert m["cos_min"] >= COS_MIN and m["rel_rmse"] <= REL_RMSE_MAX, m
+    print(m)

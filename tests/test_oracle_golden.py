@@ -48,6 +48,22 @@ def test_qoq_packer(golden_dir):
     np.testing.assert_array_equal(p, g["packed"])
 
 
+def test_qoq_int4_packer(golden_dir):
+    """The split path's packer (int32 coefficient plane) and its dequantisation; its codes, s2,
+    z and s1 equal quantize_to_qoq's on the same weights (s2 never exceeds 15: |w8| <= 112)."""
+    g = load(golden_dir, "qoq_int4")
+    p, plane = pk.quantize_to_qoq_int4(g["w"])
+    np.testing.assert_array_equal(p, g["packed"])
+    np.testing.assert_array_equal(plane, g["plane"])
+    np.testing.assert_array_equal(pk.dequantize_qoq_int4(g["packed"], g["plane"]), g["deq"])
+    f = load(golden_dir, "qoq")
+    fp, s2, z, s1 = pk.qoq_int4_to_fused(g["packed"], g["plane"])
+    np.testing.assert_array_equal(fp, f["packed"])
+    np.testing.assert_array_equal(s2, f["s2"])
+    np.testing.assert_array_equal(z, f["z"])
+    np.testing.assert_array_equal(s1.view(np.uint32), f["s1"].view(np.uint32))
+
+
 def test_int8_act(golden_dir):
     g = load(golden_dir, "int8_act")
     q, sf = pk.per_token_cast_to_int8(g["x"])
