@@ -467,11 +467,12 @@ def fused_workgroups(b):
     return _lib.load().dgm_fused_workgroups(b.hidden, b.intermediate_hidden, b.act_code)
 
 
-def mxfp4_mega_moe_split(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
-                         fast_math=True, **_):
-    """deep_gemm/mega/__init__.py:579 split API: the same layer as separate launches
-    (dispatch, L1 + SwiGLU + requant, L2, combine) with the fused path's numerics."""
-    _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, split=True, fast_math=fast_math)
+def mxfp4_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs):
+    """deep_gemm/mega/__init__.py:579 split API: the same layer as separate launches (dispatch,
+    L1 + SwiGLU + requant, L2, combine) with the fused path's numerics, on an "mxfp4" / "mxfp8"
+    fused buffer. Arguments as ``mxfp4_mega_moe`` (:340; activation_clamp default None = no
+    clamp)."""
+    _split_entry(("mxfp4", "mxfp8", "fp8"), y, l1_weights, l2_weights, sym_buffer, *args, **kwargs)
 
 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,

@@ -57,7 +57,7 @@ def run_layer(M, E, E_local, expert_begin, H, I, topk, fmt, seed, force_balanced
     y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
     dgm.fable_router_quant_topk_frontend(xs, rws, buf, force_balanced=force_balanced, select_in_mega=select_in_mega)
     layer = dgm.mxfp4_mega_moe_split if split else dgm.mxfp4_mega_moe_fused
-    layer(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats)
+    layer(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0)
     torch.cuda.synchronize()
     # ---- oracle
     logits = moe.router_logits_f32(x, rw)
@@ -173,7 +173,7 @@ def test_split_matches_fused(fmt):
     check_y(r)
     (t1, t2), _, _ = weights
     y2 = torch.empty((3, 3072), dtype=torch.bfloat16, device="cuda")
-    dgm.mxfp4_mega_moe_split(y2, t1, t2, r["buf"])
+    dgm.mxfp4_mega_moe_split(y2, t1, t2, r["buf"], activation_clamp=10.0)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
 
