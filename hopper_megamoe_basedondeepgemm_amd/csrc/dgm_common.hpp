@@ -31,10 +31,10 @@ DGM_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 
 
 // fp32 -> bf16 bits, round to nearest even, NaN kept quiet.
 DGM_DEV uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  // (a select, not a branch: a branch costs an exec-mask round per call)
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? (u >> 16) | 0x40u : r);
 }
 DGM_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
@@ -120,8 +120,8 @@ DGM_DEV float sigmoid(float g) {
 // larger keys are larger values and, on ties, lower expert ids.
 DGM_DEV uint32_t topk_key(float logit, int e) {
   uint32_t b = f32_to_bf16(logit);
-  if (b == 0x8000u) b = 0u;
-  uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  b = b == 0x8000u ? 0u : b;
+  const uint32_t o = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
   return (o << 16) | (0xffffu - (uint32_t)e);
 }
 DGM_DEV float key_value(uint32_t key) {
@@ -144,10 +144,60 @@ DGM_DEV uint32_t wave_max_u32(uint32_t v) {
   return ab > cd ? ab : cd;
 }
 
-// Top-k of one token's fp32 logits row (E <= 1024, topk <= 16) by one wave: k rounds of a
-// wave-wide max over the keys, then w_k = exp(v_k - v_0) / sum_k (sequential sum). Lane k <
-// topk receives slot k. zero_row: every slot -1 / 0. balanced: slot s -> s G + (g + 7 s) % G,
-// G = E / topk, weight 1 / topk (g = the token's global index).
+// Top-k of one token's fp32 logits row (E <= 1024, topk <= 16) by one wave. Lane l holds the
+// keys of experts l + 64 i (i < NK), sorted descending; each of the k rounds takes the
+// wave-wide maximum of the lanes' first keys (keys are distinct: they carry the expert id) and
+// the winning lane shifts its list by one. Lane k keeps slot k. Weights: w_k =
+// exp(v_k - v_0) / sum_k, the sum taken sequentially in slot order. zero_row: every slot -1 / 0.
+// balanced: slot s -> s G + (g + 7 s) % G with G = E / topk, weight 1 / topk (g = the token's
+// global index).
+template <int NK, class LoadLogit>
+DGM_DEV void select_topk_wave_nk(LoadLogit load, int E, int topk, int lane, int& idx, float& wt) {
+  // every logit is read before any key is formed (one LDS round trip, not one per key)
+  float lv[NK];
+#pragma unroll
+  for (int i = 0; i < NK; ++i) lv[i] = load(lane + 64 * i < E ? lane + 64 * i : E - 1);
+  uint32_t key[NK];
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int e = lane + 64 * i;
+    const uint32_t kv = topk_key(lv[i], e);
+    key[i] = e < E ? kv : 0u;
+  }
+  // odd-even transposition sort, descending
+#pragma unroll
+  for (int r = 0; r < NK; ++r)
+#pragma unroll
+    for (int i = r & 1; i + 1 < NK; i += 2) {
+      const uint32_t a = key[i], b = key[i + 1];
+      key[i] = a > b ? a : b;
+      key[i + 1] = a > b ? b : a;
+    }
+  float myv = 0.f, v0 = 0.f;
+  int mye = -1;
+  for (int k = 0; k < topk; ++k) {
+    const uint32_t m = wave_max_u32(key[0]);
+    if (key[0] == m) {         // the lane holding the winner
+#pragma unroll
+      for (int i = 0; i + 1 < NK; ++i) key[i] = key[i + 1];
+      key[NK - 1] = 0u;
+    }
+    const float v = key_value(m);
+    if (k == 0) v0 = v;
+    if (lane == k) {
+      myv = v;
+      mye = (int)(0xffffu - (m & 0xffffu));
+    }
+  }
+  const float ex = lane < topk ? expf(myv - v0) : 0.f;
+  float sum = 0.f;
+  for (int k = 0; k < topk; ++k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), k));
+  if (lane < topk) {
+    idx = mye;
+    wt = ex / sum;
+  }
+}
+
 template <class LoadLogit>
 DGM_DEV void select_topk_wave(LoadLogit load, int E, int topk, bool balanced, int g, bool zero_row, int lane,
                               int& idx, float& wt) {
@@ -162,46 +212,13 @@ DGM_DEV void select_topk_wave(LoadLogit load, int E, int topk, bool balanced, in
     }
     return;
   }
-  constexpr int MAXK = 16;
-  const int nk = (E + 63) >> 6;         // key slots in use (wave-uniform)
-  uint32_t key[MAXK];
-#pragma unroll
-  for (int i = 0; i < MAXK; ++i) {
-    const int e = lane + 64 * i;
-    key[i] = i < nk && e < E ? topk_key(load(e), e) : 0u;
-  }
-  float vsel[16], ex[16];
-  int esel[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if (k < topk) {
-      uint32_t m = 0u;
-#pragma unroll
-      for (int i = 0; i < MAXK; ++i)
-        if (i < nk) m = key[i] > m ? key[i] : m;
-      m = wave_max_u32(m);
-#pragma unroll
-      for (int i = 0; i < MAXK; ++i)
-        if (i < nk) key[i] = key[i] == m ? 0u : key[i];
-      vsel[k] = key_value(m);
-      esel[k] = (int)(0xffffu - (m & 0xffffu));
-    }
-  }
-  float sum = 0.f;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if (k < topk) {
-      ex[k] = expf(vsel[k] - vsel[0]);
-      sum = sum + ex[k];
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if (k < topk && k == lane) {
-      idx = esel[k];
-      wt = ex[k] / sum;
-    }
-  }
+  const int nk = (E + 63) >> 6;         // keys per lane (wave-uniform)
+  if (nk <= 1) select_topk_wave_nk<1>(load, E, topk, lane, idx, wt);
+  else if (nk <= 2) select_topk_wave_nk<2>(load, E, topk, lane, idx, wt);
+  else if (nk <= 4) select_topk_wave_nk<4>(load, E, topk, lane, idx, wt);
+  else if (nk <= 6) select_topk_wave_nk<6>(load, E, topk, lane, idx, wt);
+  else if (nk <= 8) select_topk_wave_nk<8>(load, E, topk, lane, idx, wt);
+  else select_topk_wave_nk<16>(load, E, topk, lane, idx, wt);
 }
 
 // ---------------------------------------------------------------- scopes / atomics

@@ -770,27 +770,32 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
   }
   __syncthreads();
-  if (R <= 256) {
+  if (R <= 64) {
     // one wave sorts the routes (the other waves wait at the barrier)
-    if (wv == 0) {
-      if (R <= 64) wave_dispatch<1>(s, R, p.topk, lane);
-      else if (R <= 128) wave_dispatch<2>(s, R, p.topk, lane);
-      else wave_dispatch<4>(s, R, p.topk, lane);
-    }
+    if (wv == 0) wave_dispatch<1>(s, R, p.topk, lane);
     __syncthreads();
   } else {
+    // counts, expert offsets, then each route placed in its expert's segment in arrival order
+    // (LDS atomics; the staging area `tmp` is the L1 epilogue's up-sum buffer, unused until
+    // then) and moved to its canonical position: its rank (route id) within the segment
     for (int r = tid; r < R; r += FT) {
       int e = s.exp_of_route[r];
       if (e >= 0) { atomicAdd(&s.cnt[e], 1); atomicAdd(&s.nslot[r / p.topk], 1); }
     }
     __syncthreads();
     scan_experts(s, p.E_local);
+    int* tmp = reinterpret_cast<int*>(&s.upv[0][0][0]);
+    static_assert(sizeof(s.upv) >= FUSED_MAX_ROUTES * sizeof(int), "route staging");
     for (int r = tid; r < R; r += FT) {
-      int e = s.exp_of_route[r];
-      if (e < 0) continue;
+      const int e = s.exp_of_route[r];
+      if (e >= 0) tmp[atomicAdd(&s.eoff[e], 1)] = r;
+    }
+    __syncthreads();
+    for (int q = tid; q < s.meta[1]; q += FT) {
+      const int v = tmp[q], e = s.exp_of_route[v], c = s.cnt[e], b = s.eoff[e] - c;
       int rank = 0;
-      for (int q = 0; q < r; ++q) rank += s.exp_of_route[q] == e ? 1 : 0;
-      s.routes[s.eoff[e] + rank] = r;
+      for (int j = 0; j < c; ++j) rank += tmp[b + j] < v ? 1 : 0;
+      s.routes[b + rank] = v;
     }
     __syncthreads();
   }

@@ -91,11 +91,12 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
 // of a wave-wide max select; softmax w_k = exp(v_k - v_0) / sum (sequential sum). Zero rows
 // (token_flags bit 0, with DGM_FE_ZERO_ROW_UNROUTED) get idx -1 / weight 0; forced-balanced
 // routing (DGM_FE_FORCE_BALANCED) gives slot s -> s G + (g + 7 s) % G with weight 1 / topk.
+constexpr int SELECT_TPB = 4;           // tokens (waves) per workgroup
 __global__ void __launch_bounds__(256) k_select(const float* __restrict__ logits, const int* __restrict__ token_flags,
                                                 int M, int E, int topk, int flags, int token_offset,
                                                 int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = blockIdx.x * SELECT_TPB + (threadIdx.x >> 6);
   if (t >= M) return;
   int idx = -1;
   float wt = 0.f;
@@ -541,7 +542,7 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
 #undef DGM_FE
   int st = dgm_last_launch_status();
   if (st || (flags & DGM_FE_SELECT_IN_MEGA)) return st;
-  hipLaunchKernelGGL(k_select, dim3((num_tokens + 3) / 4), dim3(256), 0, stream, logits, tflags, num_tokens,
+  hipLaunchKernelGGL(k_select, dim3((num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, logits, tflags, num_tokens,
                      num_experts, topk, flags, token_offset, (int64_t*)(buf + L->topk_idx),
                      (float*)(buf + L->topk_weights));
   return dgm_last_launch_status();
@@ -550,14 +551,19 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
 // Writes topk_idx / topk_weights from the buffer's logits (after a DGM_FE_SELECT_IN_MEGA
 // frontend call) for the paths that read them.
 static int materialize_topk(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, hipStream_t stream) {
-  hipLaunchKernelGGL(k_select, dim3((A->num_tokens + 3) / 4), dim3(256), 0, stream, (const float*)(buf + L->logits),
+  hipLaunchKernelGGL(k_select, dim3((A->num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, (const float*)(buf + L->logits),
                      (const int*)(buf + L->token_flags), A->num_tokens, A->num_experts, A->topk, A->fe_flags,
                      A->token_offset, (int64_t*)(buf + L->topk_idx), (float*)(buf + L->topk_weights));
   return dgm_last_launch_status();
 }
 
-// Every workgroup of the fused kernel reads all tokens' logits when it selects the top-k.
+// Every workgroup of the fused kernel reads all tokens' logits when it selects the top-k; that
+// costs ~1 us of SIMD time per token and workgroup (the selection rounds are sequential), so
+// above SELECT_IN_MEGA_FAST_TOKENS a separate selection launch (one wave per token over the
+// whole GPU) comes first and the fused kernel reads the result. The in-kernel frontend
+// (fe_in_mega) selects in the kernel up to SELECT_IN_MEGA_MAX_TOKENS.
 constexpr int SELECT_IN_MEGA_MAX_TOKENS = 64;
+constexpr int SELECT_IN_MEGA_FAST_TOKENS = 8;     // (one token per wave)
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
@@ -602,7 +608,7 @@ static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stre
   const DgmBufferLayout* L = A->layout;
   uint8_t* buf = (uint8_t*)A->buffer;
   {
-    const bool sel = (A->select_in_mega || A->fe_in_mega) && A->num_tokens <= SELECT_IN_MEGA_MAX_TOKENS &&
+    const bool sel = (A->fe_in_mega || (A->select_in_mega && A->num_tokens <= SELECT_IN_MEGA_FAST_TOKENS)) &&
                      (phases & 1);
     if (A->select_in_mega && !sel && (phases & 1)) {
       int st = materialize_topk(A, buf, L, stream);
