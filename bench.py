@@ -195,7 +195,7 @@ def copy_calibration(torch, mib, reps=3):
     torch.cuda.synchronize()
 
 
-def cpu_baseline(packed, M=8, sample_routes=None, reps=10, seed=7):
+def cpu_baseline(packed, M=8, sample_routes=None, reps=150, seed=7):
     """The oracle (numpy fp32 restatement) on the host cores: router + top-8 + cast for the
     M tokens, then `sample_routes` (default: all) of the 8*M expert routes (forced-balanced: one
     route per active expert), weights dequantised once before timing (as the reference's CPU path
@@ -325,7 +325,7 @@ def main():
             us, threads = cpu_baseline(packed, M=args.m)
             cpu = dict(value=round(us, 1), unit="us/layer", cores=threads, kind="port",
                        sample=f"oracle (numpy fp32): the whole M={args.m} layer (router + top-8 + cast, then "
-                              f"all {8 * args.m} expert routes with weights dequantised beforehand), median of 10; "
+                              f"all {8 * args.m} expert routes with weights dequantised beforehand), median of 150; "
                               f"A-MXFP8; {time.perf_counter() - t0:.1f} s of host time incl. the dequantisation")
             log(f"cpu baseline: {cpu}")
         except Exception as ex:  # reported, never fatal

@@ -254,91 +254,44 @@ DGM_DEV void scan_experts(S& s, int n) {
   __syncthreads();
 }
 
-// The pool table of R <= 64 * KPL routes by one wave. Keys = local expert << 16 | route id
-// (routes of other ranks sort last) over 64 lanes x KPL registers (element i = lane + 64 j);
-// sorted, they are the canonical pool order (expert asc, route asc = token asc, slot asc), and
-// expert boundaries give the active list, offsets and counts. KPL <= 2: each key's rank is
-// counted against every key (broadcast by readlane), then keys are scattered to their ranks
-// and read back in order; KPL = 4: an in-register bitonic sort. Writes s.routes, s.act,
-// s.aoff, s.meta[0..1], s.cnt (of active experts; the rest must be zero) and s.nslot (must
-// be zero).
-template <int KPL, class S>
+// The pool table of R <= 64 routes by one wave. Keys = local expert << 16 | route id (routes
+// of other ranks sort last), one per lane; sorted, they are the canonical pool order (expert
+// asc, route asc = token asc, slot asc), and expert boundaries give the active list, offsets
+// and counts. Each key's rank is counted against every key (broadcast by readlane), then the
+// keys are scattered to their ranks and read back in order. Writes s.routes, s.act, s.aoff,
+// s.meta[0..1], s.cnt (of active experts; the rest must be zero) and s.nslot (must be zero).
+template <class S>
 DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane) {
-  constexpr int N = 64 * KPL;
-  uint32_t key[KPL];
-#pragma unroll
-  for (int j = 0; j < KPL; ++j) {
-    const int i = lane + 64 * j;
-    const int e = i < R ? s.exp_of_route[i] : -1;
-    key[j] = ((e < 0 ? 0xffffu : (uint32_t)e) << 16) | (uint32_t)i;
+  const int e0 = lane < R ? s.exp_of_route[lane] : -1;
+  uint32_t key = ((e0 < 0 ? 0xffffu : (uint32_t)e0) << 16) | (uint32_t)lane;
+  int rank = 0;
+  for (int q = 0; q < 64; ++q) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, q) < key ? 1 : 0;
+  // (the route-table slots double as the sort buffer: keys of the routes are unique)
+  s.routes[rank] = (int)key;
+  key = (uint32_t)s.routes[lane];
+  const uint32_t e = key >> 16;
+  const bool valid = e != 0xffffu;
+  const uint32_t prev = (uint32_t)__shfl_up((int)key, 1);
+  const bool first = valid && (lane == 0 || (prev >> 16) != e);
+  const uint64_t fb = __ballot(first), vb = __ballot(valid);
+  const int a = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(fb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)fb, 0u));
+  if (valid) {
+    const int r = (int)(key & 0xffffu);
+    s.routes[lane] = r;
+    atomicAdd(&s.nslot[r / topk], 1);
   }
-  if constexpr (KPL <= 2) {
-    int rank[KPL];
-#pragma unroll
-    for (int j = 0; j < KPL; ++j) rank[j] = 0;
-#pragma unroll
-    for (int jj = 0; jj < KPL; ++jj)
-      for (int q = 0; q < 64; ++q) {
-        const uint32_t kq = (uint32_t)__builtin_amdgcn_readlane((int)key[jj], q);
-#pragma unroll
-        for (int j = 0; j < KPL; ++j) rank[j] += kq < key[j] ? 1 : 0;
-      }
-    // (the route-table slots double as the sort buffer: keys of the routes are unique)
-#pragma unroll
-    for (int j = 0; j < KPL; ++j) s.routes[rank[j]] = (int)key[j];
-#pragma unroll
-    for (int j = 0; j < KPL; ++j) key[j] = (uint32_t)s.routes[lane + 64 * j];
-  } else {
-#pragma unroll
-  for (int size = 2; size <= N; size <<= 1) {
-#pragma unroll
-    for (int d = size >> 1; d > 0; d >>= 1) {
-      uint32_t nk[KPL];
-#pragma unroll
-      for (int j = 0; j < KPL; ++j) {
-        const int i = lane + 64 * j;
-        const uint32_t other = d < 64 ? (uint32_t)__shfl_xor((int)key[j], d) : key[j ^ (d >> 6)];
-        const bool up = (i & size) == 0, lower = (i & d) == 0;
-        const uint32_t lo = key[j] < other ? key[j] : other, hi = key[j] < other ? other : key[j];
-        nk[j] = lower == up ? lo : hi;
-      }
-#pragma unroll
-      for (int j = 0; j < KPL; ++j) key[j] = nk[j];
-    }
+  if (first) {
+    s.act[a] = (int)e;
+    s.aoff[a] = lane;
   }
-  }
-  int base = 0, total = 0;
-  uint32_t last_prev = 0xffffffffu;     // key of element 64 j - 1
-#pragma unroll
-  for (int j = 0; j < KPL; ++j) {
-    const int i = lane + 64 * j;
-    const uint32_t e = key[j] >> 16;
-    const bool valid = e != 0xffffu;
-    const uint32_t up1 = (uint32_t)__shfl_up((int)key[j], 1);
-    const uint32_t prev = lane == 0 ? last_prev : up1;
-    const bool first = valid && (i == 0 || (prev >> 16) != e);
-    const uint64_t fb = __ballot(first), vb = __ballot(valid);
-    const int a = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(fb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)fb, 0u));
-    if (valid) {
-      const int r = (int)(key[j] & 0xffffu);
-      s.routes[i] = r;
-      atomicAdd(&s.nslot[r / topk], 1);
-    }
-    if (first) {
-      s.act[a] = (int)e;
-      s.aoff[a] = i;
-    }
-    base += __popcll(fb);
-    total += __popcll(vb);
-    last_prev = (uint32_t)__shfl((int)key[j], 63);
-  }
+  const int base = __popcll(fb), total = __popcll(vb);
   if (lane == 0) {
     s.aoff[base] = total;
     s.meta[0] = base;
     s.meta[1] = total;
   }
   // per active expert: count = next offset - offset (the wave's LDS stores above come first)
-  for (int a = lane; a < base; a += 64) s.cnt[s.act[a]] = s.aoff[a + 1] - s.aoff[a];
+  for (int i = lane; i < base; i += 64) s.cnt[s.act[i]] = s.aoff[i + 1] - s.aoff[i];
 }
 
 DGM_DEV bool spin_until(const int* p, int target, int limit, int* err) {
@@ -772,7 +725,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   __syncthreads();
   if (R <= 64) {
     // one wave sorts the routes (the other waves wait at the barrier)
-    if (wv == 0) wave_dispatch<1>(s, R, p.topk, lane);
+    if (wv == 0) wave_dispatch(s, R, p.topk, lane);
     __syncthreads();
   } else {
     // counts, expert offsets, then each route placed in its expert's segment in arrival order
