@@ -209,3 +209,14 @@ def test_select_in_mega_config1_balanced():
     check_frontend(r, "mxfp4", 8, force_balanced=True)
     check_pool(r, 48, 0)
     print(check_y(r))
+
+
+def test_large_batch_beyond_fused_limits():
+    """200 tokens at top-8: 1600 routes exceed the persistent kernel's 1024, so the fused entry
+    point runs the split path (dispatch, L1, L2, combine kernels); frontend, pool and y as
+    everywhere else."""
+    need_gpu()
+    r = run_layer(200, 16, 16, 0, 512, 256, 8, "mxfp4", seed=950, zero_rows=(7,))
+    check_frontend(r, "mxfp4", 200, zero_rows=(7,))
+    check_pool(r, 16, 0)
+    print(check_y(r, zero_rows=(7,)))
