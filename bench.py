@@ -125,7 +125,7 @@ def build_nvfp4_weights(torch, seed, n_experts, chunk=32):
     return t
 
 
-def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True):
+def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True, ep_size=1):
     """Times `steps` layer forwards, each between two HIP events on the layer's stream (the
     layer time), then `steps` more with a third event between the frontend and the fused MoE
     kernel for the split between them (an event between two launches delays the second one,
@@ -133,7 +133,8 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     (t1, t2) = weights
     fused = {"qoq": dgm.qoq_mega_moe_fused, "nvfp4": dgm.fp4_fp4_mega_moe}.get(act, dgm.mxfp4_mega_moe_fused)
     expert_bytes = {"qoq": QOQ_EXPERT_BYTES, "nvfp4": NVFP4_EXPERT_BYTES}.get(act, MXFP4_EXPERT_BYTES)
-    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act)
+    # (ep_size > 1: one EP rank's share, experts 0 .. E / ep_size - 1, on this GPU)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act, ep_size=ep_size, ep_rank=0)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     x = torch.randn((M, H), generator=g, device="cuda").to(torch.bfloat16)
@@ -271,6 +272,7 @@ def main():
     ap.add_argument("--nvfp4-sweep", default="16,64,128",
                     help="M values of the NVFP4 W4A4 sweep (seeded unbalanced routing); empty = skip")
     ap.add_argument("--no-unbalanced", action="store_true")
+    ap.add_argument("--no-c1", action="store_true", help="skip the config 1 line (one EP rank's 48 experts)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (HBM counter scaling)")
@@ -303,6 +305,14 @@ def main():
             r = time_layer(torch, dgm, M, weights, router_w, act, args.sweep_steps, args.warmup, 500 + M)
             sweep[act][M] = entry(r)
             log(f"M={M} {act}: {sweep[act][M]}")
+    if not args.no_c1:
+        # one EP rank's share (local experts 0-47 of the 384-way router),
+        # W-MXFP4 x A-MXFP4, M=8 forced-balanced: 8 rows on 8 local experts
+        share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
+        r = time_layer(torch, dgm, 8, share, router_w, "mxfp4", args.sweep_steps, args.warmup, 508, ep_size=8)
+        sweep["c1_ep_share_M8_mxfp4"] = entry(r)
+        log(f"config 1 (E48 share, M=8, mxfp4): {sweep['c1_ep_share_M8_mxfp4']}")
+        del share
     if not args.no_qoq and [v for v in args.sweep.split(",") if v]:
         log("building E384 QoQ weights ...")
         qw = build_qoq_weights(torch, 4321, E)
