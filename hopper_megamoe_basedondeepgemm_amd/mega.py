@@ -259,8 +259,9 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
     the forced-balanced rule after the router ran; ``zero_row_unrouted`` (env
     DG_FE_ZERO_ROW_UNROUTED, default 1) leaves all-zero rows unrouted. ``select_in_mega`` (env
     DG_FE_SELECT_IN_MEGA, default 0; tokens <= 64): stop after the logits and the cast; the
-    next ``mxfp4_mega_moe_fused`` on this buffer selects the top-k in its prologue (and writes
-    ``topk_idx / topk_weights``, which are not valid before that call). ``stamps``,
+    next fused call on this buffer selects the top-k (in its prologue up to 8 tokens, else in a
+    selection launch just before it) and writes ``topk_idx / topk_weights``, which are not valid
+    before that call. ``stamps``,
     ``l2_persist`` and ``wlayout`` are H20 tuning knobs with no effect here."""
     b = sym_buffer
     _lib.require_gpu(hidden, router_weight)
@@ -479,7 +480,8 @@ def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
                              cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
                              force_balanced=None, token_offset=0, phase_stamps=None, one_launch=None, **_):
     """deep_gemm/mega/__init__.py:451: frontend + fused layer from bf16 hidden states: the
-    frontend launch, then the fused launch (the top-k selected in its prologue up to 64 tokens).
+    frontend launch, then the fused launch (the top-k selected in its prologue up to 8 tokens,
+    by a selection launch between the two up to 64, by the frontend beyond).
     ``one_launch`` (env DG_ONE_LAUNCH=1; up to 64 tokens): a single launch instead, in which the
     fused kernel computes the router logits, zero-row flags and activation cast itself (spread
     over all workgroups) and meets at a grid-wide arrival counter before its prologue; same
