@@ -59,11 +59,12 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
 }
 
 // ------------------------------------------------------------------ frontend
-// Router: wave w of workgroup (bx, by) computes the logits of expert 4 bx + w for tokens
-// 4 by .. +3 (router_wave: fixed accumulation order, bit-reproducible fp32 logits);
-// workgroups with bx == 0 also record each token's all-zero flag. Cast, spread over the whole
-// grid after the router work: MXFP4 / MXFP8 8 lanes per 32-element group, NVFP4 4 lanes per
-// 16-element group, QoQ one wave per token (dgm_frontend.hpp).
+// Router rows of the grid (by < ceil(M / 4)): wave w of workgroup (bx, by) computes the logits
+// of expert 4 bx + w for tokens 4 by .. +3 (router_wave: fixed accumulation order,
+// bit-reproducible fp32 logits); workgroups with bx == 0 also record each token's all-zero
+// flag. Cast rows (the rest of the grid, running beside the router rows rather than after
+// them): MXFP4 / MXFP8 8 lanes per 32-element group, NVFP4 4 lanes per 16-element group, QoQ
+// one wave per token (dgm_frontend.hpp).
 template <int J>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
@@ -71,13 +72,18 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
                                                   uint8_t* __restrict__ sf) {
   constexpr int H = J * 512;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, token_flags,
-                        blockIdx.x == 0 && wave == 0);
-  const int64_t lane0 = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 256 + tid;
-  const int64_t nl = (int64_t)gridDim.x * gridDim.y * 256;
+  const int ry = (M + 3) / 4;
+  if ((int)blockIdx.y < ry) {
+    router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, token_flags,
+                          blockIdx.x == 0 && wave == 0);
+    return;
+  }
+  const int cy = (int)gridDim.y - ry, by = (int)blockIdx.y - ry;
+  const int64_t lane0 = ((int64_t)by * gridDim.x + blockIdx.x) * 256 + tid;
+  const int64_t nl = (int64_t)gridDim.x * cy * 256;
   if (act_format == DGM_ACT_QOQ) {
-    const int nwaves = gridDim.x * gridDim.y * 4;
-    for (int t = ((int)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave; t < M; t += nwaves)
+    const int nwaves = gridDim.x * cy * 4;
+    for (int t = (by * (int)gridDim.x + (int)blockIdx.x) * 4 + wave; t < M; t += nwaves)
       cast_qoq_token<J, false>(x, t, lane, q, sf);
   } else if (act_format == DGM_ACT_NVFP4) {
     for (int64_t i = lane0; i < (int64_t)M * (H / 16) * 4; i += nl) cast_lane_nvfp4<false>(x, i, q, sf);
@@ -523,7 +529,13 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
   if (num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)buffer;
   const int J = hidden / 512;
-  dim3 rg((num_experts + 3) / 4, (num_tokens + 3) / 4);
+  // router rows, then cast rows: one cast lane per thread (QoQ: one wave per token)
+  const int rx = (num_experts + 3) / 4;
+  const int64_t cast_threads = act_format == DGM_ACT_QOQ     ? (int64_t)num_tokens * 64
+                               : act_format == DGM_ACT_NVFP4 ? (int64_t)num_tokens * (hidden / 16) * 4
+                                                             : (int64_t)num_tokens * (hidden / 32) * 8;
+  const int64_t cast_rows = (cast_threads + (int64_t)rx * 256 - 1) / ((int64_t)rx * 256);
+  dim3 rg(rx, (num_tokens + 3) / 4 + (int)cast_rows);
   const uint16_t* x = (const uint16_t*)hidden_bf16;
   const uint16_t* w = (const uint16_t*)router_weight_bf16;
   float* logits = (float*)(buf + L->logits);
