@@ -16,6 +16,12 @@ Stages, each citing the reference rule it restates:
               bf16, clamp (gate <= c, up in [-c, c]), silu(gate)*up*w, per-32 requant
               (MXFP4: ceil_to_ue8m0(amax/6) + ties-down E2M1; MXFP8: 2^ceil(log2(amax/448))
               + E4M3), fp32 @ W2^T, fp32 index_add over experts ascending.
+  qoq         deep_gemm/quantization_qoq_fused.py:78-91 (per-token int8 cast);
+              tests/test_four_api_correctness.py:421-446 (dequantised weights, fp32 gate/up
+              without bf16 rounding, per-64 int8 requant, per-route bf16, fp32 sum).
+  nvfp4       sm100_b200/test_mega_moe.py:68-93 (W4A4 row cast: E4M3 RNE of amax/6 per 16,
+              ties-down E2M1), :431-438 (per-16 requant), optional per-expert global scales
+              of deep_gemm/mega/__init__.py:277 on the L1 / L2 outputs.
 
 Router accumulation order. The reference's logits are an fp32 GEMM whose summation order is
 unspecified (torch / cuBLAS / the frontend's K-split). This build fixes one order and uses
