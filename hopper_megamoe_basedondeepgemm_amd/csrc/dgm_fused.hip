@@ -576,7 +576,11 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT, MIDL>& r) {
 // waits for their weight tiles), [7] wall ticks in L1 epilogues.
 DGM_DEV long long wall_clock() { return (long long)__builtin_amdgcn_s_memrealtime(); }
 
-template <int KT1, int KT2, int ACT>
+// FEIN: the router, token flags and activation cast run in this launch (p.fe_in); the rows they
+// write are then read with agent-scope loads. Otherwise they were written by an earlier launch
+// and are read with ordinary loads, which the L2 caches: every workgroup reads the same few
+// activation rows at once, and L2-bypassing loads of them queue at the memory channels.
+template <int KT1, int KT2, int ACT, bool FEIN>
 __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   using Smem = FusedSmem<KT1, KT2, ACT>;
   __shared__ Smem s;
@@ -604,7 +608,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // (fe_in) router logits, zero-row flags and the activation cast, spread over the grid, with
   // write-through stores; then every workgroup waits until all have arrived (the grid is what
   // the device keeps resident, so all workgroups run at once)
-  if (p.fe_in) {
+  if constexpr (FEIN) {
     constexpr int J = H / 512;
     static_assert(H % 512 == 0, "in-kernel frontend: hidden % 512");
     // router (expert, 4-token group) pairs wave-major from the first wave of every workgroup,
@@ -671,7 +675,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       for (int i0 = 0; i0 < nv; i0 += SB * FT) {
         float v[SB];
         int fl;
-        if (p.fe_in) {
+        if constexpr (FEIN) {
 #pragma unroll
           for (int j = 0; j < SB; ++j) v[j] = ld_agent_f32(src + min(i0 + j * FT + tid, nv - 1));
           fl = __hip_atomic_load(tfs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -844,10 +848,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     };
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
-    // (agent-scope loads: the rows may have been written by this launch's in-kernel frontend)
-    auto load_slab = [xv, xs, topk](SlabRegs<KT1, ACT, true, false>& r, int a, int s0) __attribute__((always_inline)) {
+    // (agent-scope loads when this launch's in-kernel frontend wrote the rows)
+    auto load_slab = [xv, xs, topk](SlabRegs<KT1, ACT, FEIN, false>& r, int a, int s0) __attribute__((always_inline)) {
       const int* rts = s.routes + s.aoff[a] + s0;
-      slab_load<KT1, ACT, true, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
+      slab_load<KT1, ACT, FEIN, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
                                  [rts, topk](int cc) { return rts[cc] / topk; },
                                  [rts](int cc) { return s.route_w[rts[cc]]; });
     };
@@ -858,14 +862,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
     // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    if (tid == 0 && 2 * G < U1) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
     U4 wr[KR];
     uint32_t sr[ACT == DGM_ACT_NVFP4 ? KR : 1];
     uint32_t sd[SW1], sn[SW1];
-    SlabRegs<KT1, ACT, true, false> pre;
+    SlabRegs<KT1, ACT, FEIN, false> pre;
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
     if (q0 < U1) {
       load_slab(pre, q0 / QN1, 0);      // (ahead of the tiles: the store below waits for it only)
@@ -878,6 +881,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
       }
       load_scales(q0, sd);
+      // the first claim, issued after the first item's loads: every workgroup claims at once
+      // here, and the slab store below waits for the slab loads (older) but not for this
+      // contended atomic's return (memory operations complete in issue order)
+      if (tid == 0 && 2 * G < U1) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       slab_store(s, pre);
       staged = (q0 / QN1) << 16;
       __syncthreads();
@@ -1198,9 +1205,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     __syncthreads();
     const int G = gridDim.x;
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
-    // used as returned (any arithmetic on it here would wait for every load issued before it)
+    // used as returned (any arithmetic on it here would wait for every load issued before it).
+    // The first claim is issued after the first item's slab is staged (the staging waits
+    // would otherwise also wait for this atomic's return).
     int ahead = -1;
-    if (tid == 0 && 2 * G < U2) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool claimed = false;
     int q0 = (int)blockIdx.x < U2 ? (int)blockIdx.x : U2;
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
@@ -1247,6 +1256,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         }
         staged = key;
         __syncthreads();
+      }
+      if (!claimed) {
+        claimed = true;
+        if (tid == 0 && 2 * G < U2) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
@@ -1495,40 +1508,48 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[5] = wall_clock();
 }
 
-struct GridCache { int blocks[3][4][2] = {}; };
+// per (shape slot, format, FEIN): the resident grid; per (shape slot, format): the last launch's
+struct GridCache { int blocks[3][4][2] = {}; int last[3][4] = {}; };
 GridCache g_grid;
 
-template <int KT1, int KT2, int ACT>
+template <int KT1, int KT2, int ACT, bool FEIN>
 int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
-  int& nb = g_grid.blocks[slot][ACT][0];
+  int& nb = g_grid.blocks[slot][ACT][FEIN ? 1 : 0];
   if (nb == 0) {
     int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT>, FT, 0);
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT, FEIN>, FT, 0);
     if (e != hipSuccess || per_cu < 1) per_cu = 1;
     int dev = 0, cus = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     nb = per_cu * (cus > 0 ? cus : 256);
   }
-  hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT>), dim3(nb), dim3(FT), 0, stream, prm);
+  g_grid.last[slot][ACT] = nb;
+  hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FEIN>), dim3(nb), dim3(FT), 0, stream, prm);
   return dgm_last_launch_status();
+}
+
+template <int KT1, int KT2, int ACT>
+int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream) {
+  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, true>(prm, slot, stream)
+                   : launch_fused_t<KT1, KT2, ACT, false>(prm, slot, stream);
 }
 
 }  // namespace
 
 int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format) {
   int slot = hidden == 3072 ? 0 : (hidden == 512 ? 1 : 2);
-  return g_grid.blocks[slot][act_format][0];
+  return g_grid.last[slot][act_format];
 }
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream) {
 #define DGM_FUSED_SHAPE(H_, I_, SLOT)                                                          \
   if (hidden == H_ && intermediate == I_) {                                                    \
     constexpr int KA = H_ / 128, KB = I_ / 128;                                               \
-    return act == DGM_ACT_MXFP4   ? launch_fused_t<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream) \
-           : act == DGM_ACT_MXFP8 ? launch_fused_t<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream) \
-           : act == DGM_ACT_QOQ   ? launch_fused_t<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream)   \
-                                  : launch_fused_t<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream); \
+    return act == DGM_ACT_MXFP4   ? launch_fused_fe<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream) \
+           : act == DGM_ACT_MXFP8 ? launch_fused_fe<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream) \
+           : act == DGM_ACT_QOQ   ? launch_fused_fe<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream)   \
+                                  : launch_fused_fe<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream); \
   }
   DGM_FUSED_SHAPE(3072, 1280, 0)
   DGM_FUSED_SHAPE(512, 256, 1)
