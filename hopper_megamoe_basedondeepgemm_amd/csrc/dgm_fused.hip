@@ -206,7 +206,7 @@ struct FusedSmem {
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
   int is_last;
-  int claimv[2];
+  int claimv[3];            // [0] the claim ahead, [1] prefetch decision, [2] L2: a complete expert
 };
 
 // Exclusive scan of (count, active flag) over n <= FUSED_MAX_LOCAL experts.
@@ -598,8 +598,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int R = p.M * p.topk;
   int* exit_cnt = p.counters + CNT_EXIT;
   int* err = p.counters + CNT_ERROR;
-  int* l1_done = p.counters + CNT_L1;
-  int* comb = p.counters + CNT_L1 + FUSED_MAX_LOCAL;
+  int* l1_done = p.counters + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
+  int* comb = p.counters + CNT_COMB;
   long long* st = (p.stamps && (int)blockIdx.x < p.stamp_rows) ? p.stamps + (size_t)blockIdx.x * 8 : nullptr;
   long long wait_ticks = 0, l1_load_ticks = 0, l1_sig_ticks = 0;
   if (st && tid == 0) st[0] = wall_clock();
@@ -792,6 +792,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int U1 = n_active * QN1, U2 = n_active * UPE2;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
+  int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
+  // The tile ring, shared by the two phases. With MXFP and QoQ weights the L1 phase's last item
+  // rolls into the first L2 unit's tiles (unit blockIdx.x), which then stream during the L1
+  // epilogue and the phase change instead of after it.
+  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
+  constexpr int RING = KR1 > KT2 ? KR1 : KT2;
+  constexpr bool HANDOFF = ACT != DGM_ACT_NVFP4 && KR1 >= KT2;
+  U4 wr[RING];
+  bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
 
   // ================================================================ L1 phase
   // Wave w: block pair pp = w & 3 (16 of the unit's 64 features), tile gu = w >> 2 (gate or
@@ -865,7 +874,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
-    U4 wr[KR];
     uint32_t sr[ACT == DGM_ACT_NVFP4 ? KR : 1];
     uint32_t sd[SW1], sn[SW1];
     SlabRegs<KT1, ACT, FEIN, false> pre;
@@ -899,7 +907,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const int nkey = (na << 16) | ns0;
       const bool restage = has_next && nkey != staged;
       const uint8_t* cb = tile_base(q0);
-      const uint8_t* nb = !has_next ? w1v + lane * 16 : nq == q0 ? cb : tile_base(nq);   // (no next: a dummy read)
+      // no next L1 item: ring slots < KT2 take the first L2 unit's tiles (when that unit is
+      // this workgroup's), the rest dummy reads
+      const bool hand = HANDOFF && !has_next && (p.phases & 2) && (int)blockIdx.x < U2;
+      const uint8_t* dummy = w1v + lane * 16;
+      const uint8_t* nb = !has_next ? (hand ? p.w2v + ((size_t)s.act[blockIdx.x / UPE2] * NB2 + (NW * RB2) * (blockIdx.x % UPE2) + RB2 * wv) * KT2 * 1024 + lane * 16 : dummy)
+                                    : nq == q0 ? cb : tile_base(nq);
+      const uint8_t* nbd = hand ? dummy : nb;
+      if (hand) handed = true;
       const uint8_t* csb = ACT == DGM_ACT_NVFP4 ? stile_base(q0) : nullptr;
       const uint8_t* nsb = ACT != DGM_ACT_NVFP4 ? nullptr
                            : !has_next ? reinterpret_cast<const uint8_t*>(w1s) + slane : nq == q0 ? csb : stile_base(nq);
@@ -945,7 +960,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           v4i at = mfma_i8_16x16x64(qoq_codes(w.x, w.y), lo4(bop), v4i{0, 0, 0, 0});
           at = mfma_i8_16x16x64(qoq_codes(w.z, w.w), hi4(bop), at);
           if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, at);
-          else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, at);
+          else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, at);
           if constexpr (t > 0) promote(prev, md_n, x_n);         // tile t - 1
           md_n = md_c;
           x_n = x_c;
@@ -978,7 +993,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
             sr[t % KR] = ld_stream32_after(csb, (t + KR) * 128, acc);
           } else {
-            wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
+            wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);     // (no hand-off)
             sr[t % KR] = ld_stream32_after(nsb, (t + KR - KT1) * 128, acc);
           }
         });
@@ -993,7 +1008,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
           acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, acc, (int)sd[t >> 2], (int)bsw);
           if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
-          else wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);
+          else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, acc);
         });
       }
       // all but this loop's KR youngest tile loads (and scale loads) are done: the previous
@@ -1014,7 +1029,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const bool bcast = last_slab && q1 < U1;
       if (tid == 0 && bcast) s.claimv[0] = ahead;
       __syncthreads();                                   // (1) up sums visible, slab free
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pend = -1;
       int q2 = U1;
       if (bcast) {
@@ -1131,9 +1146,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         s0 += 16;
       }
     }
-    wait_mem();               // the last item's stores (and the dummy ring reads)
-    __syncthreads();
-    if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (p.phases & 2) {
+      l1_pend = pend;         // (its stores complete while the L2 phase issues its first loads)
+    } else {
+      wait_mem();             // the last item's stores (and the dummy ring reads)
+      __syncthreads();
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   if (st && tid == 0) st[2] = wall_clock();
 
@@ -1148,7 +1167,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // bumps the arrival counters of its (token, 128-row block)s (no return value).
   if (p.phases & 2) {
     static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
-    int* claim = p.counters + CNT_CLAIM + 1;
+    int* claim = p.counters + CNT_CLAIM + CNT_LINE;
     const uint8_t* w2v = p.w2v;
     const uint32_t* w2s = p.w2s;
     const float* w2r = p.w2r;
@@ -1213,17 +1232,37 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q0 = (int)blockIdx.x < U2 ? (int)blockIdx.x : U2;
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
-    U4 wr[KT2];
+    static_assert(KT2 <= RING, "the L2 ring in the shared tile registers");
     uint32_t sr[ACT == DGM_ACT_NVFP4 ? KT2 : 1];
     uint32_t sd[SW2], sn[SW2];
     SlabRegs<KT2, ACT, true> pre;
-    int ready = -1;           // an active expert whose L1 arrival is known complete
+    int ready = -1;           // (thread 0) an active expert whose L1 arrival is known complete
     bool seen = false;        // (stamps) first L1 arrival observed
     int pv = -1, ps0 = 0;     // the previous item, whose arrivals are not sent yet
+    int pr_a = 0, pr_n = 0;
+    if (p.phases & 1) {
+      // probes of the L1 arrivals of the first two units' experts, answered while the L1
+      // phase's last stores complete
+      if (tid == 0 && q0 < U2) {
+        pr_a = __hip_atomic_load(&l1_done[(q0 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q1 < U2) pr_n = __hip_atomic_load(&l1_done[(q1 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // the L1 phase's last unit: its stores have completed (every wave) -> its arrival, before
+      // any wait on other workgroups' arrivals
+      wait_mem();
+      __syncthreads();
+      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && q0 < U2 && pr_a >= QN1) ready = q0 / UPE2;
+    }
+    // (thread 0) the second unit's expert when its probe found it complete (LDS: read once, by
+    // the first item's prefetch check)
+    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= QN1 ? q1 / UPE2 : -1;
     if (q0 < U2) {
-      const uint8_t* b = tile_base(q0);
+      if (!handed) {          // (unit q0 = blockIdx.x: handed over by the L1 phase otherwise)
+        const uint8_t* b = tile_base(q0);
 #pragma unroll
-      for (int k = 0; k < KT2; ++k) wr[k] = ld_stream(b + k * 1024);
+        for (int k = 0; k < KT2; ++k) wr[k] = ld_stream(b + k * 1024);
+      }
       if constexpr (ACT == DGM_ACT_NVFP4) {
         const uint8_t* sb = stile_base(q0);
 #pragma unroll
@@ -1238,7 +1277,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
         if (a != ready) {
-          if (tid == 0 && (p.phases & 1)) spin_until(&l1_done[a], QN1, p.spin_limit, err);
+          if (tid == 0 && (p.phases & 1)) spin_until(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err);
           ready = a;
         }
         __syncthreads();
@@ -1270,8 +1309,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       bool pf = false;
       if (has_next && nkey != key) {
         if (tid == 0)
-          s.claimv[1] = !(p.phases & 1) || na == ready ||
-                        __hip_atomic_load(&l1_done[na], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
+          s.claimv[1] = !(p.phases & 1) || na == ready || na == s.claimv[2] ||
+                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
         __syncthreads();
         pf = __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0;
         if (pf) {
@@ -1496,9 +1535,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   }
   __syncthreads();
   if (s.is_last) {
-    for (int a = tid; a < n_active; a += FT) __hip_atomic_store(&l1_done[a], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int a = tid; a < n_active; a += FT) __hip_atomic_store(&l1_done[a * CNT_LINE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int i = tid; i < p.M * NBL2; i += FT) __hip_atomic_store(&comb[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < 2) __hip_atomic_store(p.counters + CNT_CLAIM + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < 2) __hip_atomic_store(p.counters + CNT_CLAIM + tid * CNT_LINE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < GRID_SLOTS)
       __hip_atomic_store(p.counters + CNT_GRID + tid * GRID_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_mem();

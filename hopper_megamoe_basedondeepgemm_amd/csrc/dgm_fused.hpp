@@ -8,12 +8,15 @@ constexpr int FUSED_MAX_LOCAL = 512;     // local experts
 constexpr int FUSED_MAX_TOKENS = 256;    // tokens per call
 constexpr int FUSED_MAX_NB64 = 64;       // hidden / 64 (hidden <= 4096); combine uses hidden / 128
 
-// int32 counters in the buffer's counter region
+// int32 counters in the buffer's counter region. Counters that many workgroups update at once
+// sit on 64-byte lines of their own (device-scope atomics on one line serialize).
+constexpr int CNT_LINE = 16;             // ints per 64-byte line
 constexpr int CNT_EXIT = 0;              // workgroups finished (last one clears everything)
 constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
-constexpr int CNT_CLAIM = 2;             // next unclaimed L1 unit, then [3] next unclaimed L2 unit
-constexpr int CNT_L1 = 64;               // [FUSED_MAX_LOCAL] L1 units done per active expert slot
-constexpr int CNT_TOTAL = CNT_L1 + FUSED_MAX_LOCAL + FUSED_MAX_TOKENS * FUSED_MAX_NB64;  // + combine counters
+constexpr int CNT_CLAIM = CNT_LINE;      // next unclaimed L1 unit; [CNT_CLAIM + CNT_LINE]: L2 unit
+constexpr int CNT_L1 = 4 * CNT_LINE;     // L1 units done per active expert slot, one line each
+constexpr int CNT_COMB = CNT_L1 + FUSED_MAX_LOCAL * CNT_LINE;   // combine arrivals per (token, block)
+constexpr int CNT_TOTAL = CNT_COMB + FUSED_MAX_TOKENS * FUSED_MAX_NB64;
 // in-kernel frontend: workgroups past the frontend work, counted on GRID_SLOTS counters (one
 // per 64-byte line; workgroup g arrives on slot g % GRID_SLOTS), so the arrivals do not all
 // serialize on one address
