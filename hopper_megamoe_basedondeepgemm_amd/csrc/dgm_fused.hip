@@ -599,7 +599,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   int* exit_cnt = p.counters + CNT_EXIT;
   int* err = p.counters + CNT_ERROR;
   int* l1_done = p.counters + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
-  int* comb = p.counters + CNT_COMB;
+  int* comb = p.counters + CNT_COMB;        // pair i: comb[i * CNT_LINE]
   long long* st = (p.stamps && (int)blockIdx.x < p.stamp_rows) ? p.stamps + (size_t)blockIdx.x * 8 : nullptr;
   long long wait_ticks = 0, l1_load_ticks = 0, l1_sig_ticks = 0;
   if (st && tid == 0) st[0] = wall_clock();
@@ -1217,7 +1217,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const int a = v / UPE2, b = v % UPE2;
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
       for (int i = i0; i < 16 * RB2 && i / RB2 < n; i += FT)
-        __hip_atomic_fetch_add(&comb[(s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2], 1,
+        __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2) * CNT_LINE], 1,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units g and G + g first, then claims (offset by 2 G), as in the L1 phase
@@ -1506,7 +1506,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {
       if (tid < PG && i0 + tid < P) {
         const int need = s.nslot[(i0 + tid) / NBL2];
-        if (need > 0) spin_until(&comb[i0 + tid], need, p.spin_limit, err);
+        if (need > 0) spin_until(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err);
       }
       __syncthreads();
       const int i = i0 + tid / CB;
@@ -1536,7 +1536,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   __syncthreads();
   if (s.is_last) {
     for (int a = tid; a < n_active; a += FT) __hip_atomic_store(&l1_done[a * CNT_LINE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int i = tid; i < p.M * NBL2; i += FT) __hip_atomic_store(&comb[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = tid; i < p.M * NBL2; i += FT) __hip_atomic_store(&comb[i * CNT_LINE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < 2) __hip_atomic_store(p.counters + CNT_CLAIM + tid * CNT_LINE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid < GRID_SLOTS)
       __hip_atomic_store(p.counters + CNT_GRID + tid * GRID_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -15,8 +15,8 @@ constexpr int CNT_EXIT = 0;              // workgroups finished (last one clears
 constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
 constexpr int CNT_CLAIM = CNT_LINE;      // next unclaimed L1 unit; [CNT_CLAIM + CNT_LINE]: L2 unit
 constexpr int CNT_L1 = 4 * CNT_LINE;     // L1 units done per active expert slot, one line each
-constexpr int CNT_COMB = CNT_L1 + FUSED_MAX_LOCAL * CNT_LINE;   // combine arrivals per (token, block)
-constexpr int CNT_TOTAL = CNT_COMB + FUSED_MAX_TOKENS * FUSED_MAX_NB64;
+constexpr int CNT_COMB = CNT_L1 + FUSED_MAX_LOCAL * CNT_LINE;   // combine arrivals per (token, 128-row block), one line each
+constexpr int CNT_TOTAL = CNT_COMB + FUSED_MAX_TOKENS * (FUSED_MAX_NB64 / 2) * CNT_LINE;
 // in-kernel frontend: workgroups past the frontend work, counted on GRID_SLOTS counters (one
 // per 64-byte line; workgroup g arrives on slot g % GRID_SLOTS), so the arrivals do not all
 // serialize on one address
