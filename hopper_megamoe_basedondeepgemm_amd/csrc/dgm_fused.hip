@@ -254,18 +254,33 @@ DGM_DEV void scan_experts(S& s, int n) {
   __syncthreads();
 }
 
-// The pool table of R <= 64 routes by one wave. Keys = local expert << 16 | route id (routes
-// of other ranks sort last), one per lane; sorted, they are the canonical pool order (expert
-// asc, route asc = token asc, slot asc), and expert boundaries give the active list, offsets
-// and counts. Each key's rank is counted against every key (broadcast by readlane), then the
-// keys are scattered to their ranks and read back in order. Writes s.routes, s.act, s.aoff,
-// s.meta[0..1], s.cnt (of active experts; the rest must be zero) and s.nslot (must be zero).
+// The pool table of R <= 64 routes. Keys = local expert << 16 | route id (routes of other
+// ranks sort last), one per lane; sorted, they are the canonical pool order (expert asc, route
+// asc = token asc, slot asc), and expert boundaries give the active list, offsets and counts.
+// Each key's rank is counted against every key (broadcast by readlane): wave w counts against
+// keys 64 / NW * w .. +64 / NW - 1 into part[w][lane] (route_key_ranks, every wave), then one
+// wave adds the parts, scatters the keys to their ranks and reads them back in order
+// (wave_dispatch). Writes s.routes, s.act, s.aoff, s.meta[0..1], s.cnt (of active experts; the
+// rest must be zero) and s.nslot (must be zero).
+DGM_DEV uint32_t route_key(int e0, int lane) {
+  return ((e0 < 0 ? 0xffffu : (uint32_t)e0) << 16) | (uint32_t)lane;
+}
 template <class S>
-DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane) {
-  const int e0 = lane < R ? s.exp_of_route[lane] : -1;
-  uint32_t key = ((e0 < 0 ? 0xffffu : (uint32_t)e0) << 16) | (uint32_t)lane;
+DGM_DEV void route_key_ranks(S& s, int R, int lane, int wv, int* part) {
+  const uint32_t key = route_key(lane < R ? s.exp_of_route[lane] : -1, lane);
+  constexpr int QW = 64 / NW;
+  static_assert(64 % NW == 0, "keys per wave");
+  int rk = 0;
+#pragma unroll
+  for (int j = 0; j < QW; ++j) rk += (uint32_t)__builtin_amdgcn_readlane((int)key, QW * wv + j) < key ? 1 : 0;
+  part[wv * 64 + lane] = rk;
+}
+template <class S>
+DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane, const int* part) {
+  uint32_t key = route_key(lane < R ? s.exp_of_route[lane] : -1, lane);
   int rank = 0;
-  for (int q = 0; q < 64; ++q) rank += (uint32_t)__builtin_amdgcn_readlane((int)key, q) < key ? 1 : 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) rank += part[w * 64 + lane];
   // (the route-table slots double as the sort buffer: keys of the routes are unique)
   s.routes[rank] = (int)key;
   key = (uint32_t)s.routes[lane];
@@ -728,8 +743,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   }
   __syncthreads();
   if (R <= 64) {
-    // one wave sorts the routes (the other waves wait at the barrier)
-    if (wv == 0) wave_dispatch(s, R, p.topk, lane);
+    // key ranks counted by every wave, then one wave sorts the routes (the other waves wait
+    // at the barrier); the parts are staged in the L1 epilogue's up-sum buffer (unused until
+    // then)
+    int* part = reinterpret_cast<int*>(&s.upv[0][0][0]);
+    static_assert(sizeof(s.upv) >= NW * 64 * sizeof(int), "rank parts");
+    route_key_ranks(s, R, lane, wv, part);
+    __syncthreads();
+    if (wv == 0) wave_dispatch(s, R, p.topk, lane, part);
     __syncthreads();
   } else {
     // counts, expert offsets, then each route placed in its expert's segment in arrival order
