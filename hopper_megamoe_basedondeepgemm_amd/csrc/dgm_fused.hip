@@ -610,6 +610,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   static_assert(I % 64 == 0, "L1 units are 64 intermediate features");
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave index: scalar
+  // one field of each 64-byte line of the parameters, read at once: the scalar cache then holds
+  // every line, and the later (lazy) parameter reads hit it instead of each paying a round trip
+  static_assert(sizeof(FusedParams) <= 256, "four parameter lines");
+  asm volatile("" ::"s"(p.w1v), "s"(p.x), "s"(p.pool_out), "s"(p.hidden));
   const int R = p.M * p.topk;
   int* exit_cnt = p.counters + CNT_EXIT;
   int* err = p.counters + CNT_ERROR;
