@@ -904,7 +904,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     SlabRegs<KT1, ACT, FEIN, false> pre;
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
     if (q0 < U1) {
-      load_slab(pre, q0 / QN1, 0);      // (ahead of the tiles: the store below waits for it only)
+      // The first item's slab is staged before any tile load is issued: every workgroup
+      // starts at once, and tile loads issued first would queue the slab loads (and so the
+      // barrier, and every wave's first K loop) behind the whole ring of every wave.
+      load_slab(pre, q0 / QN1, 0);
+      load_scales(q0, sd);
+      slab_store(s, pre);
+      staged = (q0 / QN1) << 16;
+      __syncthreads();
       const uint8_t* b = tile_base(q0);
 #pragma unroll
       for (int k = 0; k < KR; ++k) wr[k] = ld_stream(b + k * 1024);
@@ -913,14 +920,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
       }
-      load_scales(q0, sd);
       // the first claim, issued after the first item's loads: every workgroup claims at once
-      // here, and the slab store below waits for the slab loads (older) but not for this
-      // contended atomic's return (memory operations complete in issue order)
+      // here, and nothing waits for this contended atomic's return before the next item
       if (tid == 0 && 2 * G < U1) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      slab_store(s, pre);
-      staged = (q0 / QN1) << 16;
-      __syncthreads();
     }
     while (q0 < U1) {
       const int a = q0 / QN1, q = q0 % QN1;
