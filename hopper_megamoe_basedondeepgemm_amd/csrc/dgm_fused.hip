@@ -945,8 +945,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* csb = ACT == DGM_ACT_NVFP4 ? stile_base(q0) : nullptr;
       const uint8_t* nsb = ACT != DGM_ACT_NVFP4 ? nullptr
                            : !has_next ? reinterpret_cast<const uint8_t*>(w1s) + slane : nq == q0 ? csb : stile_base(nq);
-      if (has_next && nq != q0) load_scales(nq, sn);
-      if (restage) load_slab(pre, na, ns0);
+      // (MXFP, QoQ: the next item's scale and slab loads are issued in the K loop, after the
+      // tile loads of its first KT1 - KR ops, so that the loop starts as soon as its first tile
+      // is in)
+      if constexpr (ACT == DGM_ACT_NVFP4) {
+        if (has_next && nq != q0) load_scales(nq, sn);
+        if (restage) load_slab(pre, na, ns0);
+      }
       const float wt_r = s.slab_w[c];
       const float sx = ACT == DGM_ACT_QOQ ? s.xsc[c] : 1.f;       // QoQ: the token's activation scale
       const long long t_k0 = st ? wall_clock() : 0;
@@ -988,6 +993,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           at = mfma_i8_16x16x64(qoq_codes(w.z, w.w), hi4(bop), at);
           if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, at);
           else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, at);
+          if constexpr (t == KT1 - KR) {
+            if (has_next && nq != q0) load_scales(nq, sn);
+            if (restage) load_slab(pre, na, ns0);
+          }
           if constexpr (t > 0) promote(prev, md_n, x_n);         // tile t - 1
           md_n = md_c;
           x_n = x_c;
@@ -1036,6 +1045,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, acc, (int)sd[t >> 2], (int)bsw);
           if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
           else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, acc);
+          if constexpr (t == KT1 - KR) {
+            if (has_next && nq != q0) load_scales(nq, sn);
+            if (restage) load_slab(pre, na, ns0);
+          }
         });
       }
       // all but this loop's KR youngest tile loads (and scale loads) are done: the previous
