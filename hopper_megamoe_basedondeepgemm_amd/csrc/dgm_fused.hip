@@ -920,10 +920,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
       }
-      // the first claim, issued after the first item's loads: every workgroup claims at once
-      // here, and nothing waits for this contended atomic's return before the next item
-      if (tid == 0 && 2 * G < U1) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    bool more = 2 * G < U1;   // the claim counter has not run out
     while (q0 < U1) {
       const int a = q0 / QN1, q = q0 % QN1;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
@@ -954,6 +952,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       const float wt_r = s.slab_w[c];
       const float sx = ACT == DGM_ACT_QOQ ? s.xsc[c] : 1.f;       // QoQ: the token's activation scale
+      // the unit after q1, claimed at the start of the item that finishes q0 (after its loads;
+      // the value is read in this item's epilogue, by when it has returned)
+      if (tid == 0 && last_slab && q1 < U1 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -1065,9 +1066,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
       }
-      // the unit after q1 (claimed one item ago), broadcast here
+      // the unit after q1 (claimed at this item's start), broadcast here
       const bool bcast = last_slab && q1 < U1;
-      if (tid == 0 && bcast) s.claimv[0] = ahead;
+      if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) up sums visible, slab free
       if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pend = -1;
@@ -1075,11 +1076,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (bcast) {
         const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
         q2 = raw >= 0 && 2 * G + raw < U1 ? 2 * G + raw : U1;
-        if (q2 < U1) {
-          if (tid == 0) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          ahead = -1;
-        }
+        if (q2 >= U1) more = false;
       }
       if (restage) {
         slab_store(s, pre);
@@ -1264,11 +1261,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     __syncthreads();
     const int G = gridDim.x;
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
-    // used as returned (any arithmetic on it here would wait for every load issued before it).
-    // The first claim is issued after the first item's slab is staged (the staging waits
-    // would otherwise also wait for this atomic's return).
+    // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    bool claimed = false;
+    bool more = 2 * G < U2;   // the claim counter has not run out
     int q0 = (int)blockIdx.x < U2 ? (int)blockIdx.x : U2;
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
@@ -1336,10 +1331,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         staged = key;
         __syncthreads();
       }
-      if (!claimed) {
-        claimed = true;
-        if (tid == 0 && 2 * G < U2) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
       const bool has_next = nq < U2;
@@ -1372,6 +1363,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int jb = 0; jb < RB2; ++jb)
           s1r[jb] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w2r + (blk_of(q0) + jb) * 16 + 4 * kq));
       }
+      // the unit after q1, claimed at the start of the item that finishes q0 (the value is read
+      // in this item's epilogue)
+      if (tid == 0 && last_slab && q1 < U2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
       // read from LDS two ops ahead
       v4f acc[RB2];
@@ -1498,7 +1492,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         }
       }
       const bool bcast = last_slab && q1 < U2;
-      if (tid == 0 && bcast) s.claimv[0] = ahead;
+      if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) previous outputs complete, slab free
       if (pv >= 0) arrive(pv, ps0);
       pv = q0;
@@ -1507,11 +1501,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (bcast) {
         const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
         q2 = raw >= 0 && 2 * G + raw < U2 ? 2 * G + raw : U2;
-        if (q2 < U2) {
-          if (tid == 0) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          ahead = -1;
-        }
+        if (q2 >= U2) more = false;
       }
       if (pf) {
         slab_store(s, pre);
