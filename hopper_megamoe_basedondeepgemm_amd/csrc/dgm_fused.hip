@@ -818,13 +818,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
   int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
-  // The tile ring, shared by the two phases. With MXFP and QoQ weights the L1 phase's last item
-  // rolls into the first L2 unit's tiles (unit blockIdx.x), which then stream during the L1
-  // epilogue and the phase change instead of after it.
+  // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last
+  // item rolls into the first L2 unit's tiles (unit blockIdx.x), which then stream during the
+  // L1 epilogue and the phase change instead of after it.
   constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
   constexpr int RING = KR1 > KT2 ? KR1 : KT2;
-  constexpr bool HANDOFF = ACT != DGM_ACT_NVFP4 && KR1 >= KT2;
+  constexpr bool HANDOFF = KR1 >= KT2;
   U4 wr[RING];
+  uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
 
   // ================================================================ L1 phase
@@ -899,7 +900,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
-    uint32_t sr[ACT == DGM_ACT_NVFP4 ? KR : 1];
     uint32_t sd[SW1], sn[SW1];
     SlabRegs<KT1, ACT, FEIN, false> pre;
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
@@ -941,8 +941,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* nbd = hand ? dummy : nb;
       if (hand) handed = true;
       const uint8_t* csb = ACT == DGM_ACT_NVFP4 ? stile_base(q0) : nullptr;
+      const uint8_t* sdummy = reinterpret_cast<const uint8_t*>(w1s) + slane;
       const uint8_t* nsb = ACT != DGM_ACT_NVFP4 ? nullptr
-                           : !has_next ? reinterpret_cast<const uint8_t*>(w1s) + slane : nq == q0 ? csb : stile_base(nq);
+                           : !has_next ? (hand ? reinterpret_cast<const uint8_t*>(p.w2s) + ((size_t)s.act[blockIdx.x / UPE2] * NB2 + (NW * RB2) * (blockIdx.x % UPE2) + RB2 * wv) * KT2 * 128 + slane : sdummy)
+                                       : nq == q0 ? csb : stile_base(nq);
+      const uint8_t* nsbd = hand ? sdummy : nsb;
       // (MXFP, QoQ: the next item's scale and slab loads are issued in the K loop, after the
       // tile loads of its first KT1 - KR ops, so that the loop starts as soon as its first tile
       // is in)
@@ -1030,8 +1033,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
             sr[t % KR] = ld_stream32_after(csb, (t + KR) * 128, acc);
           } else {
-            wr[t % KR] = ld_stream_after(nb, (t + KR - KT1) * 1024, acc);     // (no hand-off)
-            sr[t % KR] = ld_stream32_after(nsb, (t + KR - KT1) * 128, acc);
+            wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, acc);
+            sr[t % KR] = ld_stream32_after(t + KR - KT1 < KT2 ? nsb : nsbd, (t + KR - KT1) * 128, acc);
           }
         });
       } else {
@@ -1268,7 +1271,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q1 = G + (int)blockIdx.x < U2 ? G + (int)blockIdx.x : U2;
     int s0 = 0;
     static_assert(KT2 <= RING, "the L2 ring in the shared tile registers");
-    uint32_t sr[ACT == DGM_ACT_NVFP4 ? KT2 : 1];
     uint32_t sd[SW2], sn[SW2];
     SlabRegs<KT2, ACT, true> pre;
     int ready = -1;           // (thread 0) an active expert whose L1 arrival is known complete
@@ -1297,11 +1299,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         const uint8_t* b = tile_base(q0);
 #pragma unroll
         for (int k = 0; k < KT2; ++k) wr[k] = ld_stream(b + k * 1024);
-      }
-      if constexpr (ACT == DGM_ACT_NVFP4) {
-        const uint8_t* sb = stile_base(q0);
+        if constexpr (ACT == DGM_ACT_NVFP4) {
+          const uint8_t* sb = stile_base(q0);
 #pragma unroll
-        for (int k = 0; k < KT2; ++k) sr[k] = ld_stream32(sb + k * 128);
+          for (int k = 0; k < KT2; ++k) sr[k] = ld_stream32(sb + k * 128);
+        }
       }
       load_scales(q0, sd);
     }
