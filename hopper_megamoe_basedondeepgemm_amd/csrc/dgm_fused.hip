@@ -827,6 +827,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   U4 wr[RING];
   uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
+  // L2 unit v = (active expert a, 128 RB2-row slice b): this wave's first 16-row block of it
+  auto l2_blk = [wv](int v) __attribute__((always_inline)) {
+    return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
+  };
 
   // ================================================================ L1 phase
   // Wave w: block pair pp = w & 3 (16 of the unit's 64 features), tile gu = w >> 2 (gate or
@@ -936,14 +940,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       // this workgroup's), the rest dummy reads
       const bool hand = HANDOFF && !has_next && (p.phases & 2) && (int)blockIdx.x < U2;
       const uint8_t* dummy = w1v + lane * 16;
-      const uint8_t* nb = !has_next ? (hand ? p.w2v + ((size_t)s.act[blockIdx.x / UPE2] * NB2 + (NW * RB2) * (blockIdx.x % UPE2) + RB2 * wv) * KT2 * 1024 + lane * 16 : dummy)
+      const uint8_t* nb = !has_next ? (hand ? p.w2v + l2_blk(blockIdx.x) * KT2 * 1024 + lane * 16 : dummy)
                                     : nq == q0 ? cb : tile_base(nq);
       const uint8_t* nbd = hand ? dummy : nb;
       if (hand) handed = true;
       const uint8_t* csb = ACT == DGM_ACT_NVFP4 ? stile_base(q0) : nullptr;
       const uint8_t* sdummy = reinterpret_cast<const uint8_t*>(w1s) + slane;
       const uint8_t* nsb = ACT != DGM_ACT_NVFP4 ? nullptr
-                           : !has_next ? (hand ? reinterpret_cast<const uint8_t*>(p.w2s) + ((size_t)s.act[blockIdx.x / UPE2] * NB2 + (NW * RB2) * (blockIdx.x % UPE2) + RB2 * wv) * KT2 * 128 + slane : sdummy)
+                           : !has_next ? (hand ? reinterpret_cast<const uint8_t*>(p.w2s) + l2_blk(blockIdx.x) * KT2 * 128 + slane : sdummy)
                                        : nq == q0 ? csb : stile_base(nq);
       const uint8_t* nsbd = hand ? sdummy : nsb;
       // (MXFP, QoQ: the next item's scale and slab loads are issued in the K loop, after the
@@ -1212,9 +1216,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const uint32_t* w2s = p.w2s;
     const float* w2r = p.w2r;
     const int topk = p.topk;
-    auto blk_of = [wv](int v) __attribute__((always_inline)) {
-      return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
-    };
+    const auto blk_of = l2_blk;
     auto tile_base = [w2v, lane, blk_of](int v) __attribute__((always_inline)) {
       return w2v + blk_of(v) * KT2 * 1024 + lane * 16;
     };
