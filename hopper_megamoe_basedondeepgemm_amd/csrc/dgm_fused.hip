@@ -320,6 +320,24 @@ DGM_DEV bool spin_until(const int* p, int target, int limit, int* err) {
   }
   return true;
 }
+// The same wait with two reads in flight: each read is issued before the previous one is tested
+// (two reads per round, in alternating registers: a register copy would wait for the newer
+// read), so a change is seen about half a memory round trip sooner.
+DGM_DEV bool spin_until2(const int* p, int target, int limit, int* err) {
+  int v0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int n = 0;; n += 2) {
+    const int v1 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v0 >= target) return true;
+    __builtin_amdgcn_s_sleep(1);
+    v0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v1 >= target) return true;
+    if (n > limit) {
+      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
 
 // Stage the B slab (16 columns = rows row_of(c) of a [rows, KT*128] activation matrix with
 // row_bytes and per-32 E8M0 scales) into LDS in fragment order. Column c >= n is zero.
@@ -1554,7 +1572,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {
       if (tid < PG && i0 + tid < P) {
         const int need = s.nslot[(i0 + tid) / NBL2];
-        if (need > 0) spin_until(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err);
+        if (need > 0) spin_until2(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err);
       }
       __syncthreads();
       const int i = i0 + tid / CB;
