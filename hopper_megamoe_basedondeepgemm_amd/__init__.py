@@ -6,7 +6,7 @@ from . import _lib
 from .mega import (FusedSymmBuffer, get_fused_symm_buffer_for_mega_moe,
                    transform_mxfp4_weights_for_mega_moe_fused, transform_qoq_weights_for_mega_moe_fused,
                    transform_weights_for_mega_moe,
-                   fable_router_quant_topk_frontend, mxfp4_mega_moe_fused, mxfp4_mega_moe_split,
+                   fable_router_quant_topk_frontend, fable_frontend_keys, mxfp4_mega_moe_fused, mxfp4_mega_moe_split,
                    mxfp4_mega_moe_from_bf16, qoq_mega_moe_fused, qoq_mega_moe_split,
                    transform_nvfp4_weights_for_mega_moe_fused, fp4_fp4_mega_moe, nvfp4_mega_moe,
                    transform_qoq_int4_weights_for_mega_moe_sm90)
@@ -16,7 +16,8 @@ from .utils import per_token_cast_to_fp4, per_token_cast_to_fp8, ceil_div, align
 __all__ = [
     "FusedSymmBuffer", "get_fused_symm_buffer_for_mega_moe", "transform_mxfp4_weights_for_mega_moe_fused",
     "transform_qoq_weights_for_mega_moe_fused",
-    "transform_weights_for_mega_moe", "fable_router_quant_topk_frontend", "mxfp4_mega_moe_fused",
+    "transform_weights_for_mega_moe", "fable_router_quant_topk_frontend", "fable_frontend_keys",
+    "mxfp4_mega_moe_fused",
     "mxfp4_mega_moe_split", "mxfp4_mega_moe_from_bf16", "qoq_mega_moe_fused", "qoq_mega_moe_split",
     "transform_nvfp4_weights_for_mega_moe_fused", "fp4_fp4_mega_moe", "nvfp4_mega_moe",
     "transform_qoq_int4_weights_for_mega_moe_sm90", "quantization_mxfp4", "quantization_mxfp4_fused",

@@ -25,18 +25,18 @@ EXPORTS = [
     "dgm_probe_mfma_scale_sel",
     "dgm_probe_mfma_i8", "dgm_probe_mfma_f16", "dgm_probe_cvt_fp4",
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
-    "dgm_transform_qoq_int4_weights",
+    "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer",
 ]
 
 
 class BufferLayout(ctypes.Structure):
     _fields_ = [("total_bytes", ctypes.c_size_t), ("x", ctypes.c_size_t), ("x_sf", ctypes.c_size_t),
                 ("topk_idx", ctypes.c_size_t), ("topk_weights", ctypes.c_size_t),
-                ("logits", ctypes.c_size_t), ("token_flags", ctypes.c_size_t), ("pool", ctypes.c_size_t),
+                ("logits", ctypes.c_size_t), ("fe_keys", ctypes.c_size_t), ("pool", ctypes.c_size_t),
                 ("mid", ctypes.c_size_t),
                 ("mid_sf", ctypes.c_size_t), ("partials", ctypes.c_size_t), ("counters", ctypes.c_size_t),
                 ("x_row_bytes", ctypes.c_int32), ("mid_row_bytes", ctypes.c_int32),
-                ("max_routes", ctypes.c_int32)]
+                ("max_routes", ctypes.c_int32), ("max_tokens", ctypes.c_int32)]
 
 
 class MoeArgs(ctypes.Structure):
@@ -53,7 +53,8 @@ class MoeArgs(ctypes.Structure):
                 ("phase_stamp_rows", ctypes.c_int32), ("w1_row_scales", ctypes.c_void_p),
                 ("w2_row_scales", ctypes.c_void_p), ("l1_global_scales", ctypes.c_void_p),
                 ("l2_global_scales", ctypes.c_void_p), ("fe_in_mega", ctypes.c_int32),
-                ("hidden_states", ctypes.c_void_p), ("router_weight", ctypes.c_void_p)]
+                ("hidden_states", ctypes.c_void_p), ("router_weight", ctypes.c_void_p),
+                ("fe_keys", ctypes.c_void_p), ("host_error", ctypes.c_void_p), ("debug_flags", ctypes.c_int32)]
 
 
 _lib = None
@@ -94,6 +95,7 @@ def load():
         "dgm_probe_cvt_fp4": ([vp, vp, vp, vp, i32, vp], i32),
         "dgm_transform_qoq_weights": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
         "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
+        "dgm_host_device_pointer": ([vp, ctypes.POINTER(vp)], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -121,6 +123,14 @@ def require_gpu(*tensors):
     for t in tensors:
         if t is not None and not t.is_cuda:
             raise RuntimeError("MI355X path: tensors must live on the GPU (no CPU fallback)")
+
+
+def host_device_pointer(t):
+    """Device address of a pinned host tensor (for words the kernels write and the host reads)."""
+    assert t.is_pinned()
+    out = ctypes.c_void_p()
+    check(load().dgm_host_device_pointer(ctypes.c_void_p(t.data_ptr()), ctypes.byref(out)))
+    return out.value
 
 
 def layout(max_tokens, num_experts, num_local_experts, topk, hidden, intermediate, act_format):

@@ -144,26 +144,20 @@ DGM_DEV uint32_t wave_max_u32(uint32_t v) {
   return ab > cd ? ab : cd;
 }
 
-// Top-k of one token's fp32 logits row (E <= 1024, topk <= 16) by one wave. Lane l holds the
-// keys of experts l + 64 i (i < NK), sorted descending; each of the k rounds takes the
-// wave-wide maximum of the lanes' first keys (keys are distinct: they carry the expert id) and
-// the winning lane shifts its list by one. Lane k keeps slot k. Weights: w_k =
-// exp(v_k - v_0) / sum_k, the sum taken sequentially in slot order. zero_row: every slot -1 / 0.
-// balanced: slot s -> s G + (g + 7 s) % G with G = E / topk, weight 1 / topk (g = the token's
-// global index).
-template <int NK, class LoadLogit>
-DGM_DEV void select_topk_wave_nk(LoadLogit load, int E, int topk, int lane, int& idx, float& wt) {
-  // every logit is read before any key is formed (one LDS round trip, not one per key)
-  float lv[NK];
-#pragma unroll
-  for (int i = 0; i < NK; ++i) lv[i] = load(lane + 64 * i < E ? lane + 64 * i : E - 1);
+// Top-k of one token's key row (E <= 1024, topk <= 16) by one wave; load(e) returns the
+// token's key of expert e (topk_key of its logit). Lane l holds the keys of experts l + 64 i
+// (i < NK), sorted descending; each of the k rounds takes the wave-wide maximum of the lanes'
+// first keys (keys are distinct: they carry the expert id) and the winning lane shifts its list
+// by one. Lane k keeps slot k. Weights: w_k = exp(v_k - v_0) / sum_k, the sum taken
+// sequentially in slot order.
+template <int NK, class LoadKey>
+DGM_DEV void select_topk_wave_nk(LoadKey load, int E, int topk, int lane, int& idx, float& wt) {
+  // every key is read before any is used (one memory round trip, not one per key)
   uint32_t key[NK];
 #pragma unroll
-  for (int i = 0; i < NK; ++i) {
-    const int e = lane + 64 * i;
-    const uint32_t kv = topk_key(lv[i], e);
-    key[i] = e < E ? kv : 0u;
-  }
+  for (int i = 0; i < NK; ++i) key[i] = load(lane + 64 * i < E ? lane + 64 * i : E - 1);
+#pragma unroll
+  for (int i = 0; i < NK; ++i) key[i] = lane + 64 * i < E ? key[i] : 0u;
   // odd-even transposition sort, descending
 #pragma unroll
   for (int r = 0; r < NK; ++r)
@@ -198,12 +192,15 @@ DGM_DEV void select_topk_wave_nk(LoadLogit load, int E, int topk, int lane, int&
   }
 }
 
-template <class LoadLogit>
-DGM_DEV void select_topk_wave(LoadLogit load, int E, int topk, bool balanced, int g, bool zero_row, int lane,
-                              int& idx, float& wt) {
+// The key row of an unrouted token (an all-zero hidden row under DGM_FE_ZERO_ROW_UNROUTED) starts
+// with a zero key: every slot -1 / 0 (a real key is never zero: its low half is 0xFFFF - e).
+// balanced: slot s -> s G + (g + 7 s) % G with G = E / topk, weight 1 / topk (g = the token's
+// global index).
+template <class LoadKey>
+DGM_DEV void select_topk_wave(LoadKey load, int E, int topk, bool balanced, int g, int lane, int& idx, float& wt) {
   idx = -1;
   wt = 0.f;
-  if (zero_row) return;
+  if (load(0) == 0u) return;
   if (balanced) {
     const int G = E / topk;
     if (lane < topk) {
@@ -244,6 +241,15 @@ DGM_DEV v4f mfma_scale_16x16x128(v8i a, v8i b, v4f c, int sa, int sb) {
 template <int FMT_A, int FMT_B, int OPA, int OPB>
 DGM_DEV v4f mfma_scale_16x16x128_sel(v8i a, v8i b, v4f c, int sa, int sb) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FMT_A, FMT_B, OPA, sa, OPB, sb);
+}
+
+// Keeps the scale registers of a chain of block-scaled matrix-core ops allocated until the chain's
+// result `acc` exists (each use depends on it), so that no instruction inside the chain reuses a
+// register an op that reads it as its scale may still be reading.
+template <int N>
+DGM_DEV void keep_scales_until(const uint32_t (&r)[N], v4f acc) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" ::"v"(acc[0]), "v"(r[i]));
 }
 
 // D(16x16 i32) += A(16x64 int8) * B(64x16 int8), exact. Lane l supplies A row l%16 / B column

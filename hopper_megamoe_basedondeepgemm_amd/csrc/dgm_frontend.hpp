@@ -31,12 +31,13 @@ DGM_DEV void put64(uint64_t* p, uint64_t v) {
 // Router: one wave computes the logits of expert e for tokens t0 .. t0 + 3 (rows past M are
 // clamped and not written). Lane l accumulates K = 512 j + 8 l + i (j, then i ascending) with
 // fp32 FMAs of exact bf16 products, then an xor butterfly (32..1) reduces the 64 lane sums: a
-// fixed order, so the fp32 logits are reproducible bit for bit. With write_flags the wave also
-// records each token's all-zero flag (token_flags bit 0).
+// fixed order, so the fp32 logits are reproducible bit for bit. Writes the fp32 logit and the
+// top-k key (topk_key: orderable bf16 << 16 | 0xFFFF - e); with zero_unrouted, the keys of an
+// all-zero hidden row are 0 (the token is unrouted).
 template <int J, bool AGENT>
 DGM_DEV void router_wave(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int M, int E, int e,
-                         int t0, int lane, float* __restrict__ logits, int* __restrict__ token_flags,
-                         bool write_flags) {
+                         int t0, int lane, float* __restrict__ logits, uint32_t* __restrict__ keys,
+                         bool zero_unrouted) {
   constexpr int H = J * 512;
   uint4 wv[J];
   const int ee = e < E ? e : E - 1;
@@ -66,10 +67,11 @@ DGM_DEV void router_wave(const uint16_t* __restrict__ x, const uint16_t* __restr
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) acc = acc + __shfl_xor(acc, off);
-    const bool nonzero = __any(any != 0u);
-    if (lane == 0 && t0 + tt < M) {
-      if (e < E) put32<AGENT>(reinterpret_cast<uint32_t*>(logits) + (size_t)(t0 + tt) * E + e, __float_as_uint(acc));
-      if (write_flags) put32<AGENT>(reinterpret_cast<uint32_t*>(token_flags) + t0 + tt, nonzero ? 0u : 1u);
+    const bool unrouted = zero_unrouted && !__any(any != 0u);
+    if (lane == 0 && t0 + tt < M && e < E) {
+      const size_t o = (size_t)(t0 + tt) * E + e;
+      put32<AGENT>(reinterpret_cast<uint32_t*>(logits) + o, __float_as_uint(acc));
+      put32<AGENT>(keys + o, unrouted ? 0u : topk_key(acc, e));
     }
   }
 }

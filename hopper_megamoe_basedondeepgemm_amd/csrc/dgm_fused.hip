@@ -27,13 +27,13 @@
 // of tokens without a local route.
 //
 // Hand-offs between workgroups go through HBM with agent-coherent accesses only: the data
-// (intermediate codes and scales, fp32 route outputs) is written with relaxed agent-scope
+// (intermediate codes and scales, bf16 route outputs) is written with relaxed agent-scope
 // atomic stores (write-through, "sc1") and read with agent-scope atomic loads, and the
 // producer's stores have completed (s_waitcnt) before it bumps an arrival counter. No
 // agent-scope release/acquire fence is used: on this GPU those write back / invalidate a
 // whole L2 and cost tens of microseconds each.
 //   L1 unit -> mid codes + scales of its 64 features; one item later l1_done[a] += 1
-//   L2 item -> fp32 route outputs; one item later comb[t][b] += 1 per route and 128-row block
+//   L2 item -> bf16 route outputs; one item later comb[t][b] += 1 per route and 128-row block
 //   combine -> per (token, block): wait comb == the token's local routes, sum the routes in
 //   slot order (fp32) -> bf16 y
 // The last workgroup to finish clears all counters, so the next launch starts from zero.
@@ -71,9 +71,6 @@ DGM_DEV uint64_t ld_agent64(const void* p) {
   return __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 DGM_DEV uint32_t ld_agent8(const uint8_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-DGM_DEV float ld_agent_f32(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Compiler-only ordering point: memory operations after it stay after the matrix-core ops
@@ -178,10 +175,10 @@ struct FusedSmem {
   int exp_of_route[FUSED_MAX_ROUTES];
   float route_w[FUSED_MAX_ROUTES];     // routing weight of each route
   int routes[FUSED_MAX_ROUTES];
+  int prow[FUSED_MAX_ROUTES];          // per pool row: its route's row in `partials` (slot * part_rows + token)
   int act[FUSED_MAX_LOCAL];
   int aoff[FUSED_MAX_LOCAL + 1];
   int nslot[FUSED_MAX_TOKENS];
-  int tflag[FUSED_MAX_TOKENS];         // select_in_mega: the frontend's per-token flags
   int wsum[NW][2];
   int meta[4];
   union {
@@ -309,11 +306,19 @@ DGM_DEV void wave_dispatch(S& s, int R, int topk, int lane, const int* part) {
   for (int i = lane; i < base; i += 64) s.cnt[s.act[i]] = s.aoff[i + 1] - s.aoff[i];
 }
 
-DGM_DEV bool spin_until(const int* p, int target, int limit, int* err) {
+// A bounded wait expired: the error counter is set (it stays set until the caller clears it),
+// and so is the caller's host-visible word when there is one, which the host reads without
+// synchronising (vector stores; the host word with system scope).
+DGM_DEV void raise_error(int* err, int* herr) {
+  __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (herr) __hip_atomic_store(herr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+DGM_DEV bool spin_until(const int* p, int target, int limit, int* err, int* herr) {
   int n = 0;
   while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
     if (++n > limit) {
-      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      raise_error(err, herr);
       return false;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -323,7 +328,7 @@ DGM_DEV bool spin_until(const int* p, int target, int limit, int* err) {
 // The same wait with two reads in flight: each read is issued before the previous one is tested
 // (two reads per round, in alternating registers: a register copy would wait for the newer
 // read), so a change is seen about half a memory round trip sooner.
-DGM_DEV bool spin_until2(const int* p, int target, int limit, int* err) {
+DGM_DEV bool spin_until2(const int* p, int target, int limit, int* err, int* herr) {
   int v0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int n = 0;; n += 2) {
     const int v1 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -332,7 +337,7 @@ DGM_DEV bool spin_until2(const int* p, int target, int limit, int* err) {
     v0 = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (v1 >= target) return true;
     if (n > limit) {
-      __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      raise_error(err, herr);
       return false;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -631,7 +636,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // one field of each 64-byte line of the parameters, read at once: the scalar cache then holds
   // every line, and the later (lazy) parameter reads hit it instead of each paying a round trip
   static_assert(sizeof(FusedParams) <= 256, "four parameter lines");
-  asm volatile("" ::"s"(p.w1v), "s"(p.x), "s"(p.pool_out), "s"(p.hidden));
+  asm volatile("" ::"s"(p.w1v), "s"(p.x), "s"(p.partials), "s"(p.router_w));
   const int R = p.M * p.topk;
   int* exit_cnt = p.counters + CNT_EXIT;
   int* err = p.counters + CNT_ERROR;
@@ -642,7 +647,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[0] = wall_clock();
 
   // ---------------------------------------------------------------- in-kernel frontend
-  // (fe_in) router logits, zero-row flags and the activation cast, spread over the grid, with
+  // (fe_in) router logits and keys and the activation cast, spread over the grid, with
   // write-through stores; then every workgroup waits until all have arrived (the grid is what
   // the device keeps resident, so all workgroups run at once)
   if constexpr (FEIN) {
@@ -654,8 +659,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const int ngrp = (p.M + 3) / 4, npairs = p.E * ngrp;
     for (int pi = wv * G + (int)blockIdx.x; pi < npairs; pi += NW * G) {
       const int e = pi % p.E, tg = pi / p.E;
-      router_wave<J, true>(p.hidden, p.router_w, p.M, p.E, e, 4 * tg, lane, const_cast<float*>(p.logits),
-                           const_cast<int*>(p.token_flags), e == 0);
+      router_wave<J, true>(p.hidden, p.router_w, p.M, p.E, e, 4 * tg, lane, p.logits,
+                           const_cast<uint32_t*>(p.keys), (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) != 0);
     }
     uint8_t* xq = const_cast<uint8_t*>(p.x);
     uint8_t* xsf = const_cast<uint8_t*>(p.xsf);
@@ -682,7 +687,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         const int v = __hip_atomic_load(gc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__all(v >= expect)) break;
         if (it > p.spin_limit) {
-          if (lane == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (lane == 0) raise_error(err, p.host_err);
           break;
         }
         __builtin_amdgcn_s_sleep(1);
@@ -694,47 +699,42 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // ---------------------------------------------------------------- dispatch (every WG)
   for (int t = tid; t < p.M; t += FT) s.nslot[t] = 0;
   if (p.select) {
-    // top-k from the logits, as the frontend would have done: the logits of TC tokens at a
-    // time go through LDS (the slab area, unused until the L1 phase; one coalesced pass),
+    // top-k from the frontend's keys, as the frontend would have done: the keys of TC tokens at
+    // a time go through LDS (the slab area, unused until the L1 phase; one coalesced pass),
     // then one wave selects per token
-    float* lg = reinterpret_cast<float*>(&s.bst[0][0][0]);
+    uint32_t* lg = reinterpret_cast<uint32_t*>(&s.bst[0][0][0]);
     const int TC = (int)(sizeof(s.bst) / 4) / p.E;
     for (int t0 = 0; t0 < p.M; t0 += TC) {
       const int tn = p.M - t0 < TC ? p.M - t0 : TC;
       // Rounds of SB values per thread, all loaded before any is written, so that a round costs
       // one memory round trip (a load-store loop would pay one per value). The in-kernel
-      // frontend's values (written in this launch) need agent-scope loads; the frontend
+      // frontend's keys (written in this launch) need agent-scope loads; the frontend
       // kernel's are read through the cache.
-      const float* src = p.logits + (size_t)t0 * p.E;
+      const uint32_t* src = p.keys + (size_t)t0 * p.E;
       const int nv = tn * p.E;
-      const int* tfs = p.token_flags + t0 + (tid < tn ? tid : 0);
       constexpr int SB = 8;
       for (int i0 = 0; i0 < nv; i0 += SB * FT) {
-        float v[SB];
-        int fl;
+        uint32_t v[SB];
         if constexpr (FEIN) {
 #pragma unroll
-          for (int j = 0; j < SB; ++j) v[j] = ld_agent_f32(src + min(i0 + j * FT + tid, nv - 1));
-          fl = __hip_atomic_load(tfs, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int j = 0; j < SB; ++j)
+            v[j] = __hip_atomic_load(src + min(i0 + j * FT + tid, nv - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
 #pragma unroll
           for (int j = 0; j < SB; ++j) v[j] = src[min(i0 + j * FT + tid, nv - 1)];
-          fl = *tfs;
         }
 #pragma unroll
         for (int j = 0; j < SB; ++j)
           if (i0 + j * FT + tid < nv) lg[i0 + j * FT + tid] = v[j];
-        if (i0 == 0 && tid < tn) s.tflag[t0 + tid] = fl;
       }
       __syncthreads();
       for (int tt = wv; tt < tn; tt += NW) {
         const int t = t0 + tt;
         int idx;
         float wt;
-        const float* row = lg + tt * p.E;
+        const uint32_t* row = lg + tt * p.E;
         select_topk_wave([row](int e) { return row[e]; }, p.E, p.topk, (p.fe_flags & DGM_FE_FORCE_BALANCED) != 0,
-                         p.token_offset + t, (p.fe_flags & DGM_FE_ZERO_ROW_UNROUTED) && (s.tflag[t] & 1),
-                         lane, idx, wt);
+                         p.token_offset + t, lane, idx, wt);
         if (lane < p.topk) {
           const int r = t * p.topk + lane;
           const int l = idx - p.expert_begin;
@@ -756,7 +756,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       s.route_w[r] = p.topk_w[r];
     }
   }
-  for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;   // (shares LDS with the logits staging)
+  for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;   // (shares LDS with the key staging)
   if constexpr (ACT == DGM_ACT_NVFP4) {
     for (int e = tid; e < p.E_local; e += FT) {
       s.gsl[0][e] = p.gs1 ? p.gs1[e] : 1.f;
@@ -800,6 +800,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     __syncthreads();
   }
   const int n_active = s.meta[0];
+  for (int q = tid; q < s.meta[1]; q += FT) {
+    const int r = s.routes[q], t = r / p.topk;
+    s.prow[q] = (r - t * p.topk) * p.part_rows + t;
+  }
   if (st && tid == 0) st[1] = wall_clock();
   if (blockIdx.x == 0) {
     int* meta = (int*)p.pool_out;
@@ -1225,7 +1229,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // end) rolls into the next item's tiles right after the op that consumed a slot. The next
   // item's slab (intermediate rows of another expert) is loaded ahead when that expert's L1
   // arrival is already complete, else staged at the item's start after a bounded wait. Route
-  // outputs (fp32) go to `partials`; one item later, when they have completed, each route
+  // outputs (bf16) go to `partials`; one item later, when they have completed, each route
   // bumps the arrival counters of its (token, 128-row block)s (no return value).
   if (p.phases & 2) {
     static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
@@ -1348,7 +1352,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
         if (a != ready) {
-          if (tid == 0 && (p.phases & 1)) spin_until(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err);
+          if (tid == 0 && (p.phases & 1)) spin_until(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err, p.host_err);
           ready = a;
         }
         __syncthreads();
@@ -1520,12 +1524,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       // item's stores too
       wait_vm_le<ACT == DGM_ACT_NVFP4 ? 2 * KT2 : KT2>();
       if (s0 + c < n) {
-        float* dst = p.partials + (size_t)s.routes[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+        // each route's output rounded to bf16 (the reference's per-route rule), stored slot-major
+        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
 #pragma unroll
-        for (int j = 0; j < RB2; ++j) {
-          st_agent64(dst + 16 * j, (uint64_t)__float_as_uint(acc[j][0]) | ((uint64_t)__float_as_uint(acc[j][1]) << 32));
-          st_agent64(dst + 16 * j + 2, (uint64_t)__float_as_uint(acc[j][2]) | ((uint64_t)__float_as_uint(acc[j][3]) << 32));
-        }
+        for (int j = 0; j < RB2; ++j)
+          st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
+                                       ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
       }
       const bool bcast = last_slab && q1 < U2;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
@@ -1563,32 +1567,42 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[4] = wall_clock();
 
   // ================================================================ combine
-  // (token t, 128-row block b) pairs, PG consecutive pairs per pass and workgroup: wait until
-  // every local route of t has delivered block b, then sum the routes in slot order (fp32)
-  // -> bf16 y. The waits are only on L2 items, which never wait on this phase.
+  // (token t, 128-row block b) pairs, PG consecutive pairs per pass and workgroup, two rows per
+  // thread: wait until every local route of t has delivered block b, then sum the routes' bf16
+  // outputs in slot order (fp32) -> bf16 y. The waits are only on L2 items, which never wait on
+  // this phase.
   if (p.phases & 2) {
-    constexpr int CB = 16 * NW, PG = FT / CB;
+    constexpr int BR = 16 * NW, CB = BR / 2, PG = FT / CB;
     const int P = p.M * NBL2;
     for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {
       if (tid < PG && i0 + tid < P) {
         const int need = s.nslot[(i0 + tid) / NBL2];
-        if (need > 0) spin_until2(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err);
+        if (need > 0) spin_until2(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err, p.host_err);
       }
       __syncthreads();
       const int i = i0 + tid / CB;
       if (i < P) {
-        const int t = i / NBL2, row = (i % NBL2) * CB + tid % CB;
+        const int t = i / NBL2, row = (i % NBL2) * BR + 2 * (tid % CB);
         if (s.nslot[t] > 0) {              // (y rows of tokens without a local route: zeroed by workgroup 0)
-          float sum = 0.f;
+          float s0 = 0.f, s1 = 0.f;
           for (int sl = 0; sl < p.topk; ++sl)
-            if (s.exp_of_route[t * p.topk + sl] >= 0) sum += ld_agent_f32(p.partials + ((size_t)t * p.topk + sl) * H + row);
-          p.y[(size_t)t * H + row] = f32_to_bf16(sum);
+            if (s.exp_of_route[t * p.topk + sl] >= 0) {
+              const uint32_t v = __hip_atomic_load(
+                  reinterpret_cast<const uint32_t*>(p.partials + ((size_t)sl * p.part_rows + t) * H + row),
+                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              s0 += __uint_as_float(v << 16);
+              s1 += __uint_as_float(v & 0xffff0000u);
+            }
+          *reinterpret_cast<uint32_t*>(p.y + (size_t)t * H + row) =
+              (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
         }
       }
     }
   }
 
   // ---------------------------------------------------------------- teardown
+  // (test hook: a bounded wait on a counter nothing sets, with a zero spin limit)
+  if ((p.debug & 1) && blockIdx.x == 0 && tid == 0) spin_until(p.counters + CNT_NEVER, 1, 0, err, p.host_err);
   if (st && tid == 0) {
     st[6] = l1_load_ticks;
     st[7] = l1_sig_ticks;

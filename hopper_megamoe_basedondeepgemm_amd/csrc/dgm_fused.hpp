@@ -13,6 +13,7 @@ constexpr int FUSED_MAX_NB64 = 64;       // hidden / 64 (hidden <= 4096); combin
 constexpr int CNT_LINE = 16;             // ints per 64-byte line
 constexpr int CNT_EXIT = 0;              // workgroups finished (last one clears everything)
 constexpr int CNT_ERROR = 1;             // set when a bounded wait expired
+constexpr int CNT_NEVER = 2;             // never incremented: the target of the debug wait
 constexpr int CNT_CLAIM = CNT_LINE;      // next unclaimed L1 unit; [CNT_CLAIM + CNT_LINE]: L2 unit
 constexpr int CNT_L1 = 4 * CNT_LINE;     // L1 units done per active expert slot, one line each
 constexpr int CNT_COMB = CNT_L1 + FUSED_MAX_LOCAL * CNT_LINE;   // combine arrivals per (token, 128-row block), one line each
@@ -27,6 +28,8 @@ constexpr int CNT_ALL = CNT_GRID + 1024;
 inline __host__ __device__ int a256i(int x) { return (x + 255) & ~255; }
 
 struct FusedParams {
+  // (pointers first, then the scalars; the whole block is four 64-byte lines, read at kernel
+  // entry: line 0 from w1v, line 1 from x, line 2 from partials, line 3 from router_w)
   const uint8_t* w1v;
   const uint32_t* w1s;
   const uint8_t* w2v;
@@ -39,29 +42,33 @@ struct FusedParams {
   const uint8_t* xsf;
   int64_t* topk_idx;        // read, or written by workgroup 0 when select != 0
   float* topk_w;
-  const float* logits;      // select != 0: fp32 router logits [M, E] and token flags [M]
-  const int* token_flags;
+  const uint32_t* keys;     // select != 0: top-k keys [M, E] (an unrouted token's row starts with 0)
+  float* logits;            // fe_in: fp32 router logits [M, E] written beside the keys
   uint8_t* mid;
   uint8_t* mid_sf;
-  float* partials;
+  uint16_t* partials;       // bf16 route outputs [topk][part_rows][H] (slot-major)
   uint16_t* y;
   uint8_t* pool_out;
   int* recv_stats;
   int* counters;
-  long long* stamps;     // optional [stamp_rows][8] wall-clock stamps (see k_megamoe)
-  int stamp_rows;
-  int M, topk, expert_begin, E_local;
-  int select, fe_flags, token_offset, E;   // select the top-k in the prologue (DGM_FE_* flags)
-  int fe_in;                // run the frontend (router + cast) in the kernel first: needs select
+  int* host_err;            // optional host-visible word set with the error counter (NULL: none)
+  long long* stamps;        // optional [stamp_rows][8] wall-clock stamps (see k_megamoe)
   const uint16_t* hidden;   // fe_in: bf16 [M, H] hidden states and bf16 [E, H] router weights
   const uint16_t* router_w;
-  float clamp;
-  int fast_math;
+  int stamp_rows;
+  int M, topk, expert_begin, E_local;
+  int fe_flags, token_offset, E;   // DGM_FE_* flags of the top-k selection, row 0's global id, experts
+  int part_rows;            // rows per slot of `partials` (the buffer's max_tokens)
   int spin_limit;
+  float clamp;
+  int16_t select;           // select the top-k in the prologue from `keys`
+  int16_t fe_in;            // run the frontend (router + cast) in the kernel first: needs select
+  int16_t fast_math;
   // Phases run by this launch: bit 0 dispatch + L1 (intermediate rows to `mid`, recv stats),
   // bit 1 L2 + combine. 3 = the whole layer; 1 then 2 = the split API's two launches (the
   // second reads the top-k written by the first and does not wait for L1 arrivals).
-  int phases;
+  int16_t phases;
+  int16_t debug;            // bit 0: one bounded wait that expires (tests of the error reporting)
 };
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream);

@@ -60,22 +60,20 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
 
 // ------------------------------------------------------------------ frontend
 // Router rows of the grid (by < ceil(M / 4)): wave w of workgroup (bx, by) computes the logits
-// of expert 4 bx + w for tokens 4 by .. +3 (router_wave: fixed accumulation order,
-// bit-reproducible fp32 logits); workgroups with bx == 0 also record each token's all-zero
-// flag. Cast rows (the rest of the grid, running beside the router rows rather than after
+// and top-k keys of expert 4 bx + w for tokens 4 by .. +3 (router_wave: fixed accumulation
+// order, bit-reproducible fp32 logits; zero keys for an all-zero row when zero_unrouted). Cast rows (the rest of the grid, running beside the router rows rather than after
 // them): MXFP4 / MXFP8 8 lanes per 32-element group, NVFP4 4 lanes per 16-element group, QoQ
 // one wave per token (dgm_frontend.hpp).
 template <int J>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
-                                                  int* __restrict__ token_flags, uint8_t* __restrict__ q,
-                                                  uint8_t* __restrict__ sf) {
+                                                  uint32_t* __restrict__ keys, int zero_unrouted,
+                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
   constexpr int H = J * 512;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ry = (M + 3) / 4;
   if ((int)blockIdx.y < ry) {
-    router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, token_flags,
-                          blockIdx.x == 0 && wave == 0);
+    router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, keys, zero_unrouted != 0);
     return;
   }
   const int cy = (int)gridDim.y - ry, by = (int)blockIdx.y - ry;
@@ -93,22 +91,22 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
 }
 
 // ------------------------------------------------------------------ top-k + softmax
-// One wave per token: keys orderable(bf16(logit)) << 16 | (0xFFFF - e) (-0 -> +0), k rounds
-// of a wave-wide max select; softmax w_k = exp(v_k - v_0) / sum (sequential sum). Zero rows
-// (token_flags bit 0, with DGM_FE_ZERO_ROW_UNROUTED) get idx -1 / weight 0; forced-balanced
-// routing (DGM_FE_FORCE_BALANCED) gives slot s -> s G + (g + 7 s) % G with weight 1 / topk.
+// One wave per token over its key row (orderable(bf16(logit)) << 16 | (0xFFFF - e), -0 -> +0):
+// k rounds of a wave-wide max select; softmax w_k = exp(v_k - v_0) / sum (sequential sum).
+// Unrouted tokens (a zero first key) get idx -1 / weight 0; forced-balanced routing
+// (DGM_FE_FORCE_BALANCED) gives slot s -> s G + (g + 7 s) % G with weight 1 / topk.
 constexpr int SELECT_TPB = 4;           // tokens (waves) per workgroup
-__global__ void __launch_bounds__(256) k_select(const float* __restrict__ logits, const int* __restrict__ token_flags,
-                                                int M, int E, int topk, int flags, int token_offset,
-                                                int64_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+__global__ void __launch_bounds__(256) k_select(const uint32_t* __restrict__ keys, int M, int E, int topk, int flags,
+                                                int token_offset, int64_t* __restrict__ topk_idx,
+                                                float* __restrict__ topk_w) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * SELECT_TPB + (threadIdx.x >> 6);
   if (t >= M) return;
   int idx = -1;
   float wt = 0.f;
-  const float* row = logits + (size_t)t * E;
+  const uint32_t* row = keys + (size_t)t * E;
   select_topk_wave([row](int e) { return row[e]; }, E, topk, (flags & DGM_FE_FORCE_BALANCED) != 0,
-                   token_offset + t, (flags & DGM_FE_ZERO_ROW_UNROUTED) && (token_flags[t] & 1), lane, idx, wt);
+                   token_offset + t, lane, idx, wt);
   if (lane < topk) {
     topk_idx[(size_t)t * topk + lane] = idx;
     topk_w[(size_t)t * topk + lane] = wt;
@@ -269,26 +267,33 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         sm.bs[g][l] = w;
       }
       __syncthreads();
-      // ---- matrix cores: two K halves accumulated separately and added (the persistent
-      // kernel's order, so both paths give identical results)
+      // ---- matrix cores: two K halves accumulated separately and added. Scale bytes are
+      // selected from the loaded scale dwords by the op's byte select (no VALU writes to a
+      // scale operand inside the chain of matrix-core ops)
       v4f accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
       v4f accg1 = {0.f, 0.f, 0.f, 0.f}, accu1 = {0.f, 0.f, 0.f, 0.f};
+      uint32_t bsw[KG];
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
+      for (int g = 0; g < KG; ++g) bsw[g] = sm.bs[g][lane];
+      static_for<KT>([&](auto kc) {
+        constexpr int kt = decltype(kc)::value;
         v8i bop;
         if (ACT == DGM_ACT_MXFP4) bop = u4_to_v8i(sm.b[kt][lane][0]);
         else bop = u8_to_v8i(sm.b[kt][lane][0], sm.b[kt][lane][ACT != DGM_ACT_MXFP4 ? 1 : 0]);
-        const int sh = 8 * (kt & 3);
-        int sb = (int)(sm.bs[kt >> 2][lane] >> sh);
         constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;
-        if (kt < KT / 2) {
-          accg = mfma_scale_16x16x128<4, FB>(u4_to_v8i(ag[kt]), bop, accg, (int)(sg[kt >> 2] >> sh), sb);
-          accu = mfma_scale_16x16x128<4, FB>(u4_to_v8i(au[kt]), bop, accu, (int)(su[kt >> 2] >> sh), sb);
+        constexpr int SEL = kt & 3;
+        if constexpr (kt < KT / 2) {
+          accg = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(ag[kt]), bop, accg, (int)sg[kt >> 2], (int)bsw[kt >> 2]);
+          accu = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(au[kt]), bop, accu, (int)su[kt >> 2], (int)bsw[kt >> 2]);
         } else {
-          accg1 = mfma_scale_16x16x128<4, FB>(u4_to_v8i(ag[kt]), bop, accg1, (int)(sg[kt >> 2] >> sh), sb);
-          accu1 = mfma_scale_16x16x128<4, FB>(u4_to_v8i(au[kt]), bop, accu1, (int)(su[kt >> 2] >> sh), sb);
+          accg1 = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(ag[kt]), bop, accg1, (int)sg[kt >> 2], (int)bsw[kt >> 2]);
+          accu1 = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(au[kt]), bop, accu1, (int)su[kt >> 2], (int)bsw[kt >> 2]);
         }
-      }
+      });
+      keep_scales_until(sg, accg1);
+      keep_scales_until(su, accu1);
+      keep_scales_until(bsw, accg1);
+      keep_scales_until(bsw, accu1);
       accg += accg1;
       accu += accu1;
       // ---- epilogue: lane holds features 16p + 4(l/16) + i for slab column c = l % 16
@@ -343,8 +348,8 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
 template <int KT, int ACT>
 __global__ void __launch_bounds__(256) k_l2(const uint8_t* __restrict__ w2v, const uint32_t* __restrict__ w2s,
                                             const uint8_t* __restrict__ mid, const uint8_t* __restrict__ mid_sf,
-                                            uint8_t* __restrict__ pool_base, int E_local, int H,
-                                            float* __restrict__ partials) {
+                                            uint8_t* __restrict__ pool_base, int E_local, int H, int topk,
+                                            int part_rows, uint16_t* __restrict__ partials) {
   constexpr int KG = (KT + 3) / 4;
   constexpr int I = KT * 128;
   constexpr int MB = ACT == DGM_ACT_MXFP4 ? I / 2 : I;
@@ -371,10 +376,17 @@ __global__ void __launch_bounds__(256) k_l2(const uint8_t* __restrict__ w2v, con
       const bool valid = s0 + c < n;
       const int row = r0 + s0 + (valid ? c : 0);
       v4f acc = {0.f, 0.f, 0.f, 0.f};
+      // the activation scale bytes of every K-tile, loaded before the chain of matrix-core ops
+      // into registers of their own (a lane without a route reads its slab's first row: its B
+      // operand is zero, and a real scale byte is finite); the weight scale bytes are selected
+      // from the loaded dwords by the op's byte select, so no VALU op writes a scale operand
+      // inside the chain
+      uint32_t sbv[KT];
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt) {
+      for (int kt = 0; kt < KT; ++kt) sbv[kt] = mid_sf[(size_t)row * (I / 32) + kt * 4 + kq];
+      static_for<KT>([&](auto kc) {
+        constexpr int kt = decltype(kc)::value;
         v8i bop;
-        int sb = 127;
         if (ACT == DGM_ACT_MXFP4) {
           U4 v = {0, 0, 0, 0};
           if (valid) v = *reinterpret_cast<const U4*>(mid + (size_t)row * MB + kt * 64 + kq * 16);
@@ -388,22 +400,27 @@ __global__ void __launch_bounds__(256) k_l2(const uint8_t* __restrict__ w2v, con
           }
           bop = u8_to_v8i(v0, v1);
         }
-        if (valid) sb = mid_sf[(size_t)row * (I / 32) + kt * 4 + kq];
         constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;
-        acc = mfma_scale_16x16x128<4, FB>(u4_to_v8i(av[kt]), bop, acc, (int)(sa[kt >> 2] >> (8 * (kt & 3))), sb);
-      }
+        acc = mfma_scale_16x16x128_sel<4, FB, kt & 3, 0>(u4_to_v8i(av[kt]), bop, acc, (int)sa[kt >> 2], (int)sbv[kt]);
+      });
+      keep_scales_until(sa, acc);
+      keep_scales_until(sbv, acc);
       if (valid) {
+        // the route's output rounded to bf16, slot-major [topk][part_rows][H]
         const int rid = P.routes[row];
-        float4 o = {acc[0], acc[1], acc[2], acc[3]};
-        *reinterpret_cast<float4*>(partials + (size_t)rid * H + b * 16 + 4 * kq) = o;
+        const int t = rid / topk, sl = rid - t * topk;
+        const uint2 o = make_uint2((uint32_t)f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16),
+                                   (uint32_t)f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16));
+        *reinterpret_cast<uint2*>(partials + ((size_t)sl * part_rows + t) * H + b * 16 + 4 * kq) = o;
       }
     }
   }
 }
 
 // ------------------------------------------------------------------ combine
-// y[t, n] = bf16(sum over valid local slots s ascending of partials[t*topk + s, n]).
-__global__ void k_combine(const float* __restrict__ partials, const int64_t* __restrict__ topk_idx,
+// y[t, n] = bf16(sum over valid local slots s ascending of float(partials[s, t, n])) (bf16 route
+// outputs, fp32 sum).
+__global__ void k_combine(const uint16_t* __restrict__ partials, int part_rows, const int64_t* __restrict__ topk_idx,
                           int M, int H, int topk, int expert_begin, int E_local, uint16_t* __restrict__ y) {
   const int t = blockIdx.y;
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
@@ -413,8 +430,11 @@ __global__ void k_combine(const float* __restrict__ partials, const int64_t* __r
     int64_t g = topk_idx[(size_t)t * topk + s];
     int64_t l = g - expert_begin;
     if (g < 0 || l < 0 || l >= E_local) continue;
-    float4 v = *reinterpret_cast<const float4*>(partials + ((size_t)t * topk + s) * H + n);
-    s0 += v.x; s1 += v.y; s2 += v.z; s3 += v.w;
+    const uint2 v = *reinterpret_cast<const uint2*>(partials + ((size_t)s * part_rows + t) * H + n);
+    s0 += __uint_as_float(v.x << 16);
+    s1 += __uint_as_float(v.x & 0xffff0000u);
+    s2 += __uint_as_float(v.y << 16);
+    s3 += __uint_as_float(v.y & 0xffff0000u);
   }
   uint32_t lo = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
   uint32_t hi = (uint32_t)f32_to_bf16(s2) | ((uint32_t)f32_to_bf16(s3) << 16);
@@ -450,7 +470,7 @@ int launch_experts(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, 
   int grid2 = (items2 + 3) / 4 < cus * 4 ? (items2 + 3) / 4 : cus * 4;
   hipLaunchKernelGGL((k_l2<KT2, ACT>), dim3(grid2), dim3(256), 0, stream, (const uint8_t*)A->w2_values,
                      (const uint32_t*)A->w2_scales, buf + L->mid, buf + L->mid_sf, pool, A->num_local_experts,
-                     A->hidden, (float*)(buf + L->partials));
+                     A->hidden, A->topk, L->max_tokens, (uint16_t*)(buf + L->partials));
   return dgm_last_launch_status();
 }
 
@@ -472,6 +492,16 @@ int dgm_version(void) { return 1; }
 const char* dgm_last_error(void) { return g_err; }
 
 int dgm_device_cu_count(void) { return cu_count(); }
+
+int dgm_host_device_pointer(const void* host, void** device) {
+  DGM_CHECK_ARG(host && device, "null pointer");
+  hipError_t e = hipHostGetDevicePointer(device, const_cast<void*>(host), 0);
+  if (e != hipSuccess) {
+    dgm_set_error("hipHostGetDevicePointer failed: not pinned host memory");
+    return (int)e;
+  }
+  return 0;
+}
 
 int dgm_fused_workgroups(int hidden, int intermediate, int act_format) {
   return dgm_fused_grid_blocks(hidden, intermediate, act_format);
@@ -502,16 +532,17 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   out->topk_idx = off; off += dgm_align256((size_t)R * 8);
   out->topk_weights = off; off += dgm_align256((size_t)R * 4);
   out->logits = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
-  out->token_flags = off; off += dgm_align256((size_t)max_tokens * 4);
+  out->fe_keys = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
   out->pool = off; off += dgm_align256(pool_bytes(num_local_experts, R));
   out->mid = off; off += dgm_align256((size_t)R * mb);
   out->mid_sf = off; off += dgm_align256((size_t)R * msfb);
-  out->partials = off; off += dgm_align256((size_t)R * hidden * 4);
+  out->partials = off; off += dgm_align256((size_t)R * hidden * 2);     // bf16 [topk][max_tokens][H]
   out->counters = off; off += dgm_align256((size_t)CNT_ALL * 4);
   out->total_bytes = off;
   out->x_row_bytes = (int32_t)xb;
   out->mid_row_bytes = (int32_t)mb;
   out->max_routes = R;
+  out->max_tokens = max_tokens;
   return 0;
 }
 
@@ -539,10 +570,11 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
   const uint16_t* x = (const uint16_t*)hidden_bf16;
   const uint16_t* w = (const uint16_t*)router_weight_bf16;
   float* logits = (float*)(buf + L->logits);
-  int* tflags = (int*)(buf + L->token_flags);
+  uint32_t* keys = (uint32_t*)(buf + L->fe_keys);
+  const int zero_unrouted = (flags & DGM_FE_ZERO_ROW_UNROUTED) ? 1 : 0;
 #define DGM_FE(JJ)                                                                                              \
   hipLaunchKernelGGL(k_frontend<JJ>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, act_format, logits, \
-                     tflags, buf + L->x, buf + L->x_sf)
+                     keys, zero_unrouted, buf + L->x, buf + L->x_sf)
   switch (J) {
     case 1: DGM_FE(1); break;
     case 2: DGM_FE(2); break;
@@ -554,17 +586,22 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
 #undef DGM_FE
   int st = dgm_last_launch_status();
   if (st || (flags & DGM_FE_SELECT_IN_MEGA)) return st;
-  hipLaunchKernelGGL(k_select, dim3((num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, logits, tflags, num_tokens,
+  hipLaunchKernelGGL(k_select, dim3((num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, keys, num_tokens,
                      num_experts, topk, flags, token_offset, (int64_t*)(buf + L->topk_idx),
                      (float*)(buf + L->topk_weights));
   return dgm_last_launch_status();
 }
 
-// Writes topk_idx / topk_weights from the buffer's logits (after a DGM_FE_SELECT_IN_MEGA
-// frontend call) for the paths that read them.
+// The key array the top-k is selected from under select_in_mega: the caller's, else the buffer's
+// (written by a DGM_FE_SELECT_IN_MEGA frontend call).
+static const uint32_t* select_keys(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L) {
+  return A->fe_keys ? (const uint32_t*)A->fe_keys : (const uint32_t*)(buf + L->fe_keys);
+}
+
+// Writes topk_idx / topk_weights from the select keys for the paths that read them.
 static int materialize_topk(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, hipStream_t stream) {
-  hipLaunchKernelGGL(k_select, dim3((A->num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, (const float*)(buf + L->logits),
-                     (const int*)(buf + L->token_flags), A->num_tokens, A->num_experts, A->topk, A->fe_flags,
+  hipLaunchKernelGGL(k_select, dim3((A->num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream,
+                     select_keys(A, buf, L), A->num_tokens, A->num_experts, A->topk, A->fe_flags,
                      A->token_offset, (int64_t*)(buf + L->topk_idx), (float*)(buf + L->topk_weights));
   return dgm_last_launch_status();
 }
@@ -639,8 +676,9 @@ static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stre
     p.xsf = buf + L->x_sf;
     p.topk_idx = (int64_t*)(buf + L->topk_idx);
     p.topk_w = (float*)(buf + L->topk_weights);
-    p.logits = (const float*)(buf + L->logits);
-    p.token_flags = (const int*)(buf + L->token_flags);
+    // (the in-kernel frontend writes the buffer's own keys and logits)
+    p.keys = A->fe_in_mega ? (const uint32_t*)(buf + L->fe_keys) : select_keys(A, buf, L);
+    p.logits = (float*)(buf + L->logits);
     p.select = sel ? 1 : 0;
     p.fe_in = A->fe_in_mega ? 1 : 0;
     p.hidden = (const uint16_t*)A->hidden_states;
@@ -650,11 +688,13 @@ static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stre
     p.E = A->num_experts;
     p.mid = buf + L->mid;
     p.mid_sf = buf + L->mid_sf;
-    p.partials = (float*)(buf + L->partials);
+    p.partials = (uint16_t*)(buf + L->partials);
+    p.part_rows = L->max_tokens;
     p.y = (uint16_t*)A->y;
     p.pool_out = buf + L->pool;
     p.recv_stats = A->recv_stats;
     p.counters = (int*)(buf + L->counters);
+    p.host_err = A->host_error;
     p.M = A->num_tokens;
     p.topk = A->topk;
     p.expert_begin = A->expert_begin;
@@ -665,6 +705,7 @@ static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stre
     p.stamps = (long long*)A->phase_stamps;
     p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;
     p.phases = phases;
+    p.debug = (int16_t)(A->debug_flags & 1);
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
 }
@@ -721,7 +762,7 @@ int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   }
   if (st) return st;
   dim3 cg((A->hidden / 4 + 255) / 256, A->num_tokens);
-  hipLaunchKernelGGL(k_combine, cg, dim3(256), 0, stream, (const float*)(buf + L->partials),
+  hipLaunchKernelGGL(k_combine, cg, dim3(256), 0, stream, (const uint16_t*)(buf + L->partials), L->max_tokens,
                      (const int64_t*)(buf + L->topk_idx), A->num_tokens, A->hidden, A->topk, A->expert_begin,
                      A->num_local_experts, (uint16_t*)A->y);
   return dgm_last_launch_status();

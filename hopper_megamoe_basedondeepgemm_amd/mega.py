@@ -25,8 +25,10 @@ class FusedSymmBuffer:
 
     Views: x, x_sf, topk_idx, topk_weights (frontend outputs / layer inputs), l1_acts and
     l1_acts_sf (aliases of x / x_sf: routed rows are read in place), l2_acts / l2_acts_sf
-    (L1 -> L2 activations in pool order), combine_partials (fp32 [tokens, topk, H] route
-    outputs), logits (fp32 router logits) and pool (dispatch table, int32).
+    (L1 -> L2 activations in pool order), combine_partials (bf16 [topk, tokens, H]: each local
+    route's output rounded to bf16, as the reference's view; slots without a local route are not
+    written), logits (fp32 router logits), fe_keys (int32 [tokens, E] top-k keys of the
+    frontend, see ``fable_frontend_keys``) and pool (dispatch table, int32).
     act_format "mxfp4" / "mxfp8": uint8 codes with E8M0 scale bytes per 32; "nvfp4": E2M1 codes
     (low nibble first) with E4M3 scale bytes per 16; "qoq": int8 codes, x_sf fp32 [tokens, H/128]
     (one scale per token, repeated), l2_acts_sf fp32 [routes, I/64]."""
@@ -72,6 +74,7 @@ class FusedSymmBuffer:
         self.topk_idx = view(L.topk_idx, R, torch.int64, (max_tokens, topk))
         self.topk_weights = view(L.topk_weights, R, torch.float32, (max_tokens, topk))
         self.logits = view(L.logits, max_tokens * num_experts, torch.float32, (max_tokens, num_experts))
+        self.fe_keys = view(L.fe_keys, max_tokens * num_experts, torch.int32, (max_tokens, num_experts))
         mb = L.mid_row_bytes
         if qoq:   # int8 codes, fp32 scale per 64 features
             self.l2_acts = view(L.mid, R * mb, torch.int8, (R, mb))
@@ -79,9 +82,13 @@ class FusedSymmBuffer:
         else:
             self.l2_acts = view(L.mid, R * mb, torch.uint8, (R, mb))
             self.l2_acts_sf = view(L.mid_sf, R * (intermediate // sfv), torch.uint8, (R, intermediate // sfv))
-        self.combine_partials = view(L.partials, R * hidden, torch.float32, (max_tokens, topk, hidden))
+        self.combine_partials = view(L.partials, R * hidden, torch.bfloat16, (topk, max_tokens, hidden))
         self.l1_acts, self.l1_acts_sf = self.x, self.x_sf
         self.handle = types.SimpleNamespace(buffer_ptrs=[b.data_ptr()])
+        # host-visible error word (pinned host memory the kernel writes when a bounded wait
+        # expires): checked at the start of the next call on this buffer without synchronising
+        self._host_err = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._host_err_dev = _lib.host_device_pointer(self._host_err)
 
     def pool_table(self):
         """(counts [E_local], active experts, offsets [n_active+1], routes [total]) as CPU
@@ -101,8 +108,21 @@ class FusedSymmBuffer:
         return counts, active, offsets, routes
 
     def kernel_error(self):
-        """Error flag of the persistent kernel (1 when a bounded wait expired). Synchronises."""
+        """Error flag of the persistent kernel (1 when a bounded wait expired; it stays set until
+        ``clear_error``). Synchronises."""
         return int(self.buffer[self.layout.counters + 4:self.layout.counters + 8].view(torch.int32).item())
+
+    def host_error(self):
+        """The host-visible copy of the error flag, as far as the launches on this buffer have
+        completed (no synchronisation)."""
+        return int(self._host_err[0])
+
+    def clear_error(self):
+        """Clears the error flag and its host-visible copy (synchronises)."""
+        torch.cuda.synchronize()
+        self.buffer[self.layout.counters + 4:self.layout.counters + 8].zero_()
+        self._host_err.zero_()
+        torch.cuda.synchronize()
 
     def destroy(self):
         self.buffer = None
@@ -291,12 +311,27 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
         int(token_offset), _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
 
 
+def fable_frontend_keys(sym_buffer) -> torch.Tensor:
+    """deep_gemm/mega/__init__.py:737: flat int32 view of the frontend's compact key array (token
+    t, expert x at [t * E + x]) in this buffer, the array the fused layer selects from under
+    ``select_in_mega``. Key = orderable(bf16 logit) << 16 | (0xFFFF - x); all keys of an
+    unrouted (all-zero) row are 0."""
+    return sym_buffer.fe_keys.view(-1)
+
+
 # ----------------------------------------------------------------------------- fused layer
 _ENTRY_FOR = {"qoq": "qoq_mega_moe_fused", "nvfp4": "fp4_fp4_mega_moe / nvfp4_mega_moe"}
 
 
+def _check_host_error(b):
+    if b.host_error():
+        raise RuntimeError("MegaMoE: a bounded wait of an earlier launch on this buffer expired, so that launch's "
+                           "output is wrong (workgroups not co-resident, or counters left inconsistent); "
+                           "buffer.clear_error() resets the flag")
+
+
 def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
-           fast_math=True, fmt=None, global_scales=(None, None), fe=None):
+           fast_math=True, fmt=None, global_scales=(None, None), fe=None, fe_keys=None):
     fmt = fmt or ("mxfp8" if b.act_format in ("mxfp8", "fp8") else "mxfp4")
     kind = lambda f: f if f in ("qoq", "nvfp4") else "mxfp"
     if kind(fmt) != kind(b.act_format):
@@ -337,11 +372,19 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
     assert all(t.is_contiguous() for t in (w1, sf1, w2, sf2))
     if stats is not None:
         assert stats.dtype == torch.int32 and stats.numel() == E_l
+    _check_host_error(b)
     sel = getattr(b, "_fe_select", None)
     if fe is not None:        # in-kernel frontend: (hidden, router_weight, flags, token_offset)
         hidden, router_weight, fe_flags, fe_off = fe
         sel = (fe_flags, fe_off)
         b._fe_select = None
+        fe_keys = None
+    elif fe_keys is not None:
+        # the caller's key array (the reference's compact keys: token t, expert x at t * E + x)
+        _lib.require_gpu(fe_keys)
+        assert fe_keys.dtype in (torch.int32, torch.uint32) and fe_keys.is_contiguous(), fe_keys.dtype
+        assert fe_keys.numel() >= m * b.num_experts, (fe_keys.numel(), m, b.num_experts)
+        sel = (sel[0] & _lib.FE_FORCE_BALANCED if sel else 0, sel[1] if sel else 0)
     args = _lib.MoeArgs(num_tokens=m, hidden=b.hidden, intermediate=b.intermediate_hidden,
                         num_experts=b.num_experts, expert_begin=b.expert_begin, num_local_experts=E_l,
                         topk=b.num_topk, act_format=b.act_code,
@@ -359,11 +402,17 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
                         l2_global_scales=global_scales[1].data_ptr() if global_scales[1] is not None else None,
                         fe_in_mega=int(fe is not None),
                         hidden_states=fe[0].data_ptr() if fe is not None else None,
-                        router_weight=fe[1].data_ptr() if fe is not None else None)
+                        router_weight=fe[1].data_ptr() if fe is not None else None,
+                        fe_keys=fe_keys.data_ptr() if fe_keys is not None else None,
+                        host_error=b._host_err_dev, debug_flags=getattr(b, "_debug_flags", 0))
     if phase_stamps is not None:
         assert phase_stamps.dtype == torch.int64 and phase_stamps.is_cuda and phase_stamps.is_contiguous()
     fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
     _lib.check(fn(ctypes.byref(args), _lib.stream()))
+    if os.environ.get("DG_CHECK_ERRORS", "0") == "1":     # debug: wait for the launch and check it
+        torch.cuda.synchronize()
+        if b.kernel_error():
+            raise RuntimeError("MegaMoE: a bounded wait of this launch expired; its output is wrong")
 
 
 def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
@@ -374,9 +423,14 @@ def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
     ``phase_stamps`` (optional int64 CUDA tensor [rows, 8]; workgroups >= rows skip): per-workgroup
     100 MHz wall-clock stamps (see ``fused_workgroups``). ``fast_math`` (default True, as in the
     reference): hardware exp2 / reciprocal in SiLU's sigmoid; False = IEEE expf and division.
-    ``fe_keys`` is accepted for signature compatibility."""
+    ``fe_keys``: an int32 key array [tokens, E] (``fable_frontend_keys``; the frontend's compact
+    keys, orderable bf16 logit << 16 | 0xFFFF - expert, a zero first key = unrouted token) the
+    top-k is selected from in the kernel's prologue; by default the buffer's own keys when the
+    frontend ran with ``select_in_mega``, else the buffer's ``topk_idx`` / ``topk_weights``.
+    A bounded wait that expired in an earlier launch on this buffer raises here (the host-visible
+    error word; ``DG_CHECK_ERRORS=1`` checks every launch at once, synchronising)."""
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
-           fast_math=fast_math)
+           fast_math=fast_math, fe_keys=fe_keys)
 
 
 def qoq_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,
@@ -385,9 +439,10 @@ def qoq_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, ac
     act_format="qoq")``, weights from ``transform_qoq_weights_for_mega_moe_fused``): int8
     activations with one scale per token, 4-bit weight codes with per-(row, K128) zero point and
     integer scale and per-row fp32 scale, exact int32 group sums; fp32 gate / up, SiLU * up *
-    routing weight, int8 requant per 64 features, L2, fp32 combine -> bf16 ``y``."""
+    routing weight, int8 requant per 64 features, L2 (each route rounded to bf16), fp32 combine ->
+    bf16 ``y``. ``fe_keys`` as for ``mxfp4_mega_moe_fused``."""
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
-           fast_math=fast_math, fmt="qoq")
+           fast_math=fast_math, fmt="qoq", fe_keys=fe_keys)
 
 
 def fp4_fp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats=None,

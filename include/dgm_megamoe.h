@@ -121,12 +121,12 @@ typedef struct DgmBufferLayout {
   size_t total_bytes;
   size_t x, x_sf, topk_idx, topk_weights;       /* frontend outputs / fused-layer inputs  */
   size_t logits;                                /* fp32 router logits [max_tokens, E]      */
-  size_t token_flags;                           /* int32 [max_tokens]: bit 0 = all-zero row */
+  size_t fe_keys;                               /* u32 top-k keys [max_tokens, E] (fable_frontend_keys) */
   size_t pool;                                  /* dispatch table (see DgmPoolTable)       */
   size_t mid, mid_sf;                           /* L1 -> L2 activations (pool-row order)   */
-  size_t partials;                              /* fp32 [max_tokens * topk, H] route outputs */
+  size_t partials;                              /* bf16 [topk, max_tokens, H] route outputs (combine_partials) */
   size_t counters;                              /* int32 scratch counters                  */
-  int32_t x_row_bytes, mid_row_bytes, max_routes;
+  int32_t x_row_bytes, mid_row_bytes, max_routes, max_tokens;
 } DgmBufferLayout;
 
 int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_experts, int topk,
@@ -137,9 +137,12 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
  * deep_gemm/mega/__init__.py:671 fable_router_quant_topk_frontend): bf16 router GEMV with
  * fp32 accumulation in a fixed order, bf16 logits, top-k (value desc, index asc), fp32
  * softmax of the k logits, activation cast, into the buffer views x / x_sf / topk_idx /
- * topk_weights (and fp32 logits, token flags). token_offset = global id of row 0
- * (forced-balanced rule). With DGM_FE_SELECT_IN_MEGA the top-k is left to the fused layer
- * (DgmMoeArgs.select_in_mega); topk_idx / topk_weights are written by that call instead. */
+ * topk_weights (and the fp32 logits). The top-k keys (orderable bf16 logit << 16 | 0xFFFF - e,
+ * the reference's compact key array, deep_gemm/mega/__init__.py:737) go to the fe_keys view;
+ * with DGM_FE_ZERO_ROW_UNROUTED an all-zero hidden row gets zero keys (unrouted).
+ * token_offset = global id of row 0 (forced-balanced rule). With DGM_FE_SELECT_IN_MEGA the
+ * top-k is left to the fused layer (DgmMoeArgs.select_in_mega), which selects from the keys;
+ * topk_idx / topk_weights are written by that call instead. */
 int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16,
                            int num_tokens, int hidden, int num_experts, int topk, int act_format,
                            int flags, int token_offset, void* buffer,
@@ -155,8 +158,8 @@ typedef struct DgmMoeArgs {
   int32_t act_format;
   float activation_clamp;
   int32_t fast_math;      /* 1: hardware exp2 / reciprocal in SiLU (reference default) */
-  int32_t select_in_mega; /* 1: select the top-k from the buffer's logits / token flags (after a
-                             DGM_FE_SELECT_IN_MEGA frontend call) and write topk_idx / weights */
+  int32_t select_in_mega; /* 1: select the top-k from a key array (fe_keys, else the buffer's keys
+                             after a DGM_FE_SELECT_IN_MEGA frontend call) and write topk_idx / weights */
   int32_t fe_flags;       /* with select_in_mega: the frontend's DGM_FE_* flags */
   int32_t token_offset;   /* with select_in_mega: global id of row 0 */
   const void* w1_values;  /* [E_local, 2I/16, H/128, 64, 16] */
@@ -186,6 +189,18 @@ typedef struct DgmMoeArgs {
   int32_t fe_in_mega;
   const void* hidden_states; /* bf16 [num_tokens, hidden] */
   const void* router_weight; /* bf16 [num_experts, hidden] */
+  /* With select_in_mega: the u32 key array [num_tokens, num_experts] to select from (the fe_keys
+   * argument of deep_gemm/mega/fused.py:97; a token whose first key is 0 is unrouted); NULL = the
+   * buffer's fe_keys view. */
+  const void* fe_keys;
+  /* Optional host-visible int32 word (pinned host memory, device-accessible): set to 1 when a
+   * bounded wait of the persistent kernel expires, beside the buffer's error counter, so the
+   * host can check a launch's outcome later without synchronising. NULL = none. */
+  int32_t* host_error;
+  /* Test hook, 0 in normal use. Bit 0: the persistent kernel additionally runs one bounded wait
+   * on a counter nothing sets, with a zero spin limit, so the wait expires and the error
+   * reporting (error counter, host_error) can be tested without a real failure. */
+  int32_t debug_flags;
 } DgmMoeArgs;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
@@ -196,6 +211,10 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
  * kernels; QoQ / NVFP4: the persistent kernel twice, dispatch + L1 then L2 + combine (the
  * fused kernel's limits on tokens, routes and local experts apply). fe_in_mega is rejected. */
 int dgm_megamoe_split_launch(const DgmMoeArgs* args, hipStream_t stream);
+
+/* Device address of pinned host memory (hipHostGetDevicePointer), e.g. for
+ * DgmMoeArgs.host_error. No counterpart in the reference (its error path is a device trap). */
+int dgm_host_device_pointer(const void* host, void** device);
 
 /* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the
  * current device. dgm_probe_mfma_scale: runs one V_MFMA_SCALE_F32_16X16X128_F8F6F4 on 64

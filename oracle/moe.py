@@ -15,7 +15,9 @@ Stages, each citing the reference rule it restates:
   experts     sm100_b200/test_mega_moe.py:411-486: fp32 x_dq @ W1^T, gate/up rounded to
               bf16, clamp (gate <= c, up in [-c, c]), silu(gate)*up*w, per-32 requant
               (MXFP4: ceil_to_ue8m0(amax/6) + ties-down E2M1; MXFP8: 2^ceil(log2(amax/448))
-              + E4M3), fp32 @ W2^T, fp32 index_add over experts ascending.
+              + E4M3), fp32 @ W2^T; each route's output rounded to bf16 and the routes summed
+              in fp32 in slot order (tests/test_four_api_correctness.py:443-444, the rule of
+              the H20 fused kernel's L2 epilogue, sm90_fp4_mega_moe_h20_fused_body.inl:1991-1994).
   qoq         deep_gemm/quantization_qoq_fused.py:78-91 (per-token int8 cast);
               tests/test_four_api_correctness.py:421-446 (dequantised weights, fp32 gate/up
               without bf16 rounding, per-64 int8 requant, per-route bf16, fp32 sum).
@@ -221,18 +223,19 @@ class LazyDequant:
 
 # ----------------------------------------------------------------------------- layer
 def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=10.0,
-                bf16_gate_up=True, route_bf16=False, gs1=None, gs2=None):
+                bf16_gate_up=True, route_bf16=True, gs1=None, gs2=None):
     """Expert part of the layer on dequantised inputs.
 
     x_dq [M, H] f32 (dequantised activations), topk_idx [M, k], topk_w [M, k],
     W1 [E_local, 2I, H] f32 (gate rows 0..I-1, up rows I..2I-1), W2 [E_local, H, I] f32.
+    route_bf16: each route's output rounded to bf16 (tests/test_four_api_correctness.py:443);
+    y[t] = fp32 sum of the token's local routes in slot order (:444).
     Returns (y_f32 [M, H], per-route outputs dict rid -> f32 [H])."""
     M, H = x_dq.shape
     E_local, twoI, _ = W1.shape
     I = twoI // 2
     topk = topk_idx.shape[1]
     c = np.float32(clamp)
-    y = np.zeros((M, H), dtype=np.float32)
     routes = {}
     for e in range(E_local):
         t_ids, s_ids = np.nonzero(topk_idx == expert_begin + e)
@@ -256,8 +259,19 @@ def moe_forward(x_dq, topk_idx, topk_w, W1, W2, expert_begin, act_format, clamp=
             out = round_bf16(out)
         for n, (t, s) in enumerate(zip(t_ids, s_ids)):
             routes[int(t) * topk + int(s)] = out[n]
-            y[t] = (y[t] + out[n]).astype(np.float32)
-    return y, routes
+    return combine_routes(routes, M, topk, H), routes
+
+
+def combine_routes(routes, M, topk, H):
+    """y[t] = fp32 sum of the token's route outputs in slot order (tests/test_four_api_correctness.py:444,
+    ``routes.sum(dim=1)`` over slots); tokens without a route give 0."""
+    y = np.zeros((M, H), dtype=np.float32)
+    for t in range(M):
+        for s in range(topk):
+            r = routes.get(t * topk + s)
+            if r is not None:
+                y[t] = (y[t] + r).astype(np.float32)
+    return y
 
 
 def moe_forward_qoq(x_dq, topk_idx, topk_w, W1, W2, expert_begin, clamp=10.0):

@@ -106,3 +106,43 @@ def decode_native_nvfp4(vals, scales):
     # K within the tile = 32 j + 8 g + k; rows r
     v = v.transpose(0, 1, 4, 2, 5, 3, 6)                                  # E NB r KT j g k
     return v.reshape(E, NB * 16, KT * 128).astype(np.float32)
+
+
+def oracle_routes_parallel(x_dq, idx, w, experts, deq1, deq2, expert_begin, E_local, I, act_format, workers=16,
+                           **kw):
+    """moe.moe_forward per active local expert on a thread pool (numpy releases the GIL in the
+    dequantisation and the products), the route outputs merged and combined in slot order by
+    moe.combine_routes. experts: local expert id -> (W1 args, W2 args) for deq1 / deq2 (the
+    packed bytes of that expert). Returns (y [M, H] f32, routes dict)."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import moe
+    M, topk = idx.shape
+    H = x_dq.shape[1]
+
+    class _One:
+        def __init__(self, e, fn, args, shape):
+            self.e, self.fn, self.args, self.shape = e, fn, args, shape
+
+        def __getitem__(self, i):
+            assert i == self.e
+            return self.fn(*self.args)
+
+    def one(e):
+        a1, a2 = experts[e]
+        sub = np.where(idx == expert_begin + e, idx, -1)
+        W1 = _One(e, deq1, a1, (E_local, 2 * I, H))
+        W2 = _One(e, deq2, a2, (E_local, H, I))
+        _, r = moe.moe_forward(x_dq, sub, w, W1, W2, expert_begin, act_format, **kw)
+        return r
+
+    routes = {}
+    with ThreadPoolExecutor(max_workers=min(workers, os.cpu_count() or 1)) as ex:
+        for r in ex.map(one, sorted(experts)):
+            routes.update(r)
+    return moe.combine_routes(routes, M, topk, H), routes
+
+
+def active_local_experts(idx, expert_begin, E_local):
+    loc = np.asarray(idx) - expert_begin
+    return sorted({int(v) for v in loc.ravel() if 0 <= v < E_local and v + expert_begin >= 0})

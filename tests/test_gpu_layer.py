@@ -78,6 +78,9 @@ def check_frontend(r, fmt, M, force_balanced=False, zero_rows=()):
     if not force_balanced:
         got = b.logits[:M].cpu().numpy()
         np.testing.assert_array_equal(got.view(np.uint32), r["logits"].view(np.uint32))
+    keys = moe.topk_keys(nu.f32_to_bf16_bits(r["logits"]), b.num_experts)
+    keys[list(zero_rows)] = 0                  # all-zero rows: unrouted (zero keys)
+    np.testing.assert_array_equal(b.fe_keys[:M].cpu().numpy().view(np.uint32), keys)
     np.testing.assert_array_equal(b.topk_idx[:M].cpu().numpy(), r["idx"])
     np.testing.assert_allclose(b.topk_weights[:M].cpu().numpy(), r["w"], rtol=1e-6, atol=0)
     np.testing.assert_array_equal(b.x[:M].cpu().numpy(), r["codes"])
@@ -220,3 +223,78 @@ def test_large_batch_beyond_fused_limits():
     check_frontend(r, "mxfp4", 200, zero_rows=(7,))
     check_pool(r, 16, 0)
     print(check_y(r, zero_rows=(7,)))
+
+
+def test_fe_keys_honoured():
+    """A caller's key array (the reference's fe_keys: orderable bf16 << 16 | 0xFFFF - e, a zero
+    first key = unrouted) is what the fused layer selects from: keys of other logits than the
+    router's give that routing (top-k, weights, pool, y), and a zero key row gives y == 0.
+    fable_frontend_keys is the buffer's own key array (bit-exact against the oracle)."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    M, E, H, I, topk = 6, 16, 512, 256, 4
+    weights = make_weights(E, H, I, 1101)
+    (t1, t2), W1, W2 = weights
+    rng = np.random.default_rng(1100)
+    x = randn_bf16(rng, (M, H))
+    rw = randn_bf16(rng, (E, H), 0.02)
+    other = randn_bf16(rng, (M, E))                        # logits of another router
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="mxfp8")
+    xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
+    dgm.fable_router_quant_topk_frontend(xs, rws, buf, select_in_mega=True)
+    torch.cuda.synchronize()
+    own = moe.topk_keys(nu.f32_to_bf16_bits(moe.router_logits_f32(x, rw)), E)
+    np.testing.assert_array_equal(dgm.fable_frontend_keys(buf).view(M, E).cpu().numpy().view(np.uint32), own)
+    keys = moe.topk_keys(nu.f32_to_bf16_bits(other), E).astype(np.uint32)
+    keys[2] = 0                                             # token 2 unrouted
+    fk = torch.from_numpy(keys.view(np.int32)).cuda()
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    dgm.mxfp4_mega_moe_fused(y, t1, t2, buf, fe_keys=fk)
+    torch.cuda.synchronize()
+    assert buf.kernel_error() == 0
+    idx, w, _ = moe.topk_softmax(other, topk)
+    idx[2] = -1
+    w[2] = 0.0
+    np.testing.assert_array_equal(buf.topk_idx[:M].cpu().numpy(), idx)
+    np.testing.assert_allclose(buf.topk_weights[:M].cpu().numpy(), w, rtol=1e-6, atol=0)
+    _, _, x_dq = moe.quant_act(x, "mxfp8")
+    ref, _ = moe.moe_forward(x_dq, idx, w, W1, W2, 0, "mxfp8")
+    yv = y.float().cpu().numpy()
+    assert (yv[2] == 0).all()
+    keep = [i for i in range(M) if i != 2]
+    m = moe.metrics(yv[keep], ref[keep])
+    assert m["cos_min"] >= COS_MIN and m["rel_rmse"] <= REL_RMSE_MAX, m
+
+
+def test_expired_wait_is_reported(monkeypatch):
+    """A bounded wait that expires (forced by the test hook: a wait on a counter nothing sets,
+    with a zero spin limit) sets the buffer's error counter and its host-visible word; the next
+    call on the buffer raises without synchronising; DG_CHECK_ERRORS=1 raises at once;
+    clear_error() makes the buffer usable again with unchanged results."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    weights = make_weights(16, 512, 256, 1201)
+    r = run_layer(5, 16, 16, 0, 512, 256, 4, "mxfp4", seed=1200, weights=weights)
+    check_y(r)
+    b = r["buf"]
+    (t1, t2), _, _ = weights
+    y = torch.empty((5, 512), dtype=torch.bfloat16, device="cuda")
+    b._debug_flags = 1
+    dgm.mxfp4_mega_moe_fused(y, t1, t2, b)
+    torch.cuda.synchronize()
+    assert b.kernel_error() == 1 and b.host_error() == 1
+    b._debug_flags = 0
+    with pytest.raises(RuntimeError, match="bounded wait"):
+        dgm.mxfp4_mega_moe_fused(y, t1, t2, b)
+    b.clear_error()
+    assert b.kernel_error() == 0 and b.host_error() == 0
+    monkeypatch.setenv("DG_CHECK_ERRORS", "1")
+    b._debug_flags = 1
+    with pytest.raises(RuntimeError, match="bounded wait"):
+        dgm.mxfp4_mega_moe_fused(y, t1, t2, b)
+    b._debug_flags = 0
+    b.clear_error()
+    dgm.mxfp4_mega_moe_fused(y, t1, t2, b)
+    torch.cuda.synchronize()
+    assert b.kernel_error() == 0
+    np.testing.assert_array_equal(y.float().cpu().numpy(), r["y"])

@@ -1,6 +1,6 @@
 """The one-launch layer (``mxfp4_mega_moe_from_bf16(one_launch=True)``, up to 64 tokens: router, zero-row flags and
 activation cast inside the fused kernel, before its top-k prologue) against the two-launch path
-(``fable_router_quant_topk_frontend`` + the fused layer) on the same inputs: logits, flags,
+(``fable_router_quant_topk_frontend`` + the fused layer) on the same inputs: logits, top-k keys,
 activation codes and scales, routing, pool and y must agree bit for bit (same device
 arithmetic, same order), for every activation format, with zero rows and forced-balanced
 routing, and on a second call (counters return to zero)."""
@@ -40,7 +40,8 @@ def layer_two_launch(dgm, fmt, y, x, rw, t1, t2, b, balanced):
 
 
 def snapshot(b, M):
-    return {k: getattr(b, k)[:M].clone() for k in ("x", "x_sf", "topk_idx", "topk_weights", "logits")}
+    return {k: getattr(b, k)[:M].clone() for k in ("x", "x_sf", "topk_idx", "topk_weights", "logits",
+                                                   "fe_keys")}
 
 
 @pytest.mark.parametrize("fmt,balanced", [("mxfp8", True), ("mxfp4", False), ("qoq", False), ("nvfp4", True)])

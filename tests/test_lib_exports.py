@@ -37,11 +37,12 @@ def test_host_checks_and_layout():
     with pytest.raises(RuntimeError, match="topk"):
         _lib.layout(16, 384, 48, 17, 3072, 1280, 0)
     L = _lib.layout(16, 384, 48, 8, 3072, 1280, 1)
-    offs = [L.x, L.x_sf, L.topk_idx, L.topk_weights, L.logits, L.pool, L.mid, L.mid_sf, L.partials,
+    offs = [L.x, L.x_sf, L.topk_idx, L.topk_weights, L.logits, L.fe_keys, L.pool, L.mid, L.mid_sf, L.partials,
             L.counters, L.total_bytes]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
-    assert L.x_row_bytes == 3072 and L.mid_row_bytes == 1280 and L.max_routes == 128
-    assert L.partials + 128 * 3072 * 4 <= L.counters
+    assert L.x_row_bytes == 3072 and L.mid_row_bytes == 1280 and L.max_routes == 128 and L.max_tokens == 16
+    assert L.fe_keys - L.logits >= 16 * 384 * 4
+    assert L.partials + 128 * 3072 * 2 <= L.counters        # bf16 [topk, max_tokens, H]
 
 
 def test_product_path_has_no_cpu_fallback():
