@@ -25,7 +25,7 @@ EXPORTS = [
     "dgm_probe_mfma_scale_sel",
     "dgm_probe_mfma_i8", "dgm_probe_mfma_f16", "dgm_probe_cvt_fp4",
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
-    "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer",
+    "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
 ]
 
 
@@ -86,6 +86,7 @@ def load():
                                     ctypes.POINTER(BufferLayout), vp], i32),
         "dgm_megamoe_fused_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_megamoe_split_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
+        "dgm_megamoe_fused_launch_noalloc": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_device_cu_count": ([], i32),
         "dgm_fused_workgroups": ([i32, i32, i32], i32),
         "dgm_probe_mfma_scale": ([vp, vp, vp, vp, vp, i32, i32, vp], i32),

@@ -32,4 +32,30 @@ static inline int dgm_last_launch_status() {
   return 0;
 }
 
-static inline size_t dgm_align256(size_t x) { return (x + 255) & ~(size_t)255; }
+static constexpr inline size_t dgm_align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Bytes of the dispatch table of E_local experts and max_routes routes (meta line, counts,
+// active list, offsets, route ids; each 256-byte aligned).
+static constexpr inline size_t dgm_pool_bytes(int E_local, int max_routes) {
+  return 256 + dgm_align256((size_t)E_local * 4) * 2 + dgm_align256((size_t)(E_local + 1) * 4) +
+         dgm_align256((size_t)max_routes * 4);
+}
+
+// Device memory the persistent kernel uses beyond its inputs and outputs: the dispatch table,
+// the L1 -> L2 rows and scales, the bf16 route outputs ([topk][part_rows][H]) and the int32
+// counters (which start at zero and are returned to zero by every launch).
+struct DgmWorkspace {
+  uint8_t* pool;
+  uint8_t* mid;
+  uint8_t* mid_sf;
+  uint16_t* partials;
+  int part_rows;
+  int* counters;
+};
+
+// Host-side checks of a fused-layer call (0, or DGM_ERR_INVALID_ARGUMENT with the message set).
+int dgm_check_fused_args(const DgmMoeArgs* A);
+// One launch of the persistent kernel over the workspace w, running `phases` of the layer
+// (1: dispatch + L1, 2: L2 + combine, 3: both); the top-k selection launch first when the
+// call selects from keys above the in-kernel selection's token count.
+int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, hipStream_t stream);

@@ -44,10 +44,6 @@ struct Pool {
 
 __host__ __device__ inline size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-__host__ __device__ inline size_t pool_bytes(int E_local, int max_routes) {
-  return 256 + a256((size_t)E_local * 4) * 2 + a256((size_t)(E_local + 1) * 4) + a256((size_t)max_routes * 4);
-}
-
 __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
   Pool p;
   p.meta = (int*)base;
@@ -533,7 +529,7 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   out->topk_weights = off; off += dgm_align256((size_t)R * 4);
   out->logits = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
   out->fe_keys = off; off += dgm_align256((size_t)max_tokens * num_experts * 4);
-  out->pool = off; off += dgm_align256(pool_bytes(num_local_experts, R));
+  out->pool = off; off += dgm_align256(dgm_pool_bytes(num_local_experts, R));
   out->mid = off; off += dgm_align256((size_t)R * mb);
   out->mid_sf = off; off += dgm_align256((size_t)R * msfb);
   out->partials = off; off += dgm_align256((size_t)R * hidden * 2);     // bf16 [topk][max_tokens][H]
@@ -615,6 +611,19 @@ constexpr int SELECT_IN_MEGA_MAX_TOKENS = 64;
 constexpr int SELECT_IN_MEGA_FAST_TOKENS = 8;     // (one token per wave)
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
+  const int chk = dgm_check_fused_args(A);
+  if (chk) return chk;
+  if (A->num_tokens == 0) return 0;
+  if (fused_fits(A)) return fused_launch_phases(A, 3, stream);
+  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
+                "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+  DGM_CHECK_ARG(!A->fe_in_mega, "fe_in_mega: the fused kernel's limits (tokens, routes, local experts) are exceeded");
+  return dgm_megamoe_split_launch(A, stream);
+}
+
+}  // extern "C"
+
+int dgm_check_fused_args(const DgmMoeArgs* A) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
   DGM_CHECK_ARG(A->w1_values && A->w1_scales && A->w2_values && A->w2_scales, "null weights");
   const DgmBufferLayout* L = A->layout;
@@ -627,7 +636,6 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
   DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 32 == 0, "shape");
   DGM_CHECK_ARG(A->intermediate % 128 == 0, "intermediate % 128 == 0");
-  if (A->num_tokens == 0) return 0;
   if (A->fe_in_mega) {
     DGM_CHECK_ARG(A->hidden_states && A->router_weight, "fe_in_mega: null hidden_states / router_weight");
     DGM_CHECK_ARG(((uintptr_t)A->hidden_states & 15) == 0 && ((uintptr_t)A->router_weight & 15) == 0, "16-byte alignment");
@@ -637,14 +645,8 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
     DGM_CHECK_ARG(!(A->fe_flags & DGM_FE_FORCE_BALANCED) || A->num_experts % A->topk == 0,
                   "forced-balanced needs E % topk == 0");
   }
-  if (fused_fits(A)) return fused_launch_phases(A, 3, stream);
-  DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
-                "QoQ / NVFP4 layer: the fused kernel's limits (tokens, routes, local experts) are exceeded");
-  DGM_CHECK_ARG(!A->fe_in_mega, "fe_in_mega: the fused kernel's limits (tokens, routes, local experts) are exceeded");
-  return dgm_megamoe_split_launch(A, stream);
+  return 0;
 }
-
-}  // extern "C"
 
 // The persistent kernel's limits (route, token, expert and combine-block counts of its LDS tables)
 static bool fused_fits(const DgmMoeArgs* A) {
@@ -652,8 +654,22 @@ static bool fused_fits(const DgmMoeArgs* A) {
          A->num_tokens <= FUSED_MAX_TOKENS && A->hidden / 64 <= FUSED_MAX_NB64;
 }
 
-// One launch of the persistent kernel running `phases` (FusedParams::phases) of the layer.
+// One launch of the persistent kernel running `phases` (FusedParams::phases) of the layer, with
+// the buffer's own workspace views.
 static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stream) {
+  const DgmBufferLayout* L = A->layout;
+  uint8_t* buf = (uint8_t*)A->buffer;
+  DgmWorkspace w;
+  w.pool = buf + L->pool;
+  w.mid = buf + L->mid;
+  w.mid_sf = buf + L->mid_sf;
+  w.partials = (uint16_t*)(buf + L->partials);
+  w.part_rows = L->max_tokens;
+  w.counters = (int*)(buf + L->counters);
+  return dgm_fused_launch_ws(A, phases, w, stream);
+}
+
+int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, hipStream_t stream) {
   const DgmBufferLayout* L = A->layout;
   uint8_t* buf = (uint8_t*)A->buffer;
   {
@@ -686,14 +702,14 @@ static int fused_launch_phases(const DgmMoeArgs* A, int phases, hipStream_t stre
     p.fe_flags = A->fe_flags;
     p.token_offset = A->token_offset;
     p.E = A->num_experts;
-    p.mid = buf + L->mid;
-    p.mid_sf = buf + L->mid_sf;
-    p.partials = (uint16_t*)(buf + L->partials);
-    p.part_rows = L->max_tokens;
+    p.mid = w.mid;
+    p.mid_sf = w.mid_sf;
+    p.partials = w.partials;
+    p.part_rows = w.part_rows;
     p.y = (uint16_t*)A->y;
-    p.pool_out = buf + L->pool;
+    p.pool_out = w.pool;
     p.recv_stats = A->recv_stats;
-    p.counters = (int*)(buf + L->counters);
+    p.counters = w.counters;
     p.host_err = A->host_error;
     p.M = A->num_tokens;
     p.topk = A->topk;

@@ -332,6 +332,20 @@ def _check_host_error(b):
 
 def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
            fast_math=True, fmt=None, global_scales=(None, None), fe=None, fe_keys=None):
+    _check_host_error(b)
+    args = _moe_args(y, l1, l2, b, stats, activation_clamp, num_tokens, phase_stamps, fast_math, fmt,
+                     global_scales, fe, fe_keys)
+    fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
+    _lib.check(fn(ctypes.byref(args), _lib.stream()))
+    if os.environ.get("DG_CHECK_ERRORS", "0") == "1":     # debug: wait for the launch and check it
+        torch.cuda.synchronize()
+        if b.kernel_error():
+            raise RuntimeError("MegaMoE: a bounded wait of this launch expired; its output is wrong")
+
+
+def _moe_args(y, l1, l2, b, stats, activation_clamp, num_tokens=None, phase_stamps=None, fast_math=True,
+              fmt=None, global_scales=(None, None), fe=None, fe_keys=None):
+    """The C-ABI argument block (DgmMoeArgs) of one layer call on buffer b, after the checks."""
     fmt = fmt or ("mxfp8" if b.act_format in ("mxfp8", "fp8") else "mxfp4")
     kind = lambda f: f if f in ("qoq", "nvfp4") else "mxfp"
     if kind(fmt) != kind(b.act_format):
@@ -372,7 +386,6 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
     assert all(t.is_contiguous() for t in (w1, sf1, w2, sf2))
     if stats is not None:
         assert stats.dtype == torch.int32 and stats.numel() == E_l
-    _check_host_error(b)
     sel = getattr(b, "_fe_select", None)
     if fe is not None:        # in-kernel frontend: (hidden, router_weight, flags, token_offset)
         hidden, router_weight, fe_flags, fe_off = fe
@@ -407,12 +420,7 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
                         host_error=b._host_err_dev, debug_flags=getattr(b, "_debug_flags", 0))
     if phase_stamps is not None:
         assert phase_stamps.dtype == torch.int64 and phase_stamps.is_cuda and phase_stamps.is_contiguous()
-    fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
-    _lib.check(fn(ctypes.byref(args), _lib.stream()))
-    if os.environ.get("DG_CHECK_ERRORS", "0") == "1":     # debug: wait for the launch and check it
-        torch.cuda.synchronize()
-        if b.kernel_error():
-            raise RuntimeError("MegaMoE: a bounded wait of this launch expired; its output is wrong")
+    return args
 
 
 def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, activation_clamp=10.0,

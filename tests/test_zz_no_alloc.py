@@ -1,0 +1,82 @@
+"""The allocation-free layer entry point (dgm_megamoe_fused_launch_noalloc: the persistent kernel's
+workspace in a file-scope device array instead of the caller's buffer) against the buffered entry
+point dgm_megamoe_fused_launch on the same inputs, both through the C ABI: y, top-k, top-k
+weights and recv stats bit for bit, on two calls in a row (the second with fewer tokens), for the
+in-prologue selection (<= 8 tokens) and the selection launch (> 8 tokens); and its size limit,
+which is refused on the host with a clear message."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+E, E_LOCAL, H, I, TOPK = 384, 48, 3072, 1280, 8
+
+
+def _weights(fmt):
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf
+    from hopper_megamoe_basedondeepgemm_amd import quantization_qoq_fused as qq
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1301)
+    w1 = (torch.randn((E_LOCAL, 2 * I, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn((E_LOCAL, H, I), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    if fmt == "qoq":
+        return dgm.transform_qoq_weights_for_mega_moe_fused(qq.quantize_to_qoq(w1), qq.quantize_to_qoq(w2))
+    return dgm.transform_mxfp4_weights_for_mega_moe_fused(qf.quantize_to_mxfp4(w1), qf.quantize_to_mxfp4(w2))
+
+
+def _launch(entry, args):
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    return getattr(_lib.load(), entry)(ctypes.byref(args), _lib.stream())
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "qoq"])
+def test_noalloc_matches_buffered_entry_point(fmt):
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import _lib, mega
+    t1, t2 = _weights(fmt)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, 16, TOPK, H, I, act_format=fmt, ep_size=8, ep_rank=1)
+    rng = np.random.default_rng(1300)
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    for M in (16, 5):                      # two calls in a row, the second with fewer tokens
+        print(f"no-alloc vs buffered: fmt={fmt} M={M} E={E} E_local={E_LOCAL} (EP rank 1 of 8)", flush=True)
+        x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
+        dgm.fable_router_quant_topk_frontend(x, rw, buf, select_in_mega=True)
+        out = {}
+        for entry in ("dgm_megamoe_fused_launch", "dgm_megamoe_fused_launch_noalloc"):
+            y = torch.full((M, H), 3.0, dtype=torch.bfloat16, device="cuda")
+            stats = torch.zeros(E_LOCAL, dtype=torch.int32, device="cuda")
+            args = mega._moe_args(y, t1, t2, buf, stats, 10.0, fmt=fmt)
+            _lib.check(_launch(entry, args))
+            torch.cuda.synchronize()
+            assert buf.host_error() == 0 and buf.kernel_error() == 0
+            out[entry] = (y.view(torch.int16).cpu(), stats.cpu(), buf.topk_idx[:M].cpu().clone(),
+                          buf.topk_weights[:M].cpu().clone().view(torch.int32))
+        a, b = out.values()
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)
+        assert int(a[1].sum()) > 0                 # some routes were local
+
+
+def test_noalloc_size_limit():
+    """More than 512 routes: refused on the host (no launch) with the array's limit named."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import _lib, mega
+    M = 65                                         # 65 * 8 = 520 routes
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, 64, M, TOPK, 512, 256, act_format="mxfp4")
+    w1 = (torch.zeros((64, 32, 4, 64, 16), dtype=torch.uint8, device="cuda"),
+          torch.zeros((64, 32, 1, 64, 4), dtype=torch.uint8, device="cuda"), None)
+    w2 = (torch.zeros((64, 32, 2, 64, 16), dtype=torch.uint8, device="cuda"),
+          torch.zeros((64, 32, 1, 64, 4), dtype=torch.uint8, device="cuda"), None)
+    y = torch.empty((M, 512), dtype=torch.bfloat16, device="cuda")
+    args = mega._moe_args(y, w1, w2, buf, None, 10.0, fmt="mxfp4")
+    st = _launch("dgm_megamoe_fused_launch_noalloc", args)
+    assert st == -1
+    assert b"num_tokens * topk must be <= 512" in _lib.load().dgm_last_error()
