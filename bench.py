@@ -196,7 +196,7 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     ok = bool(torch.isfinite(y.float()).all()) and buf.kernel_error() == 0
     return dict(us_median=float(np.median(us)), us_min=float(us.min()), fe_us=float(np.median(us_fe)),
                 moe_us=float(np.median(us_moe)), moe_us_min=float(us_moe.min()), n_active=n_active,
-                weight_bytes=n_active * expert_bytes, finite=ok, wall_s=wall, y=y)
+                weight_bytes=n_active * expert_bytes, finite=ok, wall_s=wall, y=y, x=x, buf=buf)
 
 
 def copy_calibration(torch, mib, reps=3):
@@ -208,55 +208,95 @@ def copy_calibration(torch, mib, reps=3):
     torch.cuda.synchronize()
 
 
-def cpu_baseline(packed, M=8, sample_routes=None, reps=150, seed=7):
-    """The oracle (numpy fp32 restatement) on the host cores: router + top-8 + cast for the
-    M tokens, then `sample_routes` (default: all) of the 8*M expert routes (forced-balanced: one
-    route per active expert), weights dequantised once before timing (as the reference's CPU path
-    does). The route time is scaled to one layer (8*M routes). Returns (us per layer, BLAS threads)."""
-    from oracle import moe, numerics as nu
-    rng = np.random.default_rng(seed)
-    x = nu.round_bf16(rng.standard_normal((M, H)).astype(np.float32))
-    rw = nu.round_bf16(rng.standard_normal((E, H)).astype(np.float32) * np.float32(0.02))
+def host_cpu():
+    """(model name, physical cores) of the host, from lscpu."""
+    import subprocess
+    model, cores, sockets = "unknown", None, 1
+    try:
+        for ln in subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout.splitlines():
+            k, _, v = ln.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "Model name":
+                model = v
+            elif k == "Core(s) per socket":
+                cores = int(v)
+            elif k == "Socket(s)":
+                sockets = int(v)
+    except Exception:
+        pass
+    return model, (cores * sockets if cores else os.cpu_count())
+
+
+def _dequant_active(packed, experts, workers=16):
+    """{expert: (W1, W2) f32} for the given experts, dequantised on a thread pool (the oracle's
+    packers; numpy releases the GIL)."""
+    import torch
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import packers as pk
+    sel = torch.tensor(experts, dtype=torch.long, device=packed[0].device)
+    p1, s1, p2, s2 = [t.index_select(0, sel).cpu().numpy() for t in packed]
+    with ThreadPoolExecutor(max_workers=min(workers, os.cpu_count() or 1)) as ex:
+        ws = list(ex.map(lambda i: (pk.dequantize_mxfp4_marlin(p1[i], s1[i]), pk.dequantize_mxfp4_marlin(p2[i], s2[i])),
+                         range(len(experts))))
+    return dict(zip(experts, ws))
+
+
+def cpu_baseline_and_parity(packed, headline, router_w, M, act, reps=150):
+    """The oracle (oracle/moe.py, numpy fp32) on the headline step's own inputs (its bf16 hidden
+    states, router weights and packed weights, forced-balanced routing): the step's parity (top-k
+    and activation codes bit-exact, y against the oracle's y: min per-row cos, rel-RMSE), and the
+    oracle layer timed on the host (router + top-8 + cast, then every expert route with the active
+    experts' weights dequantised beforehand, as the reference's CPU path does; median of `reps`).
+    Returns (cpu_baseline dict, parity dict)."""
+    from oracle import moe
+    x = headline["x"].float().cpu().numpy()
+    rw = router_w.float().cpu().numpy()
+    buf = headline["buf"]
+    logits = moe.router_logits_f32(x, rw)
     idx, w = moe.balanced_routing(M, E, TOPK)
-    routes = [(t, s) for t in range(M) for s in range(TOPK)][:sample_routes or M * TOPK]
-    used = sorted({int(idx[t, s]) for t, s in routes})
-    p1, s1, p2, s2 = [np.stack([t[e].cpu().numpy() for e in used]) for t in packed]
-    W1 = moe.LazyDequant(p1, s1)
-    W2 = moe.LazyDequant(p2, s2)
-    pre = {e: (W1[i], W2[i]) for i, e in enumerate(used)}
+    codes, sfb, x_dq = moe.quant_act(x, act)
+    experts = sorted({int(v) for v in idx.ravel()})
+    pre = _dequant_active(packed, experts)
+    W1, W2 = _Sel(pre, 0, (E, 2 * I, H)), _Sel(pre, 1, (E, H, I))
+    ref, _ = moe.moe_forward(x_dq, idx, w, W1, W2, 0, act)
+    y = headline["y"].float().cpu().numpy()
+    m = moe.metrics(y, ref)
+    parity = dict(cos_min=round(m["cos_min"], 7), rel_rmse=round(m["rel_rmse"], 6),
+                  topk_bit_exact=bool((buf.topk_idx[:M].cpu().numpy() == idx).all()),
+                  codes_bit_exact=bool((buf.x[:M].cpu().numpy() == codes).all() and (buf.x_sf[:M].cpu().numpy() == sfb).all()),
+                  gate="cos >= 0.9999 and rel-RMSE <= 0.005",
+                  oracle="oracle/moe.py on this step's inputs (A-%s, M=%d, %d active experts)" % (act.upper(), M, len(experts)))
     times = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        logits = moe.router_logits_f32(x, rw)
-        moe.topk_softmax(logits, TOPK)
-        codes, sfb, x_dq = moe.quant_act(x, "mxfp8")
-        t_front = time.perf_counter() - t0
-        t1 = time.perf_counter()
-        for t, s in routes:
-            e = int(idx[t, s])
-            sub_idx = np.full_like(idx, -1)
-            sub_idx[t, s] = e
-            moe.moe_forward(x_dq, sub_idx, w, _One(e, pre[e][0]), _One(e, pre[e][1]), 0, "mxfp8")
-        t_routes = time.perf_counter() - t1
-        times.append(t_front + t_routes * (M * TOPK) / len(routes))
+        lg = moe.router_logits_f32(x, rw)
+        moe.topk_softmax(lg, TOPK)
+        moe.quant_act(x, act)
+        moe.moe_forward(x_dq, idx, w, W1, W2, 0, act)
+        times.append(time.perf_counter() - t0)
     threads = 1
     try:
         from threadpoolctl import threadpool_info
         threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
     except Exception:
         pass
-    return float(np.median(times)) * 1e6, threads
+    model, phys = host_cpu()
+    cpu = dict(value=round(float(np.median(times)) * 1e6, 1), unit="us/layer", cores=threads, kind="port",
+               cpu_model=model, physical_cores=phys,
+               sample=f"oracle (numpy fp32) on the headline step's inputs: the whole M={M} layer (router + top-8 + "
+                      f"cast, then all {TOPK * M} expert routes with the {len(experts)} active experts' weights "
+                      f"dequantised beforehand), median of {reps}; A-{act.upper()}; cores = BLAS threads")
+    return cpu, parity
 
 
-class _One:
-    """W[e] view of a single pre-dequantised expert (others never touched)."""
+class _Sel:
+    """W[e] of pre-dequantised experts (the oracle touches only routed experts)."""
 
-    def __init__(self, e, w):
-        self.e, self.w = e, w
-        self.shape = (E,) + w.shape
+    def __init__(self, pre, i, shape):
+        self.pre, self.i, self.shape = pre, i, shape
 
-    def __getitem__(self, i):
-        return self.w
+    def __getitem__(self, e):
+        return self.pre[e][self.i]
 
 
 def main():
@@ -340,16 +380,14 @@ def main():
         log(f"unbalanced M=16 mxfp8: {sweep['mxfp8_unbalanced_M16']}")
     if args.copy_calib_mib:
         copy_calibration(torch, args.copy_calib_mib)
-    cpu = None
+    cpu, parity = None, None
     if not args.no_cpu_baseline:
         try:
             t0 = time.perf_counter()
-            us, threads = cpu_baseline(packed, M=args.m)
-            cpu = dict(value=round(us, 1), unit="us/layer", cores=threads, kind="port",
-                       sample=f"oracle (numpy fp32): the whole M={args.m} layer (router + top-8 + cast, then "
-                              f"all {8 * args.m} expert routes with weights dequantised beforehand), median of 150; "
-                              f"A-MXFP8; {time.perf_counter() - t0:.1f} s of host time incl. the dequantisation")
+            cpu, parity = cpu_baseline_and_parity(packed, main_r, router_w, args.m, args.act)
+            cpu["sample"] += f"; {time.perf_counter() - t0:.1f} s of host time incl. the dequantisation"
             log(f"cpu baseline: {cpu}")
+            log(f"headline parity: {parity}")
         except Exception as ex:  # reported, never fatal
             cpu = dict(value=None, unit="us/layer", cores=None, kind="port", sample=f"failed: {ex}")
     us = main_r["us_median"]
@@ -372,6 +410,7 @@ def main():
                      "kernel": "k_megamoe (fused persistent MoE kernel); achieved = active-expert MXFP4 weight "
                                "bytes (6,266,880 B per expert) / median kernel time (HIP events)"},
         "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(line), flush=True)
 

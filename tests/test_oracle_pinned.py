@@ -1,0 +1,211 @@
+"""Known-answer checks of the oracle's layer-level float functions (CPU).
+
+Each case is built so that every stage is exact and the expected output can be written down by
+hand (the derivation is in the comments), and so that a plausible misreading of the reference
+rule gives a different answer:
+
+  * the SwiGLU epilogue of moe_forward (sm100_b200/test_mega_moe.py:455-460;
+    tests/test_four_api_correctness.py:437-442): with no clamp, a gate >= 17 has
+    sigmoid(g) == 1.0 exactly in fp32 (1 + e^-17 rounds to 1), so silu(g) == g; with one-hot
+    weight rows, gate / up / the L2 output are chosen values, and values on the E2M1 grid
+    requantise losslessly. Caught: gate and up swapped, the routing weight dropped, the gate
+    clamped from below or not at all, the up projection clamped on one side only, gate / up not
+    rounded to bf16, the routes not rounded to bf16 per route, routes summed in expert order
+    instead of slot order;
+  * requant_mid_qoq (tests/test_four_api_correctness.py:54-60): per-64 groups (not per-128),
+    scale amax / 127 with a FLT_MIN floor, round half to even (not floor, not half away);
+  * requant_mid_nvfp4 and cast_to_nvfp4_rows (sm100_b200/test_mega_moe.py:68-93, 431-438):
+    per-16 groups (not per-32), E4M3 scale rounded to nearest even (not ceil), ties-down E2M1,
+    low nibble first, no -0;
+  * moe_forward_qoq: fp32 gate / up (no bf16 rounding) and per-route bf16 outputs."""
+import numpy as np
+import pytest
+
+from oracle import moe
+from oracle import packers as pk
+
+NOCLAMP = 1e30
+# the 16 signed E2M1 values, twice: 32 features
+U32 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, 0, -.5, -1, -1.5, -2, -3, -4, -6] * 2, dtype=np.float32)
+
+
+def layer(E_local, I, H):
+    """Identity-style weights: W1 [E, 2I, H] gate row j = e_j, up row j = e_{I+j};
+    W2 [E, H, I] row n = e_n for n < I, 0 otherwise (out[n] = act[n])."""
+    W1 = np.zeros((E_local, 2 * I, H), np.float32)
+    W2 = np.zeros((E_local, H, I), np.float32)
+    for e in range(E_local):
+        W1[e, np.arange(2 * I), np.arange(2 * I)] = 1.0
+        W2[e, np.arange(I), np.arange(I)] = 1.0
+    return W1, W2
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8", "nvfp4"])
+def test_epilogue_order_weight_and_two_routes(fmt):
+    # gate = 32 (silu 32 = 32 exactly), up = u (E2M1 values, |u| <= 6).
+    # route 0: expert 0, weight 1/32: act = 32 * u / 32 = u, amax 6 -> MXFP4 scale 1, MXFP8
+    #   scale 2^-6 (u * 64 is E4M3-exact), NVFP4 scale E4M3(6 / 6) = 1: requant exact; out = u.
+    # route 1: expert 1, weight 1/16: act = 2u (requant exact at twice the scale); W2 = 2 * I,
+    #   out = 4u. y = u + 4u = 5u (exact in fp32 and per route in bf16).
+    I, H = 32, 64
+    W1, W2 = layer(2, I, H)
+    W2[1] *= 2.0
+    x = np.zeros((1, H), np.float32)
+    x[0, :I] = 32.0
+    x[0, I:] = U32
+    idx = np.array([[0, 1]])
+    w = np.array([[1 / 32, 1 / 16]], np.float32)
+    y, routes = moe.moe_forward(x, idx, w, W1, W2, 0, fmt, clamp=NOCLAMP)
+    want = np.zeros(H, np.float32)
+    want[:I] = 5 * U32
+    np.testing.assert_array_equal(y[0], want)
+    np.testing.assert_array_equal(routes[0][:I], U32)
+    np.testing.assert_array_equal(routes[1][:I], 4 * U32)
+
+
+def test_epilogue_clamp_semantics():
+    I, H = 32, 64
+    W1, W2 = layer(1, I, H)
+    # (1) c = 32: gate 64 -> min(64, 32) = 32 (silu 32 exact); up 64 -> 32, -64 -> -32, 16, -8
+    #     stay; weight 1/256: act = 32 * up / 256 = up / 8 = 4, -4, 2, -1; amax 4 -> MXFP4
+    #     scale ceil_ue8m0(4 / 6) = 1: exact.
+    x = np.zeros((1, H), np.float32)
+    x[0, :4] = 64.0
+    x[0, I:I + 4] = [64.0, -64.0, 16.0, -8.0]
+    y, _ = moe.moe_forward(x, np.array([[0]]), np.array([[1 / 256]], np.float32), W1, W2, 0, "mxfp4", clamp=32.0)
+    np.testing.assert_array_equal(y[0, :4], [4.0, -4.0, 2.0, -1.0])
+    assert not y[0, 4:].any()
+    # (2) c = 2, gate -3 is not clamped from below: silu(-3) = -3 / (1 + e^3) = -0.142277..;
+    #     up 2, weight 1: act = -0.284555..; alone in its group: scale = ceil_ue8m0(0.284555 / 6
+    #     = 0.0474) = 2^-4; |act| / 2^-4 = 4.553 -> E2M1 4 -> -0.25. (A gate clamped to -2 would
+    #     give silu(-2) * 2 = -0.4768 -> scale 2^-3, 3.81 -> 4 -> -0.5.)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = -3.0
+    x[0, I] = 2.0
+    y, _ = moe.moe_forward(x, np.array([[0]]), np.array([[1.0]], np.float32), W1, W2, 0, "mxfp4", clamp=2.0)
+    assert y[0, 0] == -0.25 and not y[0, 1:].any()
+
+
+def test_epilogue_bf16_rounding_of_gate_and_up():
+    # Two MXFP4 groups (I = 64). Group 0: feature 0 gate = 32 + 0.125 = 32.125 (a sum of two
+    # inputs), which rounds to bf16 32.0 (a tie, to even); up 0.75, weight 1/4 -> act 6.0;
+    # feature 1: gate 32, up 1/16 -> act 0.5. amax 6 -> scale 1 -> y = 6, 0.5. Without the bf16
+    # rounding act0 = 6.0234 -> scale 2 and 0.5 / 2 = 0.25 is a tie, down to 0 -> y1 = 0.
+    # Group 1 (features 32, 33): the same through up = 0.75 + 2^-10 (bf16 0.75), gate 32.
+    I, H = 64, 2 * 64 + 2
+    W1, W2 = layer(1, I, H)
+    W1[0, 0, 2 * I] = 1.0                 # gate 0 = x[0] + x[128]
+    W1[0, I + 32, 2 * I + 1] = 1.0        # up 32 = x[96] + x[129]
+    x = np.zeros((1, H), np.float32)
+    x[0, [0, 1, 32, 33]] = 32.0
+    x[0, 2 * I] = 0.125
+    x[0, [I + 0, I + 32]] = 0.75
+    x[0, [I + 1, I + 33]] = 1 / 16
+    x[0, 2 * I + 1] = 2.0 ** -10
+    y, _ = moe.moe_forward(x, np.array([[0]]), np.array([[0.25]], np.float32), W1, W2, 0, "mxfp4", clamp=NOCLAMP)
+    want = np.zeros(H, np.float32)
+    want[[0, 1, 32, 33]] = [6.0, 0.5, 6.0, 0.5]
+    np.testing.assert_array_equal(y[0], want)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "qoq"])
+def test_routes_rounded_to_bf16_and_summed_in_slot_order(fmt):
+    # Token 0 has three routes: slot 0 -> expert 2, slot 1 -> expert 0, slot 2 -> expert 1, each
+    # with act = 32 * u / 32 = u, requantised exactly (MXFP4: u = 1, on the grid; QoQ: u =
+    # 127/128, scale u / 127 = 2^-7, code 127).
+    # Expert 2 multiplies by 1 + 2^-10: its output u (1 + 2^-10) rounds to bf16 u (the change is
+    # below half a bf16 ulp). Experts 0 and 1 scale to h = half an fp32 ulp of u (a power of
+    # two: a bf16 value). Slot order: (u + h) + h = u (each add a tie, to even); expert order:
+    # (h + h) + u = u + 2h != u; without the per-route bf16 rounding y would exceed u.
+    I, H = 64, 128
+    W1, W2 = layer(3, I, H)
+    u = np.float32(127 / 128) if fmt == "qoq" else np.float32(1.0)
+    h = np.float32(np.spacing(u) / 2)
+    W2[2] *= np.float32(1 + 2.0 ** -10)
+    W2[0] *= np.float32(h / u)
+    W2[1] *= np.float32(h / u)
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = 32.0
+    x[0, I] = u
+    idx = np.array([[2, 0, 1]])
+    w = np.array([[1 / 32] * 3], np.float32)
+    if fmt == "qoq":
+        y, routes = moe.moe_forward_qoq(x, idx, w, W1, W2, 0, clamp=NOCLAMP)
+    else:
+        y, routes = moe.moe_forward(x, idx, w, W1, W2, 0, fmt, clamp=NOCLAMP)
+    assert routes[0][0] == u                      # u (1 + 2^-10) rounded to bf16
+    assert routes[1][0] == routes[2][0] == h
+    assert y[0, 0] == u                           # slot order, not expert order
+    assert not y[0, 1:].any()
+
+
+def test_qoq_gate_up_stay_fp32():
+    # The QoQ layer keeps gate / up in fp32. Gate = 32 + 0.0625 = 32.0625 (two inputs; bf16
+    # would be 32.0), up 127/128, weight 1/32: act = 32.0625 * 127/128 / 32 = 65151/65536
+    # = 0.99412537 (exact); alone in its 64-group it requantises to itself (code 127, to an fp32
+    # ulp or two). W2 multiplies by f = 1.0029296875 / (127/128): the route is 0.99412537 f =
+    # 1.00488, above the bf16 midpoint 1 + 2^-8 -> 1.0078125. A bf16 gate would give act =
+    # 127/128 and a route 1.0029296875 below the midpoint -> 1.0.
+    I, H = 64, 2 * 64 + 1
+    W1, W2 = layer(1, I, H)
+    W1[0, 0, 2 * I] = 1.0                         # gate 0 = x[0] + x[128]
+    x = np.zeros((1, H), np.float32)
+    x[0, 0] = 32.0
+    x[0, 2 * I] = 0.0625
+    x[0, I] = 127 / 128
+    W2[0] *= np.float32(1.0029296875 / (127 / 128))
+    y, routes = moe.moe_forward_qoq(x, np.array([[0]]), np.array([[1 / 32]], np.float32), W1, W2, 0,
+                                    clamp=NOCLAMP)
+    assert routes[0][0] == 1.0078125 and y[0, 0] == 1.0078125
+    assert not y[0, 1:].any()
+
+
+def test_requant_mid_qoq_known_answers():
+    a = np.zeros((1, 192), np.float32)
+    # group 0: amax 127 -> scale 1: rint half-even of 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5,
+    # -127, 3.25 -> 0, 2, 2, -0, -2, -2, 126, -127, 3
+    a[0, :10] = [127, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -127, 3.25]
+    # group 1: amax 254 -> scale 2: 254, 3, 5, 1, -7, 253 -> /2 = 127, 1.5, 2.5, 0.5, -3.5, 126.5
+    # -> 127, 2, 2, 0, -4, 126 -> dequant 254, 4, 4, 0, -8, 252
+    a[0, 64:70] = [254, 3, 5, 1, -7, 253]
+    # group 2: all zero -> scale FLT_MIN, codes 0
+    q, sc, dq = moe.requant_mid_qoq(a)
+    np.testing.assert_array_equal(q[0, :10], [127, 0, 2, 2, 0, -2, -2, 126, -127, 3])
+    np.testing.assert_array_equal(q[0, 64:70], [127, 2, 2, 0, -4, 126])
+    assert not q[0, 10:64].any() and not q[0, 70:].any()
+    np.testing.assert_array_equal(sc[0], np.array([1.0, 2.0, np.finfo(np.float32).tiny], np.float32))
+    np.testing.assert_array_equal(dq[0, 64:70], [254, 4, 4, 0, -8, 252])
+    assert not dq[0, 128:].any() and np.isfinite(dq).all()
+
+
+# the NVFP4 case: two 16-element groups
+NV_ROW = np.zeros(32, np.float32)
+# group 0: amax 6.375, 6.375 / 6 = 1.0625 is the midpoint of E4M3 1.0 and 1.125 -> RNE 1.0
+# (0x38; ceil would give 1.125). x / 1 -> 6.375 > 5: code 7 (6); 2.25: code 4 (2); 1.25: a tie,
+# down: code 2 (1); -0.3125: code 1 with sign: 0x9 (-0.5)
+NV_ROW[:4] = [6.375, 2.25, 1.25, -0.3125]
+# group 1: amax 3, 3 / 6 = 0.5 (0x30). x / 0.5 -> 6: code 7 (3.0); 1.5: code 3 (0.75); 0.625:
+# code 1 (0.25); -3.25: code 5 with sign: 0xD (-1.5). (One scale over all 32 would give 0.75 /
+# 1 = 0.75, a tie, down to 0.5.)
+NV_ROW[16:20] = [3.0, 0.75, 0.3125, -1.625]
+
+
+def test_requant_mid_nvfp4_known_answers():
+    dq = moe.requant_mid_nvfp4(NV_ROW[None])[0]
+    want = np.zeros(32, np.float32)
+    want[:4] = [6.0, 2.0, 1.0, -0.5]
+    want[16:20] = [3.0, 0.75, 0.25, -1.5]
+    np.testing.assert_array_equal(dq, want)
+
+
+def test_cast_to_nvfp4_rows_known_answers():
+    packed, sf, sfb = pk.cast_to_nvfp4_rows(NV_ROW[None])
+    # low nibble first: (7 | 4 << 4), (2 | 9 << 4), zeros; (7 | 3 << 4), (1 | 0xD << 4), zeros
+    want = np.zeros(16, np.uint8)
+    want[[0, 1, 8, 9]] = [0x47, 0x92, 0x37, 0xD1]
+    np.testing.assert_array_equal(packed[0], want)
+    np.testing.assert_array_equal(sfb[0], [0x38, 0x30])
+    np.testing.assert_array_equal(sf[0], [1.0, 0.5])
+    # an all-zero group: amax floor 1e-30 -> E4M3(1.67e-31) = 0 -> codes 0 (no -0, no NaN)
+    p0, _, s0 = pk.cast_to_nvfp4_rows(np.zeros((1, 16), np.float32))
+    assert not p0.any() and not s0.any()
