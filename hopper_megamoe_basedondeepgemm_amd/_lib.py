@@ -10,6 +10,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdgm_megamoe.so")
+PROBE_LIB_PATH = os.path.join(_HERE, "libdgm_probe.so")     # the tests' lane-layout probes
 
 ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1, "qoq": 2, "nvfp4": 3}
 FE_FORCE_BALANCED = 1
@@ -21,9 +22,7 @@ EXPORTS = [
     "dgm_quantize_nvfp4", "dgm_quantize_qoq", "dgm_cast_int8_rows", "dgm_transform_fp4_weights",
     "dgm_fused_buffer_layout", "dgm_router_topk_launch", "dgm_megamoe_fused_launch",
     "dgm_megamoe_split_launch",
-    "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_probe_mfma_scale",
-    "dgm_probe_mfma_scale_sel",
-    "dgm_probe_mfma_i8", "dgm_probe_mfma_f16", "dgm_probe_cvt_fp4",
+    "dgm_device_cu_count", "dgm_fused_workgroups",
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
     "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
 ]
@@ -89,11 +88,6 @@ def load():
         "dgm_megamoe_fused_launch_noalloc": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_device_cu_count": ([], i32),
         "dgm_fused_workgroups": ([i32, i32, i32], i32),
-        "dgm_probe_mfma_scale": ([vp, vp, vp, vp, vp, i32, i32, vp], i32),
-        "dgm_probe_mfma_scale_sel": ([vp, vp, vp, vp, vp, i32, vp], i32),
-        "dgm_probe_mfma_i8": ([vp, vp, vp, vp], i32),
-        "dgm_probe_mfma_f16": ([vp, vp, vp, vp], i32),
-        "dgm_probe_cvt_fp4": ([vp, vp, vp, vp, i32, vp], i32),
         "dgm_transform_qoq_weights": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
         "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_host_device_pointer": ([vp, ctypes.POINTER(vp)], i32),
@@ -103,6 +97,36 @@ def load():
         fn.argtypes = args
         fn.restype = res
     _lib = lib
+    return lib
+
+
+PROBE_EXPORTS = ["dgm_probe_mfma_scale", "dgm_probe_mfma_scale_sel", "dgm_probe_mfma_i8", "dgm_probe_mfma_f16",
+                 "dgm_probe_cvt_fp4", "dgm_probe_global_load_lds"]
+_probe = None
+
+
+def load_probe():
+    """The tests' probe library (include/dgm_probe.h; raises if it has not been built)."""
+    global _probe
+    if _probe is not None:
+        return _probe
+    if not os.path.exists(PROBE_LIB_PATH):
+        raise RuntimeError(f"{PROBE_LIB_PATH} is not built; run `python -m hopper_megamoe_basedondeepgemm_amd.build`")
+    lib = ctypes.CDLL(PROBE_LIB_PATH)
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    sig = {
+        "dgm_probe_mfma_scale": ([vp, vp, vp, vp, vp, i32, i32, vp], i32),
+        "dgm_probe_mfma_scale_sel": ([vp, vp, vp, vp, vp, i32, vp], i32),
+        "dgm_probe_mfma_i8": ([vp, vp, vp, vp], i32),
+        "dgm_probe_mfma_f16": ([vp, vp, vp, vp], i32),
+        "dgm_probe_cvt_fp4": ([vp, vp, vp, vp, i32, vp], i32),
+        "dgm_probe_global_load_lds": ([vp, vp, vp], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _probe = lib
     return lib
 
 

@@ -1,7 +1,8 @@
-"""Build the HIP shared library libdgm_megamoe.so in-tree for gfx950 (hipcc, ahead of time).
+"""Build the HIP shared libraries in-tree for gfx950 (hipcc, ahead of time): libdgm_megamoe.so
+(the layer) and libdgm_probe.so (the tests' lane-layout probes).
 
 Each source is compiled to an object file in its own hipcc process (in parallel), then the
-objects are linked into the shared library."""
+objects are linked into their shared library."""
 import os
 import subprocess
 import sys
@@ -11,7 +12,9 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdgm_megamoe.so")
-SOURCES = ["dgm_megamoe.hip", "dgm_fused.hip", "dgm_packers.hip", "dgm_probe.hip", "dgm_noalloc.hip"]
+PROBE_LIB = os.path.join(HERE, "libdgm_probe.so")
+SOURCES = ["dgm_megamoe.hip", "dgm_fused.hip", "dgm_packers.hip", "dgm_noalloc.hip"]
+PROBE_SOURCES = ["dgm_probe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
@@ -32,24 +35,26 @@ def _run(cmd):
 
 
 def build(verbose=False):
-    tmp = LIB + ".tmp"
+    srcs = SOURCES + PROBE_SOURCES
     with tempfile.TemporaryDirectory(prefix="dgm_build_") as td:
-        objs = [os.path.join(td, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-        cmds = [[HIPCC] + FLAGS + ["-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(SOURCES, objs)]
+        objs = {src: os.path.join(td, os.path.splitext(src)[0] + ".o") for src in srcs}
+        cmds = [[HIPCC] + FLAGS + ["-c", os.path.join(CSRC, src), "-o", objs[src]] for src in srcs]
         if verbose:
             for c in cmds:
                 print(" ".join(c), flush=True)
         with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
             results = list(ex.map(_run, cmds))
-        for (rc, errs), src in zip(results, SOURCES):
+        for (rc, errs), src in zip(results, srcs):
             if rc != 0:
                 raise RuntimeError(f"hipcc failed on {src} ({rc}):\n{errs}")
             if verbose and errs:
                 print(errs)
-        rc, errs = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + objs + ["-o", tmp])
-        if rc != 0:
-            raise RuntimeError(f"link failed ({rc}):\n{errs}")
-    os.replace(tmp, LIB)
+        for lib, group in ((LIB, SOURCES), (PROBE_LIB, PROBE_SOURCES)):
+            tmp = lib + ".tmp"
+            rc, errs = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC"] + [objs[g] for g in group] + ["-o", tmp])
+            if rc != 0:
+                raise RuntimeError(f"link of {os.path.basename(lib)} failed ({rc}):\n{errs}")
+            os.replace(tmp, lib)
     return LIB
 
 

@@ -1,10 +1,19 @@
-// Diagnostic: one block-scaled matrix-core op on caller-provided lane fragments, so the
-// tests can check the lane layout the kernels assume (A row l%16 / B column l%16, K chunk
-// 32*(l/16), scale byte of that 32-block; D[4*(l/16)+i][l%16] in result register i).
+// Test-only probes (libdgm_probe.so, declared in include/dgm_probe.h; not part of the layer's
+// library): single instructions on caller-provided lane data, so the tests can pin the lane
+// layouts and conversions the kernels assume. One block-scaled matrix-core op: A row l%16 / B
+// column l%16, K chunk 32*(l/16), scale byte of that 32-block; D[4*(l/16)+i][l%16] in result
+// register i.
 #include "dgm_common.hpp"
-#include "dgm_abi_internal.hpp"
+#include "../../include/dgm_probe.h"
 
 using namespace dgm;
+
+#define PROBE_CHECK(cond) \
+  do {                   \
+    if (!(cond)) return -1; \
+  } while (0)
+
+static int probe_status() { return (int)hipGetLastError(); }
 
 template <int FA, int FB>
 __global__ void k_probe(const v8i* a, const v8i* b, const int* sa, const int* sb, float* out) {
@@ -25,7 +34,7 @@ __global__ void k_probe_sel(const v8i* a, const v8i* b, const int* sa, const int
 // Byte select of the scale words (E2M1 x E2M1): the scale used is byte `sel` of sa / sb.
 extern "C" int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void* sa, const void* sb,
                                         void* out, int sel, hipStream_t stream) {
-  DGM_CHECK_ARG(a && b && sa && sb && out && sel >= 0 && sel < 4, "bad argument");
+  PROBE_CHECK(a && b && sa && sb && out && sel >= 0 && sel < 4);
   const v8i* A = (const v8i*)a;
   const v8i* B = (const v8i*)b;
   switch (sel) {
@@ -34,12 +43,12 @@ extern "C" int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void
     case 2: hipLaunchKernelGGL((k_probe_sel<2>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out); break;
     default: hipLaunchKernelGGL((k_probe_sel<3>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out); break;
   }
-  return dgm_last_launch_status();
+  return probe_status();
 }
 
 extern "C" int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const void* sb,
                                     void* out, int fmt_a, int fmt_b, hipStream_t stream) {
-  DGM_CHECK_ARG(a && b && sa && sb && out, "null pointer");
+  PROBE_CHECK(a && b && sa && sb && out);
   const v8i* A = (const v8i*)a;
   const v8i* B = (const v8i*)b;
   if (fmt_a == 4 && fmt_b == 4)
@@ -49,8 +58,8 @@ extern "C" int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa
   else if (fmt_a == 0 && fmt_b == 0)
     hipLaunchKernelGGL((k_probe<0, 0>), dim3(1), dim3(64), 0, stream, A, B, (const int*)sa, (const int*)sb, (float*)out);
   else
-    DGM_CHECK_ARG(false, "fmt pairs (4,4), (4,0), (0,0)");
-  return dgm_last_launch_status();
+    return -1;       // fmt pairs (4,4), (4,0), (0,0)
+  return probe_status();
 }
 
 // One int8 matrix-core op (V_MFMA_I32_16X16X64_I8) on caller-provided lane fragments
@@ -63,9 +72,9 @@ __global__ void k_probe_i8(const v4i* a, const v4i* b, v4i* out) {
 }
 
 extern "C" int dgm_probe_mfma_i8(const void* a, const void* b, void* out, hipStream_t stream) {
-  DGM_CHECK_ARG(a && b && out, "null pointer");
+  PROBE_CHECK(a && b && out);
   hipLaunchKernelGGL(k_probe_i8, dim3(1), dim3(64), 0, stream, (const v4i*)a, (const v4i*)b, (v4i*)out);
-  return dgm_last_launch_status();
+  return probe_status();
 }
 
 // One f16 matrix-core op (V_MFMA_F32_16X16X32_F16) on caller-provided lane fragments (a, b:
@@ -77,9 +86,9 @@ __global__ void k_probe_f16(const v8h* a, const v8h* b, v4f* out) {
 }
 
 extern "C" int dgm_probe_mfma_f16(const void* a, const void* b, void* out, hipStream_t stream) {
-  DGM_CHECK_ARG(a && b && out, "null pointer");
+  PROBE_CHECK(a && b && out);
   hipLaunchKernelGGL(k_probe_f16, dim3(1), dim3(64), 0, stream, (const v8h*)a, (const v8h*)b, (v4f*)out);
-  return dgm_last_launch_status();
+  return probe_status();
 }
 
 // The conversions of the NVFP4 path: for each i < n, out_h[4 i + j] = the two f16 of
@@ -102,9 +111,28 @@ __global__ void k_probe_cvt(const uint32_t* src, const float* scale, uint32_t* o
 
 extern "C" int dgm_probe_cvt_fp4(const void* src, const void* scale, void* out_h, void* out_f, int n,
                                  hipStream_t stream) {
-  DGM_CHECK_ARG(src && scale && out_h && out_f && n >= 0, "null pointer or n < 0");
+  PROBE_CHECK(src && scale && out_h && out_f && n >= 0);
   if (n == 0) return 0;
   hipLaunchKernelGGL(k_probe_cvt, dim3((n + 255) / 256), dim3(256), 0, stream, (const uint32_t*)src,
                      (const float*)scale, (uint32_t*)out_h, (float*)out_f, n);
-  return dgm_last_launch_status();
+  return probe_status();
+}
+
+// Direct global -> LDS loads (GLOBAL_LOAD_LDS_DWORDX4, the L2 phase's weight prefetch): wave w
+// loads 1 KB of src (lane l: bytes 16 l .. +16 of the wave's KB) into LDS at a wave-uniform base,
+// then every lane reads back the 16 bytes at base + 16 l; out[w][l] = what lane l read.
+__global__ void k_probe_lds(const uint8_t* src, uint4* out) {
+  __shared__ __attribute__((aligned(16))) uint8_t buf[4][1024];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  __builtin_amdgcn_global_load_lds(src + wv * 1024 + lane * 16, (__attribute__((address_space(3))) void*)&buf[wv][0],
+                                   16, 0, 2);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  out[threadIdx.x] = *reinterpret_cast<const uint4*>(&buf[wv][lane * 16]);
+}
+
+extern "C" int dgm_probe_global_load_lds(const void* src, void* out, hipStream_t stream) {
+  PROBE_CHECK(src && out);
+  hipLaunchKernelGGL(k_probe_lds, dim3(1), dim3(256), 0, stream, (const uint8_t*)src, (uint4*)out);
+  return probe_status();
 }

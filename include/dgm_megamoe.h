@@ -230,25 +230,11 @@ int dgm_megamoe_split_launch(const DgmMoeArgs* args, hipStream_t stream);
 int dgm_host_device_pointer(const void* host, void** device);
 
 /* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the
- * current device. dgm_probe_mfma_scale: runs one V_MFMA_SCALE_F32_16X16X128_F8F6F4 on 64
- * caller-provided lane fragments (a, b: 64 x 32 bytes; sa, sb: 64 int32 scale words;
- * out: 64 x 4 fp32) so tests can pin the lane layout the kernels assume. fmt 4 = E2M1,
- * 0 = E4M3; pairs (4,4), (4,0), (0,0). */
+ * current device. dgm_fused_workgroups: workgroups of the persistent kernel for a shape (0 before
+ * its first launch). The lane-layout probes of the tests live in a library of their own
+ * (include/dgm_probe.h). */
 int dgm_device_cu_count(void);
-/* Workgroups of the persistent kernel for a shape (0 before its first launch). */
 int dgm_fused_workgroups(int hidden, int intermediate, int act_format);
-int dgm_probe_mfma_scale(const void* a, const void* b, const void* sa, const void* sb, void* out,
-                         int fmt_a, int fmt_b, hipStream_t stream);
-/* Same with E2M1 x E2M1 operands and the scale taken from byte `sel` (0..3) of sa / sb. */
-int dgm_probe_mfma_scale_sel(const void* a, const void* b, const void* sa, const void* sb, void* out,
-                             int sel, hipStream_t stream);
-/* One int8 op (V_MFMA_I32_16X16X64_I8): a, b 64 x 16 bytes, out 64 x 4 int32. */
-int dgm_probe_mfma_i8(const void* a, const void* b, void* out, hipStream_t stream);
-/* Same for V_MFMA_F32_16X16X32_F16 (a, b: 64 x 8 halves; out: 64 x 4 fp32), and the NVFP4 path's
- * conversions: for i < n, out_h[4i+j] = V_CVT_SCALEF32_PK_F16_FP4(byte j of src[i], scale[i])
- * (two f16), out_f[4i+j] = V_CVT_F32_FP8(byte j of src[i]) (E4M3). */
-int dgm_probe_mfma_f16(const void* a, const void* b, void* out, hipStream_t stream);
-int dgm_probe_cvt_fp4(const void* src, const void* scale, void* out_h, void* out_f, int n, hipStream_t stream);
 
 #ifdef __cplusplus
 }

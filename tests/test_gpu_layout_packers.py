@@ -32,7 +32,7 @@ def _probe(fa, fb, seed, sel=None):
     tsa, tsb = torch.from_numpy(sa).to(dev), torch.from_numpy(sb).to(dev)
     out = torch.zeros(64 * 4, dtype=torch.float32, device=dev)
     if sel is None:
-        _lib.check(_lib.load().dgm_probe_mfma_scale(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
+        _lib.check(_lib.load_probe().dgm_probe_mfma_scale(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
                                                     _lib.ptr(out), fa, fb, _lib.stream()))
     else:
         # the scale sits in byte `sel` of each word; the other bytes hold other (wrong) codes
@@ -42,7 +42,7 @@ def _probe(fa, fb, seed, sel=None):
         wa = (noise[0] << np.array([0, 8, 16, 24])).sum(-1).astype(np.uint32).view(np.int32)
         wb = (noise[1] << np.array([0, 8, 16, 24])).sum(-1).astype(np.uint32).view(np.int32)
         tsa, tsb = torch.from_numpy(wa).to(dev), torch.from_numpy(wb).to(dev)
-        _lib.check(_lib.load().dgm_probe_mfma_scale_sel(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
+        _lib.check(_lib.load_probe().dgm_probe_mfma_scale_sel(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(tsa), _lib.ptr(tsb),
                                                         _lib.ptr(out), sel, _lib.stream()))
     torch.cuda.synchronize()
     got = out.cpu().numpy().reshape(64, 4)
@@ -183,7 +183,7 @@ def test_mfma_i8_lane_layout():
     b = rng.integers(-128, 128, (64, 16), dtype=np.int64).astype(np.int8)
     ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
     out = torch.zeros(64 * 4, dtype=torch.int32, device="cuda")
-    _lib.check(_lib.load().dgm_probe_mfma_i8(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(out), _lib.stream()))
+    _lib.check(_lib.load_probe().dgm_probe_mfma_i8(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(out), _lib.stream()))
     torch.cuda.synchronize()
     got = out.cpu().numpy().reshape(64, 4)
     res = {}
@@ -236,7 +236,7 @@ def test_mfma_f16_lane_layout():
     b = rng.integers(-8, 9, (64, 8)).astype(np.float16)
     ta, tb = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
     out = torch.zeros(64 * 4, dtype=torch.float32, device="cuda")
-    _lib.check(_lib.load().dgm_probe_mfma_f16(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(out), _lib.stream()))
+    _lib.check(_lib.load_probe().dgm_probe_mfma_f16(_lib.ptr(ta), _lib.ptr(tb), _lib.ptr(out), _lib.stream()))
     torch.cuda.synchronize()
     got = out.cpu().numpy().reshape(64, 4)
     A = np.zeros((16, 32))
@@ -266,7 +266,7 @@ def test_cvt_fp4_f16_and_fp8():
     ts, tsc = torch.from_numpy(src.view(np.int32)).cuda(), torch.from_numpy(sc).cuda()
     oh = torch.zeros(4 * n, dtype=torch.int32, device="cuda")
     of = torch.zeros(4 * n, dtype=torch.float32, device="cuda")
-    _lib.check(_lib.load().dgm_probe_cvt_fp4(_lib.ptr(ts), _lib.ptr(tsc), _lib.ptr(oh), _lib.ptr(of), n,
+    _lib.check(_lib.load_probe().dgm_probe_cvt_fp4(_lib.ptr(ts), _lib.ptr(tsc), _lib.ptr(oh), _lib.ptr(of), n,
                                              _lib.stream()))
     torch.cuda.synchronize()
     h = oh.cpu().numpy().view(np.uint32).reshape(n, 4)
@@ -287,3 +287,15 @@ def test_cvt_fp4_f16_and_fp8():
     ref = nu.e4m3_decode(byte.astype(np.uint8))
     keep = ~np.isnan(ref)
     np.testing.assert_array_equal(f[keep], ref[keep])
+
+
+def test_global_load_lds_lane_layout():
+    """GLOBAL_LOAD_LDS_DWORDX4 (the L2 phase's prefetch of weight tiles into LDS): lane l of a
+    wave lands its 16 bytes at the wave's LDS base + 16 l, so a 1 KB tile keeps its order."""
+    need_gpu()
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    src = torch.randint(0, 256, (4096,), dtype=torch.uint8, device="cuda")
+    out = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    _lib.check(_lib.load_probe().dgm_probe_global_load_lds(_lib.ptr(src), _lib.ptr(out), _lib.stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), src.cpu())

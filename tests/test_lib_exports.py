@@ -10,23 +10,26 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def declared_symbols():
-    names = set()
-    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
-        txt = open(h).read()
-        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-        names |= set(re.findall(r"\b(dgm_\w+)\s*\(", txt))
-    return sorted(names)
+def declared_symbols(header):
+    txt = open(os.path.join(ROOT, "include", header)).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(dgm_\w+)\s*\(", txt)))
 
 
 def test_library_exports_every_declared_symbol():
+    """libdgm_megamoe.so exports what include/dgm_megamoe.h declares, libdgm_probe.so (the tests'
+    probes) what include/dgm_probe.h declares, and every header is one of the two."""
     from hopper_megamoe_basedondeepgemm_amd import _lib
-    lib = _lib.load()
-    names = declared_symbols()
-    assert len(names) >= 14
-    for n in names:
-        assert hasattr(lib, n), n
-    assert set(names) == set(_lib.EXPORTS)
+    assert sorted(os.path.basename(h) for h in glob.glob(os.path.join(ROOT, "include", "*.h"))) == \
+        ["dgm_megamoe.h", "dgm_probe.h"]
+    for header, lib, exports in (("dgm_megamoe.h", _lib.load(), _lib.EXPORTS),
+                                 ("dgm_probe.h", _lib.load_probe(), _lib.PROBE_EXPORTS)):
+        names = declared_symbols(header)
+        assert len(names) >= 5
+        for n in names:
+            assert hasattr(lib, n), n
+        assert set(names) == set(exports)
+    assert not any(n.startswith("dgm_probe") for n in declared_symbols("dgm_megamoe.h"))
 
 
 def test_host_checks_and_layout():
