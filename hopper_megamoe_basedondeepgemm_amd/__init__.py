@@ -12,6 +12,10 @@ from .mega import (FusedSymmBuffer, get_fused_symm_buffer_for_mega_moe,
                    transform_qoq_int4_weights_for_mega_moe_sm90)
 from . import quantization_mxfp4, quantization_mxfp4_fused, quantization_nvfp4, quantization_qoq_fused
 from .utils import per_token_cast_to_fp4, per_token_cast_to_fp8, ceil_div, align
+from . import checkpoint
+from .checkpoint import (mxfp4_checkpoint_to_mega_moe, nvfp4_checkpoint_to_mega_moe, mega_moe_to_mxfp4_checkpoint,
+                         mega_moe_to_nvfp4_checkpoint, untransform_mxfp4_weights_for_mega_moe_fused,
+                         untransform_nvfp4_weights_for_mega_moe_fused)
 
 __all__ = [
     "FusedSymmBuffer", "get_fused_symm_buffer_for_mega_moe", "transform_mxfp4_weights_for_mega_moe_fused",
@@ -23,4 +27,7 @@ __all__ = [
     "transform_qoq_int4_weights_for_mega_moe_sm90", "quantization_mxfp4", "quantization_mxfp4_fused",
     "quantization_nvfp4",
     "quantization_qoq_fused", "per_token_cast_to_fp4", "per_token_cast_to_fp8", "ceil_div", "align",
+    "checkpoint", "mxfp4_checkpoint_to_mega_moe", "nvfp4_checkpoint_to_mega_moe", "mega_moe_to_mxfp4_checkpoint",
+    "mega_moe_to_nvfp4_checkpoint", "untransform_mxfp4_weights_for_mega_moe_fused",
+    "untransform_nvfp4_weights_for_mega_moe_fused",
 ]

@@ -25,6 +25,7 @@ EXPORTS = [
     "dgm_device_cu_count", "dgm_fused_workgroups",
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
     "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
+    "dgm_reorder_fp4_nibbles", "dgm_untransform_fp4_weights", "dgm_untransform_nvfp4_weights",
 ]
 
 
@@ -91,6 +92,9 @@ def load():
         "dgm_transform_qoq_weights": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
         "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_host_device_pointer": ([vp, ctypes.POINTER(vp)], i32),
+        "dgm_reorder_fp4_nibbles": ([vp, vp, i64, i32, i32, vp], i32),
+        "dgm_untransform_fp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
+        "dgm_untransform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -254,14 +254,25 @@ __global__ void k_cast_int8_rows(const uint16_t* __restrict__ x, int64_t rows, i
     q[row * K + k] = (int8_t)fminf(fmaxf(rintf(bf16_to_f32(src[k]) / s), -127.f), 127.f);
 }
 
+// Source row of row r of native block q (16 rows each). l1_interleave 0: rows as they are;
+// 1: W1 with gate rows [0, N/2) then up rows [N/2, N) -> block 2p = gate rows 16p.., block
+// 2p+1 = up rows N/2 + 16p..; 2: W1 with gate and up rows interleaved (row 2i = gate row i,
+// row 2i+1 = up row i) -> the same native blocks.
+DGM_DEV int native_src_row(int q, int r, int N, int l1_interleave) {
+  if (l1_interleave == 1) return (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
+  if (l1_interleave == 2) return 2 * (16 * (q >> 1) + r) + (q & 1);
+  return 16 * q + r;
+}
+
 // ------------------------------------------------------------------ FP4 weight-layout transform
 // Source: packed [E][N][K/2] (Marlin or low-first order), scale [E][N][K/32] E8M0 bytes.
 // Destination (matrix-core fragment order, see dgm_layout in dgm_abi_internal.hpp):
 //   values [E][N/16][K/128][64 lanes][16 B]: lane l = row l%16 of the 16-row block,
 //          K = 128*kt + 32*(l/16) .. +32, byte j = K[2j] | K[2j+1] << 4.
 //   scales [E][N/16][ceil(K/512)][64 lanes][4 B]: byte j = scale of K-tile 4*g + j.
-// l1_interleave: native block q holds gate rows 16*(q/2).. (q even) or up rows
-// N/2 + 16*(q/2).. (q odd), so a (gate, up) pair of blocks covers the same 16 features.
+// l1_interleave (native_src_row): native block q holds the gate rows of features 16*(q/2)..
+// (q even) or the up rows of the same features (q odd), so a (gate, up) pair of blocks covers
+// the same 16 features.
 __global__ void k_transform_fp4(const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
                                 int E, int N, int K, int src_order, int l1_interleave,
                                 uint8_t* __restrict__ dst, uint8_t* __restrict__ sdst) {
@@ -275,9 +286,7 @@ __global__ void k_transform_fp4(const uint8_t* __restrict__ src, const uint8_t* 
   int q = (int)(t % NB);
   int e = (int)(t / NB);
   int r = lane & 15, kq = lane >> 4;
-  int src_row;
-  if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
-  else src_row = 16 * q + r;
+  const int src_row = native_src_row(q, r, N, l1_interleave);
   const uint8_t* s = src + ((int64_t)e * N + src_row) * (K / 2) + kt * 64 + kq * 16;
   U4 in = *reinterpret_cast<const U4*>(s);
   uint32_t w[4] = {in.x, in.y, in.z, in.w};
@@ -322,9 +331,7 @@ __global__ void k_transform_nvfp4(const uint8_t* __restrict__ src, const uint8_t
   const int q = (int)(t % NB);
   const int e = (int)(t / NB);
   const int r = lane & 15, g = lane >> 4;
-  int src_row;
-  if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
-  else src_row = 16 * q + r;
+  const int src_row = native_src_row(q, r, N, l1_interleave);
   const uint8_t* row = src + ((int64_t)e * N + src_row) * (K / 2) + kt * 64;
   uint32_t o[4];
 #pragma unroll
@@ -350,6 +357,104 @@ __global__ void k_transform_nvfp4(const uint8_t* __restrict__ src, const uint8_t
     const uint8_t* sr = ssrc + ((int64_t)e * N + src_row) * (K / 16) + 8 * kt + p;
     const uint32_t sd = (uint32_t)sr[0] | ((uint32_t)sr[2] << 8) | ((uint32_t)sr[4] << 16) | ((uint32_t)sr[6] << 24);
     *reinterpret_cast<uint32_t*>(sdst + tile * 128 + (16 * p + r) * 4) = sd;
+  }
+}
+
+// ------------------------------------------------------------------ checkpoint formats
+// Nibble order of one 4-byte word of packed E2M1 codes (8 codes): Marlin (byte b = n[b] << 4 |
+// n[b+4]) <-> low-nibble-first (OCP: byte j = n[2j] | n[2j+1] << 4).
+DGM_DEV uint32_t marlin_to_lowfirst32(uint32_t w) {
+  uint32_t n[8];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (w >> (8 * b)) & 0xffu;
+    n[b] = byte >> 4;
+    n[b + 4] = byte & 0xfu;
+  }
+  return lowfirst8(n);
+}
+DGM_DEV uint32_t lowfirst_to_marlin32(uint32_t w) {
+  uint32_t n[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) n[k] = (w >> (4 * k)) & 0xfu;
+  return marlin8(n);
+}
+DGM_DEV uint32_t reorder32(uint32_t w, int from, int to) {
+  if (from == to) return w;
+  return from == 0 ? marlin_to_lowfirst32(w) : lowfirst_to_marlin32(w);
+}
+
+// One thread per 16 bytes (the last thread may own fewer whole words); in place is allowed.
+__global__ void k_reorder_fp4(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t words,
+                              int from, int to) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= words) return;
+  if (i + 4 <= words) {
+    const U4 v = *reinterpret_cast<const U4*>(src + 4 * i);
+    *reinterpret_cast<U4*>(dst + 4 * i) = U4{reorder32(v.x, from, to), reorder32(v.y, from, to),
+                                             reorder32(v.z, from, to), reorder32(v.w, from, to)};
+  } else {
+    for (int64_t j = i; j < words; ++j) {
+      const uint32_t v = reinterpret_cast<const uint32_t*>(src)[j];
+      reinterpret_cast<uint32_t*>(dst)[j] = reorder32(v, from, to);
+    }
+  }
+}
+
+// Inverse of k_transform_fp4: the tile layout back to packed [E][N][K/2] (dst_order 0 Marlin,
+// 1 low-nibble-first) and E8M0 scales [E][N][K/32], rows in checkpoint order (gate rows, then
+// up rows, when l1_interleave). Same thread mapping as the forward pass.
+__global__ void k_untransform_fp4(const uint8_t* __restrict__ vals, const uint8_t* __restrict__ svals, int E, int N,
+                                  int K, int dst_order, int l1_interleave, uint8_t* __restrict__ dst,
+                                  uint8_t* __restrict__ sdst) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int KT = K / 128, NB = N / 16, KG = (KT + 3) / 4;
+  const int64_t total = (int64_t)E * NB * KT * 64;
+  if (tid >= total) return;
+  const int lane = (int)(tid & 63);
+  int64_t t = tid >> 6;
+  const int kt = (int)(t % KT); t /= KT;
+  const int q = (int)(t % NB);
+  const int e = (int)(t / NB);
+  const int r = lane & 15, kq = lane >> 4;
+  const int row = native_src_row(q, r, N, l1_interleave);
+  const int64_t tile = ((int64_t)e * NB + q) * KT + kt;
+  const U4 in = *reinterpret_cast<const U4*>(vals + tile * 1024 + lane * 16);
+  *reinterpret_cast<U4*>(dst + ((int64_t)e * N + row) * (K / 2) + kt * 64 + kq * 16) =
+      U4{reorder32(in.x, 1, dst_order), reorder32(in.y, 1, dst_order), reorder32(in.z, 1, dst_order),
+         reorder32(in.w, 1, dst_order)};
+  sdst[((int64_t)e * N + row) * (K / 32) + kt * 4 + kq] =
+      svals[((((int64_t)e * NB + q) * KG + kt / 4) * 64 + lane) * 4 + (kt & 3)];
+}
+
+// Inverse of k_transform_nvfp4: packed [E][N][K/2] (dst_order as above) and E4M3 scales
+// [E][N][K/16]. Lanes of groups 0 and 2 also write their row's eight scale bytes of the tile.
+__global__ void k_untransform_nvfp4(const uint8_t* __restrict__ vals, const uint8_t* __restrict__ svals, int E,
+                                    int N, int K, int dst_order, int l1_interleave, uint8_t* __restrict__ dst,
+                                    uint8_t* __restrict__ sdst) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int KT = K / 128, NB = N / 16;
+  const int64_t total = (int64_t)E * NB * KT * 64;
+  if (tid >= total) return;
+  const int lane = (int)(tid & 63);
+  int64_t t = tid >> 6;
+  const int kt = (int)(t % KT); t /= KT;
+  const int q = (int)(t % NB);
+  const int e = (int)(t / NB);
+  const int r = lane & 15, g = lane >> 4;
+  const int row = native_src_row(q, r, N, l1_interleave);
+  const int64_t tile = ((int64_t)e * NB + q) * KT + kt;
+  const U4 in = *reinterpret_cast<const U4*>(vals + tile * 1024 + lane * 16);
+  const uint32_t o[4] = {in.x, in.y, in.z, in.w};
+  uint8_t* drow = dst + ((int64_t)e * N + row) * (K / 2) + kt * 64;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *reinterpret_cast<uint32_t*>(drow + 16 * j + 4 * g) = reorder32(o[j], 1, dst_order);
+  if ((g & 1) == 0) {
+    const int p = g >> 1;
+    const uint32_t sd = *reinterpret_cast<const uint32_t*>(svals + tile * 128 + (16 * p + r) * 4);
+    uint8_t* sr = sdst + ((int64_t)e * N + row) * (K / 16) + 8 * kt + p;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sr[2 * j] = (uint8_t)(sd >> (8 * j));
   }
 }
 
@@ -381,9 +486,7 @@ __global__ void k_transform_qoq(const uint8_t* __restrict__ src, const uint8_t* 
   const int q = (int)(t % NB);
   const int e = (int)(t / NB);
   const int r = lane & 15, g = lane >> 4;
-  int src_row;
-  if (l1_interleave) src_row = (q & 1) ? (N / 2 + 16 * (q >> 1) + r) : (16 * (q >> 1) + r);
-  else src_row = 16 * q + r;
+  const int src_row = native_src_row(q, r, N, l1_interleave);
   const uint8_t* row = src + ((int64_t)e * N + src_row) * (K / 2);
   uint32_t n[2][16];       // codes of K = 128 kt + 64 h + 16 g + j
 #pragma unroll
@@ -536,6 +639,7 @@ int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E,
   DGM_CHECK_ARG(packed && scale_e8m0 && dst_values && dst_scales, "null pointer");
   DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 32 == 0 && K % 128 == 0, "N % 32, K % 128");
   DGM_CHECK_ARG(src_order == 0 || src_order == 1, "src_order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(l1_interleave >= 0 && l1_interleave <= 2, "l1_interleave 0, 1 or 2");
   DGM_CHECK_ARG(((uintptr_t)packed & 15) == 0 && ((uintptr_t)dst_values & 15) == 0, "16-byte alignment");
   int KT = K / 128, NB = N / 16, KG = (KT + 3) / 4;
   int64_t total = (int64_t)E * NB * KT * 64;
@@ -556,6 +660,7 @@ int dgm_transform_nvfp4_weights(const void* packed, const void* scale_e4m3, int 
   DGM_CHECK_ARG(packed && scale_e4m3 && dst_values && dst_scales, "null pointer");
   DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 32 == 0 && K % 128 == 0, "N % 32, K % 128");
   DGM_CHECK_ARG(src_order == 0 || src_order == 1, "src_order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(l1_interleave >= 0 && l1_interleave <= 2, "l1_interleave 0, 1 or 2");
   DGM_CHECK_ARG(((uintptr_t)packed & 3) == 0 && ((uintptr_t)dst_values & 15) == 0 && ((uintptr_t)dst_scales & 3) == 0,
                 "alignment");
   const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
@@ -565,12 +670,59 @@ int dgm_transform_nvfp4_weights(const void* packed, const void* scale_e4m3, int 
   return dgm_last_launch_status();
 }
 
+int dgm_reorder_fp4_nibbles(const void* src, void* dst, int64_t n_bytes, int src_order, int dst_order,
+                            hipStream_t stream) {
+  DGM_CHECK_ARG(src && dst, "null pointer");
+  DGM_CHECK_ARG(n_bytes >= 0 && n_bytes % 4 == 0, "n_bytes % 4 == 0 (8 codes per word)");
+  DGM_CHECK_ARG((src_order == 0 || src_order == 1) && (dst_order == 0 || dst_order == 1),
+                "order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(((uintptr_t)src & 15) == 0 && ((uintptr_t)dst & 15) == 0, "16-byte alignment");
+  const uint8_t* s8 = (const uint8_t*)src;
+  uint8_t* d8 = (uint8_t*)dst;
+  DGM_CHECK_ARG(s8 == d8 || s8 + n_bytes <= d8 || d8 + n_bytes <= s8, "src and dst overlap partially");
+  if (n_bytes == 0) return 0;
+  const int64_t words = n_bytes / 4;
+  hipLaunchKernelGGL(k_reorder_fp4, dim3(grid_for((words + 3) / 4, 256)), dim3(256), 0, stream, s8, d8, words,
+                     src_order, dst_order);
+  return dgm_last_launch_status();
+}
+
+int dgm_untransform_fp4_weights(const void* values, const void* scales, int E, int N, int K, int dst_order,
+                                int l1_interleave, void* packed, void* scale_e8m0, hipStream_t stream) {
+  DGM_CHECK_ARG(values && scales && packed && scale_e8m0, "null pointer");
+  DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 32 == 0 && K % 128 == 0, "N % 32, K % 128");
+  DGM_CHECK_ARG(dst_order == 0 || dst_order == 1, "dst_order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(l1_interleave >= 0 && l1_interleave <= 2, "l1_interleave 0, 1 or 2");
+  DGM_CHECK_ARG(((uintptr_t)values & 15) == 0 && ((uintptr_t)packed & 15) == 0, "16-byte alignment");
+  const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
+  hipLaunchKernelGGL(k_untransform_fp4, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)values,
+                     (const uint8_t*)scales, E, N, K, dst_order, l1_interleave, (uint8_t*)packed,
+                     (uint8_t*)scale_e8m0);
+  return dgm_last_launch_status();
+}
+
+int dgm_untransform_nvfp4_weights(const void* values, const void* scales, int E, int N, int K, int dst_order,
+                                  int l1_interleave, void* packed, void* scale_e4m3, hipStream_t stream) {
+  DGM_CHECK_ARG(values && scales && packed && scale_e4m3, "null pointer");
+  DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 32 == 0 && K % 128 == 0, "N % 32, K % 128");
+  DGM_CHECK_ARG(dst_order == 0 || dst_order == 1, "dst_order 0 = Marlin, 1 = low-nibble-first");
+  DGM_CHECK_ARG(l1_interleave >= 0 && l1_interleave <= 2, "l1_interleave 0, 1 or 2");
+  DGM_CHECK_ARG(((uintptr_t)values & 15) == 0 && ((uintptr_t)scales & 3) == 0 && ((uintptr_t)packed & 3) == 0,
+                "alignment");
+  const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
+  hipLaunchKernelGGL(k_untransform_nvfp4, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)values,
+                     (const uint8_t*)scales, E, N, K, dst_order, l1_interleave, (uint8_t*)packed,
+                     (uint8_t*)scale_e4m3);
+  return dgm_last_launch_status();
+}
+
 int dgm_transform_qoq_weights(const void* packed, const void* s2, const void* z, const void* s1, int E, int N,
                               int K, int l1_interleave, void* dst_values, void* dst_meta, void* dst_s1,
                               hipStream_t stream) {
   DGM_CHECK_ARG(packed && s2 && z && s1 && dst_values && dst_meta && dst_s1, "null pointer");
   DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "E, N, K (N % 16, K % 128)");
   DGM_CHECK_ARG(!l1_interleave || N % 32 == 0, "l1_interleave needs N % 32 == 0");
+  DGM_CHECK_ARG(l1_interleave >= 0 && l1_interleave <= 2, "l1_interleave 0, 1 or 2");
   const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
   hipLaunchKernelGGL(k_transform_qoq, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)packed,
                      (const uint8_t*)s2, (const uint8_t*)z, (const float*)s1, (const uint32_t*)nullptr, E, N, K,
@@ -583,6 +735,7 @@ int dgm_transform_qoq_int4_weights(const void* packed, const void* plane_i32, in
   DGM_CHECK_ARG(packed && plane_i32 && dst_values && dst_meta && dst_s1, "null pointer");
   DGM_CHECK_ARG(E > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "E, N, K (N % 16, K % 128)");
   DGM_CHECK_ARG(!l1_interleave || N % 32 == 0, "l1_interleave needs N % 32 == 0");
+  DGM_CHECK_ARG(l1_interleave >= 0 && l1_interleave <= 2, "l1_interleave 0, 1 or 2");
   const int64_t total = (int64_t)E * (N / 16) * (K / 128) * 64;
   hipLaunchKernelGGL(k_transform_qoq, dim3(grid_for(total, 256)), dim3(256), 0, stream, (const uint8_t*)packed,
                      (const uint8_t*)nullptr, (const uint8_t*)nullptr, (const float*)nullptr,

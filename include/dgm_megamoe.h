@@ -77,7 +77,9 @@ int dgm_cast_int8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_i8, 
  * matrix per call). packed [E, N, K/2] (src_order 0 = Marlin, 1 = low-nibble-first),
  * scale_e8m0 [E, N, K/32] -> dst_values [E, N/16, K/128, 64, 16] and
  * dst_scales [E, N/16, ceil(K/512), 64, 4] (matrix-core fragment order). l1_interleave
- * pairs gate block j with up block j (16 rows each) as the kernel's SwiGLU needs. */
+ * pairs gate block j with up block j (16 rows each) as the kernel's SwiGLU needs: 1 for W1
+ * rows [gate rows; up rows] (the reference's [E, 2I, H]), 2 for checkpoints that interleave
+ * them row by row (row 2i = gate row i, row 2i+1 = up row i); 0 for W2. */
 int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E, int N, int K,
                               int src_order, int l1_interleave, void* dst_values,
                               void* dst_scales, hipStream_t stream);
@@ -89,6 +91,28 @@ int dgm_transform_fp4_weights(const void* packed, const void* scale_e8m0, int E,
  * and dst_scales [E, N/16, K/128, 2, 16, 4] (per lane the four 16-block scales of its ops). */
 int dgm_transform_nvfp4_weights(const void* packed, const void* scale_e4m3, int E, int N, int K, int src_order,
                                 int l1_interleave, void* dst_values, void* dst_scales, hipStream_t stream);
+
+/* ------------------------------------------------------------------ checkpoint formats
+ * E2M1 nibble order of packed FP4 codes, any tensor of n_bytes (n_bytes % 4 == 0; 8 codes per
+ * 4-byte word): order 0 = Marlin (deep_gemm/quantization_mxfp4.py:66-70 and
+ * quantization_nvfp4.py:76-80: byte b = K[b] << 4 | K[b+4]), 1 = low-nibble-first (OCP MX
+ * checkpoints, deep_gemm/utils/math.py:100: byte j = K[2j] | K[2j+1] << 4). src == dst converts
+ * in place. Replaces the reference's torch nibble shuffles (quantization_mxfp4.py:66-70 one way,
+ * quantization_nvfp4.py:176-181 back). */
+int dgm_reorder_fp4_nibbles(const void* src, void* dst, int64_t n_bytes, int src_order, int dst_order,
+                            hipStream_t stream);
+
+/* Inverse of dgm_transform_fp4_weights: dst values / scales of that call -> packed [E, N, K/2]
+ * in dst_order (0 Marlin, 1 low-nibble-first) and scale_e8m0 [E, N, K/32], rows in the order
+ * l1_interleave names (as for dgm_transform_fp4_weights). Replaces the fused-layout inversion of
+ * deep_gemm/quantization_mxfp4.py:231-262 (dequantize_mxfp4_to_fp32 with fused_input). */
+int dgm_untransform_fp4_weights(const void* values, const void* scales, int E, int N, int K, int dst_order,
+                                int l1_interleave, void* packed, void* scale_e8m0, hipStream_t stream);
+
+/* Inverse of dgm_transform_nvfp4_weights: -> packed [E, N, K/2] (dst_order) and E4M3 scales
+ * [E, N, K/16]. Replaces the layout inversion of deep_gemm/quantization_nvfp4.py:155-181. */
+int dgm_untransform_nvfp4_weights(const void* values, const void* scales, int E, int N, int K, int dst_order,
+                                  int l1_interleave, void* packed, void* scale_e4m3, hipStream_t stream);
 
 /* Replaces deep_gemm/mega/fused.py:71 transform_qoq_weights_for_mega_moe_fused (one matrix per
  * call). packed [E, N, K/2] (Marlin), s2 / z u8 [E, N, K/128], s1 f32 [E, N] ->

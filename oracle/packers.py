@@ -281,3 +281,103 @@ def per_token_cast_to_int8(x):
     sf = amax / np.float32(127.0)
     q = np.clip(np.rint(x / sf), -127, 127).astype(np.int8)
     return q, sf[..., 0].astype(np.float32)
+
+
+# ----------------------------------------------------------------------------- checkpoint formats
+# The fused kernel's FP4 tile layouts (the layouts dgm_packers.hip's transform writes), restated
+# with numpy reshapes, and the nibble-order conversions between OCP checkpoints (low nibble =
+# even K, deep_gemm/utils/math.py:99-100) and the reference's Marlin order
+# (deep_gemm/quantization_mxfp4.py:66-70).
+def marlin_to_low_first(packed):
+    """Marlin bytes -> OCP low-nibble-first bytes of the same codes."""
+    return pack_low_first(unpack_marlin(np.asarray(packed)))
+
+
+def low_first_to_marlin(packed):
+    return pack_marlin(unpack_low_first(np.asarray(packed)))
+
+
+def native_src_rows(N, l1_mode):
+    """Source row of each native row (block q = i // 16, row r = i % 16). l1_mode 0: identity;
+    1: W1 as [gate rows; up rows] -> block 2p = gate rows 16p.., block 2p+1 = up rows N/2 + 16p..;
+    2: W1 with gate / up interleaved by row (row 2i = gate i, row 2i+1 = up i) -> the same blocks."""
+    i = np.arange(N)
+    q, r = i // 16, i % 16
+    if l1_mode == 1:
+        return np.where(q % 2 == 1, N // 2 + 16 * (q // 2) + r, 16 * (q // 2) + r)
+    if l1_mode == 2:
+        return 2 * (16 * (q // 2) + r) + q % 2
+    return i
+
+
+def _to_low_first(packed, order):
+    return np.asarray(packed) if order in ("low_first", "ocp") else marlin_to_low_first(packed)
+
+
+def _from_low_first(packed, order):
+    return packed if order in ("low_first", "ocp") else low_first_to_marlin(packed)
+
+
+def fp4_to_tile(packed, scale, order="marlin", l1_mode=0):
+    """MXFP4 [E, N, K/2] codes + E8M0 [E, N, K/32] -> values [E, N/16, K/128, 64, 16] (lane l =
+    row l % 16 of the block, its 32 codes K = 128 kt + 32 (l // 16) .. +32, low nibble first) and
+    scales [E, N/16, ceil(K/512), 64, 4] (byte j = the scale of K-tile 4 g + j of the lane's
+    (row, 32-group); 127 = 2^0 past the last K-tile)."""
+    lf = _to_low_first(packed, order)
+    scale = np.asarray(scale)
+    E, N, Kh = lf.shape
+    K = 2 * Kh
+    KT, NB = K // 128, N // 16
+    KG = (KT + 3) // 4
+    rows = native_src_rows(N, l1_mode)
+    lf, sc = lf[:, rows], scale[:, rows]
+    vals = lf.reshape(E, NB, 16, KT, 4, 16).transpose(0, 1, 3, 4, 2, 5).reshape(E, NB, KT, 64, 16)
+    s = sc.reshape(E, NB, 16, KT, 4).transpose(0, 1, 3, 4, 2).reshape(E, NB, KT, 64)
+    out = np.full((E, NB, KG * 4, 64), 127, np.uint8)
+    out[:, :, :KT] = s
+    out = out.reshape(E, NB, KG, 4, 64).transpose(0, 1, 2, 4, 3)
+    return np.ascontiguousarray(vals), np.ascontiguousarray(out)
+
+
+def fp4_from_tile(values, scales, order="marlin", l1_mode=0):
+    """Inverse of ``fp4_to_tile`` (the padding scale bytes are dropped)."""
+    values, scales = np.asarray(values), np.asarray(scales)
+    E, NB, KT = values.shape[:3]
+    N, K = NB * 16, KT * 128
+    lf = values.reshape(E, NB, KT, 4, 16, 16).transpose(0, 1, 4, 2, 3, 5).reshape(E, N, K // 2)
+    s = scales.transpose(0, 1, 2, 4, 3).reshape(E, NB, -1, 64)[:, :, :KT]
+    s = s.reshape(E, NB, KT, 4, 16).transpose(0, 1, 4, 2, 3).reshape(E, N, K // 32)
+    rows = native_src_rows(N, l1_mode)
+    packed, sc = np.empty_like(lf), np.empty_like(s)
+    packed[:, rows], sc[:, rows] = lf, s
+    return _from_low_first(packed, order), sc
+
+
+def nvfp4_to_tile(packed, scale, order="marlin", l1_mode=0):
+    """NVFP4 [E, N, K/2] codes + E4M3 [E, N, K/16] -> values [E, N/16, K/128, 64, 16] (lane l =
+    row l % 16; dword j = the eight codes K = 128 kt + 32 j + 8 (l // 16) .. +8, low nibble first)
+    and scales [E, N/16, K/128, 2, 16, 4] (dword (p, r) byte j = the scale of 16-block 8 kt + 2 j + p
+    of row r)."""
+    lf = _to_low_first(packed, order)
+    scale = np.asarray(scale)
+    E, N, Kh = lf.shape
+    K = 2 * Kh
+    KT, NB = K // 128, N // 16
+    rows = native_src_rows(N, l1_mode)
+    lf, sc = lf[:, rows], scale[:, rows]
+    vals = lf.reshape(E, NB, 16, KT, 4, 4, 4).transpose(0, 1, 3, 5, 2, 4, 6).reshape(E, NB, KT, 64, 16)
+    s = sc.reshape(E, NB, 16, KT, 4, 2).transpose(0, 1, 3, 5, 2, 4)
+    return np.ascontiguousarray(vals), np.ascontiguousarray(s)
+
+
+def nvfp4_from_tile(values, scales, order="marlin", l1_mode=0):
+    """Inverse of ``nvfp4_to_tile``."""
+    values, scales = np.asarray(values), np.asarray(scales)
+    E, NB, KT = values.shape[:3]
+    N, K = NB * 16, KT * 128
+    lf = values.reshape(E, NB, KT, 4, 16, 4, 4).transpose(0, 1, 4, 2, 5, 3, 6).reshape(E, N, K // 2)
+    s = scales.transpose(0, 1, 4, 2, 5, 3).reshape(E, N, K // 16)
+    rows = native_src_rows(N, l1_mode)
+    packed, sc = np.empty_like(lf), np.empty_like(s)
+    packed[:, rows], sc[:, rows] = lf, s
+    return _from_low_first(packed, order), sc
