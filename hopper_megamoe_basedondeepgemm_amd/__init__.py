@@ -9,7 +9,9 @@ from .mega import (FusedSymmBuffer, get_fused_symm_buffer_for_mega_moe,
                    fable_router_quant_topk_frontend, fable_frontend_keys, mxfp4_mega_moe_fused, mxfp4_mega_moe_split,
                    mxfp4_mega_moe_from_bf16, qoq_mega_moe_fused, qoq_mega_moe_split,
                    transform_nvfp4_weights_for_mega_moe_fused, fp4_fp4_mega_moe, nvfp4_mega_moe,
-                   transform_qoq_int4_weights_for_mega_moe_sm90)
+                   transform_qoq_int4_weights_for_mega_moe_sm90, SymmBuffer, get_symm_buffer_for_mega_moe,
+                   get_mxfp4_mega_moe_sm90_block_n, transform_mxfp4_weights_for_mega_moe_sm90, mxfp4_mega_moe,
+                   int4_mega_moe)
 from . import quantization_mxfp4, quantization_mxfp4_fused, quantization_nvfp4, quantization_qoq_fused
 from .utils import per_token_cast_to_fp4, per_token_cast_to_fp8, ceil_div, align
 from . import checkpoint
@@ -27,6 +29,8 @@ __all__ = [
     "transform_qoq_int4_weights_for_mega_moe_sm90", "quantization_mxfp4", "quantization_mxfp4_fused",
     "quantization_nvfp4",
     "quantization_qoq_fused", "per_token_cast_to_fp4", "per_token_cast_to_fp8", "ceil_div", "align",
+    "SymmBuffer", "get_symm_buffer_for_mega_moe", "get_mxfp4_mega_moe_sm90_block_n",
+    "transform_mxfp4_weights_for_mega_moe_sm90", "mxfp4_mega_moe", "int4_mega_moe",
     "checkpoint", "mxfp4_checkpoint_to_mega_moe", "nvfp4_checkpoint_to_mega_moe", "mega_moe_to_mxfp4_checkpoint",
     "mega_moe_to_nvfp4_checkpoint", "untransform_mxfp4_weights_for_mega_moe_fused",
     "untransform_nvfp4_weights_for_mega_moe_fused",

@@ -12,10 +12,12 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdgm_megamoe.so")
 PROBE_LIB_PATH = os.path.join(_HERE, "libdgm_probe.so")     # the tests' lane-layout probes
 
-ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1, "qoq": 2, "nvfp4": 3}
+ACT_FORMATS = {"mxfp4": 0, "mxfp8": 1, "fp8": 1, "qoq": 2, "nvfp4": 3, "fp8f128": 4}
 FE_FORCE_BALANCED = 1
 FE_ZERO_ROW_UNROUTED = 2
 FE_SELECT_IN_MEGA = 4
+FE_RAW_WEIGHTS = 8
+FE_NO_CAST = 16
 
 EXPORTS = [
     "dgm_version", "dgm_last_error", "dgm_quantize_mxfp4", "dgm_cast_fp4_rows", "dgm_cast_fp8_rows",
@@ -26,6 +28,7 @@ EXPORTS = [
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
     "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
     "dgm_reorder_fp4_nibbles", "dgm_untransform_fp4_weights", "dgm_untransform_nvfp4_weights",
+    "dgm_router_logits_topk_launch",
 ]
 
 
@@ -93,6 +96,7 @@ def load():
         "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_host_device_pointer": ([vp, ctypes.POINTER(vp)], i32),
         "dgm_reorder_fp4_nibbles": ([vp, vp, i64, i32, i32, vp], i32),
+        "dgm_router_logits_topk_launch": ([vp, i32, i32, i32, i32, i32, vp, ctypes.POINTER(BufferLayout), vp], i32),
         "dgm_untransform_fp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_untransform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
     }

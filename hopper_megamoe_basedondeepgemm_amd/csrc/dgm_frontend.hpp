@@ -132,6 +132,29 @@ DGM_DEV void cast_lane_nvfp4(const uint16_t* __restrict__ x, int64_t i, uint8_t*
   if (part == 0) put8<AGENT>(sf + g, code);
 }
 
+// FP8 rows with one fp32 scale per 128 (per_token_cast_to_fp8(use_ue8m0=False, gran_k=128),
+// deep_gemm/utils/math.py:26-38): 32 adjacent lanes per 128-element group, 4 elements each;
+// sf = max(amax, 1e-4) / 448, E4M3 (round to nearest even) of x * (1 / sf) (IEEE division).
+template <bool AGENT>
+DGM_DEV void cast_lane_fp8f128(const uint16_t* __restrict__ x, int64_t i, uint8_t* __restrict__ q,
+                               uint8_t* __restrict__ sf) {
+  const int64_t g = i >> 5;
+  const int part = (int)(i & 31);
+  const uint2 raw = *reinterpret_cast<const uint2*>(x + g * 128 + 4 * part);
+  const float v[4] = {__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                      __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u)};
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+#pragma unroll
+  for (int off = 1; off < 32; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float s = fmaxf(amax, 1e-4f) / 448.0f;
+  const float inv = 1.0f / s;
+  uint32_t o = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o |= e4m3_encode(v[k] * inv) << (8 * k);
+  put32<AGENT>(reinterpret_cast<uint32_t*>(q) + g * 32 + part, o);
+  if (part == 0) put32<AGENT>(reinterpret_cast<uint32_t*>(sf) + g, __float_as_uint(s));
+}
+
 // QoQ per-token int8 cast (per_token_cast_to_int8) of token t by one wave: lane l holds
 // elements 512 j + 8 l .. +7; sf = max(amax, 1e-30) / 127 (fp32), q = clamp(rne(x / sf),
 // +-127); the scale is repeated over the row's H / 128 slots.

@@ -64,10 +64,10 @@ template <int J>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
                                                   uint32_t* __restrict__ keys, int zero_unrouted,
-                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
+                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ sf, int router) {
   constexpr int H = J * 512;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ry = (M + 3) / 4;
+  const int ry = router ? (M + 3) / 4 : 0;
   if ((int)blockIdx.y < ry) {
     router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, keys, zero_unrouted != 0);
     return;
@@ -81,6 +81,8 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
       cast_qoq_token<J, false>(x, t, lane, q, sf);
   } else if (act_format == DGM_ACT_NVFP4) {
     for (int64_t i = lane0; i < (int64_t)M * (H / 16) * 4; i += nl) cast_lane_nvfp4<false>(x, i, q, sf);
+  } else if (act_format == DGM_ACT_FP8F128) {
+    for (int64_t i = lane0; i < (int64_t)M * (H / 128) * 32; i += nl) cast_lane_fp8f128<false>(x, i, q, sf);
   } else {
     for (int64_t i = lane0; i < (int64_t)M * (H / 32) * 8; i += nl) cast_lane_mx<false>(x, act_format, i, q, sf);
   }
@@ -103,10 +105,20 @@ __global__ void __launch_bounds__(256) k_select(const uint32_t* __restrict__ key
   const uint32_t* row = keys + (size_t)t * E;
   select_topk_wave([row](int e) { return row[e]; }, E, topk, (flags & DGM_FE_FORCE_BALANCED) != 0,
                    token_offset + t, lane, idx, wt);
+  // (DGM_FE_RAW_WEIGHTS: the selected logit itself, no softmax)
+  if ((flags & DGM_FE_RAW_WEIGHTS) && !(flags & DGM_FE_FORCE_BALANCED) && lane < topk && idx >= 0) wt = key_value(row[idx]);
   if (lane < topk) {
     topk_idx[(size_t)t * topk + lane] = idx;
     topk_w[(size_t)t * topk + lane] = wt;
   }
+}
+
+// Top-k keys of bf16 router logits [M, E] (the frontend's key of each logit, topk_key).
+__global__ void __launch_bounds__(256) k_keys_bf16(const uint16_t* __restrict__ logits, int64_t n, int E,
+                                                   uint32_t* __restrict__ keys) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  keys[i] = topk_key(bf16_to_f32(logits[i]), (int)(i % E));
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -176,33 +188,44 @@ __global__ void __launch_bounds__(DISPATCH_THREADS) k_dispatch(const int64_t* __
 }
 
 // ------------------------------------------------------------------ L1: gate/up + SwiGLU + requant
-// Workgroup = 2 waves; item = (active expert a, 32 intermediate features q). Wave w owns the
-// (gate, up) block pair p = 2q + w (16 features). Both weight tiles of every K-tile are
+// Workgroup = NWV waves; item = (active expert a, 16 NWV intermediate features q). Wave w owns
+// the (gate, up) block pair p = NWV q + w (16 features). Both weight tiles of every K-tile are
 // loaded into registers up front (one 1 KB coalesced run per tile), the 16-token B slab is
 // staged once per workgroup in LDS in fragment order, then 2 * KT matrix-core ops run.
-// Epilogue: bf16-round gate/up, clamp, silu(g)*u*w, per-32 requant across the two waves.
+// Epilogue: clamp, silu(g)*u*w, requant of the item's features across its waves.
+// MXFP4 / MXFP8 (2 waves): gate/up rounded to bf16, per-32 E8M0 requant.
+// FP8F128 (4 waves): the activation's fp32 scale of each (token, K-tile) multiplies that
+// K-tile's product (the op runs with a unit activation scale into a zero accumulator, then
+// acc += s * part), fp32 gate/up, per-64 power-of-two FP8 requant stored as two equal per-32
+// E8M0 bytes (so the MXFP8 L2 reads it).
+template <int ACT> constexpr int l1_waves() { return ACT == DGM_ACT_FP8F128 ? 4 : 2; }
+
 template <int KT, int ACT>
 struct L1Smem {
   static constexpr int BYTES = ACT == DGM_ACT_MXFP4 ? 16 : 32;
   static constexpr int KG = (KT + 3) / 4;
   U4 b[KT][64][BYTES / 16];
   uint32_t bs[KG][64];
-  float amax[2][16];
+  float bsf[ACT == DGM_ACT_FP8F128 ? KT : 1][16];    // FP8F128: per (K-tile, slab column) scale
+  float amax[l1_waves<ACT>()][16];
 };
 
 template <int KT, int ACT>
-__global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, const uint32_t* __restrict__ w1s,
-                                            const uint8_t* __restrict__ x, const uint8_t* __restrict__ xsf,
-                                            const float* __restrict__ topk_w, uint8_t* __restrict__ pool_base,
-                                            int E_local, int I, int topk, float clamp, int fast_math,
-                                            uint8_t* __restrict__ mid, uint8_t* __restrict__ mid_sf) {
+__global__ void __launch_bounds__(64 * l1_waves<ACT>()) k_l1(const uint8_t* __restrict__ w1v,
+                                                           const uint32_t* __restrict__ w1s,
+                                                           const uint8_t* __restrict__ x, const uint8_t* __restrict__ xsf,
+                                                           const float* __restrict__ topk_w, uint8_t* __restrict__ pool_base,
+                                                           int E_local, int I, int topk, float clamp, int fast_math,
+                                                           uint8_t* __restrict__ mid, uint8_t* __restrict__ mid_sf) {
+  constexpr int NWV = l1_waves<ACT>(), NT = 64 * NWV;
+  constexpr bool F128 = ACT == DGM_ACT_FP8F128;
   constexpr int KG = (KT + 3) / 4;
   constexpr int XB = ACT == DGM_ACT_MXFP4 ? KT * 64 : KT * 128;   // x row bytes (H/2 or H)
   constexpr int H = KT * 128;
   __shared__ L1Smem<KT, ACT> sm;
   Pool P = pool_view(pool_base, E_local);
   const int n_active = P.meta[0];
-  const int QN = I / 32;
+  const int QN = I / (16 * NWV);
   const int NB1 = I / 8;            // 16-row blocks of the 2I-row L1 weight
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int midb = ACT == DGM_ACT_MXFP4 ? I / 2 : I;
@@ -211,7 +234,7 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
     const int a = item / QN, q = item % QN;
     const int e = P.active[a];
     const int r0 = P.offsets[a], n = P.offsets[a + 1] - r0;
-    const int p = 2 * q + wv;
+    const int p = NWV * q + wv;
     // ---- A operands: gate tile (block 2p) and up tile (block 2p+1) for every K-tile
     const uint8_t* gbase = w1v + ((size_t)(e * NB1 + 2 * p) * KT) * 1024 + lane * 16;
     const uint8_t* ubase = gbase + (size_t)KT * 1024;
@@ -229,7 +252,7 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
     for (int s0 = 0; s0 < n; s0 += 16) {
       // ---- stage the B slab (routes s0..s0+15 of this expert) in fragment order
       __syncthreads();
-      for (int f = threadIdx.x; f < KT * 64; f += 128) {
+      for (int f = threadIdx.x; f < KT * 64; f += NT) {
         int kt = f >> 6, l = f & 63, c = l & 15;
         U4 v0 = {0, 0, 0, 0}, v1 = {0, 0, 0, 0};
         if (s0 + c < n) {
@@ -247,10 +270,10 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         sm.b[kt][l][0] = v0;
         if (ACT != DGM_ACT_MXFP4) sm.b[kt][l][ACT != DGM_ACT_MXFP4 ? 1 : 0] = v1;
       }
-      for (int f = threadIdx.x; f < KG * 64; f += 128) {
+      for (int f = threadIdx.x; f < KG * 64; f += NT) {
         int g = f >> 6, l = f & 63, c = l & 15;
         uint32_t w = 0x7f7f7f7fu;
-        if (s0 + c < n) {
+        if (!F128 && s0 + c < n) {
           int t = P.routes[r0 + s0 + c] / topk;
           w = 0;
 #pragma unroll
@@ -262,15 +285,23 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         }
         sm.bs[g][l] = w;
       }
+      if constexpr (F128) {
+        for (int f = threadIdx.x; f < KT * 16; f += NT) {
+          const int kt = f >> 4, c = f & 15;
+          float v = 0.f;
+          if (s0 + c < n) v = reinterpret_cast<const float*>(xsf)[(size_t)(P.routes[r0 + s0 + c] / topk) * KT + kt];
+          sm.bsf[kt][c] = v;
+        }
+      }
       __syncthreads();
-      // ---- matrix cores: two K halves accumulated separately and added. Scale bytes are
-      // selected from the loaded scale dwords by the op's byte select (no VALU writes to a
-      // scale operand inside the chain of matrix-core ops)
+      // ---- matrix cores. Scale bytes are selected from the loaded scale dwords by the op's
+      // byte select (no VALU writes to a scale operand inside the chain of matrix-core ops)
       v4f accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
       v4f accg1 = {0.f, 0.f, 0.f, 0.f}, accu1 = {0.f, 0.f, 0.f, 0.f};
       uint32_t bsw[KG];
 #pragma unroll
       for (int g = 0; g < KG; ++g) bsw[g] = sm.bs[g][lane];
+      const int c = lane & 15;
       static_for<KT>([&](auto kc) {
         constexpr int kt = decltype(kc)::value;
         v8i bop;
@@ -278,7 +309,18 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
         else bop = u8_to_v8i(sm.b[kt][lane][0], sm.b[kt][lane][ACT != DGM_ACT_MXFP4 ? 1 : 0]);
         constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;
         constexpr int SEL = kt & 3;
-        if constexpr (kt < KT / 2) {
+        if constexpr (F128) {
+          // this K-tile's products with a unit activation scale, promoted by the token's scale
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f tg = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(ag[kt]), bop, z, (int)sg[kt >> 2], (int)bsw[kt >> 2]);
+          const v4f tu = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(au[kt]), bop, z, (int)su[kt >> 2], (int)bsw[kt >> 2]);
+          const float sx = sm.bsf[kt][c];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            accg[i] = fmaf(sx, tg[i], accg[i]);
+            accu[i] = fmaf(sx, tu[i], accu[i]);
+          }
+        } else if constexpr (kt < KT / 2) {
           accg = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(ag[kt]), bop, accg, (int)sg[kt >> 2], (int)bsw[kt >> 2]);
           accu = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(au[kt]), bop, accu, (int)su[kt >> 2], (int)bsw[kt >> 2]);
         } else {
@@ -286,14 +328,20 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
           accu1 = mfma_scale_16x16x128_sel<4, FB, SEL, SEL>(u4_to_v8i(au[kt]), bop, accu1, (int)su[kt >> 2], (int)bsw[kt >> 2]);
         }
       });
-      keep_scales_until(sg, accg1);
-      keep_scales_until(su, accu1);
-      keep_scales_until(bsw, accg1);
-      keep_scales_until(bsw, accu1);
-      accg += accg1;
-      accu += accu1;
+      if constexpr (F128) {
+        keep_scales_until(sg, accg);
+        keep_scales_until(su, accu);
+        keep_scales_until(bsw, accg);
+        keep_scales_until(bsw, accu);
+      } else {
+        keep_scales_until(sg, accg1);
+        keep_scales_until(su, accu1);
+        keep_scales_until(bsw, accg1);
+        keep_scales_until(bsw, accu1);
+        accg += accg1;
+        accu += accu1;
+      }
       // ---- epilogue: lane holds features 16p + 4(l/16) + i for slab column c = l % 16
-      const int c = lane & 15;
       const bool valid = s0 + c < n;
       float act[4];
       float am = 0.f;
@@ -301,8 +349,8 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
       if (valid) wt = topk_w[P.routes[r0 + s0 + c]];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float g = fminf(round_bf16(accg[i]), clamp);
-        float u = fminf(fmaxf(round_bf16(accu[i]), -clamp), clamp);
+        float g = fminf(F128 ? accg[i] : round_bf16(accg[i]), clamp);
+        float u = fminf(fmaxf(F128 ? accu[i] : round_bf16(accu[i]), -clamp), clamp);
         float sg1 = fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
         act[i] = valid ? ((g * sg1) * u) * wt : 0.f;
         am = fmaxf(am, fabsf(act[i]));
@@ -311,7 +359,9 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
       am = fmaxf(am, __shfl_xor(am, 32));
       if (lane < 16) sm.amax[wv][lane] = am;
       __syncthreads();
-      am = fmaxf(sm.amax[0][c], sm.amax[1][c]);
+      am = sm.amax[0][c];
+#pragma unroll
+      for (int w = 1; w < NWV; ++w) am = fmaxf(am, sm.amax[w][c]);
       if (valid) {
         const int row = r0 + s0 + c;
         const int f0 = 16 * p + 4 * (lane >> 4);
@@ -324,14 +374,24 @@ __global__ void __launch_bounds__(128) k_l1(const uint8_t* __restrict__ w1v, con
           *reinterpret_cast<uint16_t*>(mid + (size_t)row * midb + f0 / 2) = (uint16_t)w;
           if (wv == 0 && lane < 16) mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
         } else {
-          float ex = ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f);
+          // MXFP8: 2^ceil(log2(max(amax, 1e-30) / 448)); FP8F128: 2^ceil(log2(max(amax / 448,
+          // FLT_MIN)))
+          float ex = F128 ? ceil_log2_f32(fmaxf(am / 448.0f, 1.17549435e-38f))
+                          : ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f);
           int code = (int)ex + 127;
           float is = e8m0_inv((uint32_t)code);
           uint32_t w = 0;
 #pragma unroll
           for (int i = 0; i < 4; ++i) w |= e4m3_encode(act[i] * is) << (8 * i);
           *reinterpret_cast<uint32_t*>(mid + (size_t)row * midb + f0) = w;
-          if (wv == 0 && lane < 16) mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
+          if (wv == 0 && lane < 16) {
+            if (F128) {
+              mid_sf[(size_t)row * (I / 32) + 2 * q] = (uint8_t)code;
+              mid_sf[(size_t)row * (I / 32) + 2 * q + 1] = (uint8_t)code;
+            } else {
+              mid_sf[(size_t)row * (I / 32) + q] = (uint8_t)code;
+            }
+          }
         }
       }
     }
@@ -454,9 +514,9 @@ template <int KT1, int KT2, int ACT>
 int launch_experts(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, hipStream_t stream) {
   const int cus = cu_count();
   uint8_t* pool = buf + L->pool;
-  int items1 = A->num_local_experts * (A->intermediate / 32);
+  int items1 = A->num_local_experts * (A->intermediate / (16 * l1_waves<ACT>()));
   int grid1 = items1 < cus * 4 ? items1 : cus * 4;
-  hipLaunchKernelGGL((k_l1<KT1, ACT>), dim3(grid1), dim3(128), 0, stream, (const uint8_t*)A->w1_values,
+  hipLaunchKernelGGL((k_l1<KT1, ACT>), dim3(grid1), dim3(64 * l1_waves<ACT>()), 0, stream, (const uint8_t*)A->w1_values,
                      (const uint32_t*)A->w1_scales, buf + L->x, buf + L->x_sf,
                      (const float*)(buf + L->topk_weights), pool, A->num_local_experts, A->intermediate,
                      A->topk, A->activation_clamp, A->fast_math, buf + L->mid, buf + L->mid_sf);
@@ -464,7 +524,9 @@ int launch_experts(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLayout* L, 
   if (st) return st;
   int items2 = A->num_local_experts * (A->hidden / 16);
   int grid2 = (items2 + 3) / 4 < cus * 4 ? (items2 + 3) / 4 : cus * 4;
-  hipLaunchKernelGGL((k_l2<KT2, ACT>), dim3(grid2), dim3(256), 0, stream, (const uint8_t*)A->w2_values,
+  // (FP8F128: the intermediate is FP8 with E8M0 bytes per 32, as MXFP8's)
+  constexpr int ACT2 = ACT == DGM_ACT_FP8F128 ? DGM_ACT_MXFP8 : ACT;
+  hipLaunchKernelGGL((k_l2<KT2, ACT2>), dim3(grid2), dim3(256), 0, stream, (const uint8_t*)A->w2_values,
                      (const uint32_t*)A->w2_scales, buf + L->mid, buf + L->mid_sf, pool, A->num_local_experts,
                      A->hidden, A->topk, L->max_tokens, (uint16_t*)(buf + L->partials));
   return dgm_last_launch_status();
@@ -510,16 +572,18 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts in (0, 1024]");
   DGM_CHECK_ARG(num_local_experts > 0 && num_local_experts <= num_experts, "num_local_experts");
   DGM_CHECK_ARG(hidden % 512 == 0 && intermediate % 128 == 0, "hidden % 512, intermediate % 128");
-  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_NVFP4, "act_format");
+  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG((int64_t)max_tokens * topk <= MAX_ROUTES_DISPATCH, "max_tokens * topk <= 4096");
   const bool fp4 = act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_NVFP4;
   const size_t xb = fp4 ? hidden / 2 : hidden;
   const size_t mb = fp4 ? intermediate / 2 : intermediate;
   // scales: E8M0 bytes per 32 (MXFP); QoQ: fp32 per token repeated over H / 128 slots (the
   // same H / 32 bytes) and fp32 per 64 intermediate features (I / 16 bytes); NVFP4: E4M3
-  // bytes per 16
+  // bytes per 16; FP8F128: fp32 per 128 K (H / 32 bytes) and E8M0 bytes per 32 intermediate
+  // features, sized as QoQ's (so one buffer serves both layers of the split recipe)
   const size_t xsfb = act_format == DGM_ACT_NVFP4 ? hidden / 16 : hidden / 32;
-  const size_t msfb = act_format == DGM_ACT_QOQ || act_format == DGM_ACT_NVFP4 ? intermediate / 16 : intermediate / 32;
+  const size_t msfb = act_format == DGM_ACT_QOQ || act_format == DGM_ACT_NVFP4 || act_format == DGM_ACT_FP8F128
+                          ? intermediate / 16 : intermediate / 32;
   const int R = max_tokens * topk;
   size_t off = 0;
   memset(out, 0, sizeof(*out));
@@ -545,24 +609,29 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
 int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16, int num_tokens,
                            int hidden, int num_experts, int topk, int act_format, int flags,
                            int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
-  DGM_CHECK_ARG(hidden_bf16 && router_weight_bf16 && buffer && L, "null pointer");
+  DGM_CHECK_ARG(hidden_bf16 && buffer && L, "null pointer");
   DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
   DGM_CHECK_ARG(num_experts <= 1024, "num_experts <= 1024");
   DGM_CHECK_ARG(hidden % 512 == 0, "hidden % 512 == 0");
   DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
-  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_NVFP4, "act_format");
+  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG(((uintptr_t)hidden_bf16 & 15) == 0 && ((uintptr_t)router_weight_bf16 & 15) == 0, "16-byte alignment");
+  DGM_CHECK_ARG(router_weight_bf16 || !(flags & (DGM_FE_FORCE_BALANCED | DGM_FE_ZERO_ROW_UNROUTED | DGM_FE_SELECT_IN_MEGA)),
+                "cast only (router_weight NULL): no routing flags");
+  DGM_CHECK_ARG(router_weight_bf16 || !(flags & DGM_FE_NO_CAST), "DGM_FE_NO_CAST needs the router weight");
   if (num_tokens == 0) return 0;
   uint8_t* buf = (uint8_t*)buffer;
   const int J = hidden / 512;
   // router rows, then cast rows: one cast lane per thread (QoQ: one wave per token)
   const int rx = (num_experts + 3) / 4;
-  const int64_t cast_threads = act_format == DGM_ACT_QOQ     ? (int64_t)num_tokens * 64
-                               : act_format == DGM_ACT_NVFP4 ? (int64_t)num_tokens * (hidden / 16) * 4
-                                                             : (int64_t)num_tokens * (hidden / 32) * 8;
-  const int64_t cast_rows = (cast_threads + (int64_t)rx * 256 - 1) / ((int64_t)rx * 256);
-  dim3 rg(rx, (num_tokens + 3) / 4 + (int)cast_rows);
+  const int64_t cast_threads = act_format == DGM_ACT_QOQ       ? (int64_t)num_tokens * 64
+                               : act_format == DGM_ACT_NVFP4   ? (int64_t)num_tokens * (hidden / 16) * 4
+                               : act_format == DGM_ACT_FP8F128 ? (int64_t)num_tokens * (hidden / 128) * 32
+                                                               : (int64_t)num_tokens * (hidden / 32) * 8;
+  const int64_t cast_rows = (flags & DGM_FE_NO_CAST) ? 0 : (cast_threads + (int64_t)rx * 256 - 1) / ((int64_t)rx * 256);
+  const int router = router_weight_bf16 ? 1 : 0;
+  dim3 rg(rx, (router ? (num_tokens + 3) / 4 : 0) + (int)cast_rows);
   const uint16_t* x = (const uint16_t*)hidden_bf16;
   const uint16_t* w = (const uint16_t*)router_weight_bf16;
   float* logits = (float*)(buf + L->logits);
@@ -570,7 +639,7 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
   const int zero_unrouted = (flags & DGM_FE_ZERO_ROW_UNROUTED) ? 1 : 0;
 #define DGM_FE(JJ)                                                                                              \
   hipLaunchKernelGGL(k_frontend<JJ>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, act_format, logits, \
-                     keys, zero_unrouted, buf + L->x, buf + L->x_sf)
+                     keys, zero_unrouted, buf + L->x, buf + L->x_sf, router)
   switch (J) {
     case 1: DGM_FE(1); break;
     case 2: DGM_FE(2); break;
@@ -580,6 +649,28 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
     default: DGM_CHECK_ARG(false, "hidden must be 512, 1024, 2048, 3072 or 4096");
   }
 #undef DGM_FE
+  int st = dgm_last_launch_status();
+  if (st || (flags & DGM_FE_SELECT_IN_MEGA) || !router) return st;
+  hipLaunchKernelGGL(k_select, dim3((num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, keys, num_tokens,
+                     num_experts, topk, flags, token_offset, (int64_t*)(buf + L->topk_idx),
+                     (float*)(buf + L->topk_weights));
+  return dgm_last_launch_status();
+}
+
+int dgm_router_logits_topk_launch(const void* logits_bf16, int num_tokens, int num_experts, int topk, int flags,
+                                  int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
+  DGM_CHECK_ARG(logits_bf16 && buffer && L, "null pointer");
+  DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
+  DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
+  DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts <= 1024");
+  DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
+  DGM_CHECK_ARG(!(flags & DGM_FE_ZERO_ROW_UNROUTED), "zero-row unrouting needs the hidden rows (dgm_router_topk_launch)");
+  if (num_tokens == 0) return 0;
+  uint8_t* buf = (uint8_t*)buffer;
+  uint32_t* keys = (uint32_t*)(buf + L->fe_keys);
+  const int64_t n = (int64_t)num_tokens * num_experts;
+  hipLaunchKernelGGL(k_keys_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, (const uint16_t*)logits_bf16, n,
+                     num_experts, keys);
   int st = dgm_last_launch_status();
   if (st || (flags & DGM_FE_SELECT_IN_MEGA)) return st;
   hipLaunchKernelGGL(k_select, dim3((num_tokens + SELECT_TPB - 1) / SELECT_TPB), dim3(256), 0, stream, keys, num_tokens,
@@ -611,6 +702,7 @@ constexpr int SELECT_IN_MEGA_MAX_TOKENS = 64;
 constexpr int SELECT_IN_MEGA_FAST_TOKENS = 8;     // (one token per wave)
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
+  if (A && A->act_format == DGM_ACT_FP8F128) return dgm_megamoe_split_launch(A, stream);
   const int chk = dgm_check_fused_args(A);
   if (chk) return chk;
   if (A->num_tokens == 0) return 0;
@@ -630,7 +722,8 @@ int dgm_check_fused_args(const DgmMoeArgs* A) {
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(A->num_local_experts > 0 && A->num_local_experts <= MAX_LOCAL_EXPERTS, "num_local_experts");
   DGM_CHECK_ARG(A->expert_begin >= 0 && A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
-  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4, "act_format");
+  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4,
+                "act_format (FP8F128 runs on dgm_megamoe_split_launch)");
   DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ || (A->w1_row_scales && A->w2_row_scales),
                 "QoQ needs the row scales s1 of both matrices");
   DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
@@ -730,7 +823,7 @@ extern "C" {
 
 int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
-  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4, "act_format");
+  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG(!A->fe_in_mega, "split path: fe_in_mega is a fused-launch option");
   if (A->act_format == DGM_ACT_QOQ || A->act_format == DGM_ACT_NVFP4) {
     // two launches of the persistent kernel: dispatch + L1, then L2 + combine
@@ -764,18 +857,20 @@ int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   int st = dgm_last_launch_status();
   if (st) return st;
   const int KT1 = A->hidden / 128, KT2 = A->intermediate / 128;
+#define DGM_SPLIT(K1, K2)                                                                       \
+  (A->act_format == DGM_ACT_MXFP4   ? launch_experts<K1, K2, DGM_ACT_MXFP4>(A, buf, L, stream)   \
+   : A->act_format == DGM_ACT_MXFP8 ? launch_experts<K1, K2, DGM_ACT_MXFP8>(A, buf, L, stream)   \
+                                    : launch_experts<K1, K2, DGM_ACT_FP8F128>(A, buf, L, stream))
   if (KT1 == 24 && KT2 == 10) {
-    st = A->act_format == DGM_ACT_MXFP4 ? launch_experts<24, 10, DGM_ACT_MXFP4>(A, buf, L, stream)
-                                        : launch_experts<24, 10, DGM_ACT_MXFP8>(A, buf, L, stream);
+    st = DGM_SPLIT(24, 10);
   } else if (KT1 == 4 && KT2 == 2) {
-    st = A->act_format == DGM_ACT_MXFP4 ? launch_experts<4, 2, DGM_ACT_MXFP4>(A, buf, L, stream)
-                                        : launch_experts<4, 2, DGM_ACT_MXFP8>(A, buf, L, stream);
+    st = DGM_SPLIT(4, 2);
   } else if (KT1 == 8 && KT2 == 4) {
-    st = A->act_format == DGM_ACT_MXFP4 ? launch_experts<8, 4, DGM_ACT_MXFP4>(A, buf, L, stream)
-                                        : launch_experts<8, 4, DGM_ACT_MXFP8>(A, buf, L, stream);
+    st = DGM_SPLIT(8, 4);
   } else {
     DGM_CHECK_ARG(false, "supported (hidden, intermediate): (3072, 1280), (512, 256), (1024, 512)");
   }
+#undef DGM_SPLIT
   if (st) return st;
   dim3 cg((A->hidden / 4 + 255) / 256, A->num_tokens);
   hipLaunchKernelGGL(k_combine, cg, dim3(256), 0, stream, (const uint16_t*)(buf + L->partials), L->max_tokens,

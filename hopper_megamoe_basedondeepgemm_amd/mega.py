@@ -31,7 +31,9 @@ class FusedSymmBuffer:
     frontend, see ``fable_frontend_keys``) and pool (dispatch table, int32).
     act_format "mxfp4" / "mxfp8": uint8 codes with E8M0 scale bytes per 32; "nvfp4": E2M1 codes
     (low nibble first) with E4M3 scale bytes per 16; "qoq": int8 codes, x_sf fp32 [tokens, H/128]
-    (one scale per token, repeated), l2_acts_sf fp32 [routes, I/64]."""
+    (one scale per token, repeated), l2_acts_sf fp32 [routes, I/64]; "fp8f128" (the split
+    recipe of ``SymmBuffer``): E4M3 codes with fp32 scales per 128 (x_sf [tokens, H/128]), an
+    E4M3 intermediate with E8M0 bytes per 32."""
 
     def __init__(self, group, num_experts, max_tokens, topk, hidden, intermediate,
                  act_format="mxfp4", ep_size=None, ep_rank=None, device=None):
@@ -64,11 +66,15 @@ class FusedSymmBuffer:
 
         xb = L.x_row_bytes
         qoq = act_format == "qoq"
+        f128 = act_format == "fp8f128"
+        sfv = 16 if act_format == "nvfp4" else 32
         if qoq:   # int8 codes, fp32 scale per token repeated over the H / 128 slots
             self.x = view(L.x, max_tokens * xb, torch.int8, (max_tokens, xb))
             self.x_sf = view(L.x_sf, max_tokens * (hidden // 128), torch.float32, (max_tokens, hidden // 128))
+        elif f128:  # E4M3 codes, fp32 scale per 128
+            self.x = view(L.x, max_tokens * xb, torch.float8_e4m3fn, (max_tokens, xb))
+            self.x_sf = view(L.x_sf, max_tokens * (hidden // 128), torch.float32, (max_tokens, hidden // 128))
         else:     # codes, E8M0 scale bytes per 32 (NVFP4: E4M3 per 16)
-            sfv = 16 if act_format == "nvfp4" else 32
             self.x = view(L.x, max_tokens * xb, torch.uint8, (max_tokens, xb))
             self.x_sf = view(L.x_sf, max_tokens * (hidden // sfv), torch.uint8, (max_tokens, hidden // sfv))
         self.topk_idx = view(L.topk_idx, R, torch.int64, (max_tokens, topk))
@@ -79,6 +85,9 @@ class FusedSymmBuffer:
         if qoq:   # int8 codes, fp32 scale per 64 features
             self.l2_acts = view(L.mid, R * mb, torch.int8, (R, mb))
             self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 64), torch.float32, (R, intermediate // 64))
+        elif f128:  # E4M3 codes, E8M0 bytes per 32 (each per-64 power-of-two scale twice)
+            self.l2_acts = view(L.mid, R * mb, torch.float8_e4m3fn, (R, mb))
+            self.l2_acts_sf = view(L.mid_sf, R * (intermediate // 32), torch.uint8, (R, intermediate // 32))
         else:
             self.l2_acts = view(L.mid, R * mb, torch.uint8, (R, mb))
             self.l2_acts_sf = view(L.mid_sf, R * (intermediate // sfv), torch.uint8, (R, intermediate // sfv))
@@ -331,10 +340,10 @@ def _check_host_error(b):
 
 
 def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, phase_stamps=None,
-           fast_math=True, fmt=None, global_scales=(None, None), fe=None, fe_keys=None):
+           fast_math=True, fmt=None, global_scales=(None, None), fe=None, fe_keys=None, act=None):
     _check_host_error(b)
     args = _moe_args(y, l1, l2, b, stats, activation_clamp, num_tokens, phase_stamps, fast_math, fmt,
-                     global_scales, fe, fe_keys)
+                     global_scales, fe, fe_keys, act)
     fn = _lib.load().dgm_megamoe_split_launch if split else _lib.load().dgm_megamoe_fused_launch
     _lib.check(fn(ctypes.byref(args), _lib.stream()))
     if os.environ.get("DG_CHECK_ERRORS", "0") == "1":     # debug: wait for the launch and check it
@@ -344,21 +353,22 @@ def _fused(y, l1, l2, b, stats, activation_clamp, num_tokens=None, split=False, 
 
 
 def _moe_args(y, l1, l2, b, stats, activation_clamp, num_tokens=None, phase_stamps=None, fast_math=True,
-              fmt=None, global_scales=(None, None), fe=None, fe_keys=None):
+              fmt=None, global_scales=(None, None), fe=None, fe_keys=None, act=None):
     """The C-ABI argument block (DgmMoeArgs) of one layer call on buffer b, after the checks."""
-    fmt = fmt or ("mxfp8" if b.act_format in ("mxfp8", "fp8") else "mxfp4")
+    act = act or b.act_format
+    fmt = fmt or "mxfp4"         # (the MXFP entries pass no format)
     kind = lambda f: f if f in ("qoq", "nvfp4") else "mxfp"
-    if kind(fmt) != kind(b.act_format):
-        raise ValueError(f"buffer was sized for {b.act_format!r}: use "
-                         f"{_ENTRY_FOR.get(b.act_format, 'mxfp4_mega_moe_fused / _split')}")
-    qoq = b.act_format == "qoq"
-    nv = b.act_format == "nvfp4"
+    if kind(fmt) != kind(act):
+        raise ValueError(f"buffer was sized for {act!r}: use "
+                         f"{_ENTRY_FOR.get(act, 'mxfp4_mega_moe_fused / _split')}")
+    qoq = act == "qoq"
+    nv = act == "nvfp4"
     if nv:
         (w1, sf1), (w2, sf2) = l1, l2
         rs1 = rs2 = None
-    else:
-        w1, sf1, rs1 = l1
-        w2, sf2, rs2 = l2
+    else:     # (values, scales[, row scales]): MXFP4 weights carry no third item that is used
+        w1, sf1, rs1 = l1[0], l1[1], (l1[2] if len(l1) > 2 else None)
+        w2, sf2, rs2 = l2[0], l2[1], (l2[2] if len(l2) > 2 else None)
     _lib.require_gpu(y, w1, sf1, w2, sf2, stats)
     assert y.dtype == torch.bfloat16 and y.is_contiguous() and y.size(1) == b.hidden
     m = y.size(0) if num_tokens is None else num_tokens
@@ -400,7 +410,7 @@ def _moe_args(y, l1, l2, b, stats, activation_clamp, num_tokens=None, phase_stam
         sel = (sel[0] & _lib.FE_FORCE_BALANCED if sel else 0, sel[1] if sel else 0)
     args = _lib.MoeArgs(num_tokens=m, hidden=b.hidden, intermediate=b.intermediate_hidden,
                         num_experts=b.num_experts, expert_begin=b.expert_begin, num_local_experts=E_l,
-                        topk=b.num_topk, act_format=b.act_code,
+                        topk=b.num_topk, act_format=_lib.ACT_FORMATS[act],
                         activation_clamp=float(activation_clamp if activation_clamp is not None else 3.0e38),
                         fast_math=int(bool(fast_math)), select_in_mega=int(sel is not None),
                         fe_flags=sel[0] if sel else 0, token_offset=sel[1] if sel else 0,
@@ -489,32 +499,80 @@ def nvfp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_exper
            split=split, fast_math=fast_math, fmt="nvfp4", global_scales=(l1_global_scales, l2_global_scales))
 
 
+def _weights_kind(l1):
+    """Activation format a layer's weights imply: QoQ (values, meta [.., 16], s1), NVFP4
+    (values, E4M3 scales [.., 2, 16, 4]) or MXFP4 (values, E8M0 scales [.., 64, 4][, None])."""
+    sf = l1[1]
+    if len(l1) == 3 and l1[2] is not None and sf.dim() == 4 and sf.size(-1) == 16:
+        return "qoq"
+    if sf.dim() == 6:
+        return "nvfp4"
+    return "mxfp"
+
+
+def _cast_into(b, hidden_input, act):
+    """The activation cast of ``hidden_input`` (bf16 [tokens, H]) into the buffer's x / x_sf."""
+    _lib.require_gpu(hidden_input)
+    assert hidden_input.dtype == torch.bfloat16 and hidden_input.size(1) == b.hidden
+    assert hidden_input.size(0) <= b.num_max_tokens_per_rank
+    h = hidden_input.contiguous()
+    _lib.check(_lib.load().dgm_router_topk_launch(
+        _lib.ptr(h), None, h.size(0), b.hidden, b.num_experts, b.num_topk, _lib.ACT_FORMATS[act], 0, 0,
+        _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
+
+
 def _split_entry(fmts, y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats=None,
                  l1_global_scales=None, l2_global_scales=None, recipe=None, activation="swiglu",
                  activation_clamp=None, fast_math=True, attn_tp_size=1, attn_tp_group=None,
                  broadcast_output=False, router_input=None, router_weight=None, router_logits=None,
-                 router_renormalize=True, tp_combine_output=None, hidden_input=None):
-    """The split API's argument list (deep_gemm/mega/__init__.py:340-433 mxfp4_mega_moe) on a
-    buffer of ``get_fused_symm_buffer_for_mega_moe``. ``router_input`` / ``router_weight``: the
-    frontend (router, top-k, activation cast) runs first on those. One GPU: attn_tp_size must be
-    1; ``router_logits``, ``tp_combine_output`` and ``hidden_input`` (the multi-rank and
-    attention-TP paths) are not provided."""
+                 router_renormalize=True, tp_combine_output=None, hidden_input=None, act=None):
+    """The split API's argument list (deep_gemm/mega/__init__.py:340-433 mxfp4_mega_moe).
+    ``hidden_input`` (bf16 [tokens, H]): cast into x / x_sf first. ``router_input`` /
+    ``router_weight``: the router and top-k run on those (x / x_sf are left as they are);
+    ``router_logits`` (bf16 [tokens, E]): the top-k of those logits. ``router_renormalize``:
+    weights = softmax over the top-k, else the selected values themselves. Otherwise the routing
+    in the buffer (topk_idx / topk_weights) is used. One GPU: attn_tp_size must be 1."""
     b = sym_buffer
-    if b.act_format not in fmts:
-        raise ValueError(f"buffer was sized for {b.act_format!r}; this entry point takes {fmts}")
+    act = act or b.act_format
+    if act not in fmts:
+        raise ValueError(f"buffer was sized for {act!r}; this entry point takes {fmts}")
     assert activation == "swiglu", activation
     assert (router_input is None) == (router_weight is None)
+    assert router_logits is None or router_input is None
+    if recipe is not None:
+        assert len(tuple(recipe)) == 3, recipe
     if attn_tp_size != 1 or tp_combine_output is not None or broadcast_output:
         raise NotImplementedError("attention-TP layouts need more than one GPU")
-    if router_logits is not None or hidden_input is not None:
-        raise NotImplementedError("router_logits / hidden_input: run fable_router_quant_topk_frontend first")
-    if b.act_format != "nvfp4" and (l1_global_scales is not None or l2_global_scales is not None):
+    if act != "nvfp4" and (l1_global_scales is not None or l2_global_scales is not None):
         raise ValueError("per-expert global scales are an NVFP4 option")
+    m = y.size(0)
+    if hidden_input is not None:
+        assert tuple(hidden_input.shape) == tuple(y.shape), (hidden_input.shape, y.shape)
+        _cast_into(b, hidden_input, act)
+    flags = 0 if router_renormalize else _lib.FE_RAW_WEIGHTS
     if router_input is not None:
-        assert router_input.shape == (y.size(0), b.hidden)
-        fable_router_quant_topk_frontend(router_input, router_weight, b)
+        _lib.require_gpu(router_input, router_weight)
+        assert router_input.dtype == torch.bfloat16 and router_weight.dtype == torch.bfloat16
+        assert tuple(router_input.shape) == (m, b.hidden)
+        assert tuple(router_weight.shape) == (b.num_experts, b.hidden)
+        if not router_renormalize:
+            raise NotImplementedError("router_input with router_renormalize=False: pass the weights' "
+                                      "logits as router_logits instead")
+        ri, rw = router_input.contiguous(), router_weight.contiguous()
+        _lib.check(_lib.load().dgm_router_topk_launch(
+            _lib.ptr(ri), _lib.ptr(rw), m, b.hidden, b.num_experts, b.num_topk, _lib.ACT_FORMATS[act],
+            _lib.FE_NO_CAST, 0, _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
+        b._fe_select = None
+    elif router_logits is not None:
+        _lib.require_gpu(router_logits)
+        assert router_logits.dtype == torch.bfloat16 and tuple(router_logits.shape) == (m, b.num_experts)
+        rl = router_logits.contiguous()
+        _lib.check(_lib.load().dgm_router_logits_topk_launch(
+            _lib.ptr(rl), m, b.num_experts, b.num_topk, flags, 0, _lib.ptr(b.buffer), ctypes.byref(b.layout),
+            _lib.stream()))
+        b._fe_select = None
     _fused(y, l1_weights, l2_weights, b, cumulative_local_expert_recv_stats, activation_clamp, split=True,
-           fast_math=fast_math, fmt=b.act_format, global_scales=(l1_global_scales, l2_global_scales))
+           fast_math=fast_math, fmt=act, global_scales=(l1_global_scales, l2_global_scales), act=act)
 
 
 def qoq_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs):
@@ -537,6 +595,108 @@ def mxfp4_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs)
     fused buffer. Arguments as ``mxfp4_mega_moe`` (:340; activation_clamp default None = no
     clamp)."""
     _split_entry(("mxfp4", "mxfp8", "fp8"), y, l1_weights, l2_weights, sym_buffer, *args, **kwargs)
+
+
+class SymmBuffer(FusedSymmBuffer):
+    """deep_gemm/mega/__init__.py:20 ``SymmBuffer``, the split path's buffer, on one GPU.
+
+    ``mma_type="fp8xmxfp4"`` (the SM90 split recipe): ``x`` E4M3 [tokens, H] with ``x_sf`` fp32
+    [tokens, H/128] (``per_token_cast_to_fp8(x, use_ue8m0=False, gran_k=128)``; the QoQ layer
+    reads int8 bytes with the per-token scale repeated, ``per_token_cast_to_int8``),
+    ``topk_idx`` int64 / ``topk_weights`` fp32 [tokens, topk]; ``l1_acts`` / ``l1_acts_sf`` alias
+    x / x_sf (routed rows are read in place); ``l2_acts`` E4M3 [routes, I] with ``l2_acts_sf``
+    E8M0 bytes [routes, I/32]. ``mma_type="fp8xfp4"``: x E4M3 with the UE8M0 scales of each
+    32 elements packed four to an int32 (``x_sf`` int32 [tokens, H/128]). ``num_ring_tokens`` sizes
+    the reference's ring pool; here every route has its own row."""
+
+    _MMA = {"fp8xmxfp4": "fp8f128", "fp8xfp4": "mxfp8"}
+
+    def __init__(self, group, num_experts, num_max_tokens_per_rank, num_topk, hidden, intermediate_hidden,
+                 num_ring_tokens=None, mma_type="fp8xfp4", activation="swiglu"):
+        assert activation == "swiglu", f"Only `swiglu` activation is supported, got `{activation}`"
+        if mma_type not in self._MMA:
+            raise ValueError(f"mma_type {mma_type!r}: one of {sorted(self._MMA)}")
+        super().__init__(group, num_experts, num_max_tokens_per_rank, num_topk, hidden, intermediate_hidden,
+                         act_format=self._MMA[mma_type])
+        self.mma_type = mma_type
+        self.num_ring_tokens = num_ring_tokens if num_ring_tokens is not None else num_max_tokens_per_rank * num_topk
+        if mma_type == "fp8xfp4":      # UE8M0 bytes per 32, four to an int32
+            self.x = self.x.view(torch.float8_e4m3fn)
+            self.x_sf = self.x_sf.view(torch.int32)
+            self.l1_acts, self.l1_acts_sf = self.x, self.x_sf
+
+    def destroy(self):
+        super().destroy()
+        self.x = self.x_sf = None
+
+
+def get_symm_buffer_for_mega_moe(group, num_experts, num_max_tokens_per_rank, num_topk, hidden,
+                                 intermediate_hidden, use_fp8_dispatch=None, mma_type="fp8xfp4",
+                                 activation="swiglu"):
+    """deep_gemm/mega/__init__.py:70: the split path's buffer (``group=None``: one GPU)."""
+    if use_fp8_dispatch is not None:
+        assert use_fp8_dispatch == (mma_type.split("x")[0] == "fp8")
+    return SymmBuffer(group, num_experts, num_max_tokens_per_rank, num_topk, hidden, intermediate_hidden,
+                      num_max_tokens_per_rank * num_topk, mma_type=mma_type, activation=activation)
+
+
+def get_mxfp4_mega_moe_sm90_block_n(hidden, intermediate_hidden, expected_m_per_rank=None):
+    """deep_gemm/mega/__init__.py:244: the SM90 N tile; accepted for the interface, one layout
+    serves every tile choice here."""
+    assert hidden % 128 == 0 and intermediate_hidden % 128 == 0
+    if expected_m_per_rank is None:
+        return 128
+    crossover = 192 if intermediate_hidden <= 2048 else 384
+    return 256 if expected_m_per_rank >= crossover else 128
+
+
+def transform_mxfp4_weights_for_mega_moe_sm90(l1_weights, l2_weights, block_n=None, block_k=128, group_size=32,
+                                              expected_m_per_rank=None):
+    """deep_gemm/mega/__init__.py:257: MXFP4 weights ``(packed [E, N, K/2] (Marlin, as
+    deep_gemm/quantization_mxfp4.py quantize_to_mxfp4 writes them), E8M0 scales [E, N, K/32])``
+    -> ``((w1_values, w1_scales), (w2_values, w2_scales))`` in the matrix-core fragment layout
+    (gate / up blocks of W1 interleaved), for ``mxfp4_mega_moe``. ``block_n`` picks an SM90
+    tile there and has no effect here."""
+    assert block_n in (None, 128, 256) and block_k == 128 and group_size == 32
+    (v1, s1, _), (v2, s2, _) = transform_mxfp4_weights_for_mega_moe_fused(l1_weights, l2_weights)
+    return (v1, s1), (v2, s2)
+
+
+def mxfp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_expert_recv_stats=None,
+                   l1_global_scales=None, l2_global_scales=None, recipe=None, activation="swiglu",
+                   activation_clamp=None, fast_math=True, attn_tp_size=1, attn_tp_group=None,
+                   broadcast_output=False, router_input=None, router_weight=None, router_logits=None,
+                   router_renormalize=True, tp_combine_output=None, hidden_input=None, _cpp_op=None):
+    """deep_gemm/mega/__init__.py:340: the split MegaMoE layer on a ``SymmBuffer``.
+
+    MXFP4 weights (``transform_mxfp4_weights_for_mega_moe_sm90``) on an ``mma_type="fp8xmxfp4"``
+    buffer: E4M3 activations with fp32 scales per 128 (each K-tile's products times its scale),
+    fp32 gate / up, clamp, SiLU * up * routing weight, E4M3 intermediate with one power-of-two
+    scale per 64 features, L2, each route rounded to bf16, fp32 slot-order combine
+    (tests/test_four_api_correctness.py:421-446). On an ``"fp8xfp4"`` buffer: the MXFP8 layer
+    (UE8M0 scales per 32). QoQ weights (``transform_qoq_int4_weights_for_mega_moe_sm90``, the
+    ``int4_mega_moe`` alias) run the QoQ W4A8 layer on the same buffer (int8 bytes in x, the
+    token's scale in x_sf). ``activation_clamp=None``: no clamp. Routing inputs as in the
+    reference: the buffer's topk_idx / topk_weights, or ``router_input`` + ``router_weight``, or
+    ``router_logits`` (bf16); ``hidden_input`` (bf16) is cast into x / x_sf first."""
+    b = sym_buffer
+    kind = _weights_kind(l1_weights)
+    if kind == "qoq":
+        if b.act_format not in ("fp8f128", "qoq"):
+            raise ValueError("QoQ weights need an mma_type='fp8xmxfp4' SymmBuffer (or a 'qoq' fused buffer)")
+        act = "qoq"
+    elif kind == "nvfp4":
+        act = "nvfp4"
+    else:
+        act = b.act_format
+    _split_entry(("fp8f128", "mxfp8", "mxfp4", "qoq", "nvfp4"), y, l1_weights, l2_weights, b,
+                 cumulative_local_expert_recv_stats, l1_global_scales, l2_global_scales, recipe, activation,
+                 activation_clamp, fast_math, attn_tp_size, attn_tp_group, broadcast_output, router_input,
+                 router_weight, router_logits, router_renormalize, tp_combine_output, hidden_input, act=act)
+
+
+# deep_gemm/mega/__init__.py:448: one entry for both weight families (the weights pick the layer)
+int4_mega_moe = mxfp4_mega_moe
 
 
 def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,

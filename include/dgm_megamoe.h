@@ -27,12 +27,23 @@ extern "C" {
 #define DGM_ACT_NVFP4 3 /* W4A4 NVFP4: E2M1 + E4M3 scale per 16 (activations and weights) */
 #define DGM_ACT_QOQ 2   /* QoQ W4A8: int8 activations with one fp32 scale per token, QoQ weights
                            (deep_gemm/quantization_qoq_fused.py:1-11) */
+#define DGM_ACT_FP8F128 4 /* E4M3 activations with one fp32 scale per 128 K
+                             (per_token_cast_to_fp8(use_ue8m0=False, gran_k=128), deep_gemm/utils/math.py:26-38),
+                             MXFP4 weights, FP8 intermediate with a power-of-two scale per 64: the
+                             "fp8xmxfp4" split recipe (deep_gemm/mega/__init__.py:70-127, 340-446;
+                             tests/test_four_api_correctness.py:54-62, 215). Split path only. */
 
 /* frontend flags */
 #define DGM_FE_FORCE_BALANCED 1     /* DG_FE_FORCE_BALANCED: tests/test_four_api_correctness.py:125-144 */
 #define DGM_FE_ZERO_ROW_UNROUTED 2  /* DG_FE_ZERO_ROW_UNROUTED: deep_gemm/mega/__init__.py:693-696 */
 #define DGM_FE_SELECT_IN_MEGA 4     /* DG_FE_SELECT_IN_MEGA: deep_gemm/mega/__init__.py:688-692 -- the frontend
                                        stops after logits + cast; the fused layer selects the top-k */
+#define DGM_FE_RAW_WEIGHTS 8        /* router_renormalize=False of deep_gemm/mega/__init__.py:340-360: the routing
+                                       weights are the selected logits themselves
+                                       (deep_gemm/include/deep_gemm/impls/sm90_mxfp4_mega_moe.cuh:1327-1343) */
+#define DGM_FE_NO_CAST 16           /* the router and top-k alone, x / x_sf untouched (the fused router of
+                                       deep_gemm/include/deep_gemm/impls/sm90_mxfp4_mega_moe.cuh:1251-1279,
+                                       router_input of deep_gemm/mega/__init__.py:340) */
 
 /* Library version and the message of the last failed host-side check (thread-local). */
 int dgm_version(void);
@@ -166,11 +177,22 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
  * with DGM_FE_ZERO_ROW_UNROUTED an all-zero hidden row gets zero keys (unrouted).
  * token_offset = global id of row 0 (forced-balanced rule). With DGM_FE_SELECT_IN_MEGA the
  * top-k is left to the fused layer (DgmMoeArgs.select_in_mega), which selects from the keys;
- * topk_idx / topk_weights are written by that call instead. */
+ * topk_idx / topk_weights are written by that call instead. router_weight_bf16 NULL: the
+ * activation cast alone (the hidden_input path of deep_gemm/mega/__init__.py:340
+ * mxfp4_mega_moe, sm90_mxfp4_mega_moe.cuh:1208-1243), no routing flags. */
 int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16,
                            int num_tokens, int hidden, int num_experts, int topk, int act_format,
                            int flags, int token_offset, void* buffer,
                            const DgmBufferLayout* layout, hipStream_t stream);
+
+/* Replaces the router_logits input of deep_gemm/mega/__init__.py:340 mxfp4_mega_moe (the SM90
+ * kernel's kRouterLogitsInput path, deep_gemm/include/deep_gemm/impls/sm90_mxfp4_mega_moe.cuh:1295-1343):
+ * bf16 logits [num_tokens, num_experts] -> the top-k keys (fe_keys view) and, unless
+ * DGM_FE_SELECT_IN_MEGA, topk_idx / topk_weights: the k largest logits (ties: the lower expert),
+ * weights = softmax over them, or the logits themselves with DGM_FE_RAW_WEIGHTS.
+ * DGM_FE_FORCE_BALANCED as for dgm_router_topk_launch. */
+int dgm_router_logits_topk_launch(const void* logits_bf16, int num_tokens, int num_experts, int topk, int flags,
+                                  int token_offset, void* buffer, const DgmBufferLayout* layout, hipStream_t stream);
 
 /* ------------------------------------------------------------------ fused layer
  * Replaces csrc/apis/mega_fused.hpp:78-102 run_fused / _C.mxfp4_mega_moe_fused and

@@ -138,6 +138,11 @@ def quant_act(x_f32, act_format):
         q, sf = packers.per_token_cast_to_fp8_ue8m0(x_f32, 32)
         sfb = ((sf.view(np.uint32) >> 23) & 0xFF).astype(np.uint8)
         return q, sfb, packers.dequant_fp8_rows(q, sf, 32)
+    if act_format == "fp8f128":
+        # the SM90 split recipe's activations: per_token_cast_to_fp8(use_ue8m0=False, gran_k=128)
+        # (deep_gemm/utils/math.py:26-38; tests/test_four_api_correctness.py:215, x_reference :226-230)
+        q, sf = packers.per_token_cast_to_fp8_f32sf(x_f32, 128)
+        return q, sf, packers.dequant_fp8_rows(q, sf, 128)
     if act_format == "nvfp4":
         # W4A4 NVFP4 row cast (sm100_b200/test_mega_moe.py:68-93, act_format 'nvfp4')
         p, sf, sfb = packers.cast_to_nvfp4_rows(x_f32)
@@ -166,7 +171,25 @@ def requant_mid(a, act_format):
         return requant_mid_qoq(a)[2]
     if act_format == "nvfp4":
         return requant_mid_nvfp4(a)
+    if act_format == "fp8f128":
+        return requant_mid_fp8_64(a)[2]
     raise ValueError(act_format)
+
+
+def requant_mid_fp8_64(a):
+    """FP8 intermediate requant of tests/test_four_api_correctness.py:54-62 (non-QoQ branch), the
+    rule of the fp8 x MXFP4 split recipe: per 64 features, scale = 2^ceil(log2(max(amax / 448,
+    tiny))), E4M3 (round to nearest even) of a / scale. Returns (E4M3 codes, E8M0 bytes of the
+    scales [.., n/64], dequantised)."""
+    a = as_f32(a)
+    g = a.reshape(*a.shape[:-1], -1, 64)
+    amax = np.abs(g).max(axis=-1, keepdims=True)
+    sa = np.maximum(amax / np.float32(448.0), FLT_TINY).astype(np.float32)
+    e = ceil_log2_f32(sa)
+    sc = np.exp2(e).astype(np.float32)
+    codes = e4m3_encode(g / sc)
+    return (codes.reshape(a.shape), (e[..., 0] + 127).astype(np.uint8),
+            (e4m3_decode(codes) * sc).reshape(a.shape).astype(np.float32))
 
 
 def requant_mid_nvfp4(a):

@@ -209,3 +209,27 @@ def test_cast_to_nvfp4_rows_known_answers():
     # an all-zero group: amax floor 1e-30 -> E4M3(1.67e-31) = 0 -> codes 0 (no -0, no NaN)
     p0, _, s0 = pk.cast_to_nvfp4_rows(np.zeros((1, 16), np.float32))
     assert not p0.any() and not s0.any()
+
+
+def test_requant_mid_fp8_64_known_answers():
+    """The fp8 x MXFP4 split recipe's intermediate (tests/test_four_api_correctness.py:54-62, non-QoQ
+    branch): per 64 features, scale = 2^ceil(log2(max(amax / 448, FLT_MIN))), E4M3 of a / scale.
+    Group 0 has amax 448 / 8 -> scale exactly 2^-3, its values on the E4M3 grid x 2^-3 come back
+    unchanged; group 1 has amax a hair above 448 -> scale 2 (ceil, not round), so 1.0 stays 1.0
+    but 448.5 becomes 448 (E4M3 of 224.25 rounds to 224); an all-zero group gets the FLT_MIN
+    floor (E8M0 code 1), not a zero or NaN scale. A per-32 or per-128 grouping, a rounded
+    (not ceil) exponent or a missing floor each give a different answer."""
+    g0 = np.zeros(64, np.float32)
+    g0[:4] = [56.0, -1.75, 0.5, 0.015625]            # 448 / 8, and E4M3 values x 2^-3
+    g1 = np.zeros(64, np.float32)
+    g1[0], g1[40], g1[41] = 448.5, 1.0, 0.01
+    g2 = np.zeros(64, np.float32)
+    codes, e, deq = moe.requant_mid_fp8_64(np.concatenate([g0, g1, g2])[None])
+    np.testing.assert_array_equal(e[0], [127 - 3, 127 + 1, 1])
+    np.testing.assert_array_equal(deq[0, :4], g0[:4])
+    assert deq[0, 64] == 448.0 and deq[0, 104] == 1.0
+    # 0.01 shares group 1's scale 2: 0.005 is an E4M3 subnormal, 2.56 x 2^-9 -> 3 x 2^-9; a
+    # per-32 group of its own (amax 1.0, scale 2^-8) would give 2.56 x 256 -> 2.5 x 256, i.e. 0.009765625
+    assert deq[0, 105] == np.float32(3 * 2.0 ** -9 * 2)
+    assert (deq[0, 128:] == 0).all() and (codes[0, 128:] == 0).all()
+    np.testing.assert_array_equal(moe.requant_mid(np.concatenate([g0, g1, g2])[None], "fp8f128"), deq)
