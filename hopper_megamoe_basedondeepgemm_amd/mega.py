@@ -36,7 +36,7 @@ class FusedSymmBuffer:
     E4M3 intermediate with E8M0 bytes per 32."""
 
     def __init__(self, group, num_experts, max_tokens, topk, hidden, intermediate,
-                 act_format="mxfp4", ep_size=None, ep_rank=None, device=None):
+                 act_format="mxfp4", ep_size=None, ep_rank=None, device=None, buffer=None):
         if group is not None:
             ep_size = group.size() if ep_size is None else ep_size
             ep_rank = group.rank() if ep_rank is None else ep_rank
@@ -56,8 +56,14 @@ class FusedSymmBuffer:
         self.expert_begin = ep_rank * self.num_local_experts
         self.layout = _lib.layout(max_tokens, num_experts, self.num_local_experts, topk, hidden,
                                   intermediate, self.act_code)
-        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
-        self.buffer = torch.zeros(self.layout.total_bytes, dtype=torch.uint8, device=dev)
+        if buffer is None:
+            dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+            self.buffer = torch.zeros(self.layout.total_bytes, dtype=torch.uint8, device=dev)
+        else:     # a caller-owned (zeroed) allocation of at least layout.total_bytes
+            _lib.require_gpu(buffer)
+            assert buffer.is_contiguous() and buffer.nbytes >= self.layout.total_bytes, \
+                (buffer.nbytes, self.layout.total_bytes)
+            self.buffer = buffer.view(torch.uint8).view(-1)
         L, b = self.layout, self.buffer
         R = max_tokens * topk
 
@@ -276,6 +282,63 @@ def transform_weights_for_mega_moe(l1, l2):
 
 # ----------------------------------------------------------------------------- frontend
 SELECT_IN_MEGA_MAX_TOKENS = 64    # every workgroup of the fused kernel reads all tokens' logits
+# csrc/fable_frontend.h kFEPath* (deep_gemm/mega/__init__.py:593): the launch-shape families of the
+# reference's frontend. Here one router kernel serves every shape; fable_frontend_path names the
+# family whose options apply (FE_PATH_CC: select_in_mega and zero-row unrouting available).
+FE_PATH_WMMA, FE_PATH_SWAPAB, FE_PATH_CC = 0, 1, 2
+
+
+def fable_frontend_path(m: int, h: int = 3072, e: int = 384, topk: int = 8) -> int:
+    """deep_gemm/mega/__init__.py:600: the option family of the frontend for (m, h, e, topk):
+    FE_PATH_CC up to SELECT_IN_MEGA_MAX_TOKENS tokens (the key array, select_in_mega and zero-row
+    unrouting apply), FE_PATH_WMMA beyond."""
+    assert m >= 0 and h % 512 == 0 and 0 < topk <= min(e, 16)
+    return FE_PATH_CC if m <= SELECT_IN_MEGA_MAX_TOKENS else FE_PATH_WMMA
+
+
+def fable_frontend_router_ctas(m: int, e: int, h: int = 3072, topk: int = 8) -> int:
+    """deep_gemm/mega/__init__.py:653: router workgroups of the frontend launch for (m, h, e,
+    topk): one wave per (expert, 4 tokens), four waves per workgroup."""
+    return ((e + 3) // 4) * ((m + 3) // 4)
+
+
+def fable_frontend_workspace_bytes(e: int, max_tokens: int = 64) -> int:
+    """deep_gemm/mega/__init__.py:597: bytes of the frontend's scratch (fp32 logits and the u32
+    key array of up to ``max_tokens`` tokens; both live in the layer buffer here)."""
+    return 2 * 4 * e * max_tokens
+
+
+def fable_frontend_workspace(sym_buffer, e: int, device=None) -> torch.Tensor:
+    """deep_gemm/mega/__init__.py:658: the frontend's workspace of ``sym_buffer``: the buffer's
+    logits and key-array region (uint8; zeroed with the buffer, no separate allocation)."""
+    b = sym_buffer
+    assert e == b.num_experts
+    L = b.layout
+    return b.buffer[L.logits:L.fe_keys + 4 * e * b.num_max_tokens_per_rank]
+
+
+def fable_router_weight_fragment_layout(router_weight: torch.Tensor) -> torch.Tensor:
+    """deep_gemm/mega/__init__.py:617: the reference's swapab A-fragment order of [E, K] bf16
+    router weights ([E/16][K/32][half][g][t][8], same shape). Accepted by the frontend with
+    ``wlayout="pre"``, which undoes it: this frontend reads row-major weights."""
+    e, k = router_weight.shape
+    assert router_weight.dtype == torch.bfloat16 and e % 16 == 0 and k % 32 == 0
+    v = router_weight.contiguous().view(e // 16, 2, 8, k // 32, 4, 8)
+    return v.permute(0, 3, 1, 2, 4, 5).contiguous().view(e, k)
+
+
+def _router_weight_row_major(router_weight, wlayout):
+    """Row-major router weights from a frontend ``wlayout`` ('row' / 'fragment': as given; 'pre':
+    the fragment order of fable_router_weight_fragment_layout, undone)."""
+    if wlayout is None:
+        wlayout = os.environ.get("DG_FE_ROUTER_WLAYOUT", "fragment")
+    if isinstance(wlayout, str):
+        wlayout = {"row": 0, "fragment": 1, "pre": 2, "0": 0, "1": 1, "2": 2}[wlayout.strip().lower()]
+    if int(wlayout) != 2:
+        return router_weight
+    e, k = router_weight.shape
+    v = router_weight.contiguous().view(e // 16, k // 32, 2, 8, 4, 8)
+    return v.permute(0, 2, 3, 1, 4, 5).contiguous().view(e, k)
 
 def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.Tensor, sym_buffer,
                                      quant: Optional[str] = None, stamps=None, l2_persist=None,
@@ -291,9 +354,12 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
     next fused call on this buffer selects the top-k (in its prologue up to 8 tokens, else in a
     selection launch just before it) and writes ``topk_idx / topk_weights``, which are not valid
     before that call. ``stamps``,
-    ``l2_persist`` and ``wlayout`` are H20 tuning knobs with no effect here."""
+    ``l2_persist`` is an H20 tuning knob with no effect here; ``wlayout="pre"`` takes router weights
+    in the fragment order of ``fable_router_weight_fragment_layout`` ("row" / "fragment": row-major
+    weights, as given)."""
     b = sym_buffer
     _lib.require_gpu(hidden, router_weight)
+    router_weight = _router_weight_row_major(router_weight, wlayout)
     assert hidden.dtype == torch.bfloat16 and router_weight.dtype == torch.bfloat16
     m, h = hidden.shape
     e = router_weight.size(0)

@@ -1,0 +1,60 @@
+"""Host-side API checks (CPU, no GPU): the buffer layouts the split recipe shares between its
+two layers, the frontend's option family and workgroup count, the reference-order router weight
+permutation and its inverse, and the ``_C`` module's names."""
+import numpy as np
+import pytest
+import torch
+
+from hopper_megamoe_basedondeepgemm_amd import _lib, mega
+
+
+def _fields(L):
+    return {f: getattr(L, f) for f, _ in _lib.BufferLayout._fields_}
+
+
+@pytest.mark.parametrize("shape", [(8, 384, 384, 8, 3072, 1280), (16, 48, 48, 8, 512, 256), (5, 32, 16, 8, 1024, 512)])
+def test_fp8f128_and_qoq_share_one_layout(shape):
+    """One split buffer serves the fp8 x MXFP4 layer and the QoQ layer (int4_mega_moe): the two
+    formats' layouts are identical field by field."""
+    a = _lib.layout(*shape, _lib.ACT_FORMATS["fp8f128"])
+    b = _lib.layout(*shape, _lib.ACT_FORMATS["qoq"])
+    assert _fields(a) == _fields(b)
+    T, E, El, k, H, I = shape
+    assert a.x_sf - a.x >= T * H and a.x_row_bytes == H and a.mid_row_bytes == I
+
+
+def test_frontend_path_and_router_workgroups():
+    assert mega.fable_frontend_path(8) == mega.FE_PATH_CC
+    assert mega.fable_frontend_path(64) == mega.FE_PATH_CC
+    assert mega.fable_frontend_path(65) == mega.FE_PATH_WMMA
+    assert mega.fable_frontend_router_ctas(8, 384) == 96 * 2
+    assert mega.fable_frontend_router_ctas(1, 48) == 12
+
+
+def test_router_weight_fragment_layout_inverse():
+    """wlayout='pre' takes the reference's fragment order (deep_gemm/mega/__init__.py:617-628):
+    lane (g, t) of half h in block (G, b) holds W[16 G + 8 h + g][32 b + 8 t .. +7]."""
+    E, K = 32, 64
+    w = torch.arange(E * K, dtype=torch.float32).reshape(E, K).to(torch.bfloat16)
+    f = mega.fable_router_weight_fragment_layout(w)
+    flat = f.reshape(-1).float().numpy()
+    G, b, h, g, t = 1, 1, 1, 3, 2          # element 0 of that lane
+    pos = ((((G * (K // 32) + b) * 2 + h) * 8 + g) * 4 + t) * 8
+    assert flat[pos] == float(w[16 * G + 8 * h + g, 32 * b + 8 * t])
+    assert torch.equal(mega._router_weight_row_major(f, "pre"), w)
+    assert mega._router_weight_row_major(w, "row") is w
+
+
+def test_c_module_names():
+    from hopper_megamoe_basedondeepgemm_amd import _C
+    for name in ("get_symm_buffer_size_for_fused_mega_moe", "mxfp4_mega_moe_fused", "qoq_mega_moe_fused",
+                 "get_symm_buffer_size_for_mega_moe", "mxfp4_mega_moe", "int4_mega_moe",
+                 "fable_router_quant_topk_frontend", "fable_frontend_router_ctas", "fable_frontend_path",
+                 "get_token_alignment_for_mega_moe", "get_ring_limit_for_mega_moe",
+                 "get_legacy_pool_tokens_for_mega_moe"):
+        assert callable(getattr(_C, name)), name
+    n, slice_fn = _C.get_symm_buffer_size_for_fused_mega_moe(1, 48, 8, 8, 3072, 1280)
+    assert n == _lib.layout(8, 48, 48, 8, 3072, 1280, _lib.ACT_FORMATS["fp8f128"]).total_bytes
+    assert _C.get_ring_limit_for_mega_moe(8, 48, 8, 1) == (64, 64)
+    with pytest.raises(ValueError):
+        _C.get_symm_buffer_size_for_mega_moe(1, 48, 8, 8, 3072, 1280, "bf16xbf16", "swiglu", 64)
