@@ -1060,6 +1060,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         promote(prev, md_n, x_n);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = (float)qa[i] * __uint_as_float(sd[MR1 + i]) * sx;
+        if (p.debug & 2) {
+          // (tests) the exact int32 accumulators: [pool row][W1 row, gate rows then up rows]
+          if (s0 + c < n) {
+            int* dq = reinterpret_cast<int*>(p.stamps) + (size_t)(r0 + s0 + c) * (2 * I) + (gu ? I : 0) +
+                      16 * (4 * q + pp) + 4 * kq;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dq[i] = qa[i];
+          }
+        }
       } else if constexpr (ACT == DGM_ACT_NVFP4) {
         // four f16 ops per tile: weights E2M1 x E4M3 -> f16 in registers, activations already
         // f16 in LDS (read one tile ahead); scale dwords stream in their own ring

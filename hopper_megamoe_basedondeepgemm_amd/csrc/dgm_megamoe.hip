@@ -812,9 +812,10 @@ int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, 
     p.fast_math = A->fast_math;
     p.spin_limit = 1 << 22;
     p.stamps = (long long*)A->phase_stamps;
-    p.stamp_rows = A->phase_stamps ? A->phase_stamp_rows : 0;
+    // (debug bit 1: phase_stamps receives the QoQ L1 accumulators instead of stamps)
+    p.stamp_rows = A->phase_stamps && !(A->debug_flags & 2) ? A->phase_stamp_rows : 0;
     p.phases = phases;
-    p.debug = (int16_t)(A->debug_flags & 1);
+    p.debug = (int16_t)(A->debug_flags & 3);
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
 }

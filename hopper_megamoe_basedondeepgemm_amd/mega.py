@@ -594,7 +594,8 @@ def _split_entry(fmts, y, l1_weights, l2_weights, sym_buffer, cumulative_local_e
                  router_renormalize=True, tp_combine_output=None, hidden_input=None, act=None):
     """The split API's argument list (deep_gemm/mega/__init__.py:340-433 mxfp4_mega_moe).
     ``hidden_input`` (bf16 [tokens, H]): cast into x / x_sf first. ``router_input`` /
-    ``router_weight``: the router and top-k run on those (x / x_sf are left as they are);
+    ``router_weight``: the router and top-k run on those (x / x_sf are left as they are; an
+    all-zero router_input row is unrouted unless DG_FE_ZERO_ROW_UNROUTED=0);
     ``router_logits`` (bf16 [tokens, E]): the top-k of those logits. ``router_renormalize``:
     weights = softmax over the top-k, else the selected values themselves. Otherwise the routing
     in the buffer (topk_idx / topk_weights) is used. One GPU: attn_tp_size must be 1."""
@@ -625,9 +626,12 @@ def _split_entry(fmts, y, l1_weights, l2_weights, sym_buffer, cumulative_local_e
             raise NotImplementedError("router_input with router_renormalize=False: pass the weights' "
                                       "logits as router_logits instead")
         ri, rw = router_input.contiguous(), router_weight.contiguous()
+        # (an all-zero router_input row is left unrouted, as the frontend does by default:
+        # env DG_FE_ZERO_ROW_UNROUTED)
+        zr = _lib.FE_ZERO_ROW_UNROUTED if os.environ.get("DG_FE_ZERO_ROW_UNROUTED", "1") == "1" else 0
         _lib.check(_lib.load().dgm_router_topk_launch(
             _lib.ptr(ri), _lib.ptr(rw), m, b.hidden, b.num_experts, b.num_topk, _lib.ACT_FORMATS[act],
-            _lib.FE_NO_CAST, 0, _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
+            _lib.FE_NO_CAST | zr, 0, _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
         b._fe_select = None
     elif router_logits is not None:
         _lib.require_gpu(router_logits)

@@ -245,7 +245,10 @@ typedef struct DgmMoeArgs {
   int32_t* host_error;
   /* Test hook, 0 in normal use. Bit 0: the persistent kernel additionally runs one bounded wait
    * on a counter nothing sets, with a zero spin limit, so the wait expires and the error
-   * reporting (error counter, host_error) can be tested without a real failure. */
+   * reporting (error counter, host_error) can be tested without a real failure. Bit 1 (QoQ, the
+   * persistent kernel): phase_stamps receives the exact int32 L1 accumulators
+   * (sum over K128 groups of s2 * sum (code - z) * x8, per route in pool order and W1 row, gate
+   * rows then up rows: int32 [routes][2 I]) instead of stamps, for bit-exact tests. */
   int32_t debug_flags;
 } DgmMoeArgs;
 

@@ -1,6 +1,8 @@
 """GPU parity of the QoQ W4A8 layer (qoq_mega_moe_fused) against the oracle.
 
-Bit-exact: the per-token int8 activation codes and scales of the frontend, the pool.
+Bit-exact: the per-token int8 activation codes and scales of the frontend, the pool, and the
+L1 int32 accumulators of every route (dumped by the kernel's debug hook) against the exact
+integer product of the weights' (code - z) * s2 with the int8 activations.
 Integer path: the intermediate int8 codes and per-64 scales the kernel hands from L1 to L2
 are checked against an exact-integer restatement of L1 (int64 group sums
 sum_k (code - z) * s2 * x8, then float(Q) * s1 * sx): scales within 1e-5 relative error,
@@ -271,3 +273,45 @@ def test_qoq_int4_packer_and_split_matches_fused():
     m = moe.metrics(yv[keep], ref[keep])
     assert m["cos_min"] >= COS_MIN and m["rel_rmse"] <= REL_RMSE_MAX, m
     print(m)
+
+
+@pytest.mark.parametrize("M,E,H,I", [(12, 16, 1024, 512), (8, 48, 3072, 1280)])
+def test_qoq_l1_int_accumulators_bit_exact(M, E, H, I):
+    """The W4A8 L1 accumulator of each (route, W1 row), sum over K128 groups g of
+    s2_g * sum_k (code - z_g) * x8_k, is exact int32 arithmetic in the kernel (int8 matrix-core
+    sums, integer zero-point correction and scale promotion): equal to the oracle's int64
+    product, element for element (the north star's 'int GEMM accumulators bit-exact')."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    topk = 8
+    print(f"qoq int accumulators M={M} E={E} H={H} I={I}", flush=True)
+    t, h1, h2 = make_qoq_weights(E, H, I, 600 + M)
+    rng = np.random.default_rng(601 + M)
+    x = randn_bf16(rng, (M, H))
+    rw = randn_bf16(rng, (E, H), 0.02)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="qoq")
+    dgm.fable_router_quant_topk_frontend(bf16_cpu(x).cuda(), bf16_cpu(rw).cuda(), buf)
+    R = M * topk
+    dump = torch.zeros(R * I, dtype=torch.int64, device="cuda")         # int32 [R][2I]
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    buf._debug_flags = 2
+    try:
+        dgm.qoq_mega_moe_fused(y, t[0], t[1], buf, activation_clamp=10.0, phase_stamps=dump)
+        torch.cuda.synchronize()
+    finally:
+        buf._debug_flags = 0
+    assert buf.kernel_error() == 0
+    got = dump.view(torch.int32).cpu().numpy().reshape(R, 2 * I).astype(np.int64)
+    _, active, offsets, routes = buf.pool_table()
+    idx = buf.topk_idx[:M].cpu().numpy()
+    x8 = buf.x[:M].cpu().numpy().astype(np.int64)
+    n_checked = 0
+    for a, e in enumerate(active.tolist()):
+        wint = pk.qoq_int_codes(h1[0][e:e + 1], h1[1][e:e + 1], h1[2][e:e + 1])[0]    # [2I, H]
+        for pr in range(int(offsets[a]), int(offsets[a + 1])):
+            rid = int(routes[pr])
+            tok = rid // topk
+            assert idx[tok, rid % topk] == e
+            np.testing.assert_array_equal(got[pr], wint @ x8[tok])
+            n_checked += 1
+    assert n_checked == R
