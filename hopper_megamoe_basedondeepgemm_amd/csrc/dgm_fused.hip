@@ -188,6 +188,8 @@ struct FusedSmem {
   float route_w[FUSED_MAX_ROUTES];     // routing weight of each route
   int routes[FUSED_MAX_ROUTES];
   int prow[FUSED_MAX_ROUTES];          // per pool row: its route's row in `partials` (slot * part_rows + token)
+  int ytok[FUSED_MAX_ROUTES];          // per pool row: its token when that token has no other local
+                                       // route (the L2 unit writes y itself), else -1
   int act[FUSED_MAX_LOCAL];
   int aoff[FUSED_MAX_LOCAL + 1];
   int nslot[FUSED_MAX_TOKENS];
@@ -819,6 +821,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   for (int q = tid; q < s.meta[1]; q += FT) {
     const int r = s.routes[q], t = r / p.topk;
     s.prow[q] = (r - t * p.topk) * p.part_rows + t;
+    // (NVFP4: always through the combine; its kernel has no registers to spare for the y store)
+    s.ytok[q] = ACT != DGM_ACT_NVFP4 && s.nslot[t] == 1 ? t : -1;
   }
   if (st && tid == 0) st[1] = wall_clock();
   if (blockIdx.x == 0) {
@@ -1311,8 +1315,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const int a = v / UPE2, b = v % UPE2;
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
       for (int i = i0; i < 16 * RB2 && i / RB2 < n; i += FT)
-        __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2) * CNT_LINE], 1,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / RB2] < 0)   // (a token's only local route writes y itself)
+          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2) * CNT_LINE], 1,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units v0 and G + v0 first, then claims (offset by 2 G)
     __syncthreads();
@@ -1588,6 +1593,17 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int j = 0; j < RB2; ++j)
           st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
                                        ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
+        // a token with no other local route: its y rows are this route's output (the combine of
+        // one bf16 route output), written here; no arrival, no combine
+        const int yt = ACT == DGM_ACT_NVFP4 ? -1 : s.ytok[r0 + s0 + c];
+        if (yt >= 0) {
+          uint16_t* yd = p.y + (size_t)yt * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+#pragma unroll
+          for (int j = 0; j < RB2; ++j)
+            *reinterpret_cast<uint64_t*>(yd + 16 * j) =
+                (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
+                ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48);
+        }
       }
       const bool bcast = last_slab && q1 < U2;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
@@ -1630,18 +1646,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // outputs in slot order (fp32) -> bf16 y. The waits are only on L2 items, which never wait on
   // this phase.
   if (p.phases & 2) {
+    constexpr int DIRECT_Y = ACT == DGM_ACT_NVFP4 ? 0 : 1;   // routes per token that need no combine
     constexpr int BR = 16 * NW, CB = BR / 2, PG = FT / CB;
     const int P = p.M * NBL2;
     for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {
       if (tid < PG && i0 + tid < P) {
         const int need = s.nslot[(i0 + tid) / NBL2];
-        if (need > 0) spin_until2(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err, p.host_err);
+        if (need > DIRECT_Y) spin_until2(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err, p.host_err);
       }
       __syncthreads();
       const int i = i0 + tid / CB;
       if (i < P) {
         const int t = i / NBL2, row = (i % NBL2) * BR + 2 * (tid % CB);
-        if (s.nslot[t] > 0) {              // (y rows of tokens without a local route: zeroed by workgroup 0)
+        // (y rows of tokens without a local route: zeroed by workgroup 0; with one: written by its
+        // L2 unit, except NVFP4's)
+        if (s.nslot[t] > DIRECT_Y) {
           float s0 = 0.f, s1 = 0.f;
           for (int sl = 0; sl < p.topk; ++sl)
             if (s.exp_of_route[t * p.topk + sl] >= 0) {
