@@ -107,12 +107,6 @@ DGM_DEV U4 ld_stream_after(const uint8_t* base, int off, v4i acc) {
   asm("" : "+v"(off) : "v"(acc[0]));
   return ld_stream(base + off);
 }
-// LDS read of element idx of base, issued only after the matrix-core op that produced `acc`
-// (so the scheduler cannot hoist it and keep its registers live across the loop)
-DGM_DEV U4 lds_after(const U4* base, int idx, v4f acc) {
-  asm("" : "+v"(idx) : "v"(acc[0]));
-  return base[idx];
-}
 DGM_DEV uint32_t ld_stream32(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
@@ -142,12 +136,6 @@ DGM_DEV v4f nvfp4_tile(U4 w, uint32_t sw, const U4 (&b)[4], v4f acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nvfp4_operand(w.z, s23.x), as_v8h(b[2]), acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(nvfp4_operand(w.w, s23.y), as_v8h(b[3]), acc, 0, 0, 0);
   return acc;
-}
-// 16 bytes per lane straight from global memory into LDS (GLOBAL_LOAD_LDS_DWORDX4, non-temporal):
-// lane l's bytes land at the wave-uniform LDS address `lds` + 16 l (pinned by a probe test).
-// Counted by vmcnt like any vector-memory load.
-DGM_DEV void load_to_lds16(const uint8_t* src, void* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 2);
 }
 DGM_DEV void st_agent32(void* p, uint32_t v) {
   __hip_atomic_store((uint32_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -213,10 +201,6 @@ struct FusedSmem {
   alignas(16) float4 qc[QX][ACT == DGM_ACT_QOQ ? KT2 : 1];
   // NVFP4: per local expert the L1 / L2 output scales (1 when not given)
   float gsl[2][ACT == DGM_ACT_NVFP4 ? FUSED_MAX_LOCAL : 1];
-  // L2: the second half of an item's weight tiles (per wave, K-tile, lane: 16 bytes), loaded
-  // into LDS while the item waits for its expert's L1 units (MXFP formats)
-  static constexpr bool L2PF = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8;
-  U4 l2pf[L2PF ? NW : 1][L2PF ? KT2 : 1][64];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
@@ -857,11 +841,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // L2 items span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks
   constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2, TI2 = RB2 * KT2;
   const int U1 = n_active * QN1, U2 = n_active * UPE2;
-  // This workgroup's first L2 unit: L2 unit v goes first to workgroup (U1 + v) mod G (and v + G
-  // second), so the L2 units start on the workgroups with the least L1 work (at small M those
-  // without an L1 unit, or with one less), which stream their L2 weights while the L1 units
-  // complete.
-  const int v0 = ((int)blockIdx.x - U1 % (int)gridDim.x + (int)gridDim.x) % (int)gridDim.x;
+  // This workgroup's first L2 unit (its second is G + v0)
+  const int v0 = (int)blockIdx.x;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
   int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
@@ -1379,7 +1360,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const int a = q0 / UPE2, b = q0 % UPE2;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const int key = (1 << 30) | (a << 16) | s0;
-      bool pfl = false;         // this item's second half of tiles is in LDS (s.l2pf)
       if (pre1) {               // (the first item, its slab loaded before the loop)
         pre1 = false;
         slab_store(s, pre);
@@ -1387,14 +1367,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         __syncthreads();
       } else if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
-        // (MXFP) the item's second half of tiles goes to LDS now and streams during the wait
-        // (the ring holds the first half); its K loop then reads them from there
-        if constexpr (Smem::L2PF && RB2 == 2) {
-          const uint8_t* cbp = tile_base(q0);
-#pragma unroll
-          for (int k = 0; k < KT2; ++k) load_to_lds16(cbp + (KT2 + k) * 1024, &s.l2pf[wv][k][0]);
-          pfl = true;
-        }
         if (a != ready) {
           if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err, p.host_err);
           ready = a;
@@ -1412,7 +1384,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           const int rb = r0 + s0;
           stage_slab<KT2, ACT, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
         }
-        if (pfl) wait_mem();      // (the prefetched tiles are in LDS)
         staged = key;
         __syncthreads();
       }
@@ -1547,14 +1518,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[j][i] *= gsc;
       } else {
-        // pfl: the second half of the tiles is in LDS (read two tiles ahead of their op), and
-        // the ring loads the next item's first half during the first half instead (afterwards
-        // it holds the next item's first KT2 tiles either way). One loop for both forms, the
-        // choice made per tile on the (uniform) flag.
-        constexpr bool PFC = Smem::L2PF && RB2 == 2;
-        const bool pfx = PFC && pfl;
         uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
-        U4 la[2] = {};
         static_for<TI2>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr int j = t / KT2, k = t % KT2;
@@ -1566,21 +1530,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             bq1 = bfrag((t + 2) % KT2);
             bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
           }
-          U4 aop = wr[k];
-          if constexpr (PFC && t >= KT2) aop = pfx ? la[t & 1] : wr[k];
-          // (tile t + 2's LDS operand, after the op before this one: two ops of lead; it takes
-          // the slot of tile t, read just above)
-          if constexpr (PFC && t + 2 >= KT2 && t + 2 < TI2) {
-            if (pfx) la[(t + 2) & 1] = lds_after(&s.l2pf[wv][0][0], (t + 2 - KT2) * 64 + lane, acc[t <= KT2 ? 0 : j]);
-          }
-          acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(aop), bop, acc[j],
+          acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
                                                                  (int)sd[j * KG2 + (k >> 2)], (int)bsw);
-          if constexpr (t + KT2 < TI2) {
-            const uint8_t* src = pfx ? nb + t * 1024 : cb + (t + KT2) * 1024;
-            wr[k] = ld_stream_after(src, 0, acc[j]);
-          } else {
-            if (!pfx) wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
-          }
+          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
         });
       }
       // all but this loop's KT2 youngest tile loads (and scale loads) are done: the previous
