@@ -203,6 +203,8 @@ struct FusedSmem {
   float gsl[2][ACT == DGM_ACT_NVFP4 ? FUSED_MAX_LOCAL : 1];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
+  // L1 half items (MXFP, 24 K-tiles): the K-half-1 waves' sums [2 gu + pair bit][lane][i]
+  float hk[(ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && KT1 == 24 ? 4 : 1][64][4];
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
   int is_last;
   int claimv[3];            // [0] the claim ahead, [1] prefetch decision, [2] L2: a complete expert
@@ -840,16 +842,29 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // wait.
   // L2 items span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks
   constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2, TI2 = RB2 * KT2;
-  const int U1 = n_active * QN1, U2 = n_active * UPE2;
+  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
+  // Half L1 units (MXFP with the K loop two ring periods long): 32 features, every 16-row block
+  // with its K split over two waves (sums added through LDS). When the whole units leave a
+  // last round that fills at most half the grid, its units are split in two: that round
+  // takes half as long. Items X1 .. are the halves: item X1 + 2 j + h = half h of unit X1 + j.
+  // Every whole unit sums the same two K-half chains (tiles 0 .. KR1 - 1, then the rest), so
+  // a split unit's result is bit-identical.
+  constexpr bool HALF1 = (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && KT1 == 2 * KR1;
+  const int U1w = n_active * QN1, U2 = n_active * UPE2;
+  const int R1 = U1w % (int)gridDim.x;
+  const int X1 = HALF1 && R1 > 0 && 2 * R1 <= (int)gridDim.x && !(p.debug & 4) ? U1w - R1 : U1w;
+  const int U1 = 2 * U1w - X1;          // L1 items
+  // (L1 arrivals are counted in 32-feature halves: a whole unit adds 2)
+  constexpr int L1_DONE = 2 * QN1;
   // This workgroup's first L2 unit (its second is G + v0)
   const int v0 = (int)blockIdx.x;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
   int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
+  int l1_pendw = 0;         // and its halves
   // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last
   // item rolls into the first L2 unit's tiles (unit v0), which then stream during the
   // L1 epilogue and the phase change instead of after it.
-  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
   constexpr int RING = KR1 > KT2 ? KR1 : KT2;
   constexpr bool HANDOFF = KR1 >= KT2;
   U4 wr[RING];
@@ -871,24 +886,37 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // complete in order and that loop waited for younger tiles); the unit's arrival is
   // signalled then.
   if (p.phases & 1) {
-    constexpr int KR = KT1 % 12 == 0 ? 12 : KT1;   // ring depth: tiles in flight per wave
+    constexpr int KR = KR1;      // ring depth: tiles in flight per wave
     static_assert(KT1 % KR == 0, "the ring depth divides the K-tile count");
-    const int pp = wv & 3, gu = wv >> 2;
     int* claim = p.counters + CNT_CLAIM;
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
     const float* w1r = p.w1r;
     const int topk = p.topk;
-    auto tile_base = [w1v, lane, pp, gu](int u) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
-      return w1v + blk * KT1 * 1024 + lane * 16;
+    // item i: its unit, and -1 (whole) or which half
+    auto unit_of = [X1](int i) __attribute__((always_inline)) { return i < X1 ? i : X1 + ((i - X1) >> 1); };
+    auto half_of = [X1](int i) __attribute__((always_inline)) { return i < X1 ? -1 : (i - X1) & 1; };
+    // This wave's 16-row weight block in item i, and its first K-tile: whole unit: block pair
+    // pp = w & 3, gate / up gu = w >> 2, full K; half h: pair 2 h + (w & 1), gu = (w >> 1) & 1,
+    // K half w >> 2.
+    auto wave_blk = [wv](int i, int u, int h) __attribute__((always_inline)) {
+      const int ppi = h < 0 ? (wv & 3) : 2 * h + (wv & 1);
+      const int gui = h < 0 ? (wv >> 2) : (wv >> 1) & 1;
+      return (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + ppi) + gui;
     };
-    // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block; QoQ:
-    // its meta dwords (4 per K-tile, spread over the lanes) and the s1 of the lane's 4 rows
+    auto tile_base = [w1v, lane, wv, unit_of, half_of, wave_blk](int i) __attribute__((always_inline)) {
+      const int u = unit_of(i), h = half_of(i);
+      const int kt0 = h < 0 ? 0 : (wv >> 2) * KR;
+      return w1v + (wave_blk(i, u, h) * KT1 + kt0) * 1024 + lane * 16;
+    };
+    // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block (a half
+    // item: of its K half, in sw[0 .. KG1 / 2)); QoQ: its meta dwords (4 per K-tile, spread over
+    // the lanes) and the s1 of the lane's 4 rows
     constexpr int MR1 = (4 * KT1 + 63) / 64;
     constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : ACT == DGM_ACT_NVFP4 ? 1 : KG1;
-    auto load_scales = [w1s, w1r, lane, pp, gu](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+    auto load_scales = [w1s, w1r, lane, wv, unit_of, half_of, wave_blk](int i, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
+      const int u = unit_of(i), h = half_of(i);
+      const size_t blk = wave_blk(i, u, h);
       if constexpr (ACT == DGM_ACT_QOQ) {
         const uint32_t* mb = w1s + blk * KT1 * 4;
 #pragma unroll
@@ -902,15 +930,20 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if constexpr (ACT == DGM_ACT_NVFP4) {
         sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
+        // (a half item runs as the K loop's second period: K half 0 gets the block's dwords
+        // rotated by half, so that its own are in sw[KG1 / 2 ..]; every element is written, so
+        // the array stays in registers)
+        const int off = HALF1 && h >= 0 ? (1 - (wv >> 2)) * (KG1 / 2) : 0;
 #pragma unroll
-        for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
+        for (int g = 0; g < KG1; ++g)
+          sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + (g < KG1 / 2 ? g + off : g - off)) * 64 + lane);
       }
     };
     // NVFP4: the lane's scale dword of each tile (128 B of E4M3 scales per 16 x 128 tile), in a
     // ring beside the tile ring
     const int slane = (((lane >> 5) << 4) | (lane & 15)) * 4;
-    auto stile_base = [w1s, slane, pp, gu](int u) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+    auto stile_base = [w1s, slane, wv](int u) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + (wv & 3)) + (wv >> 2);
       return reinterpret_cast<const uint8_t*>(w1s) + blk * KT1 * 128 + slane;
     };
     const uint8_t* xv = p.x;
@@ -929,20 +962,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
     // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
-    int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
+    int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current item
+    int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next item
     int s0 = 0;
     uint32_t sd[SW1], sn[SW1];
     SlabRegs<KT1, ACT, FEIN, false> pre;
-    int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
+    int pend = -1;            // expert slot of a finished item whose arrival is not signalled yet
+    int pendw = 0;            // and its halves (2: a whole unit)
     if (q0 < U1) {
       // The first item's slab is staged before any tile load is issued: every workgroup
       // starts at once, and tile loads issued first would queue the slab loads (and so the
       // barrier, and every wave's first K loop) behind the whole ring of every wave.
-      load_slab(pre, q0 / QN1, 0);
+      load_slab(pre, unit_of(q0) / QN1, 0);
       load_scales(q0, sd);
       slab_store(s, pre);
-      staged = (q0 / QN1) << 16;
+      staged = (unit_of(q0) / QN1) << 16;
       __syncthreads();
       const uint8_t* b = tile_base(q0);
 #pragma unroll
@@ -953,14 +987,37 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
       }
     }
+    // B operands (the staged slab's fragments) are read from LDS two K-tiles ahead of their
+    // matrix-core op. An item's first two, and its first B scale dword, are read at the end of
+    // the previous item's epilogue, before its stores: read at the loop's top, they could land
+    // in registers of those stores and wait for them (and so for the whole ring).
+    auto bfrag = [lane](int t) __attribute__((always_inline)) {
+      return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
+    };
+    auto first_k = [wv, half_of](int i) __attribute__((always_inline)) {   // a wave's first K-tile in item i
+      return HALF1 && half_of(i) >= 0 ? (wv >> 2) * KR : 0;
+    };
+    v8i bq0 = {}, bq1 = {};
+    uint32_t bs0 = 0;
+    if (q0 < U1) {
+      const int k = first_k(q0);
+      bq0 = bfrag(k);
+      bq1 = KT1 > 1 ? bfrag(k + 1) : bq0;
+      bs0 = s.bsc[k >> 2][lane];
+    }
     bool more = 2 * G < U1;   // the claim counter has not run out
     while (q0 < U1) {
-      const int a = q0 / QN1, q = q0 % QN1;
+      const int u0 = HALF1 ? unit_of(q0) : q0, h0 = HALF1 ? half_of(q0) : -1;
+      const int a = u0 / QN1, q = u0 % QN1;
+      // this wave's block in the item: pair pp, gate (gu 0) or up (gu 1), K half kh
+      const int pp = h0 < 0 ? (wv & 3) : 2 * h0 + (wv & 1);
+      const int gu = h0 < 0 ? (wv >> 2) : (wv >> 1) & 1;
+      const int kh = HALF1 && h0 >= 0 ? wv >> 2 : 0;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
       const bool has_next = nq < U1;
-      const int na = has_next ? nq / QN1 : -1;
+      const int na = has_next ? unit_of(nq) / QN1 : -1;
       const int nkey = (na << 16) | ns0;
       const bool restage = has_next && nkey != staged;
       const uint8_t* cb = tile_base(q0);
@@ -993,11 +1050,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      // B operands are read from LDS two K-tiles ahead of their matrix-core op
-      auto bfrag = [lane](int t) __attribute__((always_inline)) {
-        return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
-      };
-      v8i bq0 = bfrag(0), bq1 = KT1 > 1 ? bfrag(1) : bq0;
+      const int kb0 = kh * KR;                    // the wave's first K-tile (a half item's K half)
       if constexpr (ACT == DGM_ACT_QOQ) {
         // per K-tile: two int8 ops on the raw 4-bit codes (exact int32 sums of code * x), then,
         // one tile later (off the matrix-core result's latency), the zero-point correction
@@ -1079,22 +1132,39 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           }
         });
       } else {
-        uint32_t bs = s.bsc[0][lane];
+        // Ring periods of KR ops. A whole unit runs both (HALF1: period 0 into acc, period 1 into
+        // acc2, summed after the loop, as a half unit's two waves sum them); a half item runs
+        // period 1 only, over its K half: B operands from K-tile kd + t, A scale dwords loaded
+        // rotated into the period's registers. Either way the last period's slots take the next
+        // item's tiles.
+        const bool hf = HALF1 && h0 >= 0;
+        const int kd = kb0 - (hf ? KR : 0);
+        v4f acc2 = {0.f, 0.f, 0.f, 0.f};
+        uint32_t bs = bs0;
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
-          const v8i bop = bq0;
-          const uint32_t bsw = bs;
-          bq0 = bq1;
-          if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
-          if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
-          acc = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, acc, (int)sd[t >> 2], (int)bsw);
-          if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, acc);
-          else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, acc);
-          if constexpr (t == KT1 - KR) {
-            if (has_next && nq != q0) load_scales(nq, sn);
-            if (restage) load_slab(pre, na, ns0);
+          constexpr int pd = t / KR, tr = t % KR;
+          if (pd > 0 || !hf) {
+            constexpr bool HI = HALF1 && pd > 0;
+            const v8i bop = bq0;
+            const uint32_t bsw = bs;
+            bq0 = bq1;
+            if constexpr (t + 2 < KT1) bq1 = bfrag(kd + t + 2);
+            if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(kd + t + 1) >> 2][lane];
+            v4f& ac = HI ? acc2 : acc;
+            ac = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[tr]), bop, ac, (int)sd[t >> 2], (int)bsw);
+            if constexpr (t + KR < KT1) wr[tr] = ld_stream_after(cb, (t + KR) * 1024, ac);
+            else wr[tr] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, ac);
+            if constexpr (t == KT1 - KR) {
+              if (has_next && nq != q0) load_scales(nq, sn);
+              if (restage) load_slab(pre, na, ns0);
+            }
           }
         });
+        if constexpr (HALF1) {
+          if (hf) acc = acc2;
+          else acc += acc2;
+        }
       }
       // all but this loop's KR youngest tile loads (and scale loads) are done: the previous
       // item's stores too
@@ -1106,15 +1176,19 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= gsc;
       }
-      if (gu == 1) {
+      if (HALF1 && kh == 1) {      // (half item) K-half-1 sums, added by the K-half-0 gate waves
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s.hk[wv & 3][lane][i] = acc[i];
+      } else if (gu == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
       }
+      const bool egate = gu == 0 && kh == 0;     // this wave runs the epilogue of pair pp
       // the unit after q1 (claimed at this item's start), broadcast here
       const bool bcast = last_slab && q1 < U1;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) up sums visible, slab free
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pend = -1;
       int q2 = U1;
       if (bcast) {
@@ -1129,13 +1203,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const bool valid = s0 + c < n;
       const int pr = 4 * q + pp;                         // 16-feature block of this pair
       float act[4];
-      if (gu == 0) {
+      if (egate) {
         float am = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+          // (half item: K half 0 + K half 1, the whole unit's sum)
+          const float ga = HALF1 && h0 >= 0 ? acc[i] + s.hk[wv & 1][lane][i] : acc[i];
+          const float uv = HALF1 && h0 >= 0 ? s.upv[pp][lane][i] + s.hk[2 + (wv & 1)][lane][i] : s.upv[pp][lane][i];
           // MXFP: gate / up rounded to bf16 (the reference's L1 output); QoQ: fp32
-          const float g = fminf(ACT == DGM_ACT_QOQ ? acc[i] : round_bf16(acc[i]), p.clamp);
-          const float uv = s.upv[pp][lane][i];
+          const float g = fminf(ACT == DGM_ACT_QOQ ? ga : round_bf16(ga), p.clamp);
           const float uu = fminf(fmaxf(ACT == DGM_ACT_QOQ ? uv : round_bf16(uv), -p.clamp), p.clamp);
           const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
           act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
@@ -1146,7 +1222,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         if (lane < 16) s.amax[pp][lane] = am;
       }
       __syncthreads();                                   // (2) amax visible, next slab staged
-      if (gu == 0) {
+      if (has_next) {
+        const int k = first_k(nq);
+        bq0 = bfrag(k);
+        bq1 = KT1 > 1 ? bfrag(k + 1) : bq0;
+        bs0 = s.bsc[k >> 2][lane];
+      }
+      if (egate) {
         // requant group: QoQ 64 features (the unit), NVFP4 16 (this pair), MXFP 32 (two pairs)
         const float am = ACT == DGM_ACT_QOQ     ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
                          : ACT == DGM_ACT_NVFP4 ? s.amax[pp][c]
@@ -1216,6 +1298,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (st) l1_sig_ticks += wall_clock() - t_e0;
       if (last_slab) {
         pend = a;
+        pendw = h0 < 0 ? 2 : 1;
         if (nq != q0) {
 #pragma unroll
           for (int g = 0; g < SW1; ++g) sd[g] = sn[g];
@@ -1229,10 +1312,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
     if (p.phases & 2) {
       l1_pend = pend;         // (its stores complete while the L2 phase issues its first loads)
+      l1_pendw = pendw;
     } else {
       wait_mem();             // the last item's stores (and the dummy ring reads)
       __syncthreads();
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (st && tid == 0) st[2] = wall_clock();
@@ -1327,14 +1411,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       // the L1 phase's last unit: its stores have completed (every wave) -> its arrival, before
       // any wait on other workgroups' arrivals
       wait_mem();
-      if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= QN1 ? 1 : 0;
+      if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= L1_DONE ? 1 : 0;
       __syncthreads();
-      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid == 0 && q0 < U2 && pr_a >= QN1) ready = q0 / UPE2;
+      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], l1_pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && q0 < U2 && pr_a >= L1_DONE) ready = q0 / UPE2;
     }
     // (thread 0) the second unit's expert when its probe found it complete (LDS: read once, by
     // the first item's prefetch check)
-    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= QN1 ? q1 / UPE2 : -1;
+    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= L1_DONE ? q1 / UPE2 : -1;
     if (q0 < U2) {
       if (!handed) {          // (unit q0 = v0: handed over by the L1 phase otherwise)
         const uint8_t* b = tile_base(q0);
@@ -1368,7 +1452,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
         if (a != ready) {
-          if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err, p.host_err);
+          if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], L1_DONE, p.spin_limit, err, p.host_err);
           ready = a;
         }
         __syncthreads();
@@ -1397,7 +1481,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (has_next && nkey != key) {
         if (tid == 0)
           s.claimv[1] = !(p.phases & 1) || na == ready || na == s.claimv[2] ||
-                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
+                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= L1_DONE;
         __syncthreads();
         pf = __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0;
         if (pf) {

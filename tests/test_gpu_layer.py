@@ -181,6 +181,37 @@ def test_split_matches_fused(fmt):
     np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
 
 
+@pytest.mark.parametrize("fmt,M,topk", [("mxfp4", 2, 8), ("mxfp8", 2, 8), ("mxfp4", 1, 4)])
+def test_half_l1_units_match_whole_units_and_split(fmt, M, topk):
+    """A last, partial round of L1 units split into half units (32 features, each weight
+    block's K halves on two waves, summed through LDS). Forced-balanced routing over 48
+    experts leaves 16 (M=2, top-8) or 4 (M=1, top-4) active experts: 320 or 80 units of 64
+    features for 256 workgroups, so 64 or all 80 units run as halves. The result equals the
+    whole-unit schedule (debug bit 2) and the split API bit for bit, and the oracle to
+    tolerance."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    weights = make_weights(48, 3072, 1280, 611)
+    r = run_layer(M, 48, 48, 0, 3072, 1280, topk, fmt, seed=610 + M, force_balanced=True, weights=weights)
+    print(fmt, M, topk, check_y(r), flush=True)
+    b = r["buf"]
+    n_active = int((b.pool_table()[0] > 0).sum())
+    G = dgm.mega.fused_workgroups(b)
+    units = n_active * (1280 // 64)
+    assert units % G > 0 and 2 * (units % G) <= G, (n_active, G)     # (half units in this shape)
+    (t1, t2), _, _ = weights
+    for dbg, layer in ((4, dgm.mxfp4_mega_moe_fused), (0, dgm.mxfp4_mega_moe_split)):
+        b._debug_flags = dbg
+        try:
+            y2 = torch.empty((M, 3072), dtype=torch.bfloat16, device="cuda")
+            layer(y2, t1, t2, b, activation_clamp=10.0)
+            torch.cuda.synchronize()
+        finally:
+            b._debug_flags = 0
+        np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
+    assert b.kernel_error() == 0
+
+
 @pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8"])
 def test_select_in_mega(fmt):
     """Top-k selected in the fused kernel's prologue (frontend with select_in_mega): the same
