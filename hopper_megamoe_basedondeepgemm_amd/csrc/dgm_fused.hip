@@ -856,7 +856,17 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int U1 = 2 * U1w - X1;          // L1 items
   // (L1 arrivals are counted in 32-feature halves: a whole unit adds 2)
   constexpr int L1_DONE = 2 * QN1;
-  // This workgroup's first L2 unit (its second is G + v0)
+  // Half L2 units (MXFP): one 128-row combine block, every wave one 16-row block. As in L1, a
+  // last round that fills at most half the grid runs as halves; items X2 .. are the halves.
+  // (Splitting a full last round as well measured slower: the extra items cost more than the
+  // shorter tail saves.)
+  constexpr bool HALF2 = (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && RB2 == 2;
+  const int R2 = U2 % (int)gridDim.x;
+  const int X2 = HALF2 && R2 > 0 && 2 * R2 <= (int)gridDim.x && !(p.debug & 4) ? U2 - R2 : U2;
+  const int N2 = 2 * U2 - X2;           // L2 items
+  auto l2_unit = [X2](int i) __attribute__((always_inline)) { return HALF2 && i >= X2 ? X2 + ((i - X2) >> 1) : i; };
+  auto l2_half = [X2](int i) __attribute__((always_inline)) { return HALF2 && i >= X2 ? (i - X2) & 1 : -1; };
+  // This workgroup's first L2 item (its second is G + v0)
   const int v0 = (int)blockIdx.x;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
@@ -870,9 +880,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   U4 wr[RING];
   uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
-  // L2 unit v = (active expert a, 128 RB2-row slice b): this wave's first 16-row block of it
-  auto l2_blk = [wv](int v) __attribute__((always_inline)) {
-    return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
+  // L2 item i: unit (active expert a, 128 RB2-row slice b), whole or half hb; this wave's
+  // first 16-row block of it
+  auto l2_blk = [wv, l2_unit, l2_half](int i) __attribute__((always_inline)) {
+    const int u = l2_unit(i), h = l2_half(i);
+    return (size_t)s.act[u / UPE2] * NB2 + (NW * RB2) * (u % UPE2) + (h < 0 ? RB2 * wv : NW * h + wv);
   };
 
   // ================================================================ L1 phase
@@ -1023,7 +1035,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const uint8_t* cb = tile_base(q0);
       // no next L1 item: ring slots < KT2 take the first L2 unit's tiles (when that unit is
       // this workgroup's), the rest dummy reads
-      const bool hand = HANDOFF && !has_next && (p.phases & 2) && v0 < U2;
+      const bool hand = HANDOFF && !has_next && (p.phases & 2) && v0 < N2;
       const uint8_t* dummy = w1v + lane * 16;
       const uint8_t* nb = !has_next ? (hand ? p.w2v + l2_blk(v0) * KT2 * 1024 + lane * 16 : dummy)
                                     : nq == q0 ? cb : tile_base(nq);
@@ -1345,7 +1357,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // ahead: MXFP: E8M0 scale dwords; QoQ: meta dwords (4 per K-tile)
     constexpr int MR2 = (4 * TI2 + 63) / 64;
     constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : ACT == DGM_ACT_NVFP4 ? 1 : RB2 * KG2;
-    auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
+    auto load_scales = [w2s, lane, blk_of, l2_half](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
       if constexpr (ACT == DGM_ACT_QOQ) {
         const uint32_t* mb = w2s + blk_of(v) * KT2 * 4;
 #pragma unroll
@@ -1354,9 +1366,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if constexpr (ACT == DGM_ACT_NVFP4) {
         sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
+        // (a half item: its one block's dwords twice; every element is written, so the array
+        // stays in registers)
         const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
+        const bool h = HALF2 && l2_half(v) >= 0;
 #pragma unroll
-        for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
+        for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + (h ? g % KG2 : g) * 64);
       }
     };
     // NVFP4: the lane's scale dword of each tile, in a ring beside the tile ring
@@ -1371,17 +1386,19 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       slab_load<KT2, ACT, true, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
                                 [](int) { return 0.f; });
     };
-    // arrivals of item (unit v, slab s0): its routes' outputs for the unit's blocks are complete
-    auto arrive = [comb, tid, topk](int v, int s0) __attribute__((always_inline)) {
+    // arrivals of item (v, slab s0): its routes' outputs for the item's combine blocks (RB2, or
+    // the half's one) are complete
+    auto arrive = [comb, tid, topk, l2_unit, l2_half](int v, int s0) __attribute__((always_inline)) {
       // (topk and the thread index made opaque: what derives from them is computed here, not
       // kept live across the work loop, where it would cost registers or a spill)
       int tk = topk, i0 = tid;
       asm volatile("" : "+s"(tk), "+v"(i0));
-      const int a = v / UPE2, b = v % UPE2;
+      const int u = l2_unit(v), h = l2_half(v);
+      const int a = u / UPE2, nbk = h < 0 ? RB2 : 1, cb0 = RB2 * (u % UPE2) + (h < 0 ? 0 : h);
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
-      for (int i = i0; i < 16 * RB2 && i / RB2 < n; i += FT)
-        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / RB2] < 0)   // (a token's only local route writes y itself)
-          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2) * CNT_LINE], 1,
+      for (int i = i0; i < 16 * nbk && i / nbk < n; i += FT)
+        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / nbk] < 0)   // (a token's only local route writes y itself)
+          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / nbk] / tk) * NBL2 + cb0 + i % nbk) * CNT_LINE], 1,
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units v0 and G + v0 first, then claims (offset by 2 G)
@@ -1390,9 +1407,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
     // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    bool more = 2 * G < U2;   // the claim counter has not run out
-    int q0 = v0 < U2 ? v0 : U2;
-    int q1 = G + v0 < U2 ? G + v0 : U2;
+    bool more = 2 * G < N2;   // the claim counter has not run out
+    int q0 = v0 < N2 ? v0 : N2;
+    int q1 = G + v0 < N2 ? G + v0 : N2;
     int s0 = 0;
     static_assert(KT2 <= RING, "the L2 ring in the shared tile registers");
     uint32_t sd[SW2], sn[SW2];
@@ -1404,22 +1421,22 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     if (p.phases & 1) {
       // probes of the L1 arrivals of the first two units' experts, answered while the L1
       // phase's last stores complete
-      if (tid == 0 && q0 < U2) {
-        pr_a = __hip_atomic_load(&l1_done[(q0 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (q1 < U2) pr_n = __hip_atomic_load(&l1_done[(q1 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && q0 < N2) {
+        pr_a = __hip_atomic_load(&l1_done[(l2_unit(q0) / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q1 < N2) pr_n = __hip_atomic_load(&l1_done[(l2_unit(q1) / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       // the L1 phase's last unit: its stores have completed (every wave) -> its arrival, before
       // any wait on other workgroups' arrivals
       wait_mem();
-      if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= L1_DONE ? 1 : 0;
+      if (tid == 0) s.claimv[1] = q0 < N2 && pr_a >= L1_DONE ? 1 : 0;
       __syncthreads();
       if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], l1_pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid == 0 && q0 < U2 && pr_a >= L1_DONE) ready = q0 / UPE2;
+      if (tid == 0 && q0 < N2 && pr_a >= L1_DONE) ready = l2_unit(q0) / UPE2;
     }
     // (thread 0) the second unit's expert when its probe found it complete (LDS: read once, by
     // the first item's prefetch check)
-    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= L1_DONE ? q1 / UPE2 : -1;
-    if (q0 < U2) {
+    if (tid == 0) s.claimv[2] = q1 < N2 && pr_n >= L1_DONE ? l2_unit(q1) / UPE2 : -1;
+    if (q0 < N2) {
       if (!handed) {          // (unit q0 = v0: handed over by the L1 phase otherwise)
         const uint8_t* b = tile_base(q0);
 #pragma unroll
@@ -1436,12 +1453,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // at the item's start; its loads complete while the tiles and scales above are in flight).
     // (NVFP4 stages it at the item's start: measured no faster this way.)
     bool pre1 = false;
-    if (ACT != DGM_ACT_NVFP4 && q0 < U2 && (!(p.phases & 1) || __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0)) {
-      load_slab(pre, q0 / UPE2, 0);
+    if (ACT != DGM_ACT_NVFP4 && q0 < N2 && (!(p.phases & 1) || __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0)) {
+      load_slab(pre, l2_unit(q0) / UPE2, 0);
       pre1 = true;
     }
-    while (q0 < U2) {
-      const int a = q0 / UPE2, b = q0 % UPE2;
+    while (q0 < N2) {
+      const int a = l2_unit(q0) / UPE2, b = l2_unit(q0) % UPE2;
+      const int hb = l2_half(q0);
+      const bool hf = HALF2 && hb >= 0;       // a half item: block hb of the unit, as the K loop's second period
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const int key = (1 << 30) | (a << 16) | s0;
       if (pre1) {               // (the first item, its slab loaded before the loop)
@@ -1473,8 +1492,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
-      const bool has_next = nq < U2;
-      const int na = has_next ? nq / UPE2 : -1;
+      const bool has_next = nq < N2;
+      const int na = has_next ? l2_unit(nq) / UPE2 : -1;
       const int nkey = (1 << 30) | (na << 16) | ns0;
       // prefetch the next item's slab if it differs and its expert's L1 is complete
       bool pf = false;
@@ -1505,7 +1524,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       // the unit after q1, claimed at the start of the item that finishes q0 (the value is read
       // in this item's epilogue)
-      if (tid == 0 && last_slab && q1 < U2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && last_slab && q1 < N2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
       // read from LDS two ops ahead
       v4f acc[RB2];
@@ -1602,22 +1621,28 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[j][i] *= gsc;
       } else {
+        // (a half item runs the first block's ops only, their slots then taking the next item's
+        // tiles; its scale dwords are in every block's registers)
+        const uint8_t* ra = hf ? nb : cb + KT2 * 1024;
         uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
         static_for<TI2>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr int j = t / KT2, k = t % KT2;
-          const v8i bop = bq0;
-          const uint32_t bsw = bs0;
-          bq0 = bq1;
-          bs0 = bs1;
-          if constexpr (t + 2 < TI2) {
-            bq1 = bfrag((t + 2) % KT2);
-            bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
+          if (j == 0 || !hf) {
+            const v8i bop = bq0;
+            const uint32_t bsw = bs0;
+            bq0 = bq1;
+            bs0 = bs1;
+            if constexpr (t + 2 < TI2) {
+              bq1 = bfrag((t + 2) % KT2);
+              bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
+            }
+            acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
+                                                                   (int)sd[j * KG2 + (k >> 2)], (int)bsw);
+            if constexpr (HALF2 && j == 0) wr[k] = ld_stream_after(ra, k * 1024, acc[j]);
+            else if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+            else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
           }
-          acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
-                                                                 (int)sd[j * KG2 + (k >> 2)], (int)bsw);
-          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
-          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
         });
       }
       // all but this loop's KT2 youngest tile loads (and scale loads) are done: the previous
@@ -1625,34 +1650,38 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       wait_vm_le<ACT == DGM_ACT_NVFP4 ? 2 * KT2 : KT2>();
       if (s0 + c < n) {
         // each route's output rounded to bf16 (the reference's per-route rule), stored slot-major
-        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+        // (the wave's 16-row blocks: whole item RB2 from NW RB2 b + RB2 w, half item one)
+        const int rb16 = hf ? NW * RB2 * b + NW * hb + wv : NW * RB2 * b + RB2 * wv;
+        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + rb16 * 16 + 4 * kq;
 #pragma unroll
         for (int j = 0; j < RB2; ++j)
-          st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
-                                       ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
+          if (j == 0 || !hf)
+            st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
+                                                    ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
         // a token with no other local route: its y rows are this route's output (the combine of
         // one bf16 route output), written here; no arrival, no combine
         const int yt = ACT == DGM_ACT_NVFP4 ? -1 : s.ytok[r0 + s0 + c];
         if (yt >= 0) {
-          uint16_t* yd = p.y + (size_t)yt * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+          uint16_t* yd = p.y + (size_t)yt * H + rb16 * 16 + 4 * kq;
 #pragma unroll
           for (int j = 0; j < RB2; ++j)
-            *reinterpret_cast<uint64_t*>(yd + 16 * j) =
-                (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
-                ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48);
+            if (j == 0 || !hf)
+              *reinterpret_cast<uint64_t*>(yd + 16 * j) =
+                  (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
+                  ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48);
         }
       }
-      const bool bcast = last_slab && q1 < U2;
+      const bool bcast = last_slab && q1 < N2;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) previous outputs complete, slab free
       if (pv >= 0) arrive(pv, ps0);
       pv = q0;
       ps0 = s0;
-      int q2 = U2;
+      int q2 = N2;
       if (bcast) {
         const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        q2 = raw >= 0 && 2 * G + raw < U2 ? 2 * G + raw : U2;
-        if (q2 >= U2) more = false;
+        q2 = raw >= 0 && 2 * G + raw < N2 ? 2 * G + raw : N2;
+        if (q2 >= N2) more = false;
       }
       if (pf) {
         slab_store(s, pre);
