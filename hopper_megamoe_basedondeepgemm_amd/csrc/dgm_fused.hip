@@ -1770,13 +1770,23 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[5] = wall_clock();
 }
 
-// per (shape slot, format, FEIN): the resident grid; per (shape slot, format): the last launch's
+// per device, per (shape slot, format, FEIN): the resident grid; per (shape slot, format): the
+// last launch's (the grid is what the device keeps resident at once, so it depends on the
+// device's CU count)
+constexpr int GRID_DEVICES = 64;
 struct GridCache { int blocks[3][4][2] = {}; int last[3][4] = {}; };
-GridCache g_grid;
+GridCache g_grid[GRID_DEVICES];
+
+GridCache& grid_cache() {
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  return g_grid[dev >= 0 && dev < GRID_DEVICES ? dev : 0];
+}
 
 template <int KT1, int KT2, int ACT, bool FEIN>
 int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
-  int& nb = g_grid.blocks[slot][ACT][FEIN ? 1 : 0];
+  GridCache& gc = grid_cache();
+  int& nb = gc.blocks[slot][ACT][FEIN ? 1 : 0];
   if (nb == 0) {
     int per_cu = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT, FEIN>, FT, 0);
@@ -1786,7 +1796,7 @@ int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     nb = per_cu * (cus > 0 ? cus : 256);
   }
-  g_grid.last[slot][ACT] = nb;
+  gc.last[slot][ACT] = nb;
   hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FEIN>), dim3(nb), dim3(FT), 0, stream, prm);
   return dgm_last_launch_status();
 }
@@ -1801,7 +1811,7 @@ int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream) {
 
 int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format) {
   int slot = hidden == 3072 ? 0 : (hidden == 512 ? 1 : 2);
-  return g_grid.last[slot][act_format];
+  return grid_cache().last[slot][act_format];
 }
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream) {
