@@ -1707,23 +1707,23 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[4] = wall_clock();
 
   // ================================================================ combine
-  // (token t, 128-row block b) pairs, PG consecutive pairs per pass and workgroup, two rows per
-  // thread: wait until every local route of t has delivered block b, then sum the routes' bf16
-  // outputs in slot order (fp32) -> bf16 y. The waits are only on L2 items, which never wait on
-  // this phase.
+  // (token t, 128-row block b) pairs, one per wave, two rows per lane, spread over the grid
+  // (pair i on wave i / G of workgroup i % G): the wave's lane 0 waits until every local route
+  // of t has delivered block b, then the wave sums the routes' bf16 outputs in slot order (fp32)
+  // -> bf16 y. No wave waits for another's pair (measured: 1-1.5 us less at M=2-4 than eight
+  // consecutive pairs per workgroup behind one barrier). The waits are only on L2 items, which
+  // never wait on this phase.
   if (p.phases & 2) {
     constexpr int DIRECT_Y = ACT == DGM_ACT_NVFP4 ? 0 : 1;   // routes per token that need no combine
-    constexpr int BR = 16 * NW, CB = BR / 2, PG = FT / CB;
+    constexpr int BR = 16 * NW;
+    static_assert(BR == 2 * 64, "a wave's lanes cover a block, two rows each");
     const int P = p.M * NBL2;
-    for (int i0 = blockIdx.x * PG; i0 < P; i0 += gridDim.x * PG) {
-      if (tid < PG && i0 + tid < P) {
-        const int need = s.nslot[(i0 + tid) / NBL2];
-        if (need > DIRECT_Y) spin_until2(&comb[(i0 + tid) * CNT_LINE], need, p.spin_limit, err, p.host_err);
-      }
-      __syncthreads();
-      const int i = i0 + tid / CB;
-      if (i < P) {
-        const int t = i / NBL2, row = (i % NBL2) * BR + 2 * (tid % CB);
+    for (int i = (int)blockIdx.x + wv * (int)gridDim.x; i < P; i += (int)gridDim.x * NW) {
+      {
+        const int need = s.nslot[i / NBL2];
+        if (need > DIRECT_Y && lane == 0) spin_until2(&comb[i * CNT_LINE], need, p.spin_limit, err, p.host_err);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);    // (the partial loads below come after the wait)
+        const int t = i / NBL2, row = (i % NBL2) * BR + 2 * lane;
         // (y rows of tokens without a local route: zeroed by workgroup 0; with one: written by its
         // L2 unit, except NVFP4's)
         if (s.nslot[t] > DIRECT_Y) {
