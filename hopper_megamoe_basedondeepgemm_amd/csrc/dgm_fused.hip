@@ -203,8 +203,6 @@ struct FusedSmem {
   float gsl[2][ACT == DGM_ACT_NVFP4 ? FUSED_MAX_LOCAL : 1];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
-  // L1 half items (MXFP, 24 K-tiles): the K-half-1 waves' sums [2 gu + pair bit][lane][i]
-  float hk[(ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && KT1 == 24 ? 4 : 1][64][4];
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
   int is_last;
   int claimv[3];            // [0] the claim ahead, [1] prefetch decision, [2] L2: a complete expert
@@ -842,49 +840,24 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // wait.
   // L2 items span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks
   constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2, TI2 = RB2 * KT2;
-  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
-  // Half L1 units (MXFP with the K loop two ring periods long): 32 features, every 16-row block
-  // with its K split over two waves (sums added through LDS). When the whole units leave a
-  // last round that fills at most half the grid, its units are split in two: that round
-  // takes half as long. Items X1 .. are the halves: item X1 + 2 j + h = half h of unit X1 + j.
-  // Every whole unit sums the same two K-half chains (tiles 0 .. KR1 - 1, then the rest), so
-  // a split unit's result is bit-identical.
-  constexpr bool HALF1 = (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && KT1 == 2 * KR1;
-  const int U1w = n_active * QN1, U2 = n_active * UPE2;
-  const int R1 = U1w % (int)gridDim.x;
-  const int X1 = HALF1 && R1 > 0 && 2 * R1 <= (int)gridDim.x && !(p.debug & 4) ? U1w - R1 : U1w;
-  const int U1 = 2 * U1w - X1;          // L1 items
-  // (L1 arrivals are counted in 32-feature halves: a whole unit adds 2)
-  constexpr int L1_DONE = 2 * QN1;
-  // Half L2 units (MXFP): one 128-row combine block, every wave one 16-row block. As in L1, a
-  // last round that fills at most half the grid runs as halves; items X2 .. are the halves.
-  // (Splitting a full last round as well measured slower: the extra items cost more than the
-  // shorter tail saves.)
-  constexpr bool HALF2 = (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && RB2 == 2;
-  const int R2 = U2 % (int)gridDim.x;
-  const int X2 = HALF2 && R2 > 0 && 2 * R2 <= (int)gridDim.x && !(p.debug & 4) ? U2 - R2 : U2;
-  const int N2 = 2 * U2 - X2;           // L2 items
-  auto l2_unit = [X2](int i) __attribute__((always_inline)) { return HALF2 && i >= X2 ? X2 + ((i - X2) >> 1) : i; };
-  auto l2_half = [X2](int i) __attribute__((always_inline)) { return HALF2 && i >= X2 ? (i - X2) & 1 : -1; };
-  // This workgroup's first L2 item (its second is G + v0)
+  const int U1 = n_active * QN1, U2 = n_active * UPE2;
+  // This workgroup's first L2 unit (its second is G + v0)
   const int v0 = (int)blockIdx.x;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
   int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
-  int l1_pendw = 0;         // and its halves
   // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last
   // item rolls into the first L2 unit's tiles (unit v0), which then stream during the
   // L1 epilogue and the phase change instead of after it.
+  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
   constexpr int RING = KR1 > KT2 ? KR1 : KT2;
   constexpr bool HANDOFF = KR1 >= KT2;
   U4 wr[RING];
   uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
-  // L2 item i: unit (active expert a, 128 RB2-row slice b), whole or half hb; this wave's
-  // first 16-row block of it
-  auto l2_blk = [wv, l2_unit, l2_half](int i) __attribute__((always_inline)) {
-    const int u = l2_unit(i), h = l2_half(i);
-    return (size_t)s.act[u / UPE2] * NB2 + (NW * RB2) * (u % UPE2) + (h < 0 ? RB2 * wv : NW * h + wv);
+  // L2 unit v = (active expert a, 128 RB2-row slice b): this wave's first 16-row block of it
+  auto l2_blk = [wv](int v) __attribute__((always_inline)) {
+    return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
   };
 
   // ================================================================ L1 phase
@@ -898,37 +871,24 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // complete in order and that loop waited for younger tiles); the unit's arrival is
   // signalled then.
   if (p.phases & 1) {
-    constexpr int KR = KR1;      // ring depth: tiles in flight per wave
+    constexpr int KR = KT1 % 12 == 0 ? 12 : KT1;   // ring depth: tiles in flight per wave
     static_assert(KT1 % KR == 0, "the ring depth divides the K-tile count");
+    const int pp = wv & 3, gu = wv >> 2;
     int* claim = p.counters + CNT_CLAIM;
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
     const float* w1r = p.w1r;
     const int topk = p.topk;
-    // item i: its unit, and -1 (whole) or which half
-    auto unit_of = [X1](int i) __attribute__((always_inline)) { return i < X1 ? i : X1 + ((i - X1) >> 1); };
-    auto half_of = [X1](int i) __attribute__((always_inline)) { return i < X1 ? -1 : (i - X1) & 1; };
-    // This wave's 16-row weight block in item i, and its first K-tile: whole unit: block pair
-    // pp = w & 3, gate / up gu = w >> 2, full K; half h: pair 2 h + (w & 1), gu = (w >> 1) & 1,
-    // K half w >> 2.
-    auto wave_blk = [wv](int i, int u, int h) __attribute__((always_inline)) {
-      const int ppi = h < 0 ? (wv & 3) : 2 * h + (wv & 1);
-      const int gui = h < 0 ? (wv >> 2) : (wv >> 1) & 1;
-      return (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + ppi) + gui;
+    auto tile_base = [w1v, lane, pp, gu](int u) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
+      return w1v + blk * KT1 * 1024 + lane * 16;
     };
-    auto tile_base = [w1v, lane, wv, unit_of, half_of, wave_blk](int i) __attribute__((always_inline)) {
-      const int u = unit_of(i), h = half_of(i);
-      const int kt0 = h < 0 ? 0 : (wv >> 2) * KR;
-      return w1v + (wave_blk(i, u, h) * KT1 + kt0) * 1024 + lane * 16;
-    };
-    // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block (a half
-    // item: of its K half, in sw[0 .. KG1 / 2)); QoQ: its meta dwords (4 per K-tile, spread over
-    // the lanes) and the s1 of the lane's 4 rows
+    // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block; QoQ:
+    // its meta dwords (4 per K-tile, spread over the lanes) and the s1 of the lane's 4 rows
     constexpr int MR1 = (4 * KT1 + 63) / 64;
     constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : ACT == DGM_ACT_NVFP4 ? 1 : KG1;
-    auto load_scales = [w1s, w1r, lane, wv, unit_of, half_of, wave_blk](int i, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
-      const int u = unit_of(i), h = half_of(i);
-      const size_t blk = wave_blk(i, u, h);
+    auto load_scales = [w1s, w1r, lane, pp, gu](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
       if constexpr (ACT == DGM_ACT_QOQ) {
         const uint32_t* mb = w1s + blk * KT1 * 4;
 #pragma unroll
@@ -942,20 +902,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if constexpr (ACT == DGM_ACT_NVFP4) {
         sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
-        // (a half item runs as the K loop's second period: K half 0 gets the block's dwords
-        // rotated by half, so that its own are in sw[KG1 / 2 ..]; every element is written, so
-        // the array stays in registers)
-        const int off = HALF1 && h >= 0 ? (1 - (wv >> 2)) * (KG1 / 2) : 0;
 #pragma unroll
-        for (int g = 0; g < KG1; ++g)
-          sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + (g < KG1 / 2 ? g + off : g - off)) * 64 + lane);
+        for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
       }
     };
     // NVFP4: the lane's scale dword of each tile (128 B of E4M3 scales per 16 x 128 tile), in a
     // ring beside the tile ring
     const int slane = (((lane >> 5) << 4) | (lane & 15)) * 4;
-    auto stile_base = [w1s, slane, wv](int u) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + (wv & 3)) + (wv >> 2);
+    auto stile_base = [w1s, slane, pp, gu](int u) __attribute__((always_inline)) {
+      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
       return reinterpret_cast<const uint8_t*>(w1s) + blk * KT1 * 128 + slane;
     };
     const uint8_t* xv = p.x;
@@ -974,21 +929,20 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
     // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current item
-    int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next item
+    int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
+    int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
     uint32_t sd[SW1], sn[SW1];
     SlabRegs<KT1, ACT, FEIN, false> pre;
-    int pend = -1;            // expert slot of a finished item whose arrival is not signalled yet
-    int pendw = 0;            // and its halves (2: a whole unit)
+    int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
     if (q0 < U1) {
       // The first item's slab is staged before any tile load is issued: every workgroup
       // starts at once, and tile loads issued first would queue the slab loads (and so the
       // barrier, and every wave's first K loop) behind the whole ring of every wave.
-      load_slab(pre, unit_of(q0) / QN1, 0);
+      load_slab(pre, q0 / QN1, 0);
       load_scales(q0, sd);
       slab_store(s, pre);
-      staged = (unit_of(q0) / QN1) << 16;
+      staged = (q0 / QN1) << 16;
       __syncthreads();
       const uint8_t* b = tile_base(q0);
 #pragma unroll
@@ -1006,36 +960,27 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     auto bfrag = [lane](int t) __attribute__((always_inline)) {
       return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[t][lane][0]) : as_v8i(s.bst[t][lane][0], s.bst[t][lane][Smem::BV - 1]);
     };
-    auto first_k = [wv, half_of](int i) __attribute__((always_inline)) {   // a wave's first K-tile in item i
-      return HALF1 && half_of(i) >= 0 ? (wv >> 2) * KR : 0;
-    };
     v8i bq0 = {}, bq1 = {};
     uint32_t bs0 = 0;
     if (q0 < U1) {
-      const int k = first_k(q0);
-      bq0 = bfrag(k);
-      bq1 = KT1 > 1 ? bfrag(k + 1) : bq0;
-      bs0 = s.bsc[k >> 2][lane];
+      bq0 = bfrag(0);
+      bq1 = KT1 > 1 ? bfrag(1) : bq0;
+      bs0 = s.bsc[0][lane];
     }
     bool more = 2 * G < U1;   // the claim counter has not run out
     while (q0 < U1) {
-      const int u0 = HALF1 ? unit_of(q0) : q0, h0 = HALF1 ? half_of(q0) : -1;
-      const int a = u0 / QN1, q = u0 % QN1;
-      // this wave's block in the item: pair pp, gate (gu 0) or up (gu 1), K half kh
-      const int pp = h0 < 0 ? (wv & 3) : 2 * h0 + (wv & 1);
-      const int gu = h0 < 0 ? (wv >> 2) : (wv >> 1) & 1;
-      const int kh = HALF1 && h0 >= 0 ? wv >> 2 : 0;
+      const int a = q0 / QN1, q = q0 % QN1;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
       const bool has_next = nq < U1;
-      const int na = has_next ? unit_of(nq) / QN1 : -1;
+      const int na = has_next ? nq / QN1 : -1;
       const int nkey = (na << 16) | ns0;
       const bool restage = has_next && nkey != staged;
       const uint8_t* cb = tile_base(q0);
       // no next L1 item: ring slots < KT2 take the first L2 unit's tiles (when that unit is
       // this workgroup's), the rest dummy reads
-      const bool hand = HANDOFF && !has_next && (p.phases & 2) && v0 < N2;
+      const bool hand = HANDOFF && !has_next && (p.phases & 2) && v0 < U2;
       const uint8_t* dummy = w1v + lane * 16;
       const uint8_t* nb = !has_next ? (hand ? p.w2v + l2_blk(v0) * KT2 * 1024 + lane * 16 : dummy)
                                     : nq == q0 ? cb : tile_base(nq);
@@ -1062,7 +1007,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
-      const int kb0 = kh * KR;                    // the wave's first K-tile (a half item's K half)
       if constexpr (ACT == DGM_ACT_QOQ) {
         // per K-tile: two int8 ops on the raw 4-bit codes (exact int32 sums of code * x), then,
         // one tile later (off the matrix-core result's latency), the zero-point correction
@@ -1144,39 +1088,28 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           }
         });
       } else {
-        // Ring periods of KR ops. A whole unit runs both (HALF1: period 0 into acc, period 1 into
-        // acc2, summed after the loop, as a half unit's two waves sum them); a half item runs
-        // period 1 only, over its K half: B operands from K-tile kd + t, A scale dwords loaded
-        // rotated into the period's registers. Either way the last period's slots take the next
-        // item's tiles.
-        const bool hf = HALF1 && h0 >= 0;
-        const int kd = kb0 - (hf ? KR : 0);
+        // two chains, K-tiles 0 .. KT1 / 2 - 1 and KT1 / 2 .., summed after the loop: the split
+        // path's L1 kernel sums the same two, so the two paths agree bit for bit for any data
         v4f acc2 = {0.f, 0.f, 0.f, 0.f};
         uint32_t bs = bs0;
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
-          constexpr int pd = t / KR, tr = t % KR;
-          if (pd > 0 || !hf) {
-            constexpr bool HI = HALF1 && pd > 0;
-            const v8i bop = bq0;
-            const uint32_t bsw = bs;
-            bq0 = bq1;
-            if constexpr (t + 2 < KT1) bq1 = bfrag(kd + t + 2);
-            if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(kd + t + 1) >> 2][lane];
-            v4f& ac = HI ? acc2 : acc;
-            ac = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[tr]), bop, ac, (int)sd[t >> 2], (int)bsw);
-            if constexpr (t + KR < KT1) wr[tr] = ld_stream_after(cb, (t + KR) * 1024, ac);
-            else wr[tr] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, ac);
-            if constexpr (t == KT1 - KR) {
-              if (has_next && nq != q0) load_scales(nq, sn);
-              if (restage) load_slab(pre, na, ns0);
-            }
+          constexpr bool HI = t >= KT1 / 2;
+          const v8i bop = bq0;
+          const uint32_t bsw = bs;
+          bq0 = bq1;
+          if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
+          if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
+          v4f& ac = HI ? acc2 : acc;
+          ac = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, ac, (int)sd[t >> 2], (int)bsw);
+          if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, ac);
+          else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, ac);
+          if constexpr (t == KT1 - KR) {
+            if (has_next && nq != q0) load_scales(nq, sn);
+            if (restage) load_slab(pre, na, ns0);
           }
         });
-        if constexpr (HALF1) {
-          if (hf) acc = acc2;
-          else acc += acc2;
-        }
+        acc += acc2;
       }
       // all but this loop's KR youngest tile loads (and scale loads) are done: the previous
       // item's stores too
@@ -1188,19 +1121,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= gsc;
       }
-      if (HALF1 && kh == 1) {      // (half item) K-half-1 sums, added by the K-half-0 gate waves
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s.hk[wv & 3][lane][i] = acc[i];
-      } else if (gu == 1) {
+      if (gu == 1) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
       }
-      const bool egate = gu == 0 && kh == 0;     // this wave runs the epilogue of pair pp
       // the unit after q1 (claimed at this item's start), broadcast here
       const bool bcast = last_slab && q1 < U1;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) up sums visible, slab free
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pend = -1;
       int q2 = U1;
       if (bcast) {
@@ -1215,15 +1144,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const bool valid = s0 + c < n;
       const int pr = 4 * q + pp;                         // 16-feature block of this pair
       float act[4];
-      if (egate) {
+      if (gu == 0) {
         float am = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // (half item: K half 0 + K half 1, the whole unit's sum)
-          const float ga = HALF1 && h0 >= 0 ? acc[i] + s.hk[wv & 1][lane][i] : acc[i];
-          const float uv = HALF1 && h0 >= 0 ? s.upv[pp][lane][i] + s.hk[2 + (wv & 1)][lane][i] : s.upv[pp][lane][i];
           // MXFP: gate / up rounded to bf16 (the reference's L1 output); QoQ: fp32
-          const float g = fminf(ACT == DGM_ACT_QOQ ? ga : round_bf16(ga), p.clamp);
+          const float g = fminf(ACT == DGM_ACT_QOQ ? acc[i] : round_bf16(acc[i]), p.clamp);
+          const float uv = s.upv[pp][lane][i];
           const float uu = fminf(fmaxf(ACT == DGM_ACT_QOQ ? uv : round_bf16(uv), -p.clamp), p.clamp);
           const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
           act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
@@ -1235,12 +1162,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       __syncthreads();                                   // (2) amax visible, next slab staged
       if (has_next) {
-        const int k = first_k(nq);
-        bq0 = bfrag(k);
-        bq1 = KT1 > 1 ? bfrag(k + 1) : bq0;
-        bs0 = s.bsc[k >> 2][lane];
+        bq0 = bfrag(0);
+        bq1 = KT1 > 1 ? bfrag(1) : bq0;
+        bs0 = s.bsc[0][lane];
       }
-      if (egate) {
+      if (gu == 0) {
         // requant group: QoQ 64 features (the unit), NVFP4 16 (this pair), MXFP 32 (two pairs)
         const float am = ACT == DGM_ACT_QOQ     ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
                          : ACT == DGM_ACT_NVFP4 ? s.amax[pp][c]
@@ -1310,7 +1236,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (st) l1_sig_ticks += wall_clock() - t_e0;
       if (last_slab) {
         pend = a;
-        pendw = h0 < 0 ? 2 : 1;
         if (nq != q0) {
 #pragma unroll
           for (int g = 0; g < SW1; ++g) sd[g] = sn[g];
@@ -1324,11 +1249,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
     if (p.phases & 2) {
       l1_pend = pend;         // (its stores complete while the L2 phase issues its first loads)
-      l1_pendw = pendw;
     } else {
       wait_mem();             // the last item's stores (and the dummy ring reads)
       __syncthreads();
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (st && tid == 0) st[2] = wall_clock();
@@ -1357,7 +1281,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // ahead: MXFP: E8M0 scale dwords; QoQ: meta dwords (4 per K-tile)
     constexpr int MR2 = (4 * TI2 + 63) / 64;
     constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : ACT == DGM_ACT_NVFP4 ? 1 : RB2 * KG2;
-    auto load_scales = [w2s, lane, blk_of, l2_half](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
+    auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
       if constexpr (ACT == DGM_ACT_QOQ) {
         const uint32_t* mb = w2s + blk_of(v) * KT2 * 4;
 #pragma unroll
@@ -1366,12 +1290,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if constexpr (ACT == DGM_ACT_NVFP4) {
         sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
-        // (a half item: its one block's dwords twice; every element is written, so the array
-        // stays in registers)
         const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
-        const bool h = HALF2 && l2_half(v) >= 0;
 #pragma unroll
-        for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + (h ? g % KG2 : g) * 64);
+        for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
       }
     };
     // NVFP4: the lane's scale dword of each tile, in a ring beside the tile ring
@@ -1386,19 +1307,17 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       slab_load<KT2, ACT, true, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
                                 [](int) { return 0.f; });
     };
-    // arrivals of item (v, slab s0): its routes' outputs for the item's combine blocks (RB2, or
-    // the half's one) are complete
-    auto arrive = [comb, tid, topk, l2_unit, l2_half](int v, int s0) __attribute__((always_inline)) {
+    // arrivals of item (unit v, slab s0): its routes' outputs for the unit's blocks are complete
+    auto arrive = [comb, tid, topk](int v, int s0) __attribute__((always_inline)) {
       // (topk and the thread index made opaque: what derives from them is computed here, not
       // kept live across the work loop, where it would cost registers or a spill)
       int tk = topk, i0 = tid;
       asm volatile("" : "+s"(tk), "+v"(i0));
-      const int u = l2_unit(v), h = l2_half(v);
-      const int a = u / UPE2, nbk = h < 0 ? RB2 : 1, cb0 = RB2 * (u % UPE2) + (h < 0 ? 0 : h);
+      const int a = v / UPE2, b = v % UPE2;
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
-      for (int i = i0; i < 16 * nbk && i / nbk < n; i += FT)
-        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / nbk] < 0)   // (a token's only local route writes y itself)
-          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / nbk] / tk) * NBL2 + cb0 + i % nbk) * CNT_LINE], 1,
+      for (int i = i0; i < 16 * RB2 && i / RB2 < n; i += FT)
+        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / RB2] < 0)   // (a token's only local route writes y itself)
+          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2) * CNT_LINE], 1,
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units v0 and G + v0 first, then claims (offset by 2 G)
@@ -1407,9 +1326,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
     // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    bool more = 2 * G < N2;   // the claim counter has not run out
-    int q0 = v0 < N2 ? v0 : N2;
-    int q1 = G + v0 < N2 ? G + v0 : N2;
+    bool more = 2 * G < U2;   // the claim counter has not run out
+    int q0 = v0 < U2 ? v0 : U2;
+    int q1 = G + v0 < U2 ? G + v0 : U2;
     int s0 = 0;
     static_assert(KT2 <= RING, "the L2 ring in the shared tile registers");
     uint32_t sd[SW2], sn[SW2];
@@ -1421,22 +1340,22 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     if (p.phases & 1) {
       // probes of the L1 arrivals of the first two units' experts, answered while the L1
       // phase's last stores complete
-      if (tid == 0 && q0 < N2) {
-        pr_a = __hip_atomic_load(&l1_done[(l2_unit(q0) / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (q1 < N2) pr_n = __hip_atomic_load(&l1_done[(l2_unit(q1) / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && q0 < U2) {
+        pr_a = __hip_atomic_load(&l1_done[(q0 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q1 < U2) pr_n = __hip_atomic_load(&l1_done[(q1 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       // the L1 phase's last unit: its stores have completed (every wave) -> its arrival, before
       // any wait on other workgroups' arrivals
       wait_mem();
-      if (tid == 0) s.claimv[1] = q0 < N2 && pr_a >= L1_DONE ? 1 : 0;
+      if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= QN1 ? 1 : 0;
       __syncthreads();
-      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], l1_pendw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid == 0 && q0 < N2 && pr_a >= L1_DONE) ready = l2_unit(q0) / UPE2;
+      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && q0 < U2 && pr_a >= QN1) ready = q0 / UPE2;
     }
     // (thread 0) the second unit's expert when its probe found it complete (LDS: read once, by
     // the first item's prefetch check)
-    if (tid == 0) s.claimv[2] = q1 < N2 && pr_n >= L1_DONE ? l2_unit(q1) / UPE2 : -1;
-    if (q0 < N2) {
+    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= QN1 ? q1 / UPE2 : -1;
+    if (q0 < U2) {
       if (!handed) {          // (unit q0 = v0: handed over by the L1 phase otherwise)
         const uint8_t* b = tile_base(q0);
 #pragma unroll
@@ -1453,14 +1372,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // at the item's start; its loads complete while the tiles and scales above are in flight).
     // (NVFP4 stages it at the item's start: measured no faster this way.)
     bool pre1 = false;
-    if (ACT != DGM_ACT_NVFP4 && q0 < N2 && (!(p.phases & 1) || __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0)) {
-      load_slab(pre, l2_unit(q0) / UPE2, 0);
+    if (ACT != DGM_ACT_NVFP4 && q0 < U2 && (!(p.phases & 1) || __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0)) {
+      load_slab(pre, q0 / UPE2, 0);
       pre1 = true;
     }
-    while (q0 < N2) {
-      const int a = l2_unit(q0) / UPE2, b = l2_unit(q0) % UPE2;
-      const int hb = l2_half(q0);
-      const bool hf = HALF2 && hb >= 0;       // a half item: block hb of the unit, as the K loop's second period
+    while (q0 < U2) {
+      const int a = q0 / UPE2, b = q0 % UPE2;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const int key = (1 << 30) | (a << 16) | s0;
       if (pre1) {               // (the first item, its slab loaded before the loop)
@@ -1471,7 +1388,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
         if (a != ready) {
-          if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], L1_DONE, p.spin_limit, err, p.host_err);
+          if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err, p.host_err);
           ready = a;
         }
         __syncthreads();
@@ -1492,15 +1409,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
-      const bool has_next = nq < N2;
-      const int na = has_next ? l2_unit(nq) / UPE2 : -1;
+      const bool has_next = nq < U2;
+      const int na = has_next ? nq / UPE2 : -1;
       const int nkey = (1 << 30) | (na << 16) | ns0;
       // prefetch the next item's slab if it differs and its expert's L1 is complete
       bool pf = false;
       if (has_next && nkey != key) {
         if (tid == 0)
           s.claimv[1] = !(p.phases & 1) || na == ready || na == s.claimv[2] ||
-                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= L1_DONE;
+                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
         __syncthreads();
         pf = __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0;
         if (pf) {
@@ -1524,7 +1441,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       // the unit after q1, claimed at the start of the item that finishes q0 (the value is read
       // in this item's epilogue)
-      if (tid == 0 && last_slab && q1 < N2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && last_slab && q1 < U2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
       // read from LDS two ops ahead
       v4f acc[RB2];
@@ -1621,28 +1538,22 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[j][i] *= gsc;
       } else {
-        // (a half item runs the first block's ops only, their slots then taking the next item's
-        // tiles; its scale dwords are in every block's registers)
-        const uint8_t* ra = hf ? nb : cb + KT2 * 1024;
         uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
         static_for<TI2>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr int j = t / KT2, k = t % KT2;
-          if (j == 0 || !hf) {
-            const v8i bop = bq0;
-            const uint32_t bsw = bs0;
-            bq0 = bq1;
-            bs0 = bs1;
-            if constexpr (t + 2 < TI2) {
-              bq1 = bfrag((t + 2) % KT2);
-              bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
-            }
-            acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
-                                                                   (int)sd[j * KG2 + (k >> 2)], (int)bsw);
-            if constexpr (HALF2 && j == 0) wr[k] = ld_stream_after(ra, k * 1024, acc[j]);
-            else if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
-            else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
+          const v8i bop = bq0;
+          const uint32_t bsw = bs0;
+          bq0 = bq1;
+          bs0 = bs1;
+          if constexpr (t + 2 < TI2) {
+            bq1 = bfrag((t + 2) % KT2);
+            bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
           }
+          acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
+                                                                 (int)sd[j * KG2 + (k >> 2)], (int)bsw);
+          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
         });
       }
       // all but this loop's KT2 youngest tile loads (and scale loads) are done: the previous
@@ -1650,38 +1561,34 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       wait_vm_le<ACT == DGM_ACT_NVFP4 ? 2 * KT2 : KT2>();
       if (s0 + c < n) {
         // each route's output rounded to bf16 (the reference's per-route rule), stored slot-major
-        // (the wave's 16-row blocks: whole item RB2 from NW RB2 b + RB2 w, half item one)
-        const int rb16 = hf ? NW * RB2 * b + NW * hb + wv : NW * RB2 * b + RB2 * wv;
-        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + rb16 * 16 + 4 * kq;
+        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
 #pragma unroll
         for (int j = 0; j < RB2; ++j)
-          if (j == 0 || !hf)
-            st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
-                                                    ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
+          st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
+                                       ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
         // a token with no other local route: its y rows are this route's output (the combine of
         // one bf16 route output), written here; no arrival, no combine
         const int yt = ACT == DGM_ACT_NVFP4 ? -1 : s.ytok[r0 + s0 + c];
         if (yt >= 0) {
-          uint16_t* yd = p.y + (size_t)yt * H + rb16 * 16 + 4 * kq;
+          uint16_t* yd = p.y + (size_t)yt * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
 #pragma unroll
           for (int j = 0; j < RB2; ++j)
-            if (j == 0 || !hf)
-              *reinterpret_cast<uint64_t*>(yd + 16 * j) =
-                  (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
-                  ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48);
+            *reinterpret_cast<uint64_t*>(yd + 16 * j) =
+                (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
+                ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48);
         }
       }
-      const bool bcast = last_slab && q1 < N2;
+      const bool bcast = last_slab && q1 < U2;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) previous outputs complete, slab free
       if (pv >= 0) arrive(pv, ps0);
       pv = q0;
       ps0 = s0;
-      int q2 = N2;
+      int q2 = U2;
       if (bcast) {
         const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        q2 = raw >= 0 && 2 * G + raw < N2 ? 2 * G + raw : N2;
-        if (q2 >= N2) more = false;
+        q2 = raw >= 0 && 2 * G + raw < U2 ? 2 * G + raw : U2;
+        if (q2 >= U2) more = false;
       }
       if (pf) {
         slab_store(s, pre);

@@ -187,8 +187,7 @@ def test_config2_m16_unbalanced(mxfp4_weights, fmt):
 
 def test_config2_m2_m4_balanced(mxfp4_weights):
     """The small-M end of the sweep (the claim counters start beyond the first units only from
-    M=4 on; M=2 runs every unit from the workgroups' first two). Both leave a last, partial
-    round of L1 units (320 and 640 units for 256 workgroups), which runs as half units."""
+    M=4 on; M=2 runs every unit from the workgroups' first two)."""
     run_headline("mxfp8", 2, True, 502, mxfp4_weights)
     run_headline("mxfp4", 4, True, 504, mxfp4_weights)
 

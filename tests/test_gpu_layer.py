@@ -181,38 +181,6 @@ def test_split_matches_fused(fmt):
     np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
 
 
-@pytest.mark.parametrize("fmt,M,topk", [("mxfp4", 2, 8), ("mxfp8", 4, 8), ("mxfp4", 1, 8), ("mxfp8", 1, 4)])
-def test_half_units_match_whole_units_and_split(fmt, M, topk):
-    """A last round of units that fills at most half of the 256 workgroups runs as half units:
-    L1 halves of 32 features (each weight block's K halves on two waves, summed through LDS),
-    L2 halves of one 128-row block. Forced-balanced routing over 48 experts leaves 16, 32, 8
-    or 4 active experts: 320 / 640 / 160 / 80 L1 units (64 / 128 / none / 80 of them split) and
-    192 / 384 / 96 / 48 L2 units (none / 128 / 96 / 48 split). The result equals the whole-unit
-    schedule (debug bit 2) and the split API bit for bit, and the oracle to tolerance."""
-    need_gpu()
-    import hopper_megamoe_basedondeepgemm_amd as dgm
-    weights = make_weights(48, 3072, 1280, 611)
-    r = run_layer(M, 48, 48, 0, 3072, 1280, topk, fmt, seed=610 + M, force_balanced=True, weights=weights)
-    print(fmt, M, topk, check_y(r), flush=True)
-    b = r["buf"]
-    n_active = int((b.pool_table()[0] > 0).sum())
-    G = dgm.mega.fused_workgroups(b)
-    halves = [0 < u % G and 2 * (u % G) <= G for u in (n_active * (1280 // 64), n_active * (3072 // 256))]
-    assert any(halves), (n_active, G)
-    print("  active experts", n_active, "half units (L1, L2):", halves, flush=True)
-    (t1, t2), _, _ = weights
-    for dbg, layer in ((4, dgm.mxfp4_mega_moe_fused), (0, dgm.mxfp4_mega_moe_split)):
-        b._debug_flags = dbg
-        try:
-            y2 = torch.empty((M, 3072), dtype=torch.bfloat16, device="cuda")
-            layer(y2, t1, t2, b, activation_clamp=10.0)
-            torch.cuda.synchronize()
-        finally:
-            b._debug_flags = 0
-        np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
-    assert b.kernel_error() == 0
-
-
 @pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8"])
 def test_select_in_mega(fmt):
     """Top-k selected in the fused kernel's prologue (frontend with select_in_mega): the same
