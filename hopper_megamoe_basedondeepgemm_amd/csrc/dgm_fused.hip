@@ -204,7 +204,6 @@ struct FusedSmem {
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
-  int is_last;
   int claimv[3];            // [0] the claim ahead, [1] prefetch decision, [2] L2: a complete expert
 };
 
@@ -640,10 +639,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   static_assert(sizeof(FusedParams) <= 256, "four parameter lines");
   asm volatile("" ::"s"(p.w1v), "s"(p.x), "s"(p.partials), "s"(p.router_w));
   const int R = p.M * p.topk;
-  int* exit_cnt = p.counters + CNT_EXIT;
+  // this launch's counter set (the other one is cleared after the dispatch)
+  const int parity = __hip_atomic_load(p.counters + CNT_PARITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1;
+  int* const cset = p.counters + CNT_SET0 + parity * CNT_SET;
+  int* exit_cnt = cset + CNT_EXIT;
   int* err = p.counters + CNT_ERROR;
-  int* l1_done = p.counters + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
-  int* comb = p.counters + CNT_COMB;        // pair i: comb[i * CNT_LINE]
+  int* l1_done = cset + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
+  int* comb = cset + CNT_COMB;        // pair i: comb[i * CNT_LINE]
   long long* st = (p.stamps && (int)blockIdx.x < p.stamp_rows) ? p.stamps + (size_t)blockIdx.x * 8 : nullptr;
   long long wait_ticks = 0, l1_load_ticks = 0, l1_sig_ticks = 0;
   if (st && tid == 0) st[0] = wall_clock();
@@ -679,12 +681,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     wait_mem();                  // this wave's stores have completed
     __syncthreads();
     if (tid == 0)
-      __hip_atomic_fetch_add(p.counters + CNT_GRID + ((int)blockIdx.x % GRID_SLOTS) * GRID_STRIDE, 1,
+      __hip_atomic_fetch_add(cset + CNT_GRID + ((int)blockIdx.x % GRID_SLOTS) * GRID_STRIDE, 1,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (wv == 0) {               // lane k < GRID_SLOTS watches slot k (bounded)
       const int k = lane % GRID_SLOTS;
       const int expect = ((int)gridDim.x - k + GRID_SLOTS - 1) / GRID_SLOTS;
-      const int* gc = p.counters + CNT_GRID + k * GRID_STRIDE;
+      const int* gc = cset + CNT_GRID + k * GRID_STRIDE;
       for (int it = 0;; ++it) {
         const int v = __hip_atomic_load(gc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (__all(v >= expect)) break;
@@ -831,6 +833,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (s.nslot[t] == 0) reinterpret_cast<U4*>(p.y + (size_t)t * H)[i % (H / 8)] = U4{0, 0, 0, 0};
     }
   }
+  // The other counter set, cleared one line per thread, spread over the grid (its last user,
+  // the previous launch on this buffer, has completed). (Issued here, behind the routing loads
+  // and ahead of the first slab's, which wait about as long as these stores.)
+  {
+    int* const other = p.counters + CNT_SET0 + (1 - parity) * CNT_SET;
+    for (int l = (int)blockIdx.x + (int)gridDim.x * tid; l < CNT_SET / CNT_LINE; l += (int)gridDim.x * FT)
+      __hip_atomic_store(other + l * CNT_LINE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();        // s.cnt / s.eoff (union with the B slab) are dead from here on
 
   // Units are claimed dynamically from one atomic counter per phase, ahead of their use: L1
@@ -874,7 +884,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     constexpr int KR = KT1 % 12 == 0 ? 12 : KT1;   // ring depth: tiles in flight per wave
     static_assert(KT1 % KR == 0, "the ring depth divides the K-tile count");
     const int pp = wv & 3, gu = wv >> 2;
-    int* claim = p.counters + CNT_CLAIM;
+    int* claim = cset + CNT_CLAIM;
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
     const float* w1r = p.w1r;
@@ -1268,7 +1278,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // bumps the arrival counters of its (token, 128-row block)s (no return value).
   if (p.phases & 2) {
     static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
-    int* claim = p.counters + CNT_CLAIM + CNT_LINE;
+    int* claim = cset + CNT_CLAIM + CNT_LINE;
     const uint8_t* w2v = p.w2v;
     const uint32_t* w2s = p.w2s;
     const float* w2r = p.w2r;
@@ -1657,22 +1667,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     st[6] = l1_load_ticks;
     st[7] = l1_sig_ticks;
   }
-  wait_mem();
-  __syncthreads();
+  // The last workgroup to get here hands the next launch the other counter set. (No
+  // workgroup of this launch reads the parity again: each read it at its start, before any
+  // workgroup could count itself here.)
   if (tid == 0) {
     const int old = __hip_atomic_fetch_add(exit_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s.is_last = old == (int)gridDim.x - 1;
-  }
-  __syncthreads();
-  if (s.is_last) {
-    for (int a = tid; a < n_active; a += FT) __hip_atomic_store(&l1_done[a * CNT_LINE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (int i = tid; i < p.M * NBL2; i += FT) __hip_atomic_store(&comb[i * CNT_LINE], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < 2) __hip_atomic_store(p.counters + CNT_CLAIM + tid * CNT_LINE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid < GRID_SLOTS)
-      __hip_atomic_store(p.counters + CNT_GRID + tid * GRID_STRIDE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_mem();
-    __syncthreads();
-    if (tid == 0) __hip_atomic_store(exit_cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == (int)gridDim.x - 1)
+      __hip_atomic_store(p.counters + CNT_PARITY, 1 - parity, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (st && tid == 0) st[5] = wall_clock();
 }

@@ -23,7 +23,7 @@ constexpr size_t NA_OFF_MID = NA_OFF_POOL + dgm_align256(dgm_pool_bytes(FUSED_MA
 constexpr size_t NA_OFF_MID_SF = NA_OFF_MID + dgm_align256((size_t)NA_MAX_ROUTES * NA_MAX_INTER);
 constexpr size_t NA_OFF_PART = NA_OFF_MID_SF + dgm_align256((size_t)NA_MAX_ROUTES * (NA_MAX_INTER / 16));
 constexpr size_t NA_BYTES = NA_OFF_PART + dgm_align256((size_t)NA_MAX_ROUTES * NA_MAX_HIDDEN * 2);
-static_assert(NA_BYTES < 6u * 1024 * 1024, "a modest array");
+static_assert(NA_BYTES < 7u * 1024 * 1024, "a modest array");
 
 constexpr int NA_MAX_DEVICES = 64;
 
@@ -43,7 +43,8 @@ __global__ void k_na_clear(uint32_t* p, int n) {
 }
 
 // Once per device, with that device current: the array's device address, and its counters
-// cleared by a fill kernel on `stream` (every launch returns them to zero afterwards).
+// cleared by a fill kernel on `stream` (every launch then clears the counter set that the next
+// launch uses).
 int na_setup(int dev, hipStream_t stream, uint8_t** out) {
   std::lock_guard<std::mutex> lk(g_na_mu);
   if (!g_na_ptr[dev]) {

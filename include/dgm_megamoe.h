@@ -257,13 +257,13 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
 /* No counterpart in the reference: dgm_megamoe_fused_launch for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * The same layer, but the persistent kernel's workspace (dispatch table, L1 -> L2 rows, route
- * outputs, counters) is a file-scope device array of ~5.7 MB held by each GPU the library runs on,
+ * outputs, counters) is a file-scope device array of ~6.4 MB held by each GPU the library runs on,
  * not the buffer's views: the buffer supplies only the inputs (x / x_sf, or the keys / topk views)
  * and args->y the output; the buffer's pool, l2_acts and combine_partials views are not written.
  * Limits: num_tokens * topk <= 512, num_tokens <= 256, hidden <= 4096, intermediate <= 2048
  * (beyond them: DGM_ERR_INVALID_ARGUMENT, nothing launched). No hipMalloc / hipFree is called;
  * the first call on a device clears the array's counters with a fill kernel on `stream`, and
- * every launch returns them to zero. All calls on one GPU share its array: calls that overlap
+ * every launch clears the counter set that the next launch uses. All calls on one GPU share its array: calls that overlap
  * (unordered streams) race. Expired waits are reported only through args->host_error. */
 int dgm_megamoe_fused_launch_noalloc(const DgmMoeArgs* args, hipStream_t stream);
 
