@@ -639,10 +639,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   static_assert(sizeof(FusedParams) <= 256, "four parameter lines");
   asm volatile("" ::"s"(p.w1v), "s"(p.x), "s"(p.partials), "s"(p.router_w));
   const int R = p.M * p.topk;
-  // this launch's counter set (the other one is cleared after the dispatch)
+  // this launch's counter set (the other one is cleared after the dispatch); each workgroup
+  // counts itself once it has read the parity: the one that counts last hands the next launch
+  // the other set at its end (its count is read only then, long after it has returned)
   const int parity = __hip_atomic_load(p.counters + CNT_PARITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1;
   int* const cset = p.counters + CNT_SET0 + parity * CNT_SET;
-  int* exit_cnt = cset + CNT_EXIT;
+  int started = 0;
+  if (tid == 0) started = __hip_atomic_fetch_add(cset + CNT_STARTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   int* err = p.counters + CNT_ERROR;
   int* l1_done = cset + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
   int* comb = cset + CNT_COMB;        // pair i: comb[i * CNT_LINE]
@@ -1667,14 +1670,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     st[6] = l1_load_ticks;
     st[7] = l1_sig_ticks;
   }
-  // The last workgroup to get here hands the next launch the other counter set. (No
-  // workgroup of this launch reads the parity again: each read it at its start, before any
-  // workgroup could count itself here.)
-  if (tid == 0) {
-    const int old = __hip_atomic_fetch_add(exit_cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (old == (int)gridDim.x - 1)
-      __hip_atomic_store(p.counters + CNT_PARITY, 1 - parity, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // The workgroup that counted itself last at the start hands the next launch the other
+  // counter set: every workgroup of this launch has read the parity (each before counting
+  // itself) and none reads it again.
+  if (tid == 0 && started == (int)gridDim.x - 1)
+    __hip_atomic_store(p.counters + CNT_PARITY, 1 - parity, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (st && tid == 0) st[5] = wall_clock();
 }
 

@@ -11,16 +11,17 @@ constexpr int FUSED_MAX_NB64 = 64;       // hidden / 64 (hidden <= 4096); combin
 // int32 counters in the buffer's counter region. Counters that many workgroups update at once
 // sit on 64-byte lines of their own (device-scope atomics on one line serialize).
 // A header line, then two counter sets: a launch uses set `parity` (header word 0) and clears
-// the other set, whose last user (the previous launch on this buffer) has completed; its last
-// workgroup to finish flips the parity. So no workgroup clears counters at the end of a launch,
-// and the state lives in device memory only (graph replays included).
+// the other set, whose last user (the previous launch on this buffer) has completed; once
+// every workgroup has read the parity (each counts itself in CNT_STARTED after reading it), the
+// last one to count flips it. So no workgroup clears counters or waits on an atomic at the end
+// of a launch, and the state lives in device memory only (graph replays included).
 constexpr int CNT_LINE = 16;             // ints per 64-byte line
 constexpr int CNT_PARITY = 0;            // header: the counter set the next launch uses
 constexpr int CNT_ERROR = 1;             // header: set when a bounded wait expired
 constexpr int CNT_NEVER = 2;             // header: never incremented: the target of the debug wait
 constexpr int CNT_SET0 = CNT_LINE;       // the first set (the second follows it)
 // within a set (every counter at the start of its own line):
-constexpr int CNT_EXIT = 0;              // workgroups finished
+constexpr int CNT_STARTED = 0;           // workgroups that have read the parity
 constexpr int CNT_CLAIM = CNT_LINE;      // next unclaimed L1 unit; [CNT_CLAIM + CNT_LINE]: L2 unit
 constexpr int CNT_L1 = 4 * CNT_LINE;     // L1 units done per active expert slot, one line each
 constexpr int CNT_COMB = CNT_L1 + FUSED_MAX_LOCAL * CNT_LINE;   // combine arrivals per (token, 128-row block), one line each
