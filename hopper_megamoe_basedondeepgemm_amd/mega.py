@@ -524,7 +524,9 @@ def qoq_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, ac
     activations with one scale per token, 4-bit weight codes with per-(row, K128) zero point and
     integer scale and per-row fp32 scale, exact int32 group sums; fp32 gate / up, SiLU * up *
     routing weight, int8 requant per 64 features, L2 (each route rounded to bf16), fp32 combine ->
-    bf16 ``y``. ``fe_keys`` as for ``mxfp4_mega_moe_fused``."""
+    bf16 ``y``. ``fe_keys`` as for ``mxfp4_mega_moe_fused``. Limits per call (QoQ and NVFP4 run
+    only on the persistent kernel): tokens x topk <= 1024, tokens <= 256, local experts <= 512,
+    hidden <= 4096; beyond them the call raises RuntimeError (no launch)."""
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
            fast_math=fast_math, fmt="qoq", fe_keys=fe_keys)
 
@@ -535,7 +537,8 @@ def fp4_fp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_exp
     ``act_format="nvfp4"`` buffer (E4M3 scale per 16; weights from
     ``transform_nvfp4_weights_for_mega_moe_fused``) it runs the NVFP4 layer; on an "mxfp4"
     buffer the MXFP4 layer (weights from ``transform_mxfp4_weights_for_mega_moe_fused``).
-    ``activation_clamp=None`` = no clamp."""
+    ``activation_clamp=None`` = no clamp. NVFP4 limits per call: tokens x topk <= 1024, tokens
+    <= 256, local experts <= 512, hidden <= 4096 (RuntimeError beyond them; MXFP4 has none)."""
     b = sym_buffer
     assert b.act_format in ("mxfp4", "nvfp4"), "buffer must be created with act_format mxfp4/nvfp4"
     vec = 16 if b.act_format == "nvfp4" else 32
@@ -551,7 +554,10 @@ def nvfp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_exper
     """deep_gemm/mega/__init__.py:277 NVFP4 entry with per-expert fp32 global scales
     (``l1_global_scales`` / ``l2_global_scales`` [E_local], multiplied into the L1 / L2
     outputs), here on an ``act_format="nvfp4"`` buffer (W4A4). ``recipe``, ``kernel_family`` and
-    ``family_threshold`` select SM90 kernel families there and have no effect here."""
+    ``family_threshold`` select SM90 kernel families there; here "split" runs the same kernel as
+    two launches. Both families run on the persistent kernel, so a call holds at most 1024 routes
+    (tokens x topk), 256 tokens, 512 local experts and hidden 4096; beyond them it raises
+    RuntimeError before any launch."""
     assert sym_buffer.act_format == "nvfp4", "buffer must be created with act_format='nvfp4'"
     assert activation == "swiglu", activation
     if kernel_family not in ("auto", "split", "fused"):
@@ -650,7 +656,9 @@ def qoq_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs):
     kernel (dispatch + L1 into the buffer's intermediate rows, then L2 + combine), on an
     ``act_format="qoq"`` buffer; weights from ``transform_qoq_weights_for_mega_moe_fused`` or
     ``transform_qoq_int4_weights_for_mega_moe_sm90``. Same results as ``qoq_mega_moe_fused``
-    bit for bit. Arguments as ``mxfp4_mega_moe`` (activation_clamp default None = no clamp)."""
+    bit for bit. Arguments as ``mxfp4_mega_moe`` (activation_clamp default None = no clamp).
+    Limits per call, as for the fused launch: tokens x topk <= 1024, tokens <= 256, local
+    experts <= 512, hidden <= 4096 (RuntimeError beyond them, before any launch)."""
     _split_entry(("qoq",), y, l1_weights, l2_weights, sym_buffer, *args, **kwargs)
 
 

@@ -179,6 +179,38 @@ def test_nvfp4_global_scales_zero_rows_select_in_mega():
     print(check_y(r, zero_rows=(5, 21)))
 
 
+def test_nvfp4_limits_raise_before_launch():
+    """NVFP4 runs only on the persistent kernel: beyond 1024 routes (tokens x topk) or 256
+    tokens every entry (fp4_fp4_mega_moe, nvfp4_mega_moe fused / split / auto) raises
+    RuntimeError with no launch (y keeps its sentinel); a call within the limits on the same
+    buffer still runs."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    E, H, I = 8, 512, 256
+    (t1, t2), _, _ = make_nvfp4_weights(E, H, I, 961)
+    for M, topk, what in ((160, 8, "1280 routes"), (300, 2, "300 tokens")):
+        print(f"nvfp4 limits: M={M} topk={topk} ({what}) must raise", flush=True)
+        buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="nvfp4")
+        y = torch.full((M, H), 3.0, dtype=torch.bfloat16, device="cuda")
+        calls = [lambda: dgm.fp4_fp4_mega_moe(y, t1, t2, buf)]
+        calls += [lambda f=f: dgm.nvfp4_mega_moe(y, t1, t2, buf, kernel_family=f) for f in ("fused", "split", "auto")]
+        for call in calls:
+            with pytest.raises(RuntimeError, match="at most 1024 routes"):
+                call()
+        torch.cuda.synchronize()
+        assert bool((y == 3.0).all()), "a refused call wrote y"
+        assert buf.kernel_error() == 0
+        rng = np.random.default_rng(962)
+        m = 1024 // topk // 2
+        x = bf16_cpu(randn_bf16(rng, (m, H))).cuda()
+        rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+        dgm.fable_router_quant_topk_frontend(x, rw, buf)
+        ys = torch.full((m, H), 3.0, dtype=torch.bfloat16, device="cuda")
+        dgm.fp4_fp4_mega_moe(ys, t1, t2, buf)
+        torch.cuda.synchronize()
+        assert buf.kernel_error() == 0 and bool(torch.isfinite(ys.float()).all()) and not bool((ys == 3.0).all())
+
+
 def test_nvfp4_split_family_matches_fused():
     """kernel_family="split" (dispatch + L1, then L2 + combine: two launches) and "auto" above
     family_threshold give the fused launch's output, intermediate rows and recv stats bit for

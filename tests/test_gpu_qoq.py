@@ -204,6 +204,35 @@ def test_qoq_buffer_format_guard():
         dgm.qoq_mega_moe_fused(y, dummy, dummy, bm)
 
 
+def test_qoq_limits_raise_before_launch():
+    """QoQ runs only on the persistent kernel: a call beyond 1024 routes (tokens x topk) or 256
+    tokens raises RuntimeError from both entry points, with no launch (y keeps its sentinel),
+    and a call within the limits on the same buffer still runs."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    E, H, I = 8, 512, 256
+    (t1, t2), _, _ = make_qoq_weights(E, H, I, 951)
+    for M, topk, what in ((160, 8, "1280 routes"), (300, 2, "300 tokens")):
+        print(f"qoq limits: M={M} topk={topk} ({what}) must raise", flush=True)
+        buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format="qoq")
+        y = torch.full((M, H), 3.0, dtype=torch.bfloat16, device="cuda")
+        for fn in (dgm.qoq_mega_moe_fused, dgm.qoq_mega_moe_split):
+            with pytest.raises(RuntimeError, match="at most 1024 routes"):
+                fn(y, t1, t2, buf)
+        torch.cuda.synchronize()
+        assert bool((y == 3.0).all()), "a refused call wrote y"
+        assert buf.kernel_error() == 0
+        rng = np.random.default_rng(952)
+        m = 1024 // topk // 2
+        x = bf16_cpu(randn_bf16(rng, (m, H))).cuda()
+        rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+        dgm.fable_router_quant_topk_frontend(x, rw, buf)
+        ys = torch.full((m, H), 3.0, dtype=torch.bfloat16, device="cuda")
+        dgm.qoq_mega_moe_fused(ys, t1, t2, buf)
+        torch.cuda.synchronize()
+        assert buf.kernel_error() == 0 and bool(torch.isfinite(ys.float()).all()) and not bool((ys == 3.0).all())
+
+
 def test_qoq_int4_packer_and_split_matches_fused():
     """The split path: quantize_to_qoq_int4 (int32 coefficient plane) bit-exact against the
     oracle; transform_qoq_int4_weights_for_mega_moe_sm90 equal to the fused packer's transform of
