@@ -708,7 +708,7 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   if (A->num_tokens == 0) return 0;
   if (fused_fits(A)) return fused_launch_phases(A, 3, stream);
   DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ && A->act_format != DGM_ACT_NVFP4,
-                "QoQ / NVFP4 layer: at most 1024 routes (tokens x topk), 256 tokens, 512 local experts and hidden 4096 per call");
+                "QoQ / NVFP4 layer: at most 1024 routes (tokens x topk), 256 tokens and 512 local experts per call");
   DGM_CHECK_ARG(!A->fe_in_mega, "fe_in_mega: the fused kernel's limits (tokens, routes, local experts) are exceeded");
   return dgm_megamoe_split_launch(A, stream);
 }
@@ -838,7 +838,7 @@ int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
                   A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
     DGM_CHECK_ARG(A->hidden % 128 == 0 && A->intermediate % 128 == 0, "shape");
     if (A->num_tokens == 0) return 0;
-    DGM_CHECK_ARG(fused_fits(A), "QoQ / NVFP4 layer: at most 1024 routes (tokens x topk), 256 tokens, 512 local experts and hidden 4096 per call");
+    DGM_CHECK_ARG(fused_fits(A), "QoQ / NVFP4 layer: at most 1024 routes (tokens x topk), 256 tokens and 512 local experts per call");
     int st = fused_launch_phases(A, 1, stream);
     if (st) return st;
     return fused_launch_phases(A, 2, stream);

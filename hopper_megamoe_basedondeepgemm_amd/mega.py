@@ -525,8 +525,8 @@ def qoq_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, ac
     integer scale and per-row fp32 scale, exact int32 group sums; fp32 gate / up, SiLU * up *
     routing weight, int8 requant per 64 features, L2 (each route rounded to bf16), fp32 combine ->
     bf16 ``y``. ``fe_keys`` as for ``mxfp4_mega_moe_fused``. Limits per call (QoQ and NVFP4 run
-    only on the persistent kernel): tokens x topk <= 1024, tokens <= 256, local experts <= 512,
-    hidden <= 4096; beyond them the call raises RuntimeError (no launch)."""
+    only on the persistent kernel): tokens x topk <= 1024, tokens <= 256, local experts <= 512;
+    beyond them the call raises RuntimeError (no launch)."""
     _fused(y, l1, l2, b, cumulative_local_expert_recv_stats, activation_clamp, phase_stamps=phase_stamps,
            fast_math=fast_math, fmt="qoq", fe_keys=fe_keys)
 
@@ -538,7 +538,7 @@ def fp4_fp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_exp
     ``transform_nvfp4_weights_for_mega_moe_fused``) it runs the NVFP4 layer; on an "mxfp4"
     buffer the MXFP4 layer (weights from ``transform_mxfp4_weights_for_mega_moe_fused``).
     ``activation_clamp=None`` = no clamp. NVFP4 limits per call: tokens x topk <= 1024, tokens
-    <= 256, local experts <= 512, hidden <= 4096 (RuntimeError beyond them; MXFP4 has none)."""
+    <= 256, local experts <= 512 (RuntimeError beyond them; MXFP4 has none)."""
     b = sym_buffer
     assert b.act_format in ("mxfp4", "nvfp4"), "buffer must be created with act_format mxfp4/nvfp4"
     vec = 16 if b.act_format == "nvfp4" else 32
@@ -556,7 +556,7 @@ def nvfp4_mega_moe(y, l1_weights, l2_weights, sym_buffer, cumulative_local_exper
     outputs), here on an ``act_format="nvfp4"`` buffer (W4A4). ``recipe``, ``kernel_family`` and
     ``family_threshold`` select SM90 kernel families there; here "split" runs the same kernel as
     two launches. Both families run on the persistent kernel, so a call holds at most 1024 routes
-    (tokens x topk), 256 tokens, 512 local experts and hidden 4096; beyond them it raises
+    (tokens x topk), 256 tokens and 512 local experts; beyond them it raises
     RuntimeError before any launch."""
     assert sym_buffer.act_format == "nvfp4", "buffer must be created with act_format='nvfp4'"
     assert activation == "swiglu", activation
@@ -658,7 +658,7 @@ def qoq_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs):
     ``transform_qoq_int4_weights_for_mega_moe_sm90``. Same results as ``qoq_mega_moe_fused``
     bit for bit. Arguments as ``mxfp4_mega_moe`` (activation_clamp default None = no clamp).
     Limits per call, as for the fused launch: tokens x topk <= 1024, tokens <= 256, local
-    experts <= 512, hidden <= 4096 (RuntimeError beyond them, before any launch)."""
+    experts <= 512 (RuntimeError beyond them, before any launch)."""
     _split_entry(("qoq",), y, l1_weights, l2_weights, sym_buffer, *args, **kwargs)
 
 
