@@ -851,9 +851,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // 128 output rows b). A workgroup starts on L2 units only after the L1 counter ran out, so
   // an L2 unit's wait is only on L1 units already claimed by running workgroups, which never
   // wait.
-  // L2 items span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks
-  constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2, TI2 = RB2 * KT2;
-  const int U1 = n_active * QN1, U2 = n_active * UPE2;
+  // L2 units span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks.
+  // When the units fill at most half the grid, each is run as RB2 items of one block instead
+  // (halves; debug bit 2 keeps whole units). U2 counts the L2 items.
+  constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2;
+  const bool halves = RB2 == 2 && 2 * n_active * UPE2 <= (int)gridDim.x && !(p.debug & 4);
+  const int U1 = n_active * QN1, U2 = n_active * (halves ? NBL2 : UPE2);
   // This workgroup's first L2 unit (its second is G + v0)
   const int v0 = (int)blockIdx.x;
   const int c = lane & 15, kq = lane >> 4;
@@ -868,9 +871,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   U4 wr[RING];
   uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
-  // L2 unit v = (active expert a, 128 RB2-row slice b): this wave's first 16-row block of it
-  auto l2_blk = [wv](int v) __attribute__((always_inline)) {
-    return (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
+  // L2 item v's first 16-row block for this wave (whole units or halves)
+  auto l2_blk = [wv, halves](int v) __attribute__((always_inline)) {
+    return halves ? (size_t)s.act[v / NBL2] * NB2 + NW * (v % NBL2) + wv
+                  : (size_t)s.act[v / UPE2] * NB2 + (NW * RB2) * (v % UPE2) + RB2 * wv;
   };
 
   // ================================================================ L1 phase
@@ -1271,41 +1275,49 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[2] = wall_clock();
 
   // ================================================================ L2 phase
-  // Unit (a, b) = rows 128 RB2 b .. +128 RB2 of expert a; wave w owns the RB2 16-row blocks
-  // at 16 (NW RB2 b + RB2 w) .. (TI2 contiguous tiles over the full K). The wave streams them
+  // Item (a, b) = rows 128 RB b .. +128 RB of expert a; wave w owns the RB 16-row blocks
+  // at 16 (NW RB b + RB w) .. (TI contiguous tiles over the full K). The wave streams them
   // through a ring of KT2 tile registers; the second half of the ring (and all of it at the
   // end) rolls into the next item's tiles right after the op that consumed a slot. The next
   // item's slab (intermediate rows of another expert) is loaded ahead when that expert's L1
   // arrival is already complete, else staged at the item's start after a bounded wait. Route
   // outputs (bf16) go to `partials`; one item later, when they have completed, each route
   // bumps the arrival counters of its (token, 128-row block)s (no return value).
-  if (p.phases & 2) {
+  // The L2 phase for items of RB 128-row blocks (every wave streams RB 16-row blocks of each):
+  // whole units (RB = RB2) or, when the units fill at most half the grid, halves (RB = 1) so
+  // that all of them run at once on twice as many workgroups; one or the other per launch, each
+  // its own code (no branch inside the K loops).
+  auto l2_phase = [&](auto rb_c) __attribute__((always_inline)) {
+    constexpr int RB = decltype(rb_c)::value, UPE = NBL2 / RB, TI = RB * KT2;
     static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
     int* claim = cset + CNT_CLAIM + CNT_LINE;
     const uint8_t* w2v = p.w2v;
     const uint32_t* w2s = p.w2s;
     const float* w2r = p.w2r;
     const int topk = p.topk;
-    const auto blk_of = l2_blk;
+    // item v = (active expert a, RB * 128-row slice b): this wave's first 16-row block of it
+    auto blk_of = [wv](int v) __attribute__((always_inline)) {
+      return (size_t)s.act[v / UPE] * NB2 + (NW * RB) * (v % UPE) + RB * wv;
+    };
     auto tile_base = [w2v, lane, blk_of](int v) __attribute__((always_inline)) {
       return w2v + blk_of(v) * KT2 * 1024 + lane * 16;
     };
-    // per-item scale registers (the wave's RB2 contiguous 16-row blocks), loaded one item
+    // per-item scale registers (the wave's RB contiguous 16-row blocks), loaded one item
     // ahead: MXFP: E8M0 scale dwords; QoQ: meta dwords (4 per K-tile)
-    constexpr int MR2 = (4 * TI2 + 63) / 64;
-    constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : ACT == DGM_ACT_NVFP4 ? 1 : RB2 * KG2;
-    auto load_scales = [w2s, lane, blk_of](int v, uint32_t (&sw)[SW2]) __attribute__((always_inline)) {
+    constexpr int MR2 = (4 * TI + 63) / 64;
+    constexpr int SW2 = ACT == DGM_ACT_QOQ ? MR2 : ACT == DGM_ACT_NVFP4 ? 1 : RB * KG2;
+    auto load_scales = [w2s, lane, blk_of](int v, auto& sw) __attribute__((always_inline)) {
       if constexpr (ACT == DGM_ACT_QOQ) {
         const uint32_t* mb = w2s + blk_of(v) * KT2 * 4;
 #pragma unroll
         for (int j = 0; j < MR2; ++j)
-          sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * TI2 ? 64 * j + lane : 4 * TI2 - 1));
+          sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * TI ? 64 * j + lane : 4 * TI - 1));
       } else if constexpr (ACT == DGM_ACT_NVFP4) {
         sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
       } else {
         const uint32_t* b = w2s + blk_of(v) * KG2 * 64 + lane;
 #pragma unroll
-        for (int g = 0; g < RB2 * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
+        for (int g = 0; g < RB * KG2; ++g) sw[g] = __builtin_nontemporal_load(b + g * 64);
       }
     };
     // NVFP4: the lane's scale dword of each tile, in a ring beside the tile ring
@@ -1326,11 +1338,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       // kept live across the work loop, where it would cost registers or a spill)
       int tk = topk, i0 = tid;
       asm volatile("" : "+s"(tk), "+v"(i0));
-      const int a = v / UPE2, b = v % UPE2;
+      const int a = v / UPE, b = v % UPE;
       const int r0 = s.aoff[a] + s0, n = s.aoff[a + 1] - r0;
-      for (int i = i0; i < 16 * RB2 && i / RB2 < n; i += FT)
-        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / RB2] < 0)   // (a token's only local route writes y itself)
-          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB2] / tk) * NBL2 + RB2 * b + i % RB2) * CNT_LINE], 1,
+      for (int i = i0; i < 16 * RB && i / RB < n; i += FT)
+        if (ACT == DGM_ACT_NVFP4 || s.ytok[r0 + i / RB] < 0)   // (a token's only local route writes y itself)
+          __hip_atomic_fetch_add(&comb[((s.routes[r0 + i / RB] / tk) * NBL2 + RB * b + i % RB) * CNT_LINE], 1,
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     // units v0 and G + v0 first, then claims (offset by 2 G)
@@ -1354,8 +1366,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       // probes of the L1 arrivals of the first two units' experts, answered while the L1
       // phase's last stores complete
       if (tid == 0 && q0 < U2) {
-        pr_a = __hip_atomic_load(&l1_done[(q0 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (q1 < U2) pr_n = __hip_atomic_load(&l1_done[(q1 / UPE2) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pr_a = __hip_atomic_load(&l1_done[(q0 / UPE) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (q1 < U2) pr_n = __hip_atomic_load(&l1_done[(q1 / UPE) * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       // the L1 phase's last unit: its stores have completed (every wave) -> its arrival, before
       // any wait on other workgroups' arrivals
@@ -1363,11 +1375,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= QN1 ? 1 : 0;
       __syncthreads();
       if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid == 0 && q0 < U2 && pr_a >= QN1) ready = q0 / UPE2;
+      if (tid == 0 && q0 < U2 && pr_a >= QN1) ready = q0 / UPE;
     }
     // (thread 0) the second unit's expert when its probe found it complete (LDS: read once, by
     // the first item's prefetch check)
-    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= QN1 ? q1 / UPE2 : -1;
+    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= QN1 ? q1 / UPE : -1;
     if (q0 < U2) {
       if (!handed) {          // (unit q0 = v0: handed over by the L1 phase otherwise)
         const uint8_t* b = tile_base(q0);
@@ -1386,11 +1398,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // (NVFP4 stages it at the item's start: measured no faster this way.)
     bool pre1 = false;
     if (ACT != DGM_ACT_NVFP4 && q0 < U2 && (!(p.phases & 1) || __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0)) {
-      load_slab(pre, q0 / UPE2, 0);
+      load_slab(pre, q0 / UPE, 0);
       pre1 = true;
     }
     while (q0 < U2) {
-      const int a = q0 / UPE2, b = q0 % UPE2;
+      const int a = q0 / UPE, b = q0 % UPE;
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const int key = (1 << 30) | (a << 16) | s0;
       if (pre1) {               // (the first item, its slab loaded before the loop)
@@ -1423,7 +1435,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
       const bool has_next = nq < U2;
-      const int na = has_next ? nq / UPE2 : -1;
+      const int na = has_next ? nq / UPE : -1;
       const int nkey = (1 << 30) | (na << 16) | ns0;
       // prefetch the next item's slab if it differs and its expert's L1 is complete
       bool pf = false;
@@ -1446,10 +1458,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (has_next && nq != q0) load_scales(nq, sn);
       // QoQ: the row scales s1 of the lane's 4 rows of each block, only used after the K loop
       // (so loaded for this item, here)
-      v4u s1r[ACT == DGM_ACT_QOQ ? RB2 : 1];
+      v4u s1r[ACT == DGM_ACT_QOQ ? RB : 1];
       if constexpr (ACT == DGM_ACT_QOQ) {
 #pragma unroll
-        for (int jb = 0; jb < RB2; ++jb)
+        for (int jb = 0; jb < RB; ++jb)
           s1r[jb] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w2r + (blk_of(q0) + jb) * 16 + 4 * kq));
       }
       // the unit after q1, claimed at the start of the item that finishes q0 (the value is read
@@ -1457,9 +1469,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (tid == 0 && last_slab && q1 < U2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
       // read from LDS two ops ahead
-      v4f acc[RB2];
+      v4f acc[RB];
 #pragma unroll
-      for (int j = 0; j < RB2; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < RB; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
       auto bfrag = [lane](int k) __attribute__((always_inline)) {
         return ACT == DGM_ACT_MXFP4 ? as_v8i(s.bst[k][lane][0]) : as_v8i(s.bst[k][lane][0], s.bst[k][lane][Smem::BV - 1]);
       };
@@ -1488,12 +1500,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             acc[jb][i] = fmaf(s2, v, acc[jb][i]);
           }
         };
-        static_for<TI2>([&](auto tc) {
+        static_for<TI>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr int k = t % KT2;
           v8i bop = bq0;
           bq0 = bq1;
-          if constexpr (t + 2 < TI2) bq1 = bfrag((t + 2) % KT2);
+          if constexpr (t + 2 < TI) bq1 = bfrag((t + 2) % KT2);
           if constexpr (t >= 2) after_values(bop, acc[(t - 2) / KT2]);   // (tile t - 2 promoted)
           const U4 w = wr[k];
           const v4i c0 = {(int)(w.x & 0x0F0F0F0Fu), (int)(w.y & 0x0F0F0F0Fu), (int)(w.z & 0x0F0F0F0Fu),
@@ -1502,21 +1514,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
                           (int)(w.w & 0xF0F0F0F0u)};
           const v4i a0 = mfma_i8_16x16x64(c0, lo4(bop), v4i{0, 0, 0, 0});
           const v4i a1 = mfma_i8_16x16x64(c1, hi4(bop), v4i{0, 0, 0, 0});
-          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, a1);
-          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, a1);
+          if constexpr (t + KT2 < TI) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, a1);
+          else wr[k] = ld_stream_after(nb, (t + KT2 - TI) * 1024, a1);
           if constexpr (t > 0) promote(std::integral_constant<int, (t - 1) / KT2>{}, p0, p1, md_n, qc_n);
           md_n = md_c;
           qc_n = qc_c;
-          if constexpr (t + 1 < TI2) {
+          if constexpr (t + 1 < TI) {
             md_c = qoq_meta<t + 1>(sd, kq);
             qc_c = s.qc[c][(t + 1) % KT2];
           }
           p0 = a0;
           p1 = a1;
         });
-        promote(std::integral_constant<int, (TI2 - 1) / KT2>{}, p0, p1, md_n, qc_n);
+        promote(std::integral_constant<int, (TI - 1) / KT2>{}, p0, p1, md_n, qc_n);
 #pragma unroll
-        for (int j = 0; j < RB2; ++j) {
+        for (int j = 0; j < RB; ++j) {
           acc[j][0] *= __uint_as_float(s1r[j].x);
           acc[j][1] *= __uint_as_float(s1r[j].y);
           acc[j][2] *= __uint_as_float(s1r[j].z);
@@ -1526,47 +1538,47 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         U4 bn[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) bn[j] = s.bst[0][lane][j];
-        static_for<TI2>([&](auto tc) {
+        static_for<TI>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr int j = t / KT2, k = t % KT2;
           U4 bc[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) bc[i] = bn[i];
-          if constexpr (t + 1 < TI2) {
+          if constexpr (t + 1 < TI) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) bn[i] = s.bst[(t + 1) % KT2][lane][i];
           }
           acc[j] = nvfp4_tile(wr[k], sr[k], bc, acc[j]);
-          if constexpr (t + KT2 < TI2) {
+          if constexpr (t + KT2 < TI) {
             wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
             sr[k] = ld_stream32_after(csb, (t + KT2) * 128, acc[j]);
           } else {
-            wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
-            sr[k] = ld_stream32_after(nsb, (t + KT2 - TI2) * 128, acc[j]);
+            wr[k] = ld_stream_after(nb, (t + KT2 - TI) * 1024, acc[j]);
+            sr[k] = ld_stream32_after(nsb, (t + KT2 - TI) * 128, acc[j]);
           }
         });
         const float gsc = s.gsl[1][s.act[a]];
 #pragma unroll
-        for (int j = 0; j < RB2; ++j)
+        for (int j = 0; j < RB; ++j)
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[j][i] *= gsc;
       } else {
         uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
-        static_for<TI2>([&](auto tc) {
+        static_for<TI>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr int j = t / KT2, k = t % KT2;
           const v8i bop = bq0;
           const uint32_t bsw = bs0;
           bq0 = bq1;
           bs0 = bs1;
-          if constexpr (t + 2 < TI2) {
+          if constexpr (t + 2 < TI) {
             bq1 = bfrag((t + 2) % KT2);
             bs1 = s.bsc[((t + 2) % KT2) >> 2][lane];
           }
           acc[j] = mfma_scale_16x16x128_sel<4, FB, k & 3, k & 3>(as_v8i(wr[k]), bop, acc[j],
                                                                  (int)sd[j * KG2 + (k >> 2)], (int)bsw);
-          if constexpr (t + KT2 < TI2) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
-          else wr[k] = ld_stream_after(nb, (t + KT2 - TI2) * 1024, acc[j]);
+          if constexpr (t + KT2 < TI) wr[k] = ld_stream_after(cb, (t + KT2) * 1024, acc[j]);
+          else wr[k] = ld_stream_after(nb, (t + KT2 - TI) * 1024, acc[j]);
         });
       }
       // all but this loop's KT2 youngest tile loads (and scale loads) are done: the previous
@@ -1574,18 +1586,18 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       wait_vm_le<ACT == DGM_ACT_NVFP4 ? 2 * KT2 : KT2>();
       if (s0 + c < n) {
         // each route's output rounded to bf16 (the reference's per-route rule), stored slot-major
-        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+        uint16_t* dst = p.partials + (size_t)s.prow[r0 + s0 + c] * H + (NW * RB * b + RB * wv) * 16 + 4 * kq;
 #pragma unroll
-        for (int j = 0; j < RB2; ++j)
+        for (int j = 0; j < RB; ++j)
           st_agent64(dst + 16 * j, (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
                                        ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48));
         // a token with no other local route: its y rows are this route's output (the combine of
         // one bf16 route output), written here; no arrival, no combine
         const int yt = ACT == DGM_ACT_NVFP4 ? -1 : s.ytok[r0 + s0 + c];
         if (yt >= 0) {
-          uint16_t* yd = p.y + (size_t)yt * H + (NW * RB2 * b + RB2 * wv) * 16 + 4 * kq;
+          uint16_t* yd = p.y + (size_t)yt * H + (NW * RB * b + RB * wv) * 16 + 4 * kq;
 #pragma unroll
-          for (int j = 0; j < RB2; ++j)
+          for (int j = 0; j < RB; ++j)
             *reinterpret_cast<uint64_t*>(yd + 16 * j) =
                 (uint64_t)f32_to_bf16(acc[j][0]) | ((uint64_t)f32_to_bf16(acc[j][1]) << 16) |
                 ((uint64_t)f32_to_bf16(acc[j][2]) << 32) | ((uint64_t)f32_to_bf16(acc[j][3]) << 48);
@@ -1623,6 +1635,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     wait_mem();               // the last item's outputs (and the dummy reads)
     __syncthreads();
     if (pv >= 0) arrive(pv, ps0);
+  };
+  if (p.phases & 2) {
+    if (halves) l2_phase(std::integral_constant<int, 1>{});
+    else l2_phase(std::integral_constant<int, RB2>{});
   }
   if (st && tid == 0) st[4] = wall_clock();
 

@@ -248,7 +248,9 @@ typedef struct DgmMoeArgs {
    * reporting (error counter, host_error) can be tested without a real failure. Bit 1 (QoQ, the
    * persistent kernel): phase_stamps receives the exact int32 L1 accumulators
    * (sum over K128 groups of s2 * sum (code - z) * x8, per route in pool order and W1 row, gate
-   * rows then up rows: int32 [routes][2 I]) instead of stamps, for bit-exact tests. */
+   * rows then up rows: int32 [routes][2 I]) instead of stamps, for bit-exact tests. Bit 2: the
+   * persistent kernel runs whole L2 units even where it would run half units (units filling at
+   * most half the grid), so tests cover both forms at small shapes. */
   int32_t debug_flags;
 } DgmMoeArgs;
 
