@@ -1663,14 +1663,30 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         // (y rows of tokens without a local route: zeroed by workgroup 0; with one: written by its
         // L2 unit, except NVFP4's)
         if (s.nslot[t] > DIRECT_Y) {
-          float s0 = 0.f, s1 = 0.f;
-          for (int sl = 0; sl < p.topk; ++sl)
-            if (s.exp_of_route[t * p.topk + sl] >= 0) {
-              const uint32_t v = __hip_atomic_load(
+          // every local route's two values are requested first (one round trip for all of
+          // them), then summed in slot order (fp32; a route of another rank adds nothing)
+          constexpr int MAXK = 16;                       // (topk <= 16, checked on the host)
+          const int tk = p.topk;
+          int ex[MAXK];                                  // (all read before any is tested)
+#pragma unroll
+          for (int sl = 0; sl < MAXK; ++sl) ex[sl] = s.exp_of_route[min(t * tk + sl, FUSED_MAX_ROUTES - 1)];
+          uint32_t v[MAXK], use = 0;
+#pragma unroll
+          for (int sl = 0; sl < MAXK; ++sl) {
+            v[sl] = 0u;
+            if (sl < tk && ex[sl] >= 0) {
+              use |= 1u << sl;
+              v[sl] = __hip_atomic_load(
                   reinterpret_cast<const uint32_t*>(p.partials + ((size_t)sl * p.part_rows + t) * H + row),
                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              s0 += __uint_as_float(v << 16);
-              s1 += __uint_as_float(v & 0xffff0000u);
+            }
+          }
+          float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+          for (int sl = 0; sl < MAXK; ++sl)
+            if ((use >> sl) & 1u) {
+              s0 += __uint_as_float(v[sl] << 16);
+              s1 += __uint_as_float(v[sl] & 0xffff0000u);
             }
           *reinterpret_cast<uint32_t*>(p.y + (size_t)t * H + row) =
               (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);

@@ -481,17 +481,32 @@ __global__ void k_combine(const uint16_t* __restrict__ partials, int part_rows, 
   const int t = blockIdx.y;
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (t >= M || n >= H) return;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  for (int s = 0; s < topk; ++s) {
-    int64_t g = topk_idx[(size_t)t * topk + s];
-    int64_t l = g - expert_begin;
-    if (g < 0 || l < 0 || l >= E_local) continue;
-    const uint2 v = *reinterpret_cast<const uint2*>(partials + ((size_t)s * part_rows + t) * H + n);
-    s0 += __uint_as_float(v.x << 16);
-    s1 += __uint_as_float(v.x & 0xffff0000u);
-    s2 += __uint_as_float(v.y << 16);
-    s3 += __uint_as_float(v.y & 0xffff0000u);
+  // every local route's values are loaded first (one round trip), then summed in slot order
+  // (fp32; a route of another rank adds nothing)
+  constexpr int MAXK = 16;                         // (topk <= 16, checked on the host)
+  uint2 v[MAXK];
+  uint32_t use = 0;
+#pragma unroll
+  for (int s = 0; s < MAXK; ++s) {
+    v[s] = make_uint2(0u, 0u);
+    if (s < topk) {
+      const int64_t g = topk_idx[(size_t)t * topk + s];
+      const int64_t l = g - expert_begin;
+      if (g >= 0 && l >= 0 && l < E_local) {
+        use |= 1u << s;
+        v[s] = *reinterpret_cast<const uint2*>(partials + ((size_t)s * part_rows + t) * H + n);
+      }
+    }
   }
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+  for (int s = 0; s < MAXK; ++s)
+    if ((use >> s) & 1u) {
+      s0 += __uint_as_float(v[s].x << 16);
+      s1 += __uint_as_float(v[s].x & 0xffff0000u);
+      s2 += __uint_as_float(v[s].y << 16);
+      s3 += __uint_as_float(v[s].y & 0xffff0000u);
+    }
   uint32_t lo = (uint32_t)f32_to_bf16(s0) | ((uint32_t)f32_to_bf16(s1) << 16);
   uint32_t hi = (uint32_t)f32_to_bf16(s2) | ((uint32_t)f32_to_bf16(s3) << 16);
   *reinterpret_cast<uint2*>(y + (size_t)t * H + n) = make_uint2(lo, hi);
