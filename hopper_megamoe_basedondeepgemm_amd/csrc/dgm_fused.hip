@@ -351,7 +351,10 @@ DGM_DEV bool spin_until2(const int* p, int target, int limit, int* err, int* her
 template <int KT, int ACT, bool COHERENT, class S, class RowOf>
 DGM_DEV void stage_slab(S& s, const uint8_t* __restrict__ src, const uint8_t* __restrict__ ssrc,
                         int row_bytes, int n, RowOf row_of) {
-  const int tid = threadIdx.x;
+  // (the thread index made opaque: the addresses below are computed here, not hoisted out of
+  // the item loop and kept live, or spilled, across it)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
   for (int f = tid; f < KT * 64; f += FT) {
     const int kt = f >> 6, l = f & 63, c = l & 15;
     uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
@@ -852,10 +855,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // an L2 unit's wait is only on L1 units already claimed by running workgroups, which never
   // wait.
   // L2 units span RB2 combine blocks (128 rows each): every wave streams RB2 16-row blocks.
-  // When the units fill at most half the grid, each is run as RB2 items of one block instead
-  // (halves; debug bit 2 keeps whole units). U2 counts the L2 items.
+  // Each unit runs as RB2 items of one block instead (halves; debug bit 2 keeps whole units)
+  // when the units fill at most half the grid, or (A-MXFP) when they fill more than one round
+  // and at most 1.5: the last round, half full or less, then takes half a unit's time (an extra
+  // item costs about as much as that saves beyond two rounds). U2 counts the L2 items.
   constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2;
-  const bool halves = RB2 == 2 && 2 * n_active * UPE2 <= (int)gridDim.x && !(p.debug & 4);
+  constexpr bool WIDE = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8;
+  const int u2w = n_active * UPE2, G2 = (int)gridDim.x;
+  const bool halves = RB2 == 2 && (2 * u2w <= G2 || (WIDE && u2w > G2 && 2 * (u2w - G2) <= G2)) && !(p.debug & 4);
   const int U1 = n_active * QN1, U2 = n_active * (halves ? NBL2 : UPE2);
   // This workgroup's first L2 unit (its second is G + v0)
   const int v0 = (int)blockIdx.x;

@@ -64,3 +64,37 @@ def test_half_items_match_whole_units(fmt, M, E):
     assert torch.equal(s0, s1)
     # route outputs (slot-major bf16 rows) of the routes that were computed, both ways
     assert torch.equal(p0.view(torch.int16), p1.view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+def test_half_items_past_one_round(fmt):
+    """A-MXFP also runs halves when the units fill more than one round of the grid and at most
+    1.5 (the last round half full or less): 160 experts forced-balanced at H=512 give 320 units,
+    640 half items, so items are claimed beyond the first two per workgroup. Bit for bit equal
+    to whole units."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    M, E = 40, 160
+    print(f"L2 halves past one round fmt={fmt} M={M} E={E}", flush=True)
+    rng = np.random.default_rng(7200 + len(fmt))
+    t1, t2 = _weights(fmt, E, 7201)
+    x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    out = []
+    for flags in (0, 4):
+        b = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=fmt)
+        b._debug_flags = flags
+        y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        stats = torch.zeros(E, dtype=torch.int32, device="cuda")
+        dgm.fable_router_quant_topk_frontend(x, rw, b, select_in_mega=True, force_balanced=True)
+        _fused(dgm, fmt, y, t1, t2, b, stats)
+        torch.cuda.synchronize()
+        assert b.kernel_error() == 0 and b.host_error() == 0
+        n_active = int((b.pool_table()[0] > 0).sum())
+        out.append((y.clone(), b.combine_partials[:, :M].clone(), stats.clone(), n_active))
+    (y0, p0, s0, na), (y1, p1, s1, _) = out
+    units = na * (H // 256)
+    assert 256 < units <= 384, (units, "more than one round, at most 1.5")
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(s0, s1)
+    assert torch.equal(p0.view(torch.int16), p1.view(torch.int16))
