@@ -1291,9 +1291,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // outputs (bf16) go to `partials`; one item later, when they have completed, each route
   // bumps the arrival counters of its (token, 128-row block)s (no return value).
   // The L2 phase for items of RB 128-row blocks (every wave streams RB 16-row blocks of each):
-  // whole units (RB = RB2) or, when the units fill at most half the grid, halves (RB = 1) so
-  // that all of them run at once on twice as many workgroups; one or the other per launch, each
-  // its own code (no branch inside the K loops).
+  // whole units (RB = RB2) or halves (RB = 1, by the rule above), one or the other per launch,
+  // each its own code (no branch inside the K loops).
   auto l2_phase = [&](auto rb_c) __attribute__((always_inline)) {
     constexpr int RB = decltype(rb_c)::value, UPE = NBL2 / RB, TI = RB * KT2;
     static_assert(KT2 <= 16, "L2 ring of KT2 tile registers");
