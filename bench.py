@@ -49,6 +49,72 @@ def profiled_traffic_bytes():
     return None
 
 
+def profiled_mfma_util(kernel="k_megamoe<24,10,1,false>", workload=("M=8", "A-MXFP8")):
+    """Matrix-core busy fraction of the fused kernel at the headline workload, from the committed
+    rocprofv3 counter summary (SQ_VALU_MFMA_BUSY_CYCLES over all SIMD cycles), or None."""
+    path = os.path.join(HERE, "profiles", "k_megamoe_E384_mfma_valu_counters.txt")
+    try:
+        for ln in open(path):
+            f = ln.split()
+            if len(f) >= 8 and f[0] == kernel and tuple(f[1:3]) == workload:
+                return float(f[7])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
+    """Per-workgroup phase stamps of the fused kernel (its phase_stamps output: 100 MHz wall
+    clock at entry, dispatch table ready, L1 units done, first L1 arrival observed by the L2
+    phase, L2 units done, exit; plus the L1 K-loop and epilogue ticks): for each workload the
+    launch with the median event time of `reps`, each after a cache eviction, printed as
+    min / p10 / median / p90 / max over the workgroups in us from the earliest entry."""
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    flush_rd = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
+    names = ("entry", "dispatch ready", "L1 done", "first L1 seen", "L2 done", "exit")
+    for M, ep, act in ((2, 1, "mxfp8"), (8, 1, "mxfp8"), (16, 1, "mxfp8"), (8, 8, "mxfp4")):
+        w = share if ep > 1 else weights
+        buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act, ep_size=ep, ep_rank=0)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(4000 + M)
+        x = torch.randn((M, H), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        st = torch.zeros((1024, 8), dtype=torch.int64, device="cuda")
+        runs = []
+        for _ in range(reps):
+            flush.fill_(1)
+            flush_rd.sum()
+            dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=True, select_in_mega=True)
+            st.zero_()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            dgm.mxfp4_mega_moe_fused(y, w[0], w[1], buf, phase_stamps=st)
+            e1.record()
+            torch.cuda.synchronize()
+            runs.append((e0.elapsed_time(e1) * 1e3, st.clone()))
+        runs.sort(key=lambda r: r[0])
+        ev, st = runs[len(runs) // 2]
+        G = dgm.mega.fused_workgroups(buf)
+        a = st[:G].cpu().numpy().astype(np.float64)
+        t0 = a[:, 0].min()
+        n_active = int((buf.pool_table()[0] > 0).sum())
+        print(f"M={M} ep_share={ep} A-{act.upper()} active experts {n_active}, {G} workgroups, kernel "
+              f"{ev:.1f} us by events; us from the earliest entry (min / p10 / median / p90 / max):")
+        for c, nm in enumerate(names):
+            v = a[:, c]
+            v = (v[v > 0] - t0) / 100.0 if c == 3 else (v - t0) / 100.0    # (0: never waited)
+            if len(v):
+                q = np.percentile(v, [0, 10, 50, 90, 100])
+                print(f"  {nm:15s}" + "".join(f" {x:7.2f}" for x in q))
+        k = a[:, 6][a[:, 6] > 0] / 100.0
+        e = a[:, 7][a[:, 6] > 0] / 100.0
+        if len(k):
+            print(f"  per workgroup with L1 work: L1 K loops {np.median(k):.2f} us (median), "
+                  f"L1 epilogues {np.median(e):.2f} us (median)")
+        sys.stdout.flush()
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -314,6 +380,8 @@ def main():
     ap.add_argument("--no-unbalanced", action="store_true")
     ap.add_argument("--no-c1", action="store_true", help="skip the config 1 line (one EP rank's 48 experts)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="print the fused kernel's per-workgroup phase stamps (M=2/8/16, config 1) and exit")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (HBM counter scaling)")
     args = ap.parse_args()
@@ -328,6 +396,10 @@ def main():
     weights, packed = build_weights(torch, 1234, E)
     g = torch.Generator(device="cuda")
     g.manual_seed(99)
+    if args.phase_stamps:
+        router_w0 = (torch.randn((E, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+        phase_stamps_report(torch, dgm, weights, router_w0)
+        return
     router_w = (torch.randn((E, H), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
 
     def entry(r):
@@ -409,6 +481,10 @@ def main():
                      "traffic": profiled_traffic_bytes() if (args.m == 8 and args.act == "mxfp8") else None,
                      "kernel": "k_megamoe (fused persistent MoE kernel); achieved = active-expert MXFP4 weight "
                                "bytes (6,266,880 B per expert) / median kernel time (HIP events)"},
+        "mfma_util": {"value": profiled_mfma_util() if (args.m == 8 and args.act == "mxfp8") else None,
+                      "what": "SQ_VALU_MFMA_BUSY_CYCLES / all SIMD cycles of k_megamoe at this workload "
+                              "(rocprofv3 counters, profiles/k_megamoe_E384_mfma_valu_counters.txt): the "
+                              "layer is HBM-bound, the matrix cores mostly idle"},
         "cpu_baseline": cpu,
         "parity": parity,
     }
