@@ -1,6 +1,6 @@
 """Benchmark of the MI355X MegaMoE layer (one GPU).
 
-Headline workload = BASELINE config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
+Headline workload = benchmark config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
 layer forward from bf16 hidden states: the frontend launch (router + activation cast), then the
 fused kernel: top-8 in its prologue, dispatch, L1, L2, combine). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
@@ -418,7 +418,7 @@ def main():
             sweep[act][M] = entry(r)
             log(f"M={M} {act}: {sweep[act][M]}")
     if not args.no_c1:
-        # one EP rank's share (local experts 0-47 of the 384-way router),
+        # benchmark config 1: one EP rank's share (local experts 0-47 of the 384-way router),
         # W-MXFP4 x A-MXFP4, M=8 forced-balanced: 8 rows on 8 local experts
         share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
         r = time_layer(torch, dgm, 8, share, router_w, "mxfp4", args.sweep_steps, args.warmup, 508, ep_size=8)
@@ -471,7 +471,7 @@ def main():
         "ms_per_step": round(us / 1e3, 5), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "mxfp4xmxfp8" if args.act == "mxfp8" else "mxfp4xmxfp4",
         "data": "synthetic: seeded randn bf16 weights packed to MXFP4 on the GPU, forced-balanced routing",
-        "config": {"workload": f"E384 layer on one GPU (BASELINE config 2), W-MXFP4 x A-{args.act.upper()}, "
+        "config": {"workload": f"E384 layer on one GPU (benchmark config 2), W-MXFP4 x A-{args.act.upper()}, "
                                f"M={args.m}, forced-balanced; value = frontend + fused MoE kernel",
                    "M": args.m, "experts": E, "hidden": H, "intermediate": I, "topk": TOPK,
                    "active_experts": main_r["n_active"], "frontend_us": round(main_r["fe_us"], 2),

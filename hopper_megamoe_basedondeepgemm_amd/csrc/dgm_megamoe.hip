@@ -711,10 +711,13 @@ static int materialize_topk(const DgmMoeArgs* A, uint8_t* buf, const DgmBufferLa
 // Every workgroup of the fused kernel reads all tokens' logits when it selects the top-k; that
 // costs ~1 us of SIMD time per token and workgroup (the selection rounds are sequential), so
 // above SELECT_IN_MEGA_FAST_TOKENS a separate selection launch (one wave per token over the
-// whole GPU) comes first and the fused kernel reads the result. The in-kernel frontend
+// whole GPU) comes first and the fused kernel reads the result. Forced-balanced routing scans
+// no keys, so it is selected in the kernel up to SELECT_IN_MEGA_FAST_BALANCED tokens (at 16
+// tokens 0.5-1.4 us less than the extra launch; at 32 and 64 no gain). The in-kernel frontend
 // (fe_in_mega) selects in the kernel up to SELECT_IN_MEGA_MAX_TOKENS.
 constexpr int SELECT_IN_MEGA_MAX_TOKENS = 64;
 constexpr int SELECT_IN_MEGA_FAST_TOKENS = 8;     // (one token per wave)
+constexpr int SELECT_IN_MEGA_FAST_BALANCED = 16;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
   if (A && A->act_format == DGM_ACT_FP8F128) return dgm_megamoe_split_launch(A, stream);
@@ -781,8 +784,8 @@ int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, 
   const DgmBufferLayout* L = A->layout;
   uint8_t* buf = (uint8_t*)A->buffer;
   {
-    const bool sel = (A->fe_in_mega || (A->select_in_mega && A->num_tokens <= SELECT_IN_MEGA_FAST_TOKENS)) &&
-                     (phases & 1);
+    const int fast = (A->fe_flags & DGM_FE_FORCE_BALANCED) ? SELECT_IN_MEGA_FAST_BALANCED : SELECT_IN_MEGA_FAST_TOKENS;
+    const bool sel = (A->fe_in_mega || (A->select_in_mega && A->num_tokens <= fast)) && (phases & 1);
     if (A->select_in_mega && !sel && (phases & 1)) {
       int st = materialize_topk(A, buf, L, stream);
       if (st) return st;

@@ -1,4 +1,4 @@
-"""GPU parity at the timed workloads, at full size: BASELINE config 2 (all 384 experts resident,
+"""GPU parity at the timed workloads, at full size: benchmark config 2 (all 384 experts resident,
 W-MXFP4 x A-MXFP8 and x A-MXFP4, M=8 forced-balanced and M=16 seeded unbalanced routing),
 config 3 (QoQ W4A8, M=8 forced-balanced) and config 4 (NVFP4 W4A4, M=16 and M=64 seeded
 unbalanced), through the calls the bench makes: ``fable_router_quant_topk_frontend(...,

@@ -119,7 +119,7 @@ def test_small_layer(fmt):
 
 @pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8"])
 def test_config0_shape(fmt):
-    """E=48, H=3072, I=1280, top-8, M=2, real (unbalanced) routing."""
+    """benchmark config 0: E=48, H=3072, I=1280, top-8, M=2, real (unbalanced) routing."""
     need_gpu()
     r = run_layer(2, 48, 48, 0, 3072, 1280, 8, fmt, seed=200)
     check_frontend(r, fmt, 2)
@@ -128,7 +128,7 @@ def test_config0_shape(fmt):
 
 
 def test_config1_ep_share():
-    """384-way router, forced-balanced, one EP rank's share (experts 0..47)
+    """benchmark config 1: 384-way router, forced-balanced, one EP rank's share (experts 0..47)
     on one GPU, M=8 -> 8 rows over 48 local experts, output = the local partial."""
     need_gpu()
     r = run_layer(8, 384, 48, 0, 3072, 1280, 8, "mxfp4", seed=300, force_balanced=True)
@@ -205,11 +205,14 @@ def test_select_in_mega_zero_rows_multi_slab_and_split():
         print(split, check_y(r, zero_rows=(3, 17)))
 
 
-def test_select_in_mega_config1_balanced():
-    """BASELINE config 1 with the forced-balanced rule applied in the fused kernel's prologue."""
+@pytest.mark.parametrize("M", [8, 16])
+def test_select_in_mega_config1_balanced(M):
+    """benchmark config 1 with the forced-balanced rule applied in the fused kernel's prologue
+    (forced-balanced routing is selected there up to 16 tokens, real top-k up to 8)."""
     need_gpu()
-    r = run_layer(8, 384, 48, 0, 3072, 1280, 8, "mxfp4", seed=300, force_balanced=True, select_in_mega=True)
-    check_frontend(r, "mxfp4", 8, force_balanced=True)
+    print(f"select_in_mega config 1 balanced M={M}", flush=True)
+    r = run_layer(M, 384, 48, 0, 3072, 1280, 8, "mxfp4", seed=300 + M, force_balanced=True, select_in_mega=True)
+    check_frontend(r, "mxfp4", M, force_balanced=True)
     check_pool(r, 48, 0)
     print(check_y(r))
 

@@ -161,7 +161,7 @@ def test_qoq_small_layer():
 
 
 def test_qoq_config0_shape():
-    """BASELINE config 0 shape (E=48, H=3072, I=1280, top-8, M=2) on the QoQ path."""
+    """benchmark config 0 shape (E=48, H=3072, I=1280, top-8, M=2) on the QoQ path."""
     need_gpu()
     r = run_qoq(2, 48, 48, 0, 3072, 1280, 8, seed=710)
     check_frontend(r, 2)
