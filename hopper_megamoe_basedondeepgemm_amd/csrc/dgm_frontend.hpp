@@ -34,22 +34,12 @@ DGM_DEV void put64(uint64_t* p, uint64_t v) {
 // fixed order, so the fp32 logits are reproducible bit for bit. Writes the fp32 logit and the
 // top-k key (topk_key: orderable bf16 << 16 | 0xFFFF - e); with zero_unrouted, the keys of an
 // all-zero hidden row are 0 (the token is unrouted).
+// The logits of expert e (its router row wv, lane l holding K = 512 j + 8 l .. +7) for the four
+// token rows xv (laid out the same way), in the order stated above; rows t0 + tt >= M are not
+// written.
 template <int J, bool AGENT>
-DGM_DEV void router_wave(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int M, int E, int e,
-                         int t0, int lane, float* __restrict__ logits, uint32_t* __restrict__ keys,
-                         bool zero_unrouted) {
-  constexpr int H = J * 512;
-  uint4 wv[J];
-  const int ee = e < E ? e : E - 1;
-#pragma unroll
-  for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const uint4*>(w + (size_t)ee * H + 512 * j + 8 * lane);
-  uint4 xv[4][J];
-#pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const int t = t0 + tt < M ? t0 + tt : M - 1;
-#pragma unroll
-    for (int j = 0; j < J; ++j) xv[tt][j] = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 512 * j + 8 * lane);
-  }
+DGM_DEV void router_dot4(const uint4 (&wv)[J], const uint4 (&xv)[4][J], int M, int E, int e, int t0, int lane,
+                         float* __restrict__ logits, uint32_t* __restrict__ keys, bool zero_unrouted) {
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     float acc = 0.f;
@@ -73,6 +63,64 @@ DGM_DEV void router_wave(const uint16_t* __restrict__ x, const uint16_t* __restr
       put32<AGENT>(reinterpret_cast<uint32_t*>(logits) + o, __float_as_uint(acc));
       put32<AGENT>(keys + o, unrouted ? 0u : topk_key(acc, e));
     }
+  }
+}
+
+template <int J, bool AGENT>
+DGM_DEV void router_wave(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int M, int E, int e,
+                         int t0, int lane, float* __restrict__ logits, uint32_t* __restrict__ keys,
+                         bool zero_unrouted) {
+  constexpr int H = J * 512;
+  uint4 wv[J];
+  const int ee = e < E ? e : E - 1;
+#pragma unroll
+  for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const uint4*>(w + (size_t)ee * H + 512 * j + 8 * lane);
+  uint4 xv[4][J];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = t0 + tt < M ? t0 + tt : M - 1;
+#pragma unroll
+    for (int j = 0; j < J; ++j) xv[tt][j] = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 512 * j + 8 * lane);
+  }
+  router_dot4<J, AGENT>(wv, xv, M, E, e, t0, lane, logits, keys, zero_unrouted);
+}
+
+// Router tile of a 256-thread workgroup for larger batches: the hidden rows of tokens
+// t0 .. t0 + RT - 1 (clamped to M - 1) are staged in LDS once (xs: RT * J * 64 uint4) and wave w
+// computes expert e0 + w for all of them from its router row in registers, four tokens at a
+// time: each router row is read once per RT tokens and each hidden row once per four experts
+// (the one-wave path reads the hidden rows once per expert). Same order of operations as
+// router_wave, so the same bits.
+template <int J, int RT, bool AGENT>
+DGM_DEV void router_tile(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int M, int E, int e0,
+                         int t0, float* __restrict__ logits, uint32_t* __restrict__ keys, bool zero_unrouted,
+                         uint4* __restrict__ xs) {
+  constexpr int H = J * 512, RV = RT * J * 64;       // uint4 per tile
+  static_assert(RT % 4 == 0 && RV % 256 == 0, "tile of 4-token groups, whole rounds of 256 threads");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int e = e0 + wave, ee = e < E ? e : E - 1;
+  uint4 wv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) wv[j] = *reinterpret_cast<const uint4*>(w + (size_t)ee * H + 512 * j + 8 * lane);
+  uint4 st[RV / 256];
+#pragma unroll
+  for (int i = 0; i < RV / 256; ++i) {
+    const int v = 256 * i + tid, tt = v / (J * 64), c = v % (J * 64);
+    const int t = t0 + tt < M ? t0 + tt : M - 1;
+    st[i] = *reinterpret_cast<const uint4*>(x + (size_t)t * H + 8 * c);
+  }
+#pragma unroll
+  for (int i = 0; i < RV / 256; ++i) xs[256 * i + tid] = st[i];
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < RT / 4; ++g) {
+    uint4 xv[4][J];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) xv[tt][j] = xs[(4 * g + tt) * (J * 64) + 64 * j + lane];
+    }
+    router_dot4<J, AGENT>(wv, xv, M, E, e, t0 + 4 * g, lane, logits, keys, zero_unrouted);
   }
 }
 

@@ -55,21 +55,33 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
 }
 
 // ------------------------------------------------------------------ frontend
-// Router rows of the grid (by < ceil(M / 4)): wave w of workgroup (bx, by) computes the logits
-// and top-k keys of expert 4 bx + w for tokens 4 by .. +3 (router_wave: fixed accumulation
-// order, bit-reproducible fp32 logits; zero keys for an all-zero row when zero_unrouted). Cast rows (the rest of the grid, running beside the router rows rather than after
-// them): MXFP4 / MXFP8 8 lanes per 32-element group, NVFP4 4 lanes per 16-element group, QoQ
-// one wave per token (dgm_frontend.hpp).
-template <int J>
+// Router rows of the grid (by < ceil(M / RTOK)): workgroup (bx, by) computes the logits and
+// top-k keys of experts 4 bx .. +3 for tokens RTOK by .. +RTOK - 1 (fixed accumulation order,
+// bit-reproducible fp32 logits; zero keys for an all-zero row when zero_unrouted): RT = 0, one
+// wave per expert over 4 tokens (router_wave, RTOK = 4); RT > 0, the RT tokens' hidden rows
+// staged in LDS and shared by the four waves (router_tile, RTOK = RT; the same bits). Cast rows
+// (the rest of the grid, running beside the router rows rather than after them): MXFP4 / MXFP8
+// 8 lanes per 32-element group, NVFP4 4 lanes per 16-element group, QoQ one wave per token
+// (dgm_frontend.hpp).
+// Tiled router rows from 64 tokens on (MI355X, E384 H3072, kernel + launch by events: 64 tokens
+// 13.7 us against 15.2, 128 tokens 24.0 against 26.8; at 16 and 32 tokens the LDS staging and
+// its barrier cost 1.1-1.7 us more than the hidden-row reads they save).
+constexpr int FE_ROUTER_TILE = 8;         // tokens per router workgroup in the tiled form
+constexpr int FE_TILE_MIN_TOKENS = 64;
+template <int J, int RT>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
                                                   uint32_t* __restrict__ keys, int zero_unrouted,
                                                   uint8_t* __restrict__ q, uint8_t* __restrict__ sf, int router) {
-  constexpr int H = J * 512;
+  constexpr int H = J * 512, RTOK = RT > 0 ? RT : 4;
+  __shared__ uint4 xs[RT > 0 ? RT * J * 64 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ry = router ? (M + 3) / 4 : 0;
+  const int ry = router ? (M + RTOK - 1) / RTOK : 0;
   if ((int)blockIdx.y < ry) {
-    router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, keys, zero_unrouted != 0);
+    if constexpr (RT > 0)
+      router_tile<J, RT, false>(x, w, M, E, blockIdx.x * 4, blockIdx.y * RT, logits, keys, zero_unrouted != 0, xs);
+    else
+      router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, keys, zero_unrouted != 0);
     return;
   }
   const int cy = (int)gridDim.y - ry, by = (int)blockIdx.y - ry;
@@ -646,15 +658,21 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
                                                                : (int64_t)num_tokens * (hidden / 32) * 8;
   const int64_t cast_rows = (flags & DGM_FE_NO_CAST) ? 0 : (cast_threads + (int64_t)rx * 256 - 1) / ((int64_t)rx * 256);
   const int router = router_weight_bf16 ? 1 : 0;
-  dim3 rg(rx, (router ? (num_tokens + 3) / 4 : 0) + (int)cast_rows);
+  const bool tiled = num_tokens >= FE_TILE_MIN_TOKENS;
+  const int rtok = tiled ? FE_ROUTER_TILE : 4;
+  dim3 rg(rx, (router ? (num_tokens + rtok - 1) / rtok : 0) + (int)cast_rows);
   const uint16_t* x = (const uint16_t*)hidden_bf16;
   const uint16_t* w = (const uint16_t*)router_weight_bf16;
   float* logits = (float*)(buf + L->logits);
   uint32_t* keys = (uint32_t*)(buf + L->fe_keys);
   const int zero_unrouted = (flags & DGM_FE_ZERO_ROW_UNROUTED) ? 1 : 0;
-#define DGM_FE(JJ)                                                                                              \
-  hipLaunchKernelGGL(k_frontend<JJ>, rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, act_format, logits, \
-                     keys, zero_unrouted, buf + L->x, buf + L->x_sf, router)
+#define DGM_FE(JJ)                                                                                           \
+  if (tiled)                                                                                                 \
+    hipLaunchKernelGGL((k_frontend<JJ, FE_ROUTER_TILE>), rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, \
+                       act_format, logits, keys, zero_unrouted, buf + L->x, buf + L->x_sf, router);         \
+  else                                                                                                       \
+    hipLaunchKernelGGL((k_frontend<JJ, 0>), rg, dim3(256), 0, stream, x, w, num_tokens, num_experts,            \
+                       act_format, logits, keys, zero_unrouted, buf + L->x, buf + L->x_sf, router)
   switch (J) {
     case 1: DGM_FE(1); break;
     case 2: DGM_FE(2); break;

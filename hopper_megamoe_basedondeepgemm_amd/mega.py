@@ -282,6 +282,7 @@ def transform_weights_for_mega_moe(l1, l2):
 
 # ----------------------------------------------------------------------------- frontend
 SELECT_IN_MEGA_MAX_TOKENS = 64    # every workgroup of the fused kernel reads all tokens' logits
+FE_ROUTER_TILE_MIN_TOKENS = 64    # the frontend's router rows of 8 tokens (csrc FE_TILE_MIN_TOKENS)
 # csrc/fable_frontend.h kFEPath* (deep_gemm/mega/__init__.py:593): the launch-shape families of the
 # reference's frontend. Here one router kernel serves every shape; fable_frontend_path names the
 # family whose options apply (FE_PATH_CC: select_in_mega and zero-row unrouting available).
@@ -298,8 +299,9 @@ def fable_frontend_path(m: int, h: int = 3072, e: int = 384, topk: int = 8) -> i
 
 def fable_frontend_router_ctas(m: int, e: int, h: int = 3072, topk: int = 8) -> int:
     """deep_gemm/mega/__init__.py:653: router workgroups of the frontend launch for (m, h, e,
-    topk): one wave per (expert, 4 tokens), four waves per workgroup."""
-    return ((e + 3) // 4) * ((m + 3) // 4)
+    topk): four experts per workgroup (one wave each) over 4 tokens, or over 8 tokens from
+    FE_ROUTER_TILE_MIN_TOKENS on (the 8 hidden rows staged in LDS and shared by the waves)."""
+    return ((e + 3) // 4) * ((m + 7) // 8 if m >= FE_ROUTER_TILE_MIN_TOKENS else (m + 3) // 4)
 
 
 def fable_frontend_workspace_bytes(e: int, max_tokens: int = 64) -> int:

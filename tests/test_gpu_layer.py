@@ -217,6 +217,34 @@ def test_select_in_mega_config1_balanced(M):
     print(check_y(r))
 
 
+@pytest.mark.parametrize("M,E,H", [(64, 48, 3072), (77, 48, 3072), (130, 20, 512)])
+def test_frontend_router_tiles(M, E, H):
+    """From 64 tokens on the frontend's router workgroups stage 8 hidden rows in LDS and share
+    them over four experts: logits and keys bit-exact against the oracle as on the one-wave
+    path, including a ragged last tile (rows past M clamped, not written), zero rows and an
+    expert count that is not a multiple of four; top-k, weights and activation codes too."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    print(f"frontend router tiles M={M} E={E} H={H}", flush=True)
+    rng = np.random.default_rng(5100 + M)
+    x = randn_bf16(rng, (M, H))
+    zero_rows = (0, M - 1, M // 2)
+    for r in zero_rows:
+        x[r] = 0.0
+    rw = randn_bf16(rng, (E, H), 0.02)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, 8, H, 256, act_format="mxfp4")
+    dgm.fable_router_quant_topk_frontend(bf16_cpu(x).cuda(), bf16_cpu(rw).cuda(), buf)
+    torch.cuda.synchronize()
+    logits = moe.router_logits_f32(x, rw)
+    idx, w, _ = moe.topk_softmax(logits, 8)
+    for r in zero_rows:
+        idx[r] = -1
+        w[r] = 0.0
+    codes, sfb, _ = moe.quant_act(x, "mxfp4")
+    check_frontend(dict(buf=buf, logits=logits, idx=idx, w=w, codes=codes, sfb=sfb), "mxfp4", M,
+                   zero_rows=zero_rows)
+
+
 def test_large_batch_beyond_fused_limits():
     """200 tokens at top-8: 1600 routes exceed the persistent kernel's 1024, so the fused entry
     point runs the split path (dispatch, L1, L2, combine kernels); frontend, pool and y as

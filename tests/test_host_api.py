@@ -29,6 +29,9 @@ def test_frontend_path_and_router_workgroups():
     assert mega.fable_frontend_path(65) == mega.FE_PATH_WMMA
     assert mega.fable_frontend_router_ctas(8, 384) == 96 * 2
     assert mega.fable_frontend_router_ctas(1, 48) == 12
+    assert mega.fable_frontend_router_ctas(63, 384) == 96 * 16
+    assert mega.fable_frontend_router_ctas(64, 384) == 96 * 8
+    assert mega.fable_frontend_router_ctas(100, 48) == 12 * 13
 
 
 def test_router_weight_fragment_layout_inverse():
