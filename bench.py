@@ -307,7 +307,7 @@ def _dequant_active(packed, experts, workers=16):
     return dict(zip(experts, ws))
 
 
-def cpu_baseline_and_parity(packed, headline, router_w, M, act, reps=150):
+def cpu_baseline_and_parity(packed, headline, router_w, M, act, reps=400):
     """The oracle (oracle/moe.py, numpy fp32) on the headline step's own inputs (its bf16 hidden
     states, router weights and packed weights, forced-balanced routing): the step's parity (top-k
     and activation codes bit-exact, y against the oracle's y: min per-row cos, rel-RMSE), and the
