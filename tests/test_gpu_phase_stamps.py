@@ -1,0 +1,59 @@
+"""The fused kernel's phase stamps (the reference's phase_stamps facility: per workgroup, 100 MHz
+wall clock at entry, dispatch table ready, L1 units done, the first L1 arrival the L2 phase
+waited for, L2 units done, exit; then the wall ticks of the L1 K loops and of the L1
+epilogues). Every workgroup of the launch writes its row; the stamps of a row are in phase
+order, the two tick sums fit inside the row's span, and stamping does not change the output
+(y and the recv stats bit for bit against the same call without stamps)."""
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+H, I, TOPK = 512, 256, 4
+
+
+@pytest.mark.parametrize("M,E", [(12, 16), (40, 160)])
+@pytest.mark.parametrize("fmt", ["mxfp8", "qoq"])
+def test_phase_stamps_ordered_and_harmless(fmt, M, E):
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests.test_gpu_l2_halves import _weights, _fused
+    print(f"phase stamps fmt={fmt} M={M} E={E}", flush=True)
+    rng = np.random.default_rng(7400 + M + len(fmt))
+    t1, t2 = _weights(fmt, E, 7401 + M)
+    x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    out = []
+    for stamped in (False, True):
+        b = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=fmt)
+        y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        stats = torch.zeros(E, dtype=torch.int32, device="cuda")
+        dgm.fable_router_quant_topk_frontend(x, rw, b, select_in_mega=True)
+        st = torch.zeros((2048, 8), dtype=torch.int64, device="cuda") if stamped else None
+        if fmt == "qoq":
+            dgm.qoq_mega_moe_fused(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, phase_stamps=st)
+        else:
+            dgm.mxfp4_mega_moe_fused(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, phase_stamps=st)
+        torch.cuda.synchronize()
+        assert b.kernel_error() == 0 and b.host_error() == 0
+        out.append((y.clone(), stats.clone(), st, dgm.mega.fused_workgroups(b)))
+    (y0, s0, _, _), (y1, s1, st, G) = out
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    assert torch.equal(s0, s1)
+    a = st.cpu().numpy()
+    assert 0 < G <= a.shape[0]
+    rows, rest = a[:G], a[G:]
+    assert (rest == 0).all(), "rows past the grid are left alone"
+    entry, ready, l1, seen, l2, ex = (rows[:, i] for i in range(6))
+    assert (entry > 0).all()
+    assert (ready >= entry).all() and (l1 >= ready).all() and (l2 >= l1).all() and (ex >= l2).all()
+    w = seen > 0
+    assert ((seen[w] >= ready[w]) & (seen[w] <= ex[w])).all()
+    span = ex - entry
+    assert (rows[:, 6] >= 0).all() and (rows[:, 7] >= 0).all()
+    assert (rows[:, 6] + rows[:, 7] <= span).all()
+    # the launch's workgroups run at once: every one enters before any exits
+    assert entry.max() <= ex.min()
