@@ -636,7 +636,7 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
 int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16, int num_tokens,
                            int hidden, int num_experts, int topk, int act_format, int flags,
                            int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
-  DGM_CHECK_ARG(hidden_bf16 && buffer && L, "null pointer");
+  DGM_CHECK_ARG(buffer && L && (hidden_bf16 || num_tokens == 0), "null pointer");   // (no tokens: no rows)
   DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
   DGM_CHECK_ARG(num_experts <= 1024, "num_experts <= 1024");
@@ -692,7 +692,7 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
 
 int dgm_router_logits_topk_launch(const void* logits_bf16, int num_tokens, int num_experts, int topk, int flags,
                                   int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
-  DGM_CHECK_ARG(logits_bf16 && buffer && L, "null pointer");
+  DGM_CHECK_ARG(buffer && L && (logits_bf16 || num_tokens == 0), "null pointer");
   DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
   DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts <= 1024");
@@ -752,7 +752,7 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
 }  // extern "C"
 
 int dgm_check_fused_args(const DgmMoeArgs* A) {
-  DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
+  DGM_CHECK_ARG(A && A->buffer && A->layout && (A->y || A->num_tokens == 0), "null pointer");
   DGM_CHECK_ARG(A->w1_values && A->w1_scales && A->w2_values && A->w2_scales, "null weights");
   const DgmBufferLayout* L = A->layout;
   DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
@@ -859,7 +859,7 @@ int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, 
 extern "C" {
 
 int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
-  DGM_CHECK_ARG(A && A->buffer && A->layout && A->y, "null pointer");
+  DGM_CHECK_ARG(A && A->buffer && A->layout && (A->y || A->num_tokens == 0), "null pointer");
   DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG(!A->fe_in_mega, "split path: fe_in_mega is a fused-launch option");
   if (A->act_format == DGM_ACT_QOQ || A->act_format == DGM_ACT_NVFP4) {

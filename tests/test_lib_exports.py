@@ -48,6 +48,21 @@ def test_host_checks_and_layout():
     assert L.partials + 128 * 3072 * 2 <= L.counters        # bf16 [topk, max_tokens, H]
 
 
+def test_empty_batch_and_null_rows():
+    """No tokens: the frontend entry points return 0 before any GPU work, with no row pointers
+    (an empty tensor has none); with tokens, a missing row pointer is an error."""
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    lib = _lib.load()
+    L = _lib.layout(16, 384, 384, 8, 3072, 1280, 1)
+    buf = ctypes.c_void_p(256)              # (never dereferenced on these paths)
+    st = lib.dgm_router_topk_launch(None, None, 0, 3072, 384, 8, 1, 0, 0, buf, ctypes.byref(L), None)
+    assert st == 0
+    st = lib.dgm_router_logits_topk_launch(None, 0, 384, 8, 0, 0, buf, ctypes.byref(L), None)
+    assert st == 0
+    st = lib.dgm_router_topk_launch(None, None, 4, 3072, 384, 8, 1, 0, 0, buf, ctypes.byref(L), None)
+    assert st == -1 and b"null pointer" in lib.dgm_last_error()
+
+
 def test_product_path_has_no_cpu_fallback():
     import torch
     import hopper_megamoe_basedondeepgemm_amd as dgm
