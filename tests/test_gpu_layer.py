@@ -245,6 +245,19 @@ def test_frontend_router_tiles(M, E, H):
                    zero_rows=zero_rows)
 
 
+@pytest.mark.parametrize("select_in_mega", [False, True])
+def test_maximum_router_width_and_topk(select_in_mega):
+    """The router's limits: 1024 experts and top-16 (an EP rank's 64 local experts of them),
+    12 tokens (the top-k of a separate selection launch either way above 8 tokens): logits,
+    keys, top-k and weights bit-exact, pool table, y within tolerance."""
+    need_gpu()
+    print(f"max router width E=1024 topk=16 select_in_mega={select_in_mega}", flush=True)
+    r = run_layer(12, 1024, 64, 64, 512, 256, 16, "mxfp8", seed=960, zero_rows=(5,), select_in_mega=select_in_mega)
+    check_frontend(r, "mxfp8", 12, zero_rows=(5,))
+    check_pool(r, 64, 64)
+    print(check_y(r, zero_rows=(5,)))
+
+
 def test_large_batch_beyond_fused_limits():
     """200 tokens at top-8: 1600 routes exceed the persistent kernel's 1024, so the fused entry
     point runs the split path (dispatch, L1, L2, combine kernels); frontend, pool and y as
