@@ -258,6 +258,18 @@ def test_maximum_router_width_and_topk(select_in_mega):
     print(check_y(r, zero_rows=(5,)))
 
 
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+def test_persistent_kernel_at_its_limits(fmt):
+    """256 tokens at top-4: exactly the persistent kernel's 1024 routes and 256 tokens (its LDS
+    tables full), unbalanced routing with zero rows: frontend, pool table and y as elsewhere."""
+    need_gpu()
+    print(f"persistent kernel limits fmt={fmt} M=256 topk=4", flush=True)
+    r = run_layer(256, 16, 16, 0, 512, 256, 4, fmt, seed=970, zero_rows=(0, 255))
+    check_frontend(r, fmt, 256, zero_rows=(0, 255))
+    check_pool(r, 16, 0)
+    print(check_y(r, zero_rows=(0, 255)))
+
+
 def test_large_batch_beyond_fused_limits():
     """200 tokens at top-8: 1600 routes exceed the persistent kernel's 1024, so the fused entry
     point runs the split path (dispatch, L1, L2, combine kernels); frontend, pool and y as
