@@ -98,10 +98,17 @@ def topk_softmax(logits_f32, topk):
     return order.astype(np.int64), w, lb
 
 
-def balanced_routing(M, E, topk, token_offset=0):
-    """Forced-balanced routing (tests/test_four_api_correctness.py:125-144): global token g,
-    slot s -> expert s*G + (g + 7 s) % G with G = E / topk; weight 1/topk exactly."""
-    G = E // topk
+def balanced_routing(M, E, topk, token_offset=0, num_ranks=None):
+    """Forced-balanced routing (tests/test_four_api_correctness.py:125-144, the same rule as
+    tests/profile_four_api_h20.py:139-160): global token g, slot s -> expert
+    s*G + (g + 7 s) % G with G = E / num_ranks (the EP rank's expert count, T4:138), so slot s
+    lands on EP rank s; weight 1/topk exactly. The rule gives every rank exactly one route per
+    token only when topk == num_ranks (the reference runs 8 ranks at top-8); num_ranks defaults
+    to topk, the case the device kernels implement (their G is E / topk)."""
+    if num_ranks is None:
+        num_ranks = topk
+    assert E % num_ranks == 0 and topk <= num_ranks, (E, topk, num_ranks)
+    G = E // num_ranks
     g = np.arange(M, dtype=np.int64)[:, None] + token_offset
     s = np.arange(topk, dtype=np.int64)[None, :]
     idx = s * G + (g + 7 * s) % G

@@ -233,3 +233,52 @@ def test_requant_mid_fp8_64_known_answers():
     assert deq[0, 105] == np.float32(3 * 2.0 ** -9 * 2)
     assert (deq[0, 128:] == 0).all() and (codes[0, 128:] == 0).all()
     np.testing.assert_array_equal(moe.requant_mid(np.concatenate([g0, g1, g2])[None], "fp8f128"), deq)
+
+
+def test_balanced_routing_known_answers():
+    """Hand-worked entries of tests/test_four_api_correctness.py:138 at E384, 8 ranks (48 local
+    experts), top-8: expert = s*48 + (g + 7 s) % 48. A rule of (g + s) % 48, a slot stride of
+    E / topk taken from another E, or the token index used without the rank offset fails one."""
+    idx, w = moe.balanced_routing(48, 384, 8, num_ranks=8)
+    assert idx[1, 1] == 56           # 48 + (1 + 7) % 48
+    assert idx[5, 3] == 170          # 144 + (5 + 21) % 48 = 144 + 26
+    assert idx[47, 7] == 336         # 336 + (47 + 49) % 48 = 336 + 0
+    assert idx[0, 0] == 0 and idx[0, 1] == 55    # 48 + 7
+    assert (w == np.float32(0.125)).all()
+    # rank 3 of 8 with 2 tokens per rank: local token 1 is global token 7
+    idx_r3, _ = moe.balanced_routing(2, 384, 8, token_offset=3 * 2, num_ranks=8)
+    assert idx_r3[1, 2] == 117       # 96 + (7 + 14) % 48 = 96 + 21
+    assert idx_r3[0, 0] == 6         # 0 + 6 % 48
+    # the group size is the rank's expert count: 16 ranks of 24 experts at top-8
+    idx16, _ = moe.balanced_routing(2, 384, 8, num_ranks=16)
+    assert idx16[1, 1] == 24 + (1 + 7) % 24 and idx16[1, 7] == 7 * 24 + (1 + 49) % 24
+    # the default (num_ranks = topk) is the reference's 8 ranks x top-8 case
+    np.testing.assert_array_equal(moe.balanced_routing(48, 384, 8)[0], idx)
+    with pytest.raises(AssertionError):
+        moe.balanced_routing(2, 384, 8, num_ranks=4)   # top-8 cannot give one route per rank
+
+
+def test_cast_to_fp4_rows_amax_floor():
+    """The W4A4 row cast floors amax at 1e-30 (sm100_b200/test_mega_moe.py:82), the
+    per_token_cast_to_fp4 rule at 1e-4 (deep_gemm/utils/math.py:94). By hand:
+      all-zero group: 1e-30 / 6 = 1.67e-31 = 2^-102.24 -> 2^-102 -> E8M0 byte 127 - 102 = 25;
+                      1e-4 / 6 = 1.67e-5 = 2^-15.87 -> 2^-15 -> byte 112;
+      amax 1e-32 (below the floor): the same byte 25, every code 0 (1e-32 / 2^-102 ~ 5e-2 < 0.25);
+      amax 3 * 2^-100: amax / 6 = 2^-101 exactly -> byte 26, the max element's code 7 (6.0),
+                      a 2^-101 element code 2 (1.0), a -0.75 * 2^-101 element ties down to -0.5:
+                      code 0x9;
+      per_token_cast_to_fp4: every group here is below 1e-4 -> byte 112."""
+    x = np.zeros((1, 96), np.float32)
+    x[0, 32] = 1e-32
+    x[0, 64] = 3 * 2.0 ** -100
+    x[0, 65] = 2.0 ** -101
+    x[0, 66] = -0.75 * 2.0 ** -101
+    packed, sf, sfb = pk.cast_to_fp4_rows(x, 32)
+    assert sfb.tolist() == [[25, 25, 26]]
+    assert sf[0, 0] == np.float32(2.0 ** -102) and sf[0, 2] == np.float32(2.0 ** -101)
+    assert (packed[0, :32] == 0).all()
+    # group 2 starts at byte 32: element 64 low nibble, 65 high nibble; 66 low nibble of byte 33
+    assert packed[0, 32] == (7 | (2 << 4)) and packed[0, 33] == 0x9
+    p2, sf2 = pk.per_token_cast_to_fp4(x, 32)[:2]
+    b2 = ((sf2.view(np.uint32) >> 23) & 0xFF)
+    assert (b2 == 112).all()        # 3 * 2^-100 is below 1e-4 as well
