@@ -15,23 +15,37 @@ rank 0.
 input format tests/test_four_api_correctness.py:215 writes into this buffer), MXFP4 weights from
 ``transform_mxfp4_weights_for_mega_moe_fused``; ``qoq_mega_moe_fused`` the QoQ W4A8 layer.
 """
+import weakref
+
 import torch
 
 from . import _lib
 from . import mega
 
 
-_BUFFERS = {}       # (data_ptr, rank, activation format) -> FusedSymmBuffer over the caller's tensor
+# (data_ptr, rank, activation format) -> (shape, FusedSymmBuffer over the caller's tensor). An
+# entry lives as long as the caller's tensor object does (a finalizer on it removes the entry and
+# with it the wrapper's view of the storage), and slicing the same memory for another shape
+# replaces it.
+_BUFFERS = {}
+
+
+def _release(key, b):
+    if key in _BUFFERS and _BUFFERS[key][1] is b:
+        del _BUFFERS[key]
 
 
 def _wrap(buffer, num_ranks, num_experts, max_tokens, topk, hidden, intermediate, rank=0, act="fp8f128"):
     key = (buffer.data_ptr(), int(rank), act)
-    b = _BUFFERS.get(key)
-    if b is None or b.buffer.nbytes > buffer.nbytes:
+    shape = (int(num_ranks), int(num_experts), int(max_tokens), int(topk), int(hidden), int(intermediate))
+    hit = _BUFFERS.get(key)
+    if hit is None or hit[0] != shape or hit[1].buffer.nbytes > buffer.nbytes:
         b = mega.FusedSymmBuffer(None, num_experts, max_tokens, topk, hidden, intermediate, act_format=act,
                                  ep_size=num_ranks, ep_rank=rank, buffer=buffer)
-        _BUFFERS[key] = b
-    return b
+        _BUFFERS[key] = (shape, b)
+        weakref.finalize(buffer, _release, key, b)
+        return b
+    return hit[1]
 
 
 def _views(b, with_partials):
@@ -41,10 +55,13 @@ def _views(b, with_partials):
 
 
 def _lookup(buffer, rank, act="fp8f128"):
-    for (ptr, r, a), b in _BUFFERS.items():
-        if ptr == buffer.data_ptr() and r == int(rank):
-            return b if a == act else _wrap(buffer, b.ep_size, b.num_experts, b.num_max_tokens_per_rank, b.num_topk,
-                                            b.hidden, b.intermediate_hidden, rank, act)
+    hit = _BUFFERS.get((buffer.data_ptr(), int(rank), act))
+    if hit is not None:
+        return hit[1]
+    for (ptr, r, a), (_, b) in list(_BUFFERS.items()):
+        if ptr == buffer.data_ptr() and r == int(rank):     # the same memory in the other format
+            return _wrap(buffer, b.ep_size, b.num_experts, b.num_max_tokens_per_rank, b.num_topk,
+                         b.hidden, b.intermediate_hidden, rank, act)
     raise RuntimeError("MegaMoE buffer not sliced: call the slice function of "
                        "get_symm_buffer_size_for_(fused_)mega_moe on it first")
 
@@ -164,18 +181,28 @@ def fable_router_quant_topk_frontend(hidden, router_weight, x, x_sf, topk_idx, t
     """csrc/apis/mega.hpp:744: router + top-k + activation cast into the views of a sliced buffer
     (``x`` must be that buffer's x view); mode 0 = E4M3 with fp32 scales per 128, 1 = QoQ int8.
     With select_in_mega the keys stay in the buffer (its ``fe_keys`` view) for the layer call;
-    ``workspace``, ``stamps`` and ``l2_persist`` are not used here."""
+    with ``stamps`` the frontend workgroups' phase stamps (``fable_frontend_stamps``) are also
+    copied where the reference's wrapper reads them (``workspace`` byte 256 + 1024 E, at most 256
+    rows); ``l2_persist`` is not used here."""
     assert mode in (0, 1)
     act = "qoq" if mode == 1 else "fp8f128"
-    cands = [b for (p, r, a), b in _BUFFERS.items() if p == x.data_ptr() and a == act] or \
-            [b for (p, r, a), b in _BUFFERS.items() if p == x.data_ptr()]
+    cands = [b for (p, r, a), (_, b) in _BUFFERS.items() if p == x.data_ptr() and a == act] or \
+            [b for (p, r, a), (_, b) in _BUFFERS.items() if p == x.data_ptr()]
     if not cands:
         raise RuntimeError("x must be the x view of a sliced MegaMoE buffer")
     b = cands[0] if cands[0].act_format == act else _lookup(cands[0].buffer, cands[0].ep_rank, act)
     assert topk_idx.data_ptr() == b.topk_idx.data_ptr() and topk_weights.data_ptr() == b.topk_weights.data_ptr()
     mega.fable_router_quant_topk_frontend(hidden, router_weight, b, wlayout=int(wlayout),
                                           select_in_mega=bool(select_in_mega),
-                                          zero_row_unrouted=bool(zero_row_unrouted))
+                                          zero_row_unrouted=bool(zero_row_unrouted), stamps=int(bool(stamps)))
+    if stamps and workspace is not None:
+        e = router_weight.size(0)
+        off = 256 + 4 * 64 * e * 4          # deep_gemm/mega/__init__.py:754
+        st = mega.fable_frontend_stamps(b)[:_FRONTEND_STAMP_ROWS]
+        if workspace.nbytes >= off + _FRONTEND_STAMP_ROWS * 64:
+            region = workspace.view(torch.uint8)[off:off + _FRONTEND_STAMP_ROWS * 64].view(torch.int64).view(-1, 8)
+            region.zero_()
+            region[:st.size(0)].copy_(st)
     if select_in_mega:
         # the key array also where the reference's wrapper reads it (deep_gemm/mega/__init__.py:594,
         # workspace + 256 + 64 KB; fable_frontend_keys) and hands it back as fe_keys
@@ -186,3 +213,4 @@ def fable_router_quant_topk_frontend(hidden, router_weight, x, x_sf, topk_idx, t
 
 
 _FRONTEND_CC_KEYS_OFF = 256 + 64 * 1024
+_FRONTEND_STAMP_ROWS = 256          # deep_gemm/mega/__init__.py:590 (_FRONTEND_STAMPS_BYTES = 256 x 8 x 8)

@@ -28,8 +28,18 @@ EXPORTS = [
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
     "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
     "dgm_reorder_fp4_nibbles", "dgm_untransform_fp4_weights", "dgm_untransform_nvfp4_weights",
-    "dgm_router_logits_topk_launch",
+    "dgm_router_logits_topk_launch", "dgm_router_topk_launch_stamped", "dgm_frontend_workgroups",
+    "dgm_quantize_mxfp4_typed", "dgm_quantize_nvfp4_typed", "dgm_quantize_qoq_typed", "dgm_quantize_qoq_int4_typed",
 ]
+# source element types of the weight packers (DGM_SRC_*)
+SRC_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def src_dtype(t):
+    """The packers' code for t's element type (bf16, fp16 or fp32; anything else raises)."""
+    if t.dtype not in SRC_DTYPES:
+        raise TypeError(f"weights are packed from bf16, fp16 or fp32, got {t.dtype}")
+    return SRC_DTYPES[t.dtype]
 
 
 class BufferLayout(ctypes.Structure):
@@ -39,7 +49,10 @@ class BufferLayout(ctypes.Structure):
                 ("mid", ctypes.c_size_t),
                 ("mid_sf", ctypes.c_size_t), ("partials", ctypes.c_size_t), ("counters", ctypes.c_size_t),
                 ("x_row_bytes", ctypes.c_int32), ("mid_row_bytes", ctypes.c_int32),
-                ("max_routes", ctypes.c_int32), ("max_tokens", ctypes.c_int32)]
+                ("max_routes", ctypes.c_int32), ("max_tokens", ctypes.c_int32),
+                ("topk", ctypes.c_int32), ("num_experts", ctypes.c_int32), ("num_local_experts", ctypes.c_int32),
+                ("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32), ("act_format", ctypes.c_int32),
+                ("x_sf_row_bytes", ctypes.c_int32), ("mid_sf_row_bytes", ctypes.c_int32)]
 
 
 class MoeArgs(ctypes.Structure):
@@ -76,6 +89,10 @@ def load():
         "dgm_version": ([], i32),
         "dgm_last_error": ([], ctypes.c_char_p),
         "dgm_quantize_mxfp4": ([vp, i64, i64, i32, vp, vp, vp], i32),
+        "dgm_quantize_mxfp4_typed": ([vp, i32, i64, i64, i32, vp, vp, vp], i32),
+        "dgm_quantize_nvfp4_typed": ([vp, i32, i64, i64, vp, vp, vp], i32),
+        "dgm_quantize_qoq_typed": ([vp, i32, i64, i64, vp, vp, vp, vp, vp], i32),
+        "dgm_quantize_qoq_int4_typed": ([vp, i32, i64, i64, vp, vp, vp], i32),
         "dgm_cast_fp4_rows": ([vp, i64, i64, f32, vp, vp, vp], i32),
         "dgm_cast_fp8_rows": ([vp, i64, i64, vp, vp, vp], i32),
         "dgm_quantize_nvfp4": ([vp, i64, i64, vp, vp, vp], i32),
@@ -87,6 +104,9 @@ def load():
         "dgm_fused_buffer_layout": ([i32, i32, i32, i32, i32, i32, i32, ctypes.POINTER(BufferLayout)], i32),
         "dgm_router_topk_launch": ([vp, vp, i32, i32, i32, i32, i32, i32, i32, vp,
                                     ctypes.POINTER(BufferLayout), vp], i32),
+        "dgm_router_topk_launch_stamped": ([vp, vp, i32, i32, i32, i32, i32, i32, i32, vp,
+                                            ctypes.POINTER(BufferLayout), vp, i32, vp], i32),
+        "dgm_frontend_workgroups": ([i32, i32, i32, i32, i32, i32], i32),
         "dgm_megamoe_fused_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_megamoe_split_launch": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_megamoe_fused_launch_noalloc": ([ctypes.POINTER(MoeArgs), vp], i32),

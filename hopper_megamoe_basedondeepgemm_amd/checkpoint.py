@@ -40,12 +40,15 @@ def _as_packed3(packed):
 
 def reorder_fp4_nibbles(packed, src_order, dst_order, out=None):
     """The same E2M1 codes in another nibble order (``"ocp"`` / ``"low_first"`` <-> ``"marlin"``),
-    any shape with a last dimension of whole 4-byte words; ``out=packed`` converts in place."""
-    _lib.require_gpu(packed)
+    any shape with a last dimension of whole 4-byte words; ``out=packed`` converts in place.
+    (A Marlin word holds 8 codes of one row, so a row that ends mid-word would mix two rows.)"""
     assert packed.dtype == torch.uint8 and packed.is_contiguous(), "contiguous uint8 codes"
+    assert packed.dim() >= 1 and packed.shape[-1] % 4 == 0, \
+        f"the last dimension ({tuple(packed.shape)}) must be whole 4-byte words (8 codes)"
+    _lib.require_gpu(packed)
     if out is None:
         out = torch.empty_like(packed)
-    assert out.dtype == torch.uint8 and out.is_contiguous() and out.numel() == packed.numel()
+    assert out.dtype == torch.uint8 and out.is_contiguous() and out.shape == packed.shape
     _lib.check(_lib.load().dgm_reorder_fp4_nibbles(_lib.ptr(packed), _lib.ptr(out), packed.numel(),
                                                    _order(src_order), _order(dst_order), _lib.stream()))
     return out

@@ -53,6 +53,27 @@ struct DgmWorkspace {
   int* counters;
 };
 
+// Row bytes of the activation codes / scales and of the intermediate codes / scales that a call in
+// act_format needs (hidden H, intermediate I): MXFP4 / NVFP4 codes are half a byte, the others a
+// byte; x scales E8M0 per 32 (NVFP4 E4M3 per 16; QoQ and FP8F128 fp32 per 128, the same H / 32
+// bytes); intermediate scales E8M0 per 32 (QoQ fp32 per 64, NVFP4 E4M3 per 16, FP8F128 sized as
+// QoQ's).
+struct DgmRowBytes { size_t x, x_sf, mid, mid_sf; };
+static inline DgmRowBytes dgm_row_bytes(int act_format, int hidden, int intermediate) {
+  const bool fp4 = act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_NVFP4;
+  DgmRowBytes r;
+  r.x = fp4 ? hidden / 2 : hidden;
+  r.x_sf = act_format == DGM_ACT_NVFP4 ? hidden / 16 : hidden / 32;
+  r.mid = fp4 ? intermediate / 2 : intermediate;
+  r.mid_sf = act_format == DGM_ACT_QOQ || act_format == DGM_ACT_NVFP4 || act_format == DGM_ACT_FP8F128
+                 ? intermediate / 16 : intermediate / 32;
+  return r;
+}
+// A call's shape against the shape its buffer was laid out for (intermediate < 0: a frontend
+// call, which writes no intermediate rows; num_local_experts < 0: not checked). 0, or
+// DGM_ERR_INVALID_ARGUMENT with the message set.
+int dgm_check_layout_call(const DgmBufferLayout* L, int num_tokens, int topk, int num_experts, int num_local_experts,
+                          int hidden, int intermediate, int act_format);
 // Host-side checks of a fused-layer call (0, or DGM_ERR_INVALID_ARGUMENT with the message set).
 int dgm_check_fused_args(const DgmMoeArgs* A);
 // One launch of the persistent kernel over the workspace w, running `phases` of the layer

@@ -68,20 +68,44 @@ __host__ __device__ inline Pool pool_view(uint8_t* base, int E_local) {
 // its barrier cost 1.1-1.7 us more than the hidden-row reads they save).
 constexpr int FE_ROUTER_TILE = 8;         // tokens per router workgroup in the tiled form
 constexpr int FE_TILE_MIN_TOKENS = 64;
+// Phase stamps (the reference's DG_FE_STAMPS, deep_gemm/mega/__init__.py:743-756): with stamps
+// non-null, workgroup b = blockIdx.y * gridDim.x + blockIdx.x < stamp_rows writes row b of 8
+// int64: [0] entry, [3] (router rows) keys and logits stored by all four waves, [5] (cast rows)
+// cast stored, [6] the hardware position (HW_ID | XCC_ID << 32), [7] exit; wall clock at 100 MHz.
+DGM_DEV long long fe_clock() { return (long long)__builtin_amdgcn_s_memrealtime(); }
+DGM_DEV long long fe_hw_position() {
+  uint32_t hw, xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  return (long long)hw | ((long long)(xcc & 0xffffu) << 32);
+}
+
 template <int J, int RT>
 __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
                                                   int M, int E, int act_format, float* __restrict__ logits,
                                                   uint32_t* __restrict__ keys, int zero_unrouted,
-                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ sf, int router) {
+                                                  uint8_t* __restrict__ q, uint8_t* __restrict__ sf, int router,
+                                                  long long* __restrict__ stamps, int stamp_rows) {
   constexpr int H = J * 512, RTOK = RT > 0 ? RT : 4;
   __shared__ uint4 xs[RT > 0 ? RT * J * 64 : 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ry = router ? (M + RTOK - 1) / RTOK : 0;
+  const int brow = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+  long long* st = stamps != nullptr && brow < stamp_rows ? stamps + (size_t)brow * 8 : nullptr;
+  const long long t_entry = st ? fe_clock() : 0;
   if ((int)blockIdx.y < ry) {
     if constexpr (RT > 0)
       router_tile<J, RT, false>(x, w, M, E, blockIdx.x * 4, blockIdx.y * RT, logits, keys, zero_unrouted != 0, xs);
     else
       router_wave<J, false>(x, w, M, E, blockIdx.x * 4 + wave, blockIdx.y * 4, lane, logits, keys, zero_unrouted != 0);
+    if (st) {
+      __syncthreads();
+      if (tid == 0) {
+        const long long t = fe_clock();
+        st[0] = t_entry; st[1] = 0; st[2] = 0; st[3] = t; st[4] = 0; st[5] = 0;
+        st[6] = fe_hw_position(); st[7] = fe_clock();
+      }
+    }
     return;
   }
   const int cy = (int)gridDim.y - ry, by = (int)blockIdx.y - ry;
@@ -97,6 +121,14 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
     for (int64_t i = lane0; i < (int64_t)M * (H / 128) * 32; i += nl) cast_lane_fp8f128<false>(x, i, q, sf);
   } else {
     for (int64_t i = lane0; i < (int64_t)M * (H / 32) * 8; i += nl) cast_lane_mx<false>(x, act_format, i, q, sf);
+  }
+  if (st) {
+    __syncthreads();
+    if (tid == 0) {
+      const long long t = fe_clock();
+      st[0] = t_entry; st[1] = 0; st[2] = 0; st[3] = 0; st[4] = 0; st[5] = t;
+      st[6] = fe_hw_position(); st[7] = fe_clock();
+    }
   }
 }
 
@@ -601,16 +633,12 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   DGM_CHECK_ARG(hidden % 512 == 0 && intermediate % 128 == 0, "hidden % 512, intermediate % 128");
   DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG((int64_t)max_tokens * topk <= MAX_ROUTES_DISPATCH, "max_tokens * topk <= 4096");
-  const bool fp4 = act_format == DGM_ACT_MXFP4 || act_format == DGM_ACT_NVFP4;
-  const size_t xb = fp4 ? hidden / 2 : hidden;
-  const size_t mb = fp4 ? intermediate / 2 : intermediate;
   // scales: E8M0 bytes per 32 (MXFP); QoQ: fp32 per token repeated over H / 128 slots (the
   // same H / 32 bytes) and fp32 per 64 intermediate features (I / 16 bytes); NVFP4: E4M3
   // bytes per 16; FP8F128: fp32 per 128 K (H / 32 bytes) and E8M0 bytes per 32 intermediate
   // features, sized as QoQ's (so one buffer serves both layers of the split recipe)
-  const size_t xsfb = act_format == DGM_ACT_NVFP4 ? hidden / 16 : hidden / 32;
-  const size_t msfb = act_format == DGM_ACT_QOQ || act_format == DGM_ACT_NVFP4 || act_format == DGM_ACT_FP8F128
-                          ? intermediate / 16 : intermediate / 32;
+  const DgmRowBytes rb = dgm_row_bytes(act_format, hidden, intermediate);
+  const size_t xb = rb.x, mb = rb.mid, xsfb = rb.x_sf, msfb = rb.mid_sf;
   const int R = max_tokens * topk;
   size_t off = 0;
   memset(out, 0, sizeof(*out));
@@ -630,15 +658,83 @@ int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_exper
   out->mid_row_bytes = (int32_t)mb;
   out->max_routes = R;
   out->max_tokens = max_tokens;
+  out->topk = topk;
+  out->num_experts = num_experts;
+  out->num_local_experts = num_local_experts;
+  out->hidden = hidden;
+  out->intermediate = intermediate;
+  out->act_format = act_format;
+  out->x_sf_row_bytes = (int32_t)xsfb;
+  out->mid_sf_row_bytes = (int32_t)msfb;
   return 0;
+}
+
+}  // extern "C"
+
+int dgm_check_layout_call(const DgmBufferLayout* L, int num_tokens, int topk, int num_experts, int num_local_experts,
+                          int hidden, int intermediate, int act_format) {
+  DGM_CHECK_ARG(L != nullptr, "null layout");
+  DGM_CHECK_ARG(L->max_routes == L->max_tokens * L->topk && L->topk > 0,
+                "the layout was not made by dgm_fused_buffer_layout");
+  DGM_CHECK_ARG(num_tokens >= 0 && num_tokens <= L->max_tokens, "num_tokens exceeds the buffer's max_tokens");
+  DGM_CHECK_ARG(topk > 0 && topk <= L->topk, "topk exceeds the buffer's topk (route outputs are [topk][max_tokens][H])");
+  DGM_CHECK_ARG(num_experts > 0 && num_experts <= L->num_experts, "num_experts exceeds the buffer's");
+  DGM_CHECK_ARG(num_local_experts < 0 || num_local_experts <= L->num_local_experts,
+                "num_local_experts exceeds the buffer's (dispatch table)");
+  DGM_CHECK_ARG(hidden == L->hidden, "hidden differs from the buffer's");
+  DGM_CHECK_ARG(intermediate < 0 || intermediate == L->intermediate, "intermediate differs from the buffer's");
+  const DgmRowBytes rb = dgm_row_bytes(act_format, hidden, intermediate < 0 ? L->intermediate : intermediate);
+  DGM_CHECK_ARG(rb.x <= (size_t)L->x_row_bytes && rb.x_sf <= (size_t)L->x_sf_row_bytes,
+                "the activation format needs wider x / x_sf rows than the buffer's");
+  DGM_CHECK_ARG(intermediate < 0 || (rb.mid <= (size_t)L->mid_row_bytes && rb.mid_sf <= (size_t)L->mid_sf_row_bytes),
+                "the activation format needs wider intermediate rows than the buffer's");
+  return 0;
+}
+
+extern "C" {
+
+}  // extern "C"
+
+// The frontend launch's grid: router rows (4 experts x 4 tokens per workgroup, 8 tokens from
+// FE_TILE_MIN_TOKENS on) and, beside them, cast rows of one cast lane per thread (QoQ: one wave
+// per token).
+static dim3 fe_grid(int num_tokens, int hidden, int num_experts, int act_format, int flags, bool router) {
+  const int rx = (num_experts + 3) / 4;
+  const int64_t cast_threads = act_format == DGM_ACT_QOQ       ? (int64_t)num_tokens * 64
+                               : act_format == DGM_ACT_NVFP4   ? (int64_t)num_tokens * (hidden / 16) * 4
+                               : act_format == DGM_ACT_FP8F128 ? (int64_t)num_tokens * (hidden / 128) * 32
+                                                               : (int64_t)num_tokens * (hidden / 32) * 8;
+  const int64_t cast_rows = (flags & DGM_FE_NO_CAST) ? 0 : (cast_threads + (int64_t)rx * 256 - 1) / ((int64_t)rx * 256);
+  const int rtok = num_tokens >= FE_TILE_MIN_TOKENS ? FE_ROUTER_TILE : 4;
+  return dim3(rx, (router ? (num_tokens + rtok - 1) / rtok : 0) + (int)cast_rows);
+}
+
+extern "C" {
+
+int dgm_frontend_workgroups(int num_tokens, int hidden, int num_experts, int act_format, int flags, int router) {
+  if (num_tokens <= 0 || hidden <= 0 || num_experts <= 0) return 0;
+  const dim3 g = fe_grid(num_tokens, hidden, num_experts, act_format, flags, router != 0);
+  return (int)(g.x * g.y);
 }
 
 int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf16, int num_tokens,
                            int hidden, int num_experts, int topk, int act_format, int flags,
                            int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
+  return dgm_router_topk_launch_stamped(hidden_bf16, router_weight_bf16, num_tokens, hidden, num_experts, topk,
+                                        act_format, flags, token_offset, buffer, L, nullptr, 0, stream);
+}
+
+int dgm_router_topk_launch_stamped(const void* hidden_bf16, const void* router_weight_bf16, int num_tokens,
+                                   int hidden, int num_experts, int topk, int act_format, int flags,
+                                   int token_offset, void* buffer, const DgmBufferLayout* L, int64_t* stamps,
+                                   int stamp_rows, hipStream_t stream) {
   DGM_CHECK_ARG(buffer && L && (hidden_bf16 || num_tokens == 0), "null pointer");   // (no tokens: no rows)
-  DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
+  DGM_CHECK_ARG(act_format >= DGM_ACT_MXFP4 && act_format <= DGM_ACT_FP8F128, "act_format");
+  {
+    const int chk = dgm_check_layout_call(L, num_tokens, topk, num_experts, -1, hidden, -1, act_format);
+    if (chk) return chk;
+  }
   DGM_CHECK_ARG(num_experts <= 1024, "num_experts <= 1024");
   DGM_CHECK_ARG(hidden % 512 == 0, "hidden % 512 == 0");
   DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
@@ -648,19 +744,13 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
                 "cast only (router_weight NULL): no routing flags");
   DGM_CHECK_ARG(router_weight_bf16 || !(flags & DGM_FE_NO_CAST), "DGM_FE_NO_CAST needs the router weight");
   if (num_tokens == 0) return 0;
+  DGM_CHECK_ARG(stamp_rows >= 0 && (stamps != nullptr || stamp_rows == 0), "stamps / stamp_rows");
   uint8_t* buf = (uint8_t*)buffer;
   const int J = hidden / 512;
-  // router rows, then cast rows: one cast lane per thread (QoQ: one wave per token)
-  const int rx = (num_experts + 3) / 4;
-  const int64_t cast_threads = act_format == DGM_ACT_QOQ       ? (int64_t)num_tokens * 64
-                               : act_format == DGM_ACT_NVFP4   ? (int64_t)num_tokens * (hidden / 16) * 4
-                               : act_format == DGM_ACT_FP8F128 ? (int64_t)num_tokens * (hidden / 128) * 32
-                                                               : (int64_t)num_tokens * (hidden / 32) * 8;
-  const int64_t cast_rows = (flags & DGM_FE_NO_CAST) ? 0 : (cast_threads + (int64_t)rx * 256 - 1) / ((int64_t)rx * 256);
   const int router = router_weight_bf16 ? 1 : 0;
   const bool tiled = num_tokens >= FE_TILE_MIN_TOKENS;
-  const int rtok = tiled ? FE_ROUTER_TILE : 4;
-  dim3 rg(rx, (router ? (num_tokens + rtok - 1) / rtok : 0) + (int)cast_rows);
+  const dim3 rg = fe_grid(num_tokens, hidden, num_experts, act_format, flags, router != 0);
+  long long* stamp_ptr = (long long*)stamps;
   const uint16_t* x = (const uint16_t*)hidden_bf16;
   const uint16_t* w = (const uint16_t*)router_weight_bf16;
   float* logits = (float*)(buf + L->logits);
@@ -669,10 +759,12 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
 #define DGM_FE(JJ)                                                                                           \
   if (tiled)                                                                                                 \
     hipLaunchKernelGGL((k_frontend<JJ, FE_ROUTER_TILE>), rg, dim3(256), 0, stream, x, w, num_tokens, num_experts, \
-                       act_format, logits, keys, zero_unrouted, buf + L->x, buf + L->x_sf, router);         \
+                       act_format, logits, keys, zero_unrouted, buf + L->x, buf + L->x_sf, router, stamp_ptr, \
+                       stamp_rows);                                                                          \
   else                                                                                                       \
     hipLaunchKernelGGL((k_frontend<JJ, 0>), rg, dim3(256), 0, stream, x, w, num_tokens, num_experts,            \
-                       act_format, logits, keys, zero_unrouted, buf + L->x, buf + L->x_sf, router)
+                       act_format, logits, keys, zero_unrouted, buf + L->x, buf + L->x_sf, router, stamp_ptr,   \
+                       stamp_rows)
   switch (J) {
     case 1: DGM_FE(1); break;
     case 2: DGM_FE(2); break;
@@ -693,8 +785,12 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
 int dgm_router_logits_topk_launch(const void* logits_bf16, int num_tokens, int num_experts, int topk, int flags,
                                   int token_offset, void* buffer, const DgmBufferLayout* L, hipStream_t stream) {
   DGM_CHECK_ARG(buffer && L && (logits_bf16 || num_tokens == 0), "null pointer");
-  DGM_CHECK_ARG(num_tokens >= 0 && (int64_t)num_tokens * topk <= L->max_routes, "num_tokens exceeds the buffer");
   DGM_CHECK_ARG(topk > 0 && topk <= 16 && topk <= num_experts, "topk");
+  {
+    // (no activation rows are written: the buffer's own format and hidden size)
+    const int chk = dgm_check_layout_call(L, num_tokens, topk, num_experts, -1, L->hidden, -1, L->act_format);
+    if (chk) return chk;
+  }
   DGM_CHECK_ARG(num_experts > 0 && num_experts <= 1024, "num_experts <= 1024");
   DGM_CHECK_ARG(!(flags & DGM_FE_FORCE_BALANCED) || num_experts % topk == 0, "forced-balanced needs E % topk == 0");
   DGM_CHECK_ARG(!(flags & DGM_FE_ZERO_ROW_UNROUTED), "zero-row unrouting needs the hidden rows (dgm_router_topk_launch)");
@@ -755,7 +851,13 @@ int dgm_check_fused_args(const DgmMoeArgs* A) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && (A->y || A->num_tokens == 0), "null pointer");
   DGM_CHECK_ARG(A->w1_values && A->w1_scales && A->w2_values && A->w2_scales, "null weights");
   const DgmBufferLayout* L = A->layout;
-  DGM_CHECK_ARG(A->num_tokens >= 0 && (int64_t)A->num_tokens * A->topk <= L->max_routes, "num_tokens exceeds the buffer");
+  DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
+  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_FP8F128, "act_format");
+  {
+    const int chk = dgm_check_layout_call(L, A->num_tokens, A->topk, A->num_experts, A->num_local_experts, A->hidden,
+                                          A->intermediate, A->act_format);
+    if (chk) return chk;
+  }
   DGM_CHECK_ARG(A->num_local_experts > 0 && A->num_local_experts <= MAX_LOCAL_EXPERTS, "num_local_experts");
   DGM_CHECK_ARG(A->expert_begin >= 0 && A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
   DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4,
@@ -862,6 +964,12 @@ int dgm_megamoe_split_launch(const DgmMoeArgs* A, hipStream_t stream) {
   DGM_CHECK_ARG(A && A->buffer && A->layout && (A->y || A->num_tokens == 0), "null pointer");
   DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG(!A->fe_in_mega, "split path: fe_in_mega is a fused-launch option");
+  DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");
+  {
+    const int chk = dgm_check_layout_call(A->layout, A->num_tokens, A->topk, A->num_experts, A->num_local_experts,
+                                          A->hidden, A->intermediate, A->act_format);
+    if (chk) return chk;
+  }
   if (A->act_format == DGM_ACT_QOQ || A->act_format == DGM_ACT_NVFP4) {
     // two launches of the persistent kernel: dispatch + L1, then L2 + combine
     DGM_CHECK_ARG(A->w1_values && A->w1_scales && A->w2_values && A->w2_scales, "null weights");

@@ -11,10 +11,11 @@
 
 namespace {
 
-// Limits of the array: routes (tokens * topk), hidden and intermediate sizes.
+// Limits of the array: routes (tokens * topk), hidden and intermediate sizes (the largest shape
+// the persistent kernel is built for: H 3072, I 1280).
 constexpr int NA_MAX_ROUTES = 512;
-constexpr int NA_MAX_HIDDEN = 4096;
-constexpr int NA_MAX_INTER = 2048;
+constexpr int NA_MAX_HIDDEN = 3072;
+constexpr int NA_MAX_INTER = 1280;
 // Regions (each 256-byte aligned): counters, dispatch table, intermediate rows (at most one byte
 // per feature) and their scales (at most I / 16 bytes per row), route outputs (bf16).
 constexpr size_t NA_OFF_CNT = 0;
@@ -23,7 +24,7 @@ constexpr size_t NA_OFF_MID = NA_OFF_POOL + dgm_align256(dgm_pool_bytes(FUSED_MA
 constexpr size_t NA_OFF_MID_SF = NA_OFF_MID + dgm_align256((size_t)NA_MAX_ROUTES * NA_MAX_INTER);
 constexpr size_t NA_OFF_PART = NA_OFF_MID_SF + dgm_align256((size_t)NA_MAX_ROUTES * (NA_MAX_INTER / 16));
 constexpr size_t NA_BYTES = NA_OFF_PART + dgm_align256((size_t)NA_MAX_ROUTES * NA_MAX_HIDDEN * 2);
-static_assert(NA_BYTES < 7u * 1024 * 1024, "a modest array");
+static_assert(NA_BYTES < 5u * 1024 * 1024, "a modest array");
 
 constexpr int NA_MAX_DEVICES = 64;
 
@@ -74,7 +75,7 @@ extern "C" int dgm_megamoe_fused_launch_noalloc(const DgmMoeArgs* A, hipStream_t
   DGM_CHECK_ARG(A->num_tokens <= FUSED_MAX_TOKENS && A->num_local_experts <= FUSED_MAX_LOCAL,
                 "no-alloc layer: num_tokens <= 256 and num_local_experts <= 512");
   DGM_CHECK_ARG(A->hidden <= NA_MAX_HIDDEN && A->intermediate <= NA_MAX_INTER,
-                "no-alloc layer: hidden <= 4096 and intermediate <= 2048 (the workspace array's size)");
+                "no-alloc layer: hidden <= 3072 and intermediate <= 1280 (the workspace array's size)");
   if (A->num_tokens == 0) return 0;
   int dev = 0;
   const hipError_t e = hipGetDevice(&dev);

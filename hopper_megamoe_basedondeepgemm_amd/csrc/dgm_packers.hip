@@ -28,6 +28,55 @@ DGM_DEV void load32_bf16(const uint16_t* p, float* v) {
   }
 }
 
+// Source element types of the weight packers (the reference packers take any float tensor and
+// compute on its fp32 value: weight.to(torch.float32)); every one converts to fp32 exactly.
+enum SrcType { SRC_BF16 = 0, SRC_F16 = 1, SRC_F32 = 2 };
+
+DGM_DEV float half_bits_to_f32(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// N (a multiple of 8) consecutive elements starting at element `off` of a SRC array (16-byte
+// aligned there) as fp32.
+template <int SRC, int N>
+DGM_DEV void load_vals(const void* base, int64_t off, float* v) {
+  static_assert(N % 8 == 0, "whole 16-byte loads");
+  if constexpr (SRC == SRC_F32) {
+    const U4* q = reinterpret_cast<const U4*>(reinterpret_cast<const float*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const U4 r = q[i];
+      v[4 * i] = __uint_as_float(r.x);
+      v[4 * i + 1] = __uint_as_float(r.y);
+      v[4 * i + 2] = __uint_as_float(r.z);
+      v[4 * i + 3] = __uint_as_float(r.w);
+    }
+  } else {
+    const U4* q = reinterpret_cast<const U4*>(reinterpret_cast<const uint16_t*>(base) + off);
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const U4 r = q[i];
+      const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (SRC == SRC_BF16) {
+          v[i * 8 + 2 * j] = __uint_as_float(w[j] << 16);
+          v[i * 8 + 2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        } else {
+          v[i * 8 + 2 * j] = half_bits_to_f32(w[j] & 0xffffu);
+          v[i * 8 + 2 * j + 1] = half_bits_to_f32(w[j] >> 16);
+        }
+      }
+    }
+  }
+}
+
+// Element i of a SRC array as fp32.
+template <int SRC>
+DGM_DEV float load_one(const void* base, int64_t i) {
+  if constexpr (SRC == SRC_F32) return reinterpret_cast<const float*>(base)[i];
+  else if constexpr (SRC == SRC_F16) return half_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+  else return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+}
+
 // Marlin byte order of 8 nibbles n[0..7]: byte b = n[b] << 4 | n[b+4]  -> one u32.
 DGM_DEV uint32_t marlin8(const uint32_t* n) {
   uint32_t w = 0;
@@ -45,12 +94,13 @@ DGM_DEV uint32_t lowfirst8(const uint32_t* n) {
 
 // ------------------------------------------------------------------ MXFP4 weight packers
 // rule 0: quantization_mxfp4_fused.quantize_to_mxfp4; rule 1: quantization_mxfp4.quantize_to_mxfp4.
-__global__ void k_quantize_mxfp4(const uint16_t* __restrict__ w, int64_t groups, int rule,
+template <int SRC>
+__global__ void k_quantize_mxfp4(const void* __restrict__ w, int64_t groups, int rule,
                                  uint32_t* __restrict__ packed, uint8_t* __restrict__ scale) {
   int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= groups) return;
   float v[32];
-  load32_bf16(w + g * 32, v);
+  load_vals<SRC, 32>(w, g * 32, v);
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -156,23 +206,13 @@ DGM_DEV float ue4m3_value(uint32_t c) {
   return (1.0f + (float)m * 0.125f) * exp2f((float)((int)eb - 7));
 }
 
-__global__ void k_quantize_nvfp4(const uint16_t* __restrict__ w, int64_t groups16,
+template <int SRC>
+__global__ void k_quantize_nvfp4(const void* __restrict__ w, int64_t groups16,
                                  uint32_t* __restrict__ packed, uint8_t* __restrict__ scale) {
   int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= groups16) return;
-  float v[32];
-  // 16 elements: load 32 B
-  const U4* q = reinterpret_cast<const U4*>(w + g * 16);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    U4 r = q[i];
-    uint32_t ww[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[i * 8 + 2 * j] = __uint_as_float(ww[j] << 16);
-      v[i * 8 + 2 * j + 1] = __uint_as_float(ww[j] & 0xffff0000u);
-    }
-  }
+  float v[16];
+  load_vals<SRC, 16>(w, g * 16, v);
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -195,25 +235,26 @@ __global__ void k_quantize_nvfp4(const uint16_t* __restrict__ w, int64_t groups1
 // One wave per weight row: row amax -> s1 (bf16), then lane-per-K128-group codes.
 // plane != null: the split path's int4 form (s2 clamped to 127 instead of 15, which |w8| <= 112
 // never reaches; s2 | z << 8 | bf16(s1) << 16 per (row, K128 group) instead of s2o / zo / s1o)
-__global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int K,
+template <int SRC>
+__global__ void k_quantize_qoq(const void* __restrict__ w, int64_t rows, int K,
                                uint8_t* __restrict__ packed, uint8_t* __restrict__ s2o,
                                uint8_t* __restrict__ zo, float* __restrict__ s1o, uint32_t* __restrict__ plane) {
   int lane = threadIdx.x & 63;
   int64_t row = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* src = w + row * K;
+  const int64_t src = row * K;        // the row's first element
   float amax = 0.f;
-  for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(bf16_to_f32(src[k])));
+  for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(load_one<SRC>(w, src + k)));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
   float s1 = round_bf16(fmaxf(amax / 120.0f, 1e-30f));
   if (lane == 0 && !plane) s1o[row] = s1;
   int G = K / 128;
   for (int g = lane; g < G; g += 64) {
-    const uint16_t* p = src + g * 128;
+    const int64_t p = src + g * 128;
     float mn = 1e30f, mx = -1e30f;
     for (int i = 0; i < 128; ++i) {
-      float w8 = fminf(fmaxf(rintf(bf16_to_f32(p[i]) / s1), -112.f), 112.f);
+      float w8 = fminf(fmaxf(rintf(load_one<SRC>(w, p + i) / s1), -112.f), 112.f);
       mn = fminf(mn, w8);
       mx = fmaxf(mx, w8);
     }
@@ -223,7 +264,7 @@ __global__ void k_quantize_qoq(const uint16_t* __restrict__ w, int64_t rows, int
     for (int c8 = 0; c8 < 16; ++c8) {
       uint32_t n[8];
       for (int i = 0; i < 8; ++i) {
-        float w8 = fminf(fmaxf(rintf(bf16_to_f32(p[c8 * 8 + i]) / s1), -112.f), 112.f);
+        float w8 = fminf(fmaxf(rintf(load_one<SRC>(w, p + c8 * 8 + i) / s1), -112.f), 112.f);
         n[i] = (uint32_t)fminf(fmaxf(rintf(w8 / s2 + z), 0.f), 15.f);
       }
       dst[c8] = marlin8(n);
@@ -385,7 +426,9 @@ DGM_DEV uint32_t reorder32(uint32_t w, int from, int to) {
 }
 
 // One thread per 16 bytes (the last thread may own fewer whole words); in place is allowed.
-__global__ void k_reorder_fp4(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t words,
+// (src == dst converts in place: each thread reads its words before it writes them, so no
+// __restrict__ here)
+__global__ void k_reorder_fp4(const uint8_t* src, uint8_t* dst, int64_t words,
                               int from, int to) {
   const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= words) return;
@@ -554,14 +597,28 @@ extern "C" {
 
 int dgm_quantize_mxfp4(const void* w_bf16, int64_t rows, int64_t K, int rule,
                        void* packed, void* scale_e8m0, hipStream_t stream) {
+  return dgm_quantize_mxfp4_typed(w_bf16, DGM_SRC_BF16, rows, K, rule, packed, scale_e8m0, stream);
+}
+
+int dgm_quantize_mxfp4_typed(const void* w_bf16, int src_dtype, int64_t rows, int64_t K, int rule,
+                             void* packed, void* scale_e8m0, hipStream_t stream) {
   DGM_CHECK_ARG(w_bf16 && packed && scale_e8m0, "null pointer");
+  DGM_CHECK_ARG(src_dtype >= DGM_SRC_BF16 && src_dtype <= DGM_SRC_F32, "src_dtype 0 bf16, 1 fp16, 2 fp32");
   DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 32 == 0, "K must be a positive multiple of 32");
   DGM_CHECK_ARG(rule == 0 || rule == 1, "rule must be 0 (fused) or 1 (split)");
   DGM_CHECK_ARG(((uintptr_t)w_bf16 & 15) == 0 && ((uintptr_t)packed & 15) == 0, "16-byte alignment");
   int64_t groups = rows * (K / 32);
   if (groups == 0) return 0;
-  hipLaunchKernelGGL(k_quantize_mxfp4, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
-                     (const uint16_t*)w_bf16, groups, rule, (uint32_t*)packed, (uint8_t*)scale_e8m0);
+  const dim3 gd(grid_for(groups, 256));
+  if (src_dtype == DGM_SRC_F32)
+    hipLaunchKernelGGL(k_quantize_mxfp4<SRC_F32>, gd, dim3(256), 0, stream, w_bf16, groups, rule, (uint32_t*)packed,
+                       (uint8_t*)scale_e8m0);
+  else if (src_dtype == DGM_SRC_F16)
+    hipLaunchKernelGGL(k_quantize_mxfp4<SRC_F16>, gd, dim3(256), 0, stream, w_bf16, groups, rule, (uint32_t*)packed,
+                       (uint8_t*)scale_e8m0);
+  else
+    hipLaunchKernelGGL(k_quantize_mxfp4<SRC_BF16>, gd, dim3(256), 0, stream, w_bf16, groups, rule, (uint32_t*)packed,
+                       (uint8_t*)scale_e8m0);
   return dgm_last_launch_status();
 }
 
@@ -591,36 +648,72 @@ int dgm_cast_fp8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_e4m3,
 
 int dgm_quantize_nvfp4(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* scale_ue4m3,
                        hipStream_t stream) {
+  return dgm_quantize_nvfp4_typed(w_bf16, DGM_SRC_BF16, rows, K, packed, scale_ue4m3, stream);
+}
+
+int dgm_quantize_nvfp4_typed(const void* w_bf16, int src_dtype, int64_t rows, int64_t K, void* packed,
+                             void* scale_ue4m3, hipStream_t stream) {
   DGM_CHECK_ARG(w_bf16 && packed && scale_ue4m3, "null pointer");
+  DGM_CHECK_ARG(src_dtype >= DGM_SRC_BF16 && src_dtype <= DGM_SRC_F32, "src_dtype 0 bf16, 1 fp16, 2 fp32");
   DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 16 == 0, "K must be a positive multiple of 16");
   DGM_CHECK_ARG(((uintptr_t)w_bf16 & 15) == 0 && ((uintptr_t)packed & 7) == 0, "alignment");
   int64_t groups = rows * (K / 16);
   if (groups == 0) return 0;
-  hipLaunchKernelGGL(k_quantize_nvfp4, dim3(grid_for(groups, 256)), dim3(256), 0, stream,
-                     (const uint16_t*)w_bf16, groups, (uint32_t*)packed, (uint8_t*)scale_ue4m3);
+  const dim3 gd(grid_for(groups, 256));
+  if (src_dtype == DGM_SRC_F32)
+    hipLaunchKernelGGL(k_quantize_nvfp4<SRC_F32>, gd, dim3(256), 0, stream, w_bf16, groups, (uint32_t*)packed,
+                       (uint8_t*)scale_ue4m3);
+  else if (src_dtype == DGM_SRC_F16)
+    hipLaunchKernelGGL(k_quantize_nvfp4<SRC_F16>, gd, dim3(256), 0, stream, w_bf16, groups, (uint32_t*)packed,
+                       (uint8_t*)scale_ue4m3);
+  else
+    hipLaunchKernelGGL(k_quantize_nvfp4<SRC_BF16>, gd, dim3(256), 0, stream, w_bf16, groups, (uint32_t*)packed,
+                       (uint8_t*)scale_ue4m3);
   return dgm_last_launch_status();
 }
 
-int dgm_quantize_qoq(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* s2, void* z,
-                     void* s1_f32, hipStream_t stream) {
-  DGM_CHECK_ARG(w_bf16 && packed && s2 && z && s1_f32, "null pointer");
+}  // extern "C"
+
+// The QoQ packer over a source of src_dtype: s2 / z / s1 planes, or (plane non-null) the int32
+// coefficient plane of the split path's int4 form.
+static int quantize_qoq_any(const void* w, int src_dtype, int64_t rows, int64_t K, void* packed, void* s2, void* z,
+                            void* s1, void* plane, hipStream_t stream) {
+  DGM_CHECK_ARG(src_dtype >= DGM_SRC_BF16 && src_dtype <= DGM_SRC_F32, "src_dtype 0 bf16, 1 fp16, 2 fp32");
   DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 128 == 0, "K must be a positive multiple of 128");
   if (rows == 0) return 0;
-  hipLaunchKernelGGL(k_quantize_qoq, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
-                     (const uint16_t*)w_bf16, rows, (int)K, (uint8_t*)packed, (uint8_t*)s2,
-                     (uint8_t*)z, (float*)s1_f32, (uint32_t*)nullptr);
+  const dim3 gd(grid_for(rows, 4));
+#define DGM_QOQ(SRC)                                                                                             \
+  hipLaunchKernelGGL(k_quantize_qoq<SRC>, gd, dim3(256), 0, stream, w, rows, (int)K, (uint8_t*)packed, (uint8_t*)s2, \
+                     (uint8_t*)z, (float*)s1, (uint32_t*)plane)
+  if (src_dtype == DGM_SRC_F32) DGM_QOQ(SRC_F32);
+  else if (src_dtype == DGM_SRC_F16) DGM_QOQ(SRC_F16);
+  else DGM_QOQ(SRC_BF16);
+#undef DGM_QOQ
   return dgm_last_launch_status();
+}
+
+extern "C" {
+
+int dgm_quantize_qoq(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* s2, void* z,
+                     void* s1_f32, hipStream_t stream) {
+  return dgm_quantize_qoq_typed(w_bf16, DGM_SRC_BF16, rows, K, packed, s2, z, s1_f32, stream);
+}
+
+int dgm_quantize_qoq_typed(const void* w_bf16, int src_dtype, int64_t rows, int64_t K, void* packed, void* s2,
+                           void* z, void* s1_f32, hipStream_t stream) {
+  DGM_CHECK_ARG(w_bf16 && packed && s2 && z && s1_f32, "null pointer");
+  return quantize_qoq_any(w_bf16, src_dtype, rows, K, packed, s2, z, s1_f32, nullptr, stream);
 }
 
 int dgm_quantize_qoq_int4(const void* w_bf16, int64_t rows, int64_t K, void* packed, void* plane_i32,
                           hipStream_t stream) {
+  return dgm_quantize_qoq_int4_typed(w_bf16, DGM_SRC_BF16, rows, K, packed, plane_i32, stream);
+}
+
+int dgm_quantize_qoq_int4_typed(const void* w_bf16, int src_dtype, int64_t rows, int64_t K, void* packed,
+                                void* plane_i32, hipStream_t stream) {
   DGM_CHECK_ARG(w_bf16 && packed && plane_i32, "null pointer");
-  DGM_CHECK_ARG(rows >= 0 && K > 0 && K % 128 == 0, "K must be a positive multiple of 128");
-  if (rows == 0) return 0;
-  hipLaunchKernelGGL(k_quantize_qoq, dim3(grid_for(rows, 4)), dim3(256), 0, stream,
-                     (const uint16_t*)w_bf16, rows, (int)K, (uint8_t*)packed, (uint8_t*)nullptr,
-                     (uint8_t*)nullptr, (float*)nullptr, (uint32_t*)plane_i32);
-  return dgm_last_launch_status();
+  return quantize_qoq_any(w_bf16, src_dtype, rows, K, packed, nullptr, nullptr, nullptr, plane_i32, stream);
 }
 
 int dgm_cast_int8_rows(const void* x_bf16, int64_t rows, int64_t K, void* q_i8, void* sf_f32,

@@ -355,10 +355,11 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
     DG_FE_SELECT_IN_MEGA, default 0; tokens <= 64): stop after the logits and the cast; the
     next fused call on this buffer selects the top-k (in its prologue up to 8 tokens, else in a
     selection launch just before it) and writes ``topk_idx / topk_weights``, which are not valid
-    before that call. ``stamps``,
-    ``l2_persist`` is an H20 tuning knob with no effect here; ``wlayout="pre"`` takes router weights
-    in the fragment order of ``fable_router_weight_fragment_layout`` ("row" / "fragment": row-major
-    weights, as given)."""
+    before that call. ``stamps`` (env DG_FE_STAMPS, default 0): every frontend workgroup records
+    phase stamps, read back with ``fable_frontend_stamps`` (the stamp rows are allocated on the
+    first stamped call and kept with the buffer). ``l2_persist`` is an H20 tuning knob with no
+    effect here; ``wlayout="pre"`` takes router weights in the fragment order of
+    ``fable_router_weight_fragment_layout`` ("row" / "fragment": row-major weights, as given)."""
     b = sym_buffer
     _lib.require_gpu(hidden, router_weight)
     router_weight = _router_weight_row_major(router_weight, wlayout)
@@ -381,11 +382,58 @@ def fable_router_quant_topk_frontend(hidden: torch.Tensor, router_weight: torch.
     b._fe_select = (flags, int(token_offset)) if select_in_mega else None
     if select_in_mega:
         flags |= _lib.FE_SELECT_IN_MEGA
+    if stamps is None:
+        stamps = int(os.environ.get("DG_FE_STAMPS", "0"))
+    st_ptr, st_rows = None, 0
+    if stamps:
+        st_rows = _lib.load().dgm_frontend_workgroups(m, h, e, b.act_code, flags, 1)
+        have = getattr(b, "_fe_stamps", None)
+        if have is None or have.size(0) < st_rows:
+            b._fe_stamps = torch.zeros((max(st_rows, 1), 8), dtype=torch.int64, device=b.buffer.device)
+        b._fe_stamps.zero_()
+        st_ptr = b._fe_stamps
+    b._fe_stamp_rows = st_rows
     hidden = hidden.contiguous()
     router_weight = router_weight.contiguous()
-    _lib.check(_lib.load().dgm_router_topk_launch(
+    _lib.check(_lib.load().dgm_router_topk_launch_stamped(
         _lib.ptr(hidden), _lib.ptr(router_weight), m, h, e, b.num_topk, b.act_code, flags,
-        int(token_offset), _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.stream()))
+        int(token_offset), _lib.ptr(b.buffer), ctypes.byref(b.layout), _lib.ptr(st_ptr), st_rows, _lib.stream()))
+
+
+def fable_frontend_stamps(sym_buffer, e: int = None) -> torch.Tensor:
+    """deep_gemm/mega/__init__.py:743: int64 [workgroups, 8] phase stamps of the last frontend call
+    made with ``stamps=1`` on this buffer, in ns (the GPU's 100 MHz wall clock x 10; unused slots
+    0). Rows: the router workgroups ([0] entry, [3] logits and keys stored, [6] hardware position
+    HW_ID | XCC_ID << 32, [7] exit), then the cast workgroups ([0] entry, [5] cast stored, [6],
+    [7]). The top-k selection runs in a launch of its own (or in the fused layer's prologue) and
+    is not stamped here; the fused layer has its own ``phase_stamps``."""
+    b = sym_buffer
+    assert e is None or e == b.num_experts
+    rows = getattr(b, "_fe_stamp_rows", 0)
+    if not rows:
+        raise RuntimeError("no stamped frontend call on this buffer: pass stamps=1 (or DG_FE_STAMPS=1)")
+    out = b._fe_stamps[:rows].clone()
+    pos = out[:, 6].clone()
+    out.mul_(10)
+    out[:, 6] = pos
+    return out
+
+
+def get_nvfp4_mega_moe_sm90_block_n(intermediate_hidden: int) -> int:
+    """deep_gemm/mega/__init__.py:226: the SM90 NVFP4 N tile (128), kept for callers that pass it
+    on; the MI355X layout (``transform_nvfp4_weights_for_mega_moe_fused``) has one tile shape."""
+    assert intermediate_hidden > 0 and intermediate_hidden % 128 == 0
+    return 128
+
+
+def get_nvfp4_mega_moe_sm90_weight_layout(hidden: int, intermediate_hidden: int) -> str:
+    """deep_gemm/mega/__init__.py:232: the packed-value layout the SM90 NVFP4 path caches for a
+    model shape ("prmt_groups" when hidden > 2 * intermediate_hidden, else "marlin"). Kept for
+    callers that record it; ``transform_nvfp4_weights_for_mega_moe_fused`` takes Marlin or
+    low-nibble-first codes and writes one MI355X layout for every shape."""
+    assert hidden > 0 and hidden % 128 == 0
+    assert intermediate_hidden > 0 and intermediate_hidden % 128 == 0
+    return "prmt_groups" if hidden > 2 * intermediate_hidden else "marlin"
 
 
 def fable_frontend_keys(sym_buffer) -> torch.Tensor:

@@ -21,13 +21,14 @@ def quantize_to_qoq_int4(weight: torch.Tensor, group_size: int = 128):
     """Returns ``(packed uint8 [E, N, K/2] (Marlin), plane int32 [E, N, K/128])`` with plane =
     s2 | z << 8 | bf16(s1) << 16 per (row, K128 group)."""
     assert group_size == 128
+    assert weight.dim() == 3
+    code = _lib.src_dtype(weight)
     _lib.require_gpu(weight)
-    assert weight.dtype == torch.bfloat16 and weight.dim() == 3
     w = weight.contiguous()
     E, N, K = w.shape
     assert K % 128 == 0
     packed = torch.empty((E, N, K // 2), dtype=torch.uint8, device=w.device)
     plane = torch.empty((E, N, K // 128), dtype=torch.int32, device=w.device)
-    _lib.check(_lib.load().dgm_quantize_qoq_int4(_lib.ptr(w), E * N, K, _lib.ptr(packed), _lib.ptr(plane),
-                                                 _lib.stream()))
+    _lib.check(_lib.load().dgm_quantize_qoq_int4_typed(_lib.ptr(w), code, E * N, K, _lib.ptr(packed), _lib.ptr(plane),
+                                                       _lib.stream()))
     return packed, plane

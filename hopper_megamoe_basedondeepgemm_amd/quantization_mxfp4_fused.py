@@ -13,21 +13,23 @@ MXFP4_GROUP_SIZE = 32
 
 
 def _pack(weight, rule):
+    assert weight.is_floating_point()
+    code = _lib.src_dtype(weight)        # bf16 / fp16 / fp32, read as their fp32 values
     _lib.require_gpu(weight)
-    assert weight.dtype == torch.bfloat16, "weights are packed from bf16"
     w = weight.contiguous()
     *outer, K = w.shape
     assert K % MXFP4_GROUP_SIZE == 0
     rows = w.numel() // K
     packed = torch.empty((*outer, K // 2), dtype=torch.uint8, device=w.device)
     scale = torch.empty((*outer, K // 32), dtype=torch.uint8, device=w.device)
-    _lib.check(_lib.load().dgm_quantize_mxfp4(_lib.ptr(w), rows, K, rule, _lib.ptr(packed),
-                                              _lib.ptr(scale), _lib.stream()))
+    _lib.check(_lib.load().dgm_quantize_mxfp4_typed(_lib.ptr(w), code, rows, K, rule, _lib.ptr(packed),
+                                                    _lib.ptr(scale), _lib.stream()))
     return packed, scale
 
 
 def quantize_to_mxfp4(weight: torch.Tensor, group_size: int = MXFP4_GROUP_SIZE):
-    """bf16 ``(..., K)`` -> ``(packed uint8 (..., K/2) Marlin order, scale_e8m0 uint8 (..., K/32))``."""
+    """bf16 / fp16 / fp32 ``(..., K)`` -> ``(packed uint8 (..., K/2) Marlin order, scale_e8m0 uint8
+    (..., K/32))``."""
     assert group_size == MXFP4_GROUP_SIZE
     return _pack(weight, 0)
 

@@ -13,9 +13,11 @@ QOQ_GROUP_SIZE = 128
 
 
 def quantize_to_qoq(weight: torch.Tensor, group_size: int = QOQ_GROUP_SIZE):
+    """bf16 / fp16 / fp32 ``(..., K)`` -> ``(packed (..., K/2) Marlin, s2 (..., K/128), z (..., K/128),
+    s1 fp32 (...))``."""
     assert group_size == QOQ_GROUP_SIZE
+    code = _lib.src_dtype(weight)
     _lib.require_gpu(weight)
-    assert weight.dtype == torch.bfloat16
     w = weight.contiguous()
     *outer, K = w.shape
     rows = w.numel() // K
@@ -24,8 +26,8 @@ def quantize_to_qoq(weight: torch.Tensor, group_size: int = QOQ_GROUP_SIZE):
     s2 = torch.empty((*outer, K // 128), dtype=torch.uint8, device=dev)
     z = torch.empty((*outer, K // 128), dtype=torch.uint8, device=dev)
     s1 = torch.empty(tuple(outer), dtype=torch.float32, device=dev)
-    _lib.check(_lib.load().dgm_quantize_qoq(_lib.ptr(w), rows, K, _lib.ptr(packed), _lib.ptr(s2), _lib.ptr(z),
-                                            _lib.ptr(s1), _lib.stream()))
+    _lib.check(_lib.load().dgm_quantize_qoq_typed(_lib.ptr(w), code, rows, K, _lib.ptr(packed), _lib.ptr(s2),
+                                                  _lib.ptr(z), _lib.ptr(s1), _lib.stream()))
     return packed, s2, z, s1
 
 

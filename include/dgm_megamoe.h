@@ -56,6 +56,24 @@ const char* dgm_last_error(void);
 int dgm_quantize_mxfp4(const void* w_bf16, int64_t rows, int64_t K, int rule,
                        void* packed, void* scale_e8m0, hipStream_t stream);
 
+/* Element types of the weight packers' source (the reference packers take any float tensor and
+ * compute on its fp32 value, weight.to(torch.float32): deep_gemm/quantization_mxfp4_fused.py:36,
+ * quantization_mxfp4.py:54, quantization_nvfp4.py:62-66, quantization_qoq_fused.py:20). */
+#define DGM_SRC_BF16 0
+#define DGM_SRC_F16 1
+#define DGM_SRC_F32 2
+
+/* The weight packers over a source of src_dtype (DGM_SRC_*); the untyped entry points are
+ * these with DGM_SRC_BF16. The source is 16-byte aligned. */
+int dgm_quantize_mxfp4_typed(const void* w, int src_dtype, int64_t rows, int64_t K, int rule,
+                             void* packed, void* scale_e8m0, hipStream_t stream);
+int dgm_quantize_nvfp4_typed(const void* w, int src_dtype, int64_t rows, int64_t K, void* packed,
+                             void* scale_ue4m3, hipStream_t stream);
+int dgm_quantize_qoq_typed(const void* w, int src_dtype, int64_t rows, int64_t K, void* packed, void* s2,
+                           void* z, void* s1_f32, hipStream_t stream);
+int dgm_quantize_qoq_int4_typed(const void* w, int src_dtype, int64_t rows, int64_t K, void* packed,
+                                void* plane_i32, hipStream_t stream);
+
 /* Replaces sm100_b200/test_mega_moe.py:78 cast_to_fp4_rows (amax_floor 1e-30) and
  * deep_gemm/utils/math.py:85 per_token_cast_to_fp4(use_ue8m0=True, gran_k=32) (amax_floor 1e-4).
  * x_bf16 [rows, K] -> packed [rows, K/2] (low nibble = even K), sf_e8m0 [rows, K/32]. */
@@ -162,6 +180,13 @@ typedef struct DgmBufferLayout {
   size_t partials;                              /* bf16 [topk, max_tokens, H] route outputs (combine_partials) */
   size_t counters;                              /* int32 scratch counters                  */
   int32_t x_row_bytes, mid_row_bytes, max_routes, max_tokens;
+  /* the shape the buffer was laid out for: every launch on it is refused (DGM_ERR_INVALID_ARGUMENT,
+     before anything is enqueued) unless num_tokens <= max_tokens, topk <= topk, num_experts <=
+     num_experts, num_local_experts <= num_local_experts, hidden (and intermediate) equal, and the
+     call's activation format needs at most x_row_bytes / x_sf_row_bytes / mid_row_bytes /
+     mid_sf_row_bytes per row */
+  int32_t topk, num_experts, num_local_experts, hidden, intermediate, act_format;
+  int32_t x_sf_row_bytes, mid_sf_row_bytes;
 } DgmBufferLayout;
 
 int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_experts, int topk,
@@ -184,6 +209,22 @@ int dgm_router_topk_launch(const void* hidden_bf16, const void* router_weight_bf
                            int num_tokens, int hidden, int num_experts, int topk, int act_format,
                            int flags, int token_offset, void* buffer,
                            const DgmBufferLayout* layout, hipStream_t stream);
+
+/* dgm_router_topk_launch with the reference's frontend phase stamps (stamps=1 of
+ * deep_gemm/mega/__init__.py:671, read back by fable_frontend_stamps, :743-756): stamps is
+ * int64 [stamp_rows, 8]; frontend workgroup b (< stamp_rows; rows are the router workgroups,
+ * then the cast workgroups) writes [0] entry, [3] its logits and keys stored (router rows),
+ * [5] its cast stored (cast rows), [6] its hardware position (HW_ID | XCC_ID << 32), [7] exit,
+ * on the 100 MHz wall clock; unused slots 0. NULL / 0 rows = no stamps. */
+int dgm_router_topk_launch_stamped(const void* hidden_bf16, const void* router_weight_bf16,
+                                   int num_tokens, int hidden, int num_experts, int topk, int act_format,
+                                   int flags, int token_offset, void* buffer, const DgmBufferLayout* layout,
+                                   int64_t* stamps, int stamp_rows, hipStream_t stream);
+
+/* Workgroups of the frontend launch for a shape (router = 0: the cast alone), i.e. the rows
+ * dgm_router_topk_launch_stamped can stamp. Replaces deep_gemm/mega/__init__.py:653
+ * fable_frontend_router_ctas for sizing the stamps (that one counts router workgroups only). */
+int dgm_frontend_workgroups(int num_tokens, int hidden, int num_experts, int act_format, int flags, int router);
 
 /* Replaces the router_logits input of deep_gemm/mega/__init__.py:340 mxfp4_mega_moe (the SM90
  * kernel's kRouterLogitsInput path, deep_gemm/include/deep_gemm/impls/sm90_mxfp4_mega_moe.cuh:1295-1343):
@@ -259,10 +300,10 @@ int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
 /* No counterpart in the reference: dgm_megamoe_fused_launch for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
  * The same layer, but the persistent kernel's workspace (dispatch table, L1 -> L2 rows, route
- * outputs, counters) is a file-scope device array of ~6.4 MB held by each GPU the library runs on,
+ * outputs, counters) is a file-scope device array of ~4.9 MB held by each GPU the library runs on,
  * not the buffer's views: the buffer supplies only the inputs (x / x_sf, or the keys / topk views)
  * and args->y the output; the buffer's pool, l2_acts and combine_partials views are not written.
- * Limits: num_tokens * topk <= 512, num_tokens <= 256, hidden <= 4096, intermediate <= 2048
+ * Limits: num_tokens * topk <= 512, num_tokens <= 256, hidden <= 3072, intermediate <= 1280
  * (beyond them: DGM_ERR_INVALID_ARGUMENT, nothing launched). No hipMalloc / hipFree is called;
  * the first call on a device clears the array's counters with a fill kernel on `stream`, and
  * every launch clears the counter set that the next launch uses. All calls on one GPU share its array: calls that overlap

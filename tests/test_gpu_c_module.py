@@ -139,3 +139,26 @@ def test_c_frontend_cast_and_select_in_mega_keys():
 def np_bf16_bits(a):
     from oracle import numerics as nu
     return nu.f32_to_bf16_bits(a)
+
+
+def test_c_buffer_cache_follows_the_callers_tensor():
+    """A sliced buffer is remembered per (address, rank, format) for as long as the caller's
+    tensor lives: slicing the same memory for another shape replaces the wrapper (the later
+    layer calls then use the new shape), and dropping the tensor drops the entry (and the view
+    that kept its memory)."""
+    need_gpu()
+    import gc
+    from hopper_megamoe_basedondeepgemm_amd import _C
+    n, slice_fn = _C.get_symm_buffer_size_for_fused_mega_moe(1, 32, 8, 8, 1024, 512)
+    n2, slice_fn2 = _C.get_symm_buffer_size_for_fused_mega_moe(1, 32, 4, 8, 1024, 512)
+    assert n2 < n
+    raw = torch.zeros(n, dtype=torch.int8, device="cuda")
+    key = (raw.data_ptr(), 0, "fp8f128")
+    slice_fn(raw)
+    assert _C._lookup(raw, 0).num_max_tokens_per_rank == 8
+    views = slice_fn2(raw)
+    assert _C._lookup(raw, 0).num_max_tokens_per_rank == 4 and tuple(views[2].shape) == (4, 8)
+    assert key in _C._BUFFERS
+    del raw, views
+    gc.collect()
+    assert key not in _C._BUFFERS

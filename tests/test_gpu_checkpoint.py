@@ -29,11 +29,17 @@ def test_reorder_fp4_nibbles(n_bytes):
 
 
 def test_reorder_rejects_partial_words():
+    """Rows of partial words: refused by the Python helper (a word would straddle two rows) and,
+    for a byte count that is not whole words, by the C ABI itself."""
     need_gpu()
-    from hopper_megamoe_basedondeepgemm_amd import checkpoint as ck
+    from hopper_megamoe_basedondeepgemm_amd import checkpoint as ck, _lib
     t = torch.zeros(6, dtype=torch.uint8, device="cuda")
-    with pytest.raises(RuntimeError, match="n_bytes % 4"):
+    with pytest.raises(AssertionError, match="4-byte words"):
         ck.ocp_to_marlin(t)
+    with pytest.raises(AssertionError, match="4-byte words"):
+        ck.ocp_to_marlin(torch.zeros((2, 6), dtype=torch.uint8, device="cuda"))
+    with pytest.raises(RuntimeError, match="n_bytes % 4"):
+        _lib.check(_lib.load().dgm_reorder_fp4_nibbles(_lib.ptr(t), _lib.ptr(t), 6, 1, 0, _lib.stream()))
 
 
 def _weights(seed, E, I, H, nvfp4):

@@ -138,6 +138,48 @@ def test_packers_bit_exact():
     np.testing.assert_array_equal(sf8.cpu().numpy(), rsf8)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_packers_take_fp32_and_fp16_weights(dtype):
+    """The weight packers read bf16, fp16 or fp32 weights at their fp32 value, as the reference's
+    do (weight.to(torch.float32): deep_gemm/quantization_mxfp4_fused.py:36, quantization_mxfp4.py:54,
+    quantization_nvfp4.py:62, quantization_qoq_fused.py:20): codes and scales bit-exact against the
+    oracle on the same values, with values that bf16 cannot hold, an all-zero group, an amax a
+    hair above 6 * 2^k (where the log2 rule keeps 2^k) and E2M1 midpoints."""
+    need_gpu()
+    from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf, quantization_mxfp4 as qs
+    from hopper_megamoe_basedondeepgemm_amd import quantization_nvfp4 as qn, quantization_qoq_fused as qq
+    rng = np.random.default_rng(17)
+    w = (rng.standard_normal((3, 64, 512)) * 0.02).astype(np.float32)
+    w[0, 0, :32] = 0.0
+    w[0, 1, 3] = np.float32(6.0 * 2.0 ** -9) * np.float32(1 + 2 ** -22)      # amax / 6 a hair above 2^-9
+    w[0, 2] = np.tile(np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5, 6], np.float32) / 8, 64)
+    if dtype == torch.float16:
+        w = w.astype(np.float16).astype(np.float32)
+    else:
+        assert (nu.round_bf16(w) != w).mean() > 0.9          # mostly values bf16 cannot hold
+    tw = torch.from_numpy(w).to(dtype).cuda()
+    print(f"packers from {dtype}", flush=True)
+    for fn, ref in ((qf.quantize_to_mxfp4, pk.quantize_to_mxfp4_fused),
+                    (qs.quantize_to_mxfp4, pk.quantize_to_mxfp4_split),
+                    (qn.quantize_to_nvfp4, pk.quantize_to_nvfp4)):
+        p, s = fn(tw)
+        rp, rs = ref(w)
+        np.testing.assert_array_equal(s.cpu().numpy(), rs)
+        np.testing.assert_array_equal(p.cpu().numpy(), rp)
+    p, s2, z, s1 = qq.quantize_to_qoq(tw)
+    rp, rs2, rz, rs1 = pk.quantize_to_qoq(w)
+    np.testing.assert_array_equal(s1.cpu().numpy(), rs1)
+    np.testing.assert_array_equal(s2.cpu().numpy(), rs2)
+    np.testing.assert_array_equal(z.cpu().numpy(), rz)
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)
+    p, plane = qs.quantize_to_qoq_int4(tw)
+    rp, rplane = pk.quantize_to_qoq_int4(w)
+    np.testing.assert_array_equal(plane.cpu().numpy(), rplane)
+    np.testing.assert_array_equal(p.cpu().numpy(), rp)
+    with pytest.raises(TypeError, match="bf16, fp16 or fp32"):
+        qf.quantize_to_mxfp4(tw.double())
+
+
 def test_transform_dequant_invariant():
     """dequant(transform(q)) == interleave(dequant(q)) (the reference's transform check,
     tests/test_mxfp4_mega_moe_sm90_correctness.py:153-182), for L1 (interleaved) and L2."""

@@ -57,3 +57,43 @@ def test_phase_stamps_ordered_and_harmless(fmt, M, E):
     assert (rows[:, 6] + rows[:, 7] <= span).all()
     # the launch's workgroups run at once: every one enters before any exits
     assert entry.max() <= ex.min()
+
+
+@pytest.mark.parametrize("M,act", [(8, "mxfp8"), (3, "qoq"), (64, "nvfp4")])
+def test_frontend_stamps(M, act):
+    """fable_frontend_stamps (deep_gemm/mega/__init__.py:743-756) after a frontend call with
+    stamps=1: one row per frontend workgroup (router rows, then cast rows), entry <= the phase
+    stamp <= exit in ns, the hardware position recorded, and the stamped call writes the same
+    logits, keys and activation codes bit for bit as the call without stamps; no stamped call
+    yet raises."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    E, Hh = 384, 3072
+    print(f"frontend stamps M={M} act={act}", flush=True)
+    rng = np.random.default_rng(7500 + M)
+    x = bf16_cpu(randn_bf16(rng, (M, Hh))).cuda()
+    rw = bf16_cpu(randn_bf16(rng, (E, Hh), 0.02)).cuda()
+    outs = []
+    for stamps in (0, 1):
+        b = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, 8, Hh, 1280, act_format=act)
+        if not stamps:
+            with pytest.raises(RuntimeError, match="stamps=1"):
+                dgm.fable_frontend_stamps(b, E)
+        dgm.fable_router_quant_topk_frontend(x, rw, b, select_in_mega=True, stamps=stamps)
+        torch.cuda.synchronize()
+        outs.append((b.logits[:M].clone(), b.fe_keys[:M].clone(), b.x[:M].clone(), b.x_sf[:M].clone(), b))
+    for u, v in zip(outs[0][:4], outs[1][:4]):
+        assert torch.equal(u.view(torch.uint8), v.view(torch.uint8))
+    b = outs[1][4]
+    st = dgm.fable_frontend_stamps(b, E).cpu().numpy()
+    n_router = dgm.fable_frontend_router_ctas(M, E, Hh)
+    assert st.shape[0] == _lib.load().dgm_frontend_workgroups(M, Hh, E, b.act_code, _lib.FE_SELECT_IN_MEGA |
+                                                             _lib.FE_ZERO_ROW_UNROUTED, 1) > n_router
+    entry, ex = st[:, 0], st[:, 7]
+    assert (entry > 0).all() and (ex >= entry).all()
+    r, c = st[:n_router], st[n_router:]
+    assert ((r[:, 3] >= r[:, 0]) & (r[:, 3] <= r[:, 7]) & (r[:, 5] == 0)).all()
+    assert ((c[:, 5] >= c[:, 0]) & (c[:, 5] <= c[:, 7]) & (c[:, 3] == 0)).all()
+    assert (ex.max() - entry.min()) < 10_000_000          # one launch: well under 10 ms
+    assert len(np.unique(st[:, 6])) > 1                    # workgroups on more than one CU / wave slot

@@ -18,7 +18,9 @@ def test_fp8f128_and_qoq_share_one_layout(shape):
     formats' layouts are identical field by field."""
     a = _lib.layout(*shape, _lib.ACT_FORMATS["fp8f128"])
     b = _lib.layout(*shape, _lib.ACT_FORMATS["qoq"])
-    assert _fields(a) == _fields(b)
+    fa, fb = _fields(a), _fields(b)
+    assert fa.pop("act_format") != fb.pop("act_format")
+    assert fa == fb
     T, E, El, k, H, I = shape
     assert a.x_sf - a.x >= T * H and a.x_row_bytes == H and a.mid_row_bytes == I
 
@@ -78,3 +80,11 @@ def test_bench_reads_its_committed_profiles():
     u = bench.profiled_mfma_util()
     assert u is not None and 0 < u < 0.2, u
     assert bench.profiled_mfma_util("k_megamoe<24,10,3,false>", ("M=64", "NVFP4")) > u   # (VALU co-bound, busier)
+
+
+def test_reorder_fp4_nibbles_refuses_rows_of_partial_words():
+    """A Marlin word holds 8 codes of one row: a last dimension that is not whole 4-byte words
+    would let a word straddle two rows, so the checkpoint helper refuses it before any launch."""
+    from hopper_megamoe_basedondeepgemm_amd import checkpoint
+    with pytest.raises(AssertionError, match="4-byte words"):
+        checkpoint.reorder_fp4_nibbles(torch.zeros((3, 6), dtype=torch.uint8), "ocp", "marlin")

@@ -69,3 +69,52 @@ def test_product_path_has_no_cpu_fallback():
     w = torch.zeros((2, 64), dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="GPU"):
         dgm.quantization_mxfp4_fused.quantize_to_mxfp4(w)
+
+
+def test_launches_refuse_calls_beyond_the_buffers_shape():
+    """Every launch checks the call's shape against the one its buffer was laid out for, before
+    anything is enqueued: route outputs are [topk][max_tokens][H] and x rows [max_tokens, H or
+    H/2], so a larger topk (even with fewer tokens, same routes), more tokens (with a smaller
+    topk), another hidden / intermediate size, more experts, or an activation format with wider
+    rows would write past the views."""
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    lib = _lib.load()
+    L = _lib.layout(16, 384, 48, 8, 3072, 1280, _lib.ACT_FORMATS["mxfp4"])
+    assert (L.topk, L.num_experts, L.num_local_experts, L.hidden, L.intermediate) == (8, 384, 48, 3072, 1280)
+    assert L.x_row_bytes == 1536 and L.x_sf_row_bytes == 96 and L.mid_row_bytes == 640 and L.mid_sf_row_bytes == 40
+    buf, p = ctypes.c_void_p(256), ctypes.c_void_p(4096)     # (never dereferenced: refused first)
+
+    def fe(tokens, hidden, experts, topk, act):
+        st = lib.dgm_router_topk_launch(p, p, tokens, hidden, experts, topk, act, 0, 0, buf, ctypes.byref(L), None)
+        return st, lib.dgm_last_error()
+
+    st, msg = fe(8, 3072, 384, 16, 0)          # 8 x 16 = 128 routes fit, but slot 8.. would overrun
+    assert st == -1 and b"topk exceeds" in msg
+    st, msg = fe(32, 3072, 384, 4, 0)          # 32 x 4 = 128 routes, but 32 > 16 token rows
+    assert st == -1 and b"max_tokens" in msg
+    st, msg = fe(8, 4096, 384, 8, 0)
+    assert st == -1 and b"hidden differs" in msg
+    st, msg = fe(8, 3072, 512, 8, 0)
+    assert st == -1 and b"num_experts exceeds" in msg
+    st, msg = fe(8, 3072, 384, 8, _lib.ACT_FORMATS["mxfp8"])    # E4M3 rows are twice as wide
+    assert st == -1 and b"wider x" in msg
+    st = lib.dgm_router_logits_topk_launch(p, 8, 384, 16, 0, 0, buf, ctypes.byref(L), None)
+    assert st == -1 and b"topk exceeds" in lib.dgm_last_error()
+
+    def moe(**kw):
+        a = _lib.MoeArgs(num_tokens=8, hidden=3072, intermediate=1280, num_experts=384, expert_begin=0,
+                         num_local_experts=48, topk=8, act_format=0, activation_clamp=10.0, fast_math=1,
+                         w1_values=4096, w1_scales=4096, w2_values=4096, w2_scales=4096, y=4096, buffer=256,
+                         layout=ctypes.pointer(L))
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+    for fn in (lib.dgm_megamoe_fused_launch, lib.dgm_megamoe_split_launch, lib.dgm_megamoe_fused_launch_noalloc):
+        for kw, what in (({"topk": 16, "num_tokens": 8}, b"topk exceeds"),
+                         ({"topk": 4, "num_tokens": 32}, b"max_tokens"),
+                         ({"intermediate": 2048}, b"intermediate differs"),
+                         ({"num_local_experts": 96, "num_experts": 384}, b"num_local_experts exceeds"),
+                         ({"act_format": _lib.ACT_FORMATS["mxfp8"]}, b"wider x")):
+            st = fn(ctypes.byref(moe(**kw)), None)
+            assert st == -1 and what in lib.dgm_last_error(), (fn, kw, lib.dgm_last_error())
