@@ -1,7 +1,8 @@
-"""GPU parity at the timed workloads, at full size: benchmark config 2 (all 384 experts resident,
-W-MXFP4 x A-MXFP8 and x A-MXFP4, M=8 forced-balanced and M=16 seeded unbalanced routing),
-config 3 (QoQ W4A8, M=8 forced-balanced) and config 4 (NVFP4 W4A4, M=16 and M=64 seeded
-unbalanced), through the calls the bench makes: ``fable_router_quant_topk_frontend(...,
+"""GPU parity at every workload the bench times, at full size: benchmark config 2 (all 384
+experts resident, W-MXFP4 x A-MXFP8 and x A-MXFP4, M=2/4/8/16 forced-balanced and M=16 seeded
+unbalanced routing), config 3 (QoQ W4A8, M=2/4/8/16 forced-balanced) and config 4 (NVFP4 W4A4,
+M=16, 64 and 128 seeded unbalanced; 128 tokens are the persistent kernel's 1024-route limit),
+through the calls the bench makes: ``fable_router_quant_topk_frontend(...,
 select_in_mega=True)`` then the fused layer. These shapes run the persistent kernel's dynamic
 claim path (more L1 and L2 units than twice the grid) and its L1 -> L2 hand-off at the size the
 bench times.
@@ -201,3 +202,24 @@ def test_config3_qoq_m8_balanced(qoq_weights):
 def test_config4_nvfp4_unbalanced(nvfp4_weights, M):
     """Config 4: the NVFP4 W4A4 layer with 384 resident experts and seeded unbalanced routing."""
     run_headline("nvfp4", M, False, 900 + M, nvfp4_weights)
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
+def test_config2_m16_balanced(mxfp4_weights, fmt):
+    """Config 2 at M=16 forced-balanced (128 active experts, 2560 L1 and 1536 L2 units: the
+    sweep's best-fraction point), both activation formats. Forced-balanced routing at 16 tokens
+    is selected in the fused kernel's prologue."""
+    run_headline(fmt, 16, True, 516, mxfp4_weights)
+
+
+@pytest.mark.parametrize("M", [2, 4, 16])
+def test_config3_qoq_sweep_balanced(qoq_weights, M):
+    """Config 3's other timed points: QoQ W4A8 with 384 resident experts at M=2, 4 and 16
+    forced-balanced."""
+    run_headline("qoq", M, True, 600 + M, qoq_weights)
+
+
+def test_config4_nvfp4_m128_unbalanced(nvfp4_weights):
+    """Config 4 at M=128 (seeded unbalanced routing over 384 resident experts): 1024 routes, the
+    persistent kernel's limit, with the most active experts of any timed point."""
+    run_headline("nvfp4", 128, False, 1028, nvfp4_weights)

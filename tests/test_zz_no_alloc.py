@@ -2,8 +2,9 @@
 workspace in a file-scope device array instead of the caller's buffer) against the buffered entry
 point dgm_megamoe_fused_launch on the same inputs, both through the C ABI: y, top-k, top-k
 weights and recv stats bit for bit, on two calls in a row (the second with fewer tokens), for the
-in-prologue selection (<= 8 tokens) and the selection launch (> 8 tokens); and its size limit,
-which is refused on the host with a clear message."""
+in-prologue selection (<= 8 tokens) and the selection launch (> 8 tokens), at the array's route
+limit (512) for MXFP8 and NVFP4; and its size limit, which is refused on the host with a clear
+message."""
 import ctypes
 
 import numpy as np
@@ -14,12 +15,13 @@ from tests.gpu_common import need_gpu, bf16_cpu, randn_bf16
 
 pytestmark = pytest.mark.gpu
 
-E, E_LOCAL, H, I, TOPK = 384, 48, 3072, 1280, 8
+H, I, TOPK = 3072, 1280, 8
 
 
-def _weights(fmt):
+def _weights(fmt, E_LOCAL):
     import hopper_megamoe_basedondeepgemm_amd as dgm
     from hopper_megamoe_basedondeepgemm_amd import quantization_mxfp4_fused as qf
+    from hopper_megamoe_basedondeepgemm_amd import quantization_nvfp4 as qn
     from hopper_megamoe_basedondeepgemm_amd import quantization_qoq_fused as qq
     g = torch.Generator(device="cuda")
     g.manual_seed(1301)
@@ -27,6 +29,8 @@ def _weights(fmt):
     w2 = (torch.randn((E_LOCAL, H, I), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
     if fmt == "qoq":
         return dgm.transform_qoq_weights_for_mega_moe_fused(qq.quantize_to_qoq(w1), qq.quantize_to_qoq(w2))
+    if fmt == "nvfp4":
+        return dgm.transform_nvfp4_weights_for_mega_moe_fused(qn.quantize_to_nvfp4(w1), qn.quantize_to_nvfp4(w2))
     return dgm.transform_mxfp4_weights_for_mega_moe_fused(qf.quantize_to_mxfp4(w1), qf.quantize_to_mxfp4(w2))
 
 
@@ -35,23 +39,28 @@ def _launch(entry, args):
     return getattr(_lib.load(), entry)(ctypes.byref(args), _lib.stream())
 
 
-@pytest.mark.parametrize("fmt", ["mxfp8", "qoq"])
-def test_noalloc_matches_buffered_entry_point(fmt):
+@pytest.mark.parametrize("fmt,sizes,E,ep_size", [("mxfp8", (16, 5), 384, 8), ("qoq", (16, 5), 384, 8),
+                                                   # the array's limit: 64 tokens x top-8 = 512 local routes
+                                                   ("mxfp8", (64, 40), 48, 1), ("nvfp4", (64, 40), 48, 1)])
+def test_noalloc_matches_buffered_entry_point(fmt, sizes, E, ep_size):
     need_gpu()
     import hopper_megamoe_basedondeepgemm_amd as dgm
     from hopper_megamoe_basedondeepgemm_amd import _lib, mega
-    t1, t2 = _weights(fmt)
-    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, 16, TOPK, H, I, act_format=fmt, ep_size=8, ep_rank=1)
+    e_local = E // ep_size
+    t1, t2 = _weights(fmt, e_local)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, max(sizes), TOPK, H, I, act_format=fmt, ep_size=ep_size,
+                                                 ep_rank=1 % ep_size)
     rng = np.random.default_rng(1300)
     rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
-    for M in (16, 5):                      # two calls in a row, the second with fewer tokens
-        print(f"no-alloc vs buffered: fmt={fmt} M={M} E={E} E_local={E_LOCAL} (EP rank 1 of 8)", flush=True)
+    for M in sizes:                        # two calls in a row, the second with fewer tokens
+        print(f"no-alloc vs buffered: fmt={fmt} M={M} E={E} E_local={e_local} (EP rank {1 % ep_size} of {ep_size})",
+              flush=True)
         x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
         dgm.fable_router_quant_topk_frontend(x, rw, buf, select_in_mega=True)
         out = {}
         for entry in ("dgm_megamoe_fused_launch", "dgm_megamoe_fused_launch_noalloc"):
             y = torch.full((M, H), 3.0, dtype=torch.bfloat16, device="cuda")
-            stats = torch.zeros(E_LOCAL, dtype=torch.int32, device="cuda")
+            stats = torch.zeros(e_local, dtype=torch.int32, device="cuda")
             args = mega._moe_args(y, t1, t2, buf, stats, 10.0, fmt=fmt)
             _lib.check(_launch(entry, args))
             torch.cuda.synchronize()
