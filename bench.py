@@ -3,10 +3,12 @@
 Headline workload = benchmark config 2: the full E384 / H3072 / I1280 / top-8 layer resident on
 one GPU (W-MXFP4 x A-MXFP8), forced-balanced routing, M=8 tokens per step (one step = one
 layer forward from bf16 hidden states: the frontend launch (router + activation cast), then the
-fused kernel: top-8 in its prologue, dispatch, L1, L2, combine). Also sweeps M = 2, 4, 8, 16 for both activation formats (A-MXFP8 and A-MXFP4) and
-the QoQ W4A8 layer (int8 activations, QoQ 4-bit weights), the NVFP4 W4A4 layer at M = 16, 64,
-128 with seeded unbalanced routing (config 4), and one seeded unbalanced-routing A-MXFP8 run at
-M=16. Before every timed step >= 1 GiB is written and
+fused kernel: top-8 in its prologue, dispatch, L1, L2, combine). Also sweeps M = 2, 4, 8, 16 for
+three activation formats (A-MXFP8, A-MXFP4, and the reference fused buffer's E4M3 with fp32
+scales per 128) and the QoQ W4A8 layer (int8 activations, QoQ 4-bit weights), config 0 (48
+experts, M=2, softmax routing) and config 1 (one EP rank's 48 experts of the 384-way router,
+M=8), the NVFP4 W4A4 layer at M = 16, 64, 128 with seeded unbalanced routing (config 4), and
+one seeded unbalanced-routing A-MXFP8 run at M=16. Before every timed step >= 1 GiB is written and
 then 1 GiB of other data is read, so neither the 256 MB MALL nor the L2s hold weights (and
 no dirty lines are left to drain inside the timed region); per step, HIP events on the
 layer's stream bracket the layer (and, for two launches, the frontend and the fused kernel).
@@ -115,6 +117,51 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
         sys.stdout.flush()
 
 
+def probes_report(torch, reps=15):
+    """The platform figures the fused kernel is measured against (the probe library,
+    include/dgm_probe.h), each launch after a 1 GiB write + 1 GiB read eviction, HIP events on the
+    launch stream, median of `reps`:
+      * HBM read probe: the fused kernel's streaming pattern (runs of 24 consecutive 1 KB tiles per
+        wave, a ring of non-temporal loads, 256 workgroups of 8 waves) without its arithmetic, at
+        the weight bytes of config 1 (50 MB) and of the headline (401 MB), ring depths 4 / 12 / 24;
+      * the launch floor: an empty kernel of 256 x 512 and 1 x 64 threads."""
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    lib = _lib.load_probe()
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    flush_rd = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+    src = torch.ones(64 * MXFP4_EXPERT_BYTES // 4 + 4096, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        ts = []
+        for _ in range(reps):
+            flush.fill_(1)
+            flush_rd.sum()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        return float(np.median(ts)), float(np.min(ts))
+
+    print("HBM read probe (256 workgroups x 8 waves, runs of 24 x 1 KB tiles, non-temporal loads), "
+          "median / min of %d after a 1 GiB eviction:" % reps)
+    for experts in (8, 64):
+        nbytes = experts * MXFP4_EXPERT_BYTES // (24 * 1024) * (24 * 1024)
+        for depth in (4, 12, 24):
+            med, mn = timed(lambda: _lib.check(lib.dgm_probe_stream_read(_lib.ptr(src), nbytes, depth, 256,
+                                                                          _lib.ptr(sink), _lib.stream())))
+            print(f"  {nbytes / 1e6:7.1f} MB  ring {depth:2d}: {med:7.2f} us ({mn:7.2f} min) = "
+                  f"{nbytes / (med * 1e-6) / 1e12:5.2f} TB/s")
+    print("empty kernel (returns at entry), median / min of %d after a 1 GiB eviction:" % reps)
+    for blocks, threads in ((256, 512), (1, 64)):
+        med, mn = timed(lambda: _lib.check(lib.dgm_probe_empty_launch(blocks, threads, _lib.stream())))
+        print(f"  {blocks:4d} x {threads:3d} threads: {med:6.2f} us ({mn:6.2f} min) by events")
+    sys.stdout.flush()
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -191,7 +238,8 @@ def build_nvfp4_weights(torch, seed, n_experts, chunk=32):
     return t
 
 
-def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True, ep_size=1):
+def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force_balanced=True, ep_size=1,
+               n_experts=E):
     """Times `steps` layer forwards, each between two HIP events on the layer's stream (the
     layer time), then `steps` more with a third event between the frontend and the fused MoE
     kernel for the split between them (an event between two launches delays the second one,
@@ -200,7 +248,8 @@ def time_layer(torch, dgm, M, weights, router_w, act, steps, warmup, seed, force
     fused = {"qoq": dgm.qoq_mega_moe_fused, "nvfp4": dgm.fp4_fp4_mega_moe}.get(act, dgm.mxfp4_mega_moe_fused)
     expert_bytes = {"qoq": QOQ_EXPERT_BYTES, "nvfp4": NVFP4_EXPERT_BYTES}.get(act, MXFP4_EXPERT_BYTES)
     # (ep_size > 1: one EP rank's share, experts 0 .. E / ep_size - 1, on this GPU)
-    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act, ep_size=ep_size, ep_rank=0)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, n_experts, M, TOPK, H, I, act_format=act, ep_size=ep_size,
+                                                 ep_rank=0)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
     x = torch.randn((M, H), generator=g, device="cuda").to(torch.bfloat16)
@@ -340,12 +389,7 @@ def cpu_baseline_and_parity(packed, headline, router_w, M, act, reps=400):
         moe.quant_act(x, act)
         moe.moe_forward(x_dq, idx, w, W1, W2, 0, act)
         times.append(time.perf_counter() - t0)
-    threads = 1
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        pass
+    threads = _blas_threads()
     model, phys = host_cpu()
     cpu = dict(value=round(float(np.median(times)) * 1e6, 1), unit="us/layer", cores=threads, kind="port",
                cpu_model=model, physical_cores=phys,
@@ -353,6 +397,57 @@ def cpu_baseline_and_parity(packed, headline, router_w, M, act, reps=400):
                       f"cast, then all {TOPK * M} expert routes with the {len(experts)} active experts' weights "
                       f"dequantised beforehand), median of {reps}; A-{act.upper()}; cores = BLAS threads")
     return cpu, parity
+
+
+def _blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        return 1
+
+
+def cpu_config_baselines(packed, c0, c1, router_w, reps=60):
+    """The oracle timed on the host at BASELINE's configs 0 and 1, on the inputs of the GPU runs of
+    the same configs (their bf16 hidden states; the same packed weights, experts 0-47):
+      c0: E=48 (router weight = rows 0-47 of the 384-way one), M=2, softmax top-8, A-MXFP4;
+      c1: one EP rank's share of the 384-way layer, M=8 forced-balanced, A-MXFP4 (the 384-way
+          router for this rank's tokens, then its 8 local routes).
+    Per forward: router GEMV + top-8 + activation cast + the local routes (the routed experts'
+    weights dequantised beforehand); median of `reps`. Returns {name: dict}."""
+    from oracle import moe
+    out = {}
+    rw = router_w.float().cpu().numpy()
+    for name, r, rwn, balanced in (("c0_E48_M2_mxfp4", c0, rw[:48], False), ("c1_ep_share_M8_mxfp4", c1, rw, True)):
+        if r is None:
+            continue
+        x = r["x"].float().cpu().numpy()
+        M = x.shape[0]
+        logits = moe.router_logits_f32(x, rwn)
+        idx, w, _ = moe.topk_softmax(logits, TOPK)
+        if balanced:
+            idx, w = moe.balanced_routing(M, rwn.shape[0], TOPK)
+        experts = sorted({int(v) for v in idx.ravel() if 0 <= v < 48})
+        pre = _dequant_active(packed, experts)
+        W1, W2 = _Sel(pre, 0, (48, 2 * I, H)), _Sel(pre, 1, (48, H, I))
+        codes, sfb, x_dq = moe.quant_act(x, "mxfp4")
+        ref, _ = moe.moe_forward(x_dq, idx, w, W1, W2, 0, "mxfp4")
+        m = moe.metrics(r["y"].float().cpu().numpy(), ref)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            lg = moe.router_logits_f32(x, rwn)
+            moe.topk_softmax(lg, TOPK)
+            moe.quant_act(x, "mxfp4")
+            moe.moe_forward(x_dq, idx, w, W1, W2, 0, "mxfp4")
+            times.append(time.perf_counter() - t0)
+        n_routes = int(((idx >= 0) & (idx < 48)).sum())
+        out[name] = dict(value=round(float(np.median(times)) * 1e6, 1), unit="us/layer", cores=_blas_threads(),
+                         kind="port", gpu_us=round(r["us_median"], 2),
+                         gpu_parity=dict(cos_min=round(m["cos_min"], 7), rel_rmse=round(m["rel_rmse"], 6)),
+                         sample=f"oracle (numpy fp32): {M} tokens, {n_routes} local routes on {len(experts)} experts, "
+                                f"median of {reps}")
+    return out
 
 
 class _Sel:
@@ -372,7 +467,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--m", type=int, default=8, help="M of the headline line")
     ap.add_argument("--act", default="mxfp8", choices=["mxfp8", "mxfp4"], help="activation format of the headline line")
-    ap.add_argument("--sweep", default="2,4,8,16", help="M values of the sweep (both activation formats)")
+    ap.add_argument("--sweep", default="2,4,8,16",
+                    help="M values of the sweep (A-MXFP8, A-MXFP4 and the fused buffer's A-FP8 with fp32 scales per 128)")
     ap.add_argument("--sweep-steps", type=int, default=10)
     ap.add_argument("--no-qoq", action="store_true", help="skip the QoQ W4A8 sweep")
     ap.add_argument("--nvfp4-sweep", default="16,64,128",
@@ -382,6 +478,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phase-stamps", action="store_true",
                     help="print the fused kernel's per-workgroup phase stamps (M=2/8/16, config 1) and exit")
+    ap.add_argument("--probes", action="store_true",
+                    help="print the platform probes (HBM read bandwidth of the streaming pattern, empty-kernel "
+                         "launch floor) and exit")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB (HBM counter scaling)")
     args = ap.parse_args()
@@ -392,6 +491,9 @@ def main():
     import torch
     import hopper_megamoe_basedondeepgemm_amd as dgm
     torch.cuda.set_device(0)
+    if args.probes:
+        probes_report(torch)
+        return
     log("building E384 weights ...")
     weights, packed = build_weights(torch, 1234, E)
     g = torch.Generator(device="cuda")
@@ -411,18 +513,25 @@ def main():
     main_r = time_layer(torch, dgm, args.m, weights, router_w, args.act, args.steps, args.warmup, 500 + args.m)
     log(f"headline M={args.m} {args.act}: {entry(main_r)}")
     sweep = {}
-    for act in ("mxfp8", "mxfp4"):
+    for act in ("mxfp8", "mxfp4", "fp8f128"):
         sweep[act] = {}
         for M in [int(v) for v in args.sweep.split(",") if v]:
             r = time_layer(torch, dgm, M, weights, router_w, act, args.sweep_steps, args.warmup, 500 + M)
             sweep[act][M] = entry(r)
             log(f"M={M} {act}: {sweep[act][M]}")
+    c0_r = c1_r = None
     if not args.no_c1:
+        share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
+        # benchmark config 0 on the GPU: 48 experts (all local), a 48-way router (rows 0-47 of the
+        # 384-way one), M=2, softmax top-8 routing, W-MXFP4 x A-MXFP4
+        c0_r = time_layer(torch, dgm, 2, share, router_w[:E // 8].contiguous(), "mxfp4", args.sweep_steps,
+                          args.warmup, 202, force_balanced=False, n_experts=E // 8)
+        sweep["c0_E48_M2_mxfp4"] = entry(c0_r)
+        log(f"config 0 (E48, M=2, mxfp4, softmax routing): {sweep['c0_E48_M2_mxfp4']}")
         # benchmark config 1: one EP rank's share (local experts 0-47 of the 384-way router),
         # W-MXFP4 x A-MXFP4, M=8 forced-balanced: 8 rows on 8 local experts
-        share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
-        r = time_layer(torch, dgm, 8, share, router_w, "mxfp4", args.sweep_steps, args.warmup, 508, ep_size=8)
-        sweep["c1_ep_share_M8_mxfp4"] = entry(r)
+        c1_r = time_layer(torch, dgm, 8, share, router_w, "mxfp4", args.sweep_steps, args.warmup, 508, ep_size=8)
+        sweep["c1_ep_share_M8_mxfp4"] = entry(c1_r)
         log(f"config 1 (E48 share, M=8, mxfp4): {sweep['c1_ep_share_M8_mxfp4']}")
         del share
     if not args.no_qoq and [v for v in args.sweep.split(",") if v]:
@@ -458,6 +567,7 @@ def main():
             t0 = time.perf_counter()
             cpu, parity = cpu_baseline_and_parity(packed, main_r, router_w, args.m, args.act)
             cpu["sample"] += f"; {time.perf_counter() - t0:.1f} s of host time incl. the dequantisation"
+            cpu["configs"] = cpu_config_baselines(packed, c0_r, c1_r, router_w)
             log(f"cpu baseline: {cpu}")
             log(f"headline parity: {parity}")
         except Exception as ex:  # reported, never fatal

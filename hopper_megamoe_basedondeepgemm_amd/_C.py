@@ -13,7 +13,8 @@ rank 0.
 
 ``mxfp4_mega_moe_fused`` runs the layer on E4M3 activations with fp32 scales per 128 (the
 input format tests/test_four_api_correctness.py:215 writes into this buffer), MXFP4 weights from
-``transform_mxfp4_weights_for_mega_moe_fused``; ``qoq_mega_moe_fused`` the QoQ W4A8 layer.
+``transform_mxfp4_weights_for_mega_moe_fused``, as one launch of the persistent kernel;
+``qoq_mega_moe_fused`` the QoQ W4A8 layer.
 """
 import weakref
 
@@ -86,12 +87,10 @@ def _run_fused(act, y, l1, l2, stats, s1, s2, buffer, ptrs, rank, max_tokens, nu
     assert len(ptrs) == b.ep_size, (len(ptrs), b.ep_size)
     w1 = (l1[0], l1[1], s1)
     w2 = (l2[0], l2[1], s2)
-    if act == "fp8f128":      # (the persistent kernel takes per-32 scales; this format runs split)
-        mega._fused(y, w1, w2, b, stats, clamp, split=True, fast_math=fast_math, fmt="fp8f128",
-                    fe_keys=fe_keys, act=act)
-    else:
-        mega._fused(y, w1, w2, b, stats, clamp, phase_stamps=phase_stamps, fast_math=fast_math, fmt=act,
-                    fe_keys=fe_keys, act=act)
+    # one launch of the persistent kernel (beyond its limits, 1024 routes, 256 tokens, 512 local
+    # experts, the E4M3 layer runs as the split path's kernels, with the same results)
+    mega._fused(y, w1, w2, b, stats, clamp, phase_stamps=phase_stamps, fast_math=fast_math, fmt=act,
+                fe_keys=fe_keys, act=act)
 
 
 def mxfp4_mega_moe_fused(y, l1, l2, stats, s1, s2, buffer, ptrs, rank, max_tokens, num_experts, topk, clamp,

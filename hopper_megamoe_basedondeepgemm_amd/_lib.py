@@ -129,7 +129,7 @@ def load():
 
 
 PROBE_EXPORTS = ["dgm_probe_mfma_scale", "dgm_probe_mfma_scale_sel", "dgm_probe_mfma_i8", "dgm_probe_mfma_f16",
-                 "dgm_probe_cvt_fp4", "dgm_probe_global_load_lds"]
+                 "dgm_probe_cvt_fp4", "dgm_probe_global_load_lds", "dgm_probe_stream_read", "dgm_probe_empty_launch"]
 _probe = None
 
 
@@ -149,6 +149,8 @@ def load_probe():
         "dgm_probe_mfma_f16": ([vp, vp, vp, vp], i32),
         "dgm_probe_cvt_fp4": ([vp, vp, vp, vp, i32, vp], i32),
         "dgm_probe_global_load_lds": ([vp, vp, vp], i32),
+        "dgm_probe_stream_read": ([vp, ctypes.c_int64, i32, i32, vp, vp], i32),
+        "dgm_probe_empty_launch": ([i32, i32, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

@@ -244,8 +244,10 @@ DGM_DEV v4f mfma_scale_16x16x128_sel(v8i a, v8i b, v4f c, int sa, int sb) {
 }
 
 // Keeps the scale registers of a chain of block-scaled matrix-core ops allocated until the chain's
-// result `acc` exists (each use depends on it), so that no instruction inside the chain reuses a
-// register an op that reads it as its scale may still be reading.
+// last op has issued (the result `acc` is an input here), so that no instruction inside the chain
+// writes a register a later op of the chain reads as its scale. With the scale operands taken
+// from loaded dwords (never computed by VALU ops between the ops), the chain's scales are written
+// only by memory loads.
 template <int N>
 DGM_DEV void keep_scales_until(const uint32_t (&r)[N], v4f acc) {
 #pragma unroll

@@ -36,7 +36,9 @@
 //   L2 item -> bf16 route outputs; one item later comb[t][b] += 1 per route and 128-row block
 //   combine -> per (token, block): wait comb == the token's local routes, sum the routes in
 //   slot order (fp32) -> bf16 y
-// The last workgroup to finish clears all counters, so the next launch starts from zero.
+// Counters come in two sets picked by a parity word: a launch uses one set and clears the other
+// (after its dispatch) for the next launch; the workgroup that counts itself last at entry flips
+// the parity at its end. No workgroup clears or waits on counters at the end of a launch.
 #include "dgm_common.hpp"
 #include "dgm_abi_internal.hpp"
 #include "dgm_fused.hpp"
@@ -201,6 +203,8 @@ struct FusedSmem {
   alignas(16) float4 qc[QX][ACT == DGM_ACT_QOQ ? KT2 : 1];
   // NVFP4: per local expert the L1 / L2 output scales (1 when not given)
   float gsl[2][ACT == DGM_ACT_NVFP4 ? FUSED_MAX_LOCAL : 1];
+  // FP8F128 input rows (L1): the token's fp32 activation scale of each K-tile [K-tile][column]
+  float xf[ACT == DGM_ACT_FP8F128 ? KT1 : 1][16];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
@@ -602,6 +606,20 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT, MIDL>& r) {
       }
     }
     if (!MIDL && tid < 16) s.xsc[tid] = (r.ok >> 8) & 1u ? r.fsc : 0.f;
+  } else if constexpr (ACT == DGM_ACT_FP8F128) {
+    // input rows with one fp32 scale per K-tile (the dword slab_load read for K-tile 4 g + j is
+    // that scale: the same row pitch as four E8M0 bytes): per (K-tile, column) to s.xf; the
+    // block-scaled op gets unit activation scales
+    if (tid < KG * 64) {
+      s.bsc[tid >> 6][tid & 63] = 0x7f7f7f7fu;
+      if ((tid & 63) < 16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int kt = 4 * (tid >> 6) + j;
+          if (kt < KT) s.xf[kt][tid & 63] = (r.ok >> (8 + j)) & 1u ? __uint_as_float(r.sb[j]) : 0.f;
+        }
+      }
+    }
   } else if (tid < KG * 64) {
     uint32_t w = 0;
 #pragma unroll
@@ -631,6 +649,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   constexpr int KG1 = (KT1 + 3) / 4, KG2 = (KT2 + 3) / 4;
   constexpr int H = KT1 * 128, I = KT2 * 128;
   constexpr bool FP4A = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_NVFP4;   // E2M1 activations
+  // FP8F128: E4M3 input rows with an fp32 scale per K-tile (each K-tile's product promoted by
+  // it); the intermediate is MXFP8's (E4M3, E8M0 per 32), so the L2 phase runs as MXFP8's
+  constexpr bool F128 = ACT == DGM_ACT_FP8F128;
+  constexpr int ACT2 = F128 ? DGM_ACT_MXFP8 : ACT;
   constexpr int XB = FP4A ? H / 2 : H;     // activation row bytes
   constexpr int MB = FP4A ? I / 2 : I;     // intermediate row bytes
   constexpr int QN1 = I / 64, NB1 = I / 8, NB2 = H / 16, NBL2 = H / (16 * NW);
@@ -680,6 +702,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     } else if constexpr (ACT == DGM_ACT_NVFP4) {
       for (int64_t i = (int64_t)cw * 64 + lane; i < (int64_t)p.M * (H / 16) * 4; i += (int64_t)NW * G * 64)
         cast_lane_nvfp4<true>(p.hidden, i, xq, xsf);
+    } else if constexpr (F128) {
+      for (int64_t i = (int64_t)cw * 64 + lane; i < (int64_t)p.M * (H / 128) * 32; i += (int64_t)NW * G * 64)
+        cast_lane_fp8f128<true>(p.hidden, i, xq, xsf);
     } else {
       for (int64_t i = (int64_t)cw * 64 + lane; i < (int64_t)p.M * (H / 32) * 8; i += (int64_t)NW * G * 64)
         cast_lane_mx<true>(p.hidden, ACT, i, xq, xsf);
@@ -860,7 +885,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // and at most 1.5: the last round, half full or less, then takes half a unit's time (an extra
   // item costs about as much as that saves beyond two rounds). U2 counts the L2 items.
   constexpr int RB2 = NBL2 % 2 == 0 ? 2 : 1, UPE2 = NBL2 / RB2;
-  constexpr bool WIDE = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8;
+  constexpr bool WIDE = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8 || F128;
   const int u2w = n_active * UPE2, G2 = (int)gridDim.x;
   const bool halves = RB2 == 2 && (2 * u2w <= G2 || (WIDE && u2w > G2 && 2 * (u2w - G2) <= G2)) && !(p.debug & 4);
   const int U1 = n_active * QN1, U2 = n_active * (halves ? NBL2 : UPE2);
@@ -1111,6 +1136,41 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             sr[t % KR] = ld_stream32_after(t + KR - KT1 < KT2 ? nsb : nsbd, (t + KR - KT1) * 128, acc);
           }
         });
+      } else if constexpr (F128) {
+        // one chain, as the split path's L1 kernel: per K-tile the block-scaled op with a unit
+        // activation scale into a zero accumulator, then acc += s * part with the token's fp32
+        // scale s of that K-tile, one tile later (off the op's latency). A compiler ordering
+        // point keeps each op after the promote two tiles back (independent ops would otherwise
+        // all be issued first, every result kept live).
+        uint32_t bs = bs0;
+        float xf_c = s.xf[0][c], xf_p = 0.f;
+        v4f prev = {0.f, 0.f, 0.f, 0.f};
+        static_for<KT1>([&](auto tc) {
+          constexpr int t = decltype(tc)::value;
+          v8i bop = bq0;
+          const uint32_t bsw = bs;
+          bq0 = bq1;
+          if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
+          if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
+          if constexpr (t >= 2) after_values(bop, acc);      // (tile t - 2 promoted)
+          const v4f part = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, v4f{0.f, 0.f, 0.f, 0.f},
+                                                                         (int)sd[t >> 2], (int)bsw);
+          if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, part);
+          else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, part);
+          if constexpr (t > 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = fmaf(xf_p, prev[i], acc[i]);     // tile t - 1
+          }
+          xf_p = xf_c;
+          if constexpr (t + 1 < KT1) xf_c = s.xf[t + 1][c];
+          prev = part;
+          if constexpr (t == KT1 - KR) {
+            if (has_next && nq != q0) load_scales(nq, sn);
+            if (restage) load_slab(pre, na, ns0);
+          }
+        });
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(xf_p, prev[i], acc[i]);
       } else {
         // two chains, K-tiles 0 .. KT1 / 2 - 1 and KT1 / 2 .., summed after the loop: the split
         // path's L1 kernel sums the same two, so the two paths agree bit for bit for any data
@@ -1172,10 +1232,12 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         float am = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // MXFP: gate / up rounded to bf16 (the reference's L1 output); QoQ: fp32
-          const float g = fminf(ACT == DGM_ACT_QOQ ? acc[i] : round_bf16(acc[i]), p.clamp);
+          // MXFP: gate / up rounded to bf16 (the reference's L1 output); QoQ, FP8F128: fp32
+          // (tests/test_four_api_correctness.py:437-442)
+          constexpr bool F32GU = ACT == DGM_ACT_QOQ || F128;
+          const float g = fminf(F32GU ? acc[i] : round_bf16(acc[i]), p.clamp);
           const float uv = s.upv[pp][lane][i];
-          const float uu = fminf(fmaxf(ACT == DGM_ACT_QOQ ? uv : round_bf16(uv), -p.clamp), p.clamp);
+          const float uu = fminf(fmaxf(F32GU ? uv : round_bf16(uv), -p.clamp), p.clamp);
           const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
           act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
           am = fmaxf(am, fabsf(act[i]));
@@ -1191,8 +1253,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         bs0 = s.bsc[0][lane];
       }
       if (gu == 0) {
-        // requant group: QoQ 64 features (the unit), NVFP4 16 (this pair), MXFP 32 (two pairs)
-        const float am = ACT == DGM_ACT_QOQ     ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
+        // requant group: QoQ, FP8F128 64 features (the unit), NVFP4 16 (this pair), MXFP 32 (two
+        // pairs)
+        const float am = ACT == DGM_ACT_QOQ || F128 ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
                          : ACT == DGM_ACT_NVFP4 ? s.amax[pp][c]
                                                 : fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
         const int row = r0 + s0 + c;
@@ -1243,7 +1306,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
             if ((pp & 1) == 0) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
           }
         } else {
-          const int code = (int)ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f) + 127;
+          // E4M3 with a power-of-two scale per 32 (MXFP8: 2^ceil(log2(max(amax, 1e-30) / 448)))
+          // or per 64 (FP8F128: 2^ceil(log2(max(amax / 448, FLT_MIN))), tests/test_four_api_
+          // correctness.py:54-62, stored as two equal E8M0 bytes per 32)
+          const int code = (int)(F128 ? ceil_log2_f32(fmaxf(am / 448.0f, 1.17549435e-38f))
+                                      : ceil_log2_f32(fmaxf(am, 1e-30f) / 448.0f)) + 127;
           const float isc = e8m0_inv((uint32_t)code);
           uint32_t w = 0;
 #pragma unroll
@@ -1333,9 +1400,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     };
     const uint8_t* midv = p.mid;
     const uint8_t* mids = p.mid_sf;
-    auto load_slab = [midv, mids](SlabRegs<KT2, ACT, true>& r, int a, int s0) __attribute__((always_inline)) {
+    auto load_slab = [midv, mids](SlabRegs<KT2, ACT2, true>& r, int a, int s0) __attribute__((always_inline)) {
       const int rb = s.aoff[a] + s0;
-      slab_load<KT2, ACT, true, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
+      slab_load<KT2, ACT2, true, true>(r, midv, mids, MB, s.aoff[a + 1] - rb, [rb](int cc) { return rb + cc; },
                                 [](int) { return 0.f; });
     };
     // arrivals of item (unit v, slab s0): its routes' outputs for the unit's blocks are complete
@@ -1363,7 +1430,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int s0 = 0;
     static_assert(KT2 <= RING, "the L2 ring in the shared tile registers");
     uint32_t sd[SW2], sn[SW2];
-    SlabRegs<KT2, ACT, true> pre;
+    SlabRegs<KT2, ACT2, true> pre;
     int ready = -1;           // (thread 0) an active expert whose L1 arrival is known complete
     bool seen = false;        // (stamps) first L1 arrival observed
     int pv = -1, ps0 = 0;     // the previous item, whose arrivals are not sent yet
@@ -1433,7 +1500,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           slab_store(s, pre);
         } else {
           const int rb = r0 + s0;
-          stage_slab<KT2, ACT, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
+          stage_slab<KT2, ACT2, true>(s, p.mid, p.mid_sf, MB, n - s0, [rb](int cc) { return rb + cc; });
         }
         staged = key;
         __syncthreads();
@@ -1720,7 +1787,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 // last launch's (the grid is what the device keeps resident at once, so it depends on the
 // device's CU count)
 constexpr int GRID_DEVICES = 64;
-struct GridCache { int blocks[3][4][2] = {}; int last[3][4] = {}; };
+struct GridCache { int blocks[3][5][2] = {}; int last[3][5] = {}; };
 GridCache g_grid[GRID_DEVICES];
 
 GridCache& grid_cache() {
@@ -1757,6 +1824,7 @@ int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream) {
 
 int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format) {
   int slot = hidden == 3072 ? 0 : (hidden == 512 ? 1 : 2);
+  if (act_format < DGM_ACT_MXFP4 || act_format > DGM_ACT_FP8F128) return 0;
   return grid_cache().last[slot][act_format];
 }
 
@@ -1767,7 +1835,8 @@ int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, 
     return act == DGM_ACT_MXFP4   ? launch_fused_fe<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream) \
            : act == DGM_ACT_MXFP8 ? launch_fused_fe<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream) \
            : act == DGM_ACT_QOQ   ? launch_fused_fe<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream)   \
-                                  : launch_fused_fe<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream); \
+           : act == DGM_ACT_NVFP4 ? launch_fused_fe<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream) \
+                                  : launch_fused_fe<KA, KB, DGM_ACT_FP8F128>(prm, SLOT, stream); \
   }
   DGM_FUSED_SHAPE(3072, 1280, 0)
   DGM_FUSED_SHAPE(512, 256, 1)

@@ -834,7 +834,6 @@ constexpr int SELECT_IN_MEGA_FAST_TOKENS = 8;     // (one token per wave)
 constexpr int SELECT_IN_MEGA_FAST_BALANCED = 16;
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* A, hipStream_t stream) {
-  if (A && A->act_format == DGM_ACT_FP8F128) return dgm_megamoe_split_launch(A, stream);
   const int chk = dgm_check_fused_args(A);
   if (chk) return chk;
   if (A->num_tokens == 0) return 0;
@@ -860,8 +859,7 @@ int dgm_check_fused_args(const DgmMoeArgs* A) {
   }
   DGM_CHECK_ARG(A->num_local_experts > 0 && A->num_local_experts <= MAX_LOCAL_EXPERTS, "num_local_experts");
   DGM_CHECK_ARG(A->expert_begin >= 0 && A->expert_begin + A->num_local_experts <= A->num_experts, "expert range");
-  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_NVFP4,
-                "act_format (FP8F128 runs on dgm_megamoe_split_launch)");
+  DGM_CHECK_ARG(A->act_format >= DGM_ACT_MXFP4 && A->act_format <= DGM_ACT_FP8F128, "act_format");
   DGM_CHECK_ARG(A->act_format != DGM_ACT_QOQ || (A->w1_row_scales && A->w2_row_scales),
                 "QoQ needs the row scales s1 of both matrices");
   DGM_CHECK_ARG(A->topk > 0 && A->topk <= 16, "topk");

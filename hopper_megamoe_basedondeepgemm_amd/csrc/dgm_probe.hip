@@ -136,3 +136,71 @@ extern "C" int dgm_probe_global_load_lds(const void* src, void* out, hipStream_t
   hipLaunchKernelGGL(k_probe_lds, dim3(1), dim3(256), 0, stream, (const uint8_t*)src, (uint4*)out);
   return probe_status();
 }
+
+// ------------------------------------------------------------------ platform probes
+// HBM read probe: the fused kernel's streaming pattern without its arithmetic. Each wave reads
+// runs of RUN = 24 consecutive 1 KB tiles (one 16-row weight block over K = 3072 in the MXFP4
+// layout) through a ring of DEPTH non-temporal 16-byte-per-lane loads: after consuming a tile
+// it issues the tile DEPTH positions later. Runs are dealt to the waves of the grid in turn
+// (run r to wave r % waves); the XOR of everything read goes to sink[0] only if it equals a
+// value the data never gives, so no load is dropped.
+constexpr int PROBE_RUN = 24;
+typedef unsigned probe_v4u __attribute__((ext_vector_type(4)));
+
+template <int DEPTH>
+__global__ void __launch_bounds__(512) k_probe_stream(const uint8_t* __restrict__ src, int64_t runs,
+                                                      unsigned* __restrict__ sink) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+  const int64_t r0 = (int64_t)blockIdx.x * (blockDim.x >> 6) + wv;
+  const int64_t my_runs = r0 < runs ? (runs - r0 + nwaves - 1) / nwaves : 0;
+  const int64_t nj = my_runs * PROBE_RUN;          // tiles this wave reads
+  auto tile_off = [&](int64_t j) {
+    return ((r0 + (j / PROBE_RUN) * nwaves) * PROBE_RUN + j % PROBE_RUN) * 1024 + lane * 16;
+  };
+  unsigned acc = 0;
+  probe_v4u v[DEPTH];
+#pragma unroll
+  for (int k = 0; k < DEPTH; ++k)
+    v[k] = k < nj ? __builtin_nontemporal_load(reinterpret_cast<const probe_v4u*>(src + tile_off(k))) : probe_v4u{0, 0, 0, 0};
+  for (int64_t j0 = 0; j0 < nj; j0 += DEPTH) {
+#pragma unroll
+    for (int k = 0; k < DEPTH; ++k) {
+      const int64_t j = j0 + k;
+      if (j < nj) {
+        acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+        if (j + DEPTH < nj) {
+          int64_t off = tile_off(j + DEPTH);
+          asm volatile("" : "+v"(off) : "v"(acc));       // (issued after the consume)
+          v[k] = __builtin_nontemporal_load(reinterpret_cast<const probe_v4u*>(src + off));
+        }
+      }
+    }
+  }
+  if (acc == 0xdeadbeefu) sink[0] = acc;
+}
+
+extern "C" int dgm_probe_stream_read(const void* src, int64_t bytes, int depth, int blocks, void* sink,
+                                     hipStream_t stream) {
+  PROBE_CHECK(src && sink && bytes >= 0 && blocks > 0 && blocks <= 65536);
+  PROBE_CHECK(((uintptr_t)src & 15) == 0);
+  const int64_t runs = bytes / (PROBE_RUN * 1024);
+  const uint8_t* s = (const uint8_t*)src;
+  unsigned* o = (unsigned*)sink;
+  switch (depth) {
+    case 4: hipLaunchKernelGGL((k_probe_stream<4>), dim3(blocks), dim3(512), 0, stream, s, runs, o); break;
+    case 12: hipLaunchKernelGGL((k_probe_stream<12>), dim3(blocks), dim3(512), 0, stream, s, runs, o); break;
+    case 24: hipLaunchKernelGGL((k_probe_stream<24>), dim3(blocks), dim3(512), 0, stream, s, runs, o); break;
+    default: return -1;
+  }
+  return probe_status();
+}
+
+// The launch floor: a kernel that returns at entry.
+__global__ void k_probe_empty() {}
+
+extern "C" int dgm_probe_empty_launch(int blocks, int threads, hipStream_t stream) {
+  PROBE_CHECK(blocks > 0 && blocks <= 65536 && threads > 0 && threads <= 1024);
+  hipLaunchKernelGGL(k_probe_empty, dim3(blocks), dim3(threads), 0, stream);
+  return probe_status();
+}

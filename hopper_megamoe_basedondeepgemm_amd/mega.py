@@ -553,7 +553,10 @@ def mxfp4_mega_moe_fused(y, l1, l2, b, cumulative_local_expert_recv_stats=None, 
                          fast_math=True, phase_stamps=None, fe_keys=None):
     """deep_gemm/mega/fused.py:97: the layer over the routing and activations already in the
     buffer (written by ``fable_router_quant_topk_frontend`` or by the caller): dispatch,
-    L1 + SwiGLU + requant, L2, top-k combine into ``y`` (bf16 [tokens, H]).
+    L1 + SwiGLU + requant, L2, top-k combine into ``y`` (bf16 [tokens, H]), as one launch of the
+    persistent kernel. On an "fp8f128" buffer (the reference's fused buffer: E4M3 activations with
+    fp32 scales per 128) it runs that recipe: each K-tile's product promoted by its scale, fp32
+    gate / up, a power-of-two E4M3 intermediate per 64 features.
     ``phase_stamps`` (optional int64 CUDA tensor [rows, 8]; workgroups >= rows skip): per-workgroup
     100 MHz wall-clock stamps (see ``fused_workgroups``). ``fast_math`` (default True, as in the
     reference): hardware exp2 / reciprocal in SiLU's sigmoid; False = IEEE expf and division.

@@ -31,7 +31,8 @@ extern "C" {
                              (per_token_cast_to_fp8(use_ue8m0=False, gran_k=128), deep_gemm/utils/math.py:26-38),
                              MXFP4 weights, FP8 intermediate with a power-of-two scale per 64: the
                              "fp8xmxfp4" split recipe (deep_gemm/mega/__init__.py:70-127, 340-446;
-                             tests/test_four_api_correctness.py:54-62, 215). Split path only. */
+                             tests/test_four_api_correctness.py:54-62, 215) and the fused buffer's
+                             recipe (csrc/apis/mega_fused.hpp:78-102). Both launch paths. */
 
 /* frontend flags */
 #define DGM_FE_FORCE_BALANCED 1     /* DG_FE_FORCE_BALANCED: tests/test_four_api_correctness.py:125-144 */

@@ -32,6 +32,16 @@ int dgm_probe_cvt_fp4(const void* src, const void* scale, void* out_h, void* out
  * into LDS and read back the 16 bytes at base + 16 * lane (out: 256 x 16 bytes). */
 int dgm_probe_global_load_lds(const void* src, void* out, hipStream_t stream);
 
+/* Platform probes (the figures the fused kernel's design is measured against).
+ * dgm_probe_stream_read: HBM read bandwidth of the fused kernel's streaming pattern without its
+ * arithmetic: `blocks` workgroups of 8 waves; each wave reads runs of 24 consecutive 1 KB tiles
+ * (the first bytes / 24 KB whole runs of src, 16-byte aligned, each read once) through a ring of
+ * `depth` (4, 12 or 24) non-temporal loads. sink: one writable device word.
+ * dgm_probe_empty_launch: a kernel of `blocks` x `threads` that returns at entry (the launch
+ * floor). */
+int dgm_probe_stream_read(const void* src, int64_t bytes, int depth, int blocks, void* sink, hipStream_t stream);
+int dgm_probe_empty_launch(int blocks, int threads, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
