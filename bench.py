@@ -75,9 +75,17 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
     flush_rd = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
     share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
     names = ("entry", "dispatch ready", "L1 done", "first L1 seen", "L2 done", "exit")
-    for M, ep, act in ((2, 1, "mxfp8"), (8, 1, "mxfp8"), (16, 1, "mxfp8"), (8, 8, "mxfp4")):
+    bufs = {}
+    # (M=2 and config 1 in both of the kernel's forms, on one buffer: the default, and the opt-in
+    # early weight streaming, debug flag bit 3)
+    for M, ep, act, flags in ((2, 1, "mxfp8", 0), (2, 1, "mxfp8", 8), (8, 1, "mxfp8", 0), (16, 1, "mxfp8", 0),
+                              (8, 8, "mxfp4", 0), (8, 8, "mxfp4", 8)):
         w = share if ep > 1 else weights
-        buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act, ep_size=ep, ep_rank=0)
+        buf = bufs.get((M, ep, act))
+        if buf is None:
+            buf = bufs[(M, ep, act)] = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=act,
+                                                                              ep_size=ep, ep_rank=0)
+        buf._debug_flags = flags
         g = torch.Generator(device="cuda")
         g.manual_seed(4000 + M)
         x = torch.randn((M, H), generator=g, device="cuda").to(torch.bfloat16)
@@ -101,7 +109,8 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
         a = st[:G].cpu().numpy().astype(np.float64)
         t0 = a[:, 0].min()
         n_active = int((buf.pool_table()[0] > 0).sum())
-        print(f"M={M} ep_share={ep} A-{act.upper()} active experts {n_active}, {G} workgroups, kernel "
+        form = dgm.mega.FUSED_FORMS.get(dgm.mega.fused_last_form(buf), "?")
+        print(f"M={M} ep_share={ep} A-{act.upper()} ({form} form) active experts {n_active}, {G} workgroups, kernel "
               f"{ev:.1f} us by events; us from the earliest entry (min / p10 / median / p90 / max):")
         for c, nm in enumerate(names):
             v = a[:, c]

@@ -24,7 +24,7 @@ EXPORTS = [
     "dgm_quantize_nvfp4", "dgm_quantize_qoq", "dgm_cast_int8_rows", "dgm_transform_fp4_weights",
     "dgm_fused_buffer_layout", "dgm_router_topk_launch", "dgm_megamoe_fused_launch",
     "dgm_megamoe_split_launch",
-    "dgm_device_cu_count", "dgm_fused_workgroups",
+    "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_fused_last_form",
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
     "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
     "dgm_reorder_fp4_nibbles", "dgm_untransform_fp4_weights", "dgm_untransform_nvfp4_weights",
@@ -112,6 +112,7 @@ def load():
         "dgm_megamoe_fused_launch_noalloc": ([ctypes.POINTER(MoeArgs), vp], i32),
         "dgm_device_cu_count": ([], i32),
         "dgm_fused_workgroups": ([i32, i32, i32], i32),
+        "dgm_fused_last_form": ([i32, i32, i32], i32),
         "dgm_transform_qoq_weights": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
         "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_host_device_pointer": ([vp, ctypes.POINTER(vp)], i32),

@@ -185,6 +185,7 @@ struct FusedSmem {
   int nslot[FUSED_MAX_TOKENS];
   int wsum[NW][2];
   int meta[4];
+  uint32_t amask[FUSED_MAX_LOCAL / 32];   // (early streaming) active local experts, bit e
   union {
     struct {                           // dispatch only
       int cnt[FUSED_MAX_LOCAL];
@@ -266,6 +267,30 @@ DGM_DEV void scan_experts(S& s, int n) {
 // rest must be zero) and s.nslot (must be zero).
 DGM_DEV uint32_t route_key(int e0, int lane) {
   return ((e0 < 0 ? 0xffffu : (uint32_t)e0) << 16) | (uint32_t)lane;
+}
+
+// Position of the n-th set bit (from 0, ascending) of the NWD-word bit string m, or -1 when it
+// has fewer than n + 1; the same (scalar) value in every lane of the calling wave. Word i sits
+// in lane i; an inclusive prefix of the words' bit counts finds the word, then its lower bits
+// are dropped one at a time.
+template <int NWD>
+DGM_DEV int nth_set_bit(const uint32_t* m, int n, int lane) {
+  static_assert(NWD <= 64, "one word per lane");
+  const uint32_t w = lane < NWD ? m[lane] : 0u;
+  const int cnt = __popc(w);
+  int inc = cnt;
+#pragma unroll
+  for (int off = 1; off < NWD; off <<= 1) {
+    const int o = __shfl_up(inc, off);
+    if (lane >= off) inc += o;
+  }
+  const uint64_t hit = __ballot(inc > n && inc - cnt <= n);
+  if (hit == 0) return -1;
+  const int L = __ffsll((unsigned long long)hit) - 1;
+  uint32_t word = (uint32_t)__shfl((int)w, L);
+  const int k = n - (__shfl(inc, L) - __shfl(cnt, L));
+  for (int i = 0; i < k; ++i) word &= word - 1;
+  return __builtin_amdgcn_readfirstlane(32 * L + __ffs((int)word) - 1);
 }
 template <class S>
 DGM_DEV void route_key_ranks(S& s, int R, int lane, int wv, int* part) {
@@ -640,7 +665,13 @@ DGM_DEV long long wall_clock() { return (long long)__builtin_amdgcn_s_memrealtim
 // write are then read with agent-scope loads. Otherwise they were written by an earlier launch
 // and are read with ordinary loads, which the L2 caches: every workgroup reads the same few
 // activation rows at once, and L2-bypassing loads of them queue at the memory channels.
-template <int KT1, int KT2, int ACT, bool FEIN>
+// EARLY (early weight streaming; small routed sets, one wave's dispatch): the workgroup's first
+// L1 unit is found from a mask of the active experts as the top-k is read, and its slab, scales
+// and tile ring are requested before the pool table is built. An opt-in form (debug bit 3), not
+// the default: measured slower at every size it applies to, since each wave's dispatch code
+// then waits behind the acceptance of its own tile requests, and the ring's second half is
+// requested no earlier.
+template <int KT1, int KT2, int ACT, bool FEIN, bool EARLY>
 __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   using Smem = FusedSmem<KT1, KT2, ACT>;
   __shared__ Smem s;
@@ -667,10 +698,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // this launch's counter set (the other one is cleared after the dispatch); each workgroup
   // counts itself once it has read the parity: the one that counts last hands the next launch
   // the other set at its end (its count is read only then, long after it has returned)
+  // (EARLY: counted behind the early requests, which then do not wait for it)
   const int parity = __hip_atomic_load(p.counters + CNT_PARITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1;
   int* const cset = p.counters + CNT_SET0 + parity * CNT_SET;
   int started = 0;
-  if (tid == 0) started = __hip_atomic_fetch_add(cset + CNT_STARTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  auto count_start = [&]() __attribute__((always_inline)) {
+    if (tid == 0) started = __hip_atomic_fetch_add(cset + CNT_STARTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  if constexpr (!EARLY) count_start();
   int* err = p.counters + CNT_ERROR;
   int* l1_done = cset + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
   int* comb = cset + CNT_COMB;        // pair i: comb[i * CNT_LINE]
@@ -731,8 +766,48 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     __syncthreads();
   }
 
+  // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last
+  // item rolls into the first L2 unit's tiles (unit v0), which then stream during the
+  // L1 epilogue and the phase change instead of after it.
+  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
+  constexpr int RING = KR1 > KT2 ? KR1 : KT2;
+  constexpr bool HANDOFF = KR1 >= KT2;
+  U4 wr[RING];
+  uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
+  // The L1 phase's wave w streams 16-row block pair pp = w & 3 (16 of a unit's 64 features),
+  // tile gu = w >> 2 (gate or up) of local expert e's unit q: block l1_blk(e, q).
+  const int pp = wv & 3, gu = wv >> 2;
+  auto l1_blk = [pp, gu](int e, int q) __attribute__((always_inline)) {
+    return (size_t)e * NB1 + 2 * (4 * q + pp) + gu;
+  };
+  // per-item L1 scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block; QoQ:
+  // its meta dwords (4 per K-tile, spread over the lanes) and the s1 of the lane's 4 rows
+  constexpr int MR1 = (4 * KT1 + 63) / 64;
+  constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : ACT == DGM_ACT_NVFP4 ? 1 : KG1;
+  auto load_scales_blk = [w1s = p.w1s, w1r = p.w1r, lane](size_t blk, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
+    if constexpr (ACT == DGM_ACT_QOQ) {
+      const uint32_t* mb = w1s + blk * KT1 * 4;
+#pragma unroll
+      for (int j = 0; j < MR1; ++j)
+        sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * KT1 ? 64 * j + lane : 4 * KT1 - 1));
+      const v4u r = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w1r + blk * 16 + 4 * (lane >> 4)));
+      sw[MR1] = r.x;
+      sw[MR1 + 1] = r.y;
+      sw[MR1 + 2] = r.z;
+      sw[MR1 + 3] = r.w;
+    } else if constexpr (ACT == DGM_ACT_NVFP4) {
+      sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
+    } else {
+#pragma unroll
+      for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
+    }
+  };
+  uint32_t sd[SW1];                        // the current L1 item's scale registers
+  SlabRegs<KT1, ACT, FEIN, false> pre;     // an L1 slab on its way to LDS
+
   // ---------------------------------------------------------------- dispatch (every WG)
   for (int t = tid; t < p.M; t += FT) s.nslot[t] = 0;
+  if (EARLY && tid < FUSED_MAX_LOCAL / 32) s.amask[tid] = 0u;
   if (p.select) {
     // top-k from the frontend's keys, as the frontend would have done: the keys of TC tokens at
     // a time go through LDS (the slab area, unused until the L1 phase; one coalesced pass),
@@ -773,7 +848,9 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         if (lane < p.topk) {
           const int r = t * p.topk + lane;
           const int l = idx - p.expert_begin;
-          s.exp_of_route[r] = (idx >= 0 && l >= 0 && l < p.E_local) ? l : -1;
+          const bool mine = idx >= 0 && l >= 0 && l < p.E_local;
+          s.exp_of_route[r] = mine ? l : -1;
+          if (EARLY && mine) atomicOr(&s.amask[l >> 5], 1u << (l & 31));
           s.route_w[r] = wt;
           if (blockIdx.x == 0) {
             p.topk_idx[r] = idx;
@@ -784,10 +861,13 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       __syncthreads();
     }
   } else {
+    if constexpr (EARLY) __syncthreads();     // (the mask is clear)
     for (int r = tid; r < R; r += FT) {
       int64_t g = p.topk_idx[r];
       int64_t l = g - p.expert_begin;
-      s.exp_of_route[r] = (g >= 0 && l >= 0 && l < p.E_local) ? (int)l : -1;
+      const bool mine = g >= 0 && l >= 0 && l < p.E_local;
+      s.exp_of_route[r] = mine ? (int)l : -1;
+      if (EARLY && mine) atomicOr(&s.amask[l >> 5], 1u << (l & 31));
       s.route_w[r] = p.topk_w[r];
     }
   }
@@ -799,6 +879,33 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
   }
   __syncthreads();
+  if constexpr (EARLY) {
+    // The workgroup's first L1 unit is unit blockIdx.x: active expert blockIdx.x / QN1 in
+    // ascending order, i.e. the mask's set bit of that index. Its first slab (the expert's
+    // first 16 routes in route order, the pool's order within an expert), its scales and its
+    // tile ring are requested now, in that order, and arrive while the pool table is built.
+    // (R <= 64: the routes are one wave's lanes.)
+    const int e0 = (p.phases & 1) ? nth_set_bit<FUSED_MAX_LOCAL / 32>(s.amask, (int)blockIdx.x / QN1, lane) : -1;
+    // Nothing older is in flight from here on (the top-k loads were consumed above): without
+    // this wait the compiler's wait counting, merging the paths with and without these
+    // requests, put full waits (for the whole tile ring) into the dispatch's LDS code.
+    wait_mem();
+    if (e0 >= 0) {
+      const uint64_t m = __ballot(lane < R && s.exp_of_route[lane] == e0);
+      uint64_t mc = m;
+      for (int i = 0; i < (lane & 15); ++i) mc &= mc - 1;     // drop the first c members
+      const int rt = mc ? (int)__builtin_ctzll(mc) : 0;         // the route of slab column c
+      const int topk = p.topk;
+      slab_load<KT1, ACT, FEIN, false>(pre, p.x, p.xsf, XB, (int)__popcll(m), [rt, topk](int) { return rt / topk; },
+                                       [rt](int) { return s.route_w[rt]; });
+      const size_t blk = l1_blk(e0, (int)blockIdx.x % QN1);
+      load_scales_blk(blk, sd);
+      const uint8_t* b = p.w1v + blk * KT1 * 1024 + lane * 16;
+#pragma unroll
+      for (int k = 0; k < KR1; ++k) wr[k] = ld_stream(b + k * 1024);
+    }
+    count_start();
+  }
   if (R <= 64) {
     // key ranks counted by every wave, then one wave sorts the routes (the other waves wait
     // at the barrier); the parts are staged in the L1 epilogue's up-sum buffer (unused until
@@ -851,7 +958,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     if (tid == 0) { meta[0] = n_active; meta[1] = s.meta[1]; }
     for (int e = tid; e < p.E_local; e += FT) {
       gcnt[e] = s.cnt[e];
-      if (p.recv_stats && (p.phases & 1)) p.recv_stats[e] += s.cnt[e];
+      if (p.recv_stats && (p.phases & 1)) {
+        // (EARLY: an add with no return value, which does not wait for the requests above)
+        if constexpr (EARLY) {
+          if (s.cnt[e]) atomicAdd(p.recv_stats + e, s.cnt[e]);
+        } else {
+          p.recv_stats[e] += s.cnt[e];
+        }
+      }
     }
     for (int a = tid; a <= n_active; a += FT) {
       goff[a] = s.aoff[a];
@@ -894,14 +1008,6 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
   int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
-  // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last
-  // item rolls into the first L2 unit's tiles (unit v0), which then stream during the
-  // L1 epilogue and the phase change instead of after it.
-  constexpr int KR1 = KT1 % 12 == 0 ? 12 : KT1;
-  constexpr int RING = KR1 > KT2 ? KR1 : KT2;
-  constexpr bool HANDOFF = KR1 >= KT2;
-  U4 wr[RING];
-  uint32_t sr[ACT == DGM_ACT_NVFP4 ? RING : 1];
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
   // L2 item v's first 16-row block for this wave (whole units or halves)
   auto l2_blk = [wv, halves](int v) __attribute__((always_inline)) {
@@ -922,45 +1028,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (p.phases & 1) {
     constexpr int KR = KT1 % 12 == 0 ? 12 : KT1;   // ring depth: tiles in flight per wave
     static_assert(KT1 % KR == 0, "the ring depth divides the K-tile count");
-    const int pp = wv & 3, gu = wv >> 2;
     int* claim = cset + CNT_CLAIM;
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
-    const float* w1r = p.w1r;
     const int topk = p.topk;
-    auto tile_base = [w1v, lane, pp, gu](int u) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
-      return w1v + blk * KT1 * 1024 + lane * 16;
+    auto tile_base = [w1v, lane, l1_blk](int u) __attribute__((always_inline)) {
+      return w1v + l1_blk(s.act[u / QN1], u % QN1) * KT1 * 1024 + lane * 16;
     };
-    // per-item scale registers: MXFP: the E8M0 scale dwords of the wave's 16-row block; QoQ:
-    // its meta dwords (4 per K-tile, spread over the lanes) and the s1 of the lane's 4 rows
-    constexpr int MR1 = (4 * KT1 + 63) / 64;
-    constexpr int SW1 = ACT == DGM_ACT_QOQ ? MR1 + 4 : ACT == DGM_ACT_NVFP4 ? 1 : KG1;
-    auto load_scales = [w1s, w1r, lane, pp, gu](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
-      if constexpr (ACT == DGM_ACT_QOQ) {
-        const uint32_t* mb = w1s + blk * KT1 * 4;
-#pragma unroll
-        for (int j = 0; j < MR1; ++j)
-          sw[j] = __builtin_nontemporal_load(mb + (64 * j + lane < 4 * KT1 ? 64 * j + lane : 4 * KT1 - 1));
-        const v4u r = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w1r + blk * 16 + 4 * (lane >> 4)));
-        sw[MR1] = r.x;
-        sw[MR1 + 1] = r.y;
-        sw[MR1 + 2] = r.z;
-        sw[MR1 + 3] = r.w;
-      } else if constexpr (ACT == DGM_ACT_NVFP4) {
-        sw[0] = 0u;      // (the NVFP4 scales stream with the tiles)
-      } else {
-#pragma unroll
-        for (int g = 0; g < KG1; ++g) sw[g] = __builtin_nontemporal_load(w1s + (blk * KG1 + g) * 64 + lane);
-      }
+    auto load_scales = [load_scales_blk, l1_blk](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
+      load_scales_blk(l1_blk(s.act[u / QN1], u % QN1), sw);
     };
     // NVFP4: the lane's scale dword of each tile (128 B of E4M3 scales per 16 x 128 tile), in a
     // ring beside the tile ring
     const int slane = (((lane >> 5) << 4) | (lane & 15)) * 4;
-    auto stile_base = [w1s, slane, pp, gu](int u) __attribute__((always_inline)) {
-      const size_t blk = (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + pp) + gu;
-      return reinterpret_cast<const uint8_t*>(w1s) + blk * KT1 * 128 + slane;
+    auto stile_base = [w1s, slane, l1_blk](int u) __attribute__((always_inline)) {
+      return reinterpret_cast<const uint8_t*>(w1s) + l1_blk(s.act[u / QN1], u % QN1) * KT1 * 128 + slane;
     };
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
@@ -981,25 +1063,30 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
     int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
     int s0 = 0;
-    uint32_t sd[SW1], sn[SW1];
-    SlabRegs<KT1, ACT, FEIN, false> pre;
+    uint32_t sn[SW1];
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
     if (q0 < U1) {
       // The first item's slab is staged before any tile load is issued: every workgroup
       // starts at once, and tile loads issued first would queue the slab loads (and so the
       // barrier, and every wave's first K loop) behind the whole ring of every wave.
-      load_slab(pre, q0 / QN1, 0);
-      load_scales(q0, sd);
+      // (EARLY: all three were requested during the dispatch; q0 < U1 exactly when the mask
+      // had an active expert q0 / QN1.)
+      if constexpr (!EARLY) {
+        load_slab(pre, q0 / QN1, 0);
+        load_scales(q0, sd);
+      }
       slab_store(s, pre);
       staged = (q0 / QN1) << 16;
       __syncthreads();
-      const uint8_t* b = tile_base(q0);
+      if constexpr (!EARLY) {
+        const uint8_t* b = tile_base(q0);
 #pragma unroll
-      for (int k = 0; k < KR; ++k) wr[k] = ld_stream(b + k * 1024);
-      if constexpr (ACT == DGM_ACT_NVFP4) {
-        const uint8_t* sb = stile_base(q0);
+        for (int k = 0; k < KR; ++k) wr[k] = ld_stream(b + k * 1024);
+        if constexpr (ACT == DGM_ACT_NVFP4) {
+          const uint8_t* sb = stile_base(q0);
 #pragma unroll
-        for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
+          for (int k = 0; k < KR; ++k) sr[k] = ld_stream32(sb + k * 128);
+        }
       }
     }
     // B operands (the staged slab's fragments) are read from LDS two K-tiles ahead of their
@@ -1783,11 +1870,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[5] = wall_clock();
 }
 
-// per device, per (shape slot, format, FEIN): the resident grid; per (shape slot, format): the
-// last launch's (the grid is what the device keeps resident at once, so it depends on the
-// device's CU count)
+// per device, per (shape slot, format, form: plain / FEIN / EARLY): the resident grid; per
+// (shape slot, format): the last launch's grid and form (the grid is what the device keeps
+// resident at once, so it depends on the device's CU count)
 constexpr int GRID_DEVICES = 64;
-struct GridCache { int blocks[3][5][2] = {}; int last[3][5] = {}; };
+struct GridCache { int blocks[3][5][3] = {}; int last[3][5] = {}; int form[3][5] = {}; };
 GridCache g_grid[GRID_DEVICES];
 
 GridCache& grid_cache() {
@@ -1796,13 +1883,13 @@ GridCache& grid_cache() {
   return g_grid[dev >= 0 && dev < GRID_DEVICES ? dev : 0];
 }
 
-template <int KT1, int KT2, int ACT, bool FEIN>
+template <int KT1, int KT2, int ACT, bool FEIN, bool EARLY>
 int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
   GridCache& gc = grid_cache();
-  int& nb = gc.blocks[slot][ACT][FEIN ? 1 : 0];
+  int& nb = gc.blocks[slot][ACT][FEIN ? 1 : EARLY ? 2 : 0];
   if (nb == 0) {
     int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT, FEIN>, FT, 0);
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT, FEIN, EARLY>, FT, 0);
     if (e != hipSuccess || per_cu < 1) per_cu = 1;
     int dev = 0, cus = 0;
     (void)hipGetDevice(&dev);
@@ -1810,14 +1897,28 @@ int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
     nb = per_cu * (cus > 0 ? cus : 256);
   }
   gc.last[slot][ACT] = nb;
-  hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FEIN>), dim3(nb), dim3(FT), 0, stream, prm);
+  gc.form[slot][ACT] = FEIN ? 1 : EARLY ? 2 : 0;
+  hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FEIN, EARLY>), dim3(nb), dim3(FT), 0, stream, prm);
   return dgm_last_launch_status();
+}
+
+// Early weight streaming (debug bit 3; MXFP4 / MXFP8 activations, the frontend run before the
+// launch): where the routes fit one wave and at most 32 of them are expected to be local (all,
+// or a share E_local / E of them under expert parallelism: decode batches of up to 4 tokens at
+// top-8).
+bool use_early(const FusedParams& prm, int act) {
+  const long long R = (long long)prm.M * prm.topk;
+  return (act == DGM_ACT_MXFP4 || act == DGM_ACT_MXFP8) && !prm.fe_in && (prm.phases & 1) && R <= 64 &&
+         R * prm.E_local <= 32LL * prm.E && (prm.debug & 8);
 }
 
 template <int KT1, int KT2, int ACT>
 int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream) {
-  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, true>(prm, slot, stream)
-                   : launch_fused_t<KT1, KT2, ACT, false>(prm, slot, stream);
+  if constexpr (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) {
+    if (use_early(prm, ACT)) return launch_fused_t<KT1, KT2, ACT, false, true>(prm, slot, stream);
+  }
+  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, true, false>(prm, slot, stream)
+                   : launch_fused_t<KT1, KT2, ACT, false, false>(prm, slot, stream);
 }
 
 }  // namespace
@@ -1826,6 +1927,13 @@ int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format) {
   int slot = hidden == 3072 ? 0 : (hidden == 512 ? 1 : 2);
   if (act_format < DGM_ACT_MXFP4 || act_format > DGM_ACT_FP8F128) return 0;
   return grid_cache().last[slot][act_format];
+}
+
+int dgm_fused_form(int hidden, int intermediate, int act_format) {
+  int slot = hidden == 3072 ? 0 : (hidden == 512 ? 1 : 2);
+  if (act_format < DGM_ACT_MXFP4 || act_format > DGM_ACT_FP8F128) return -1;
+  const GridCache& gc = grid_cache();
+  return gc.last[slot][act_format] ? gc.form[slot][act_format] : -1;
 }
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream) {

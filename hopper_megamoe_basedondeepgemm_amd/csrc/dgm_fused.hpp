@@ -78,8 +78,10 @@ struct FusedParams {
   // second reads the top-k written by the first and does not wait for L1 arrivals).
   int16_t phases;
   int16_t debug;            // bit 0: one bounded wait that expires (tests of the error reporting);
-                            // bit 1 (QoQ): the int32 L1 accumulators to `stamps` [routes][2 I]
+                            // bit 1 (QoQ): the int32 L1 accumulators to `stamps` [routes][2 I];
+                            // bit 2: whole L2 units only; bit 3: early weight streaming
 };
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream);
 int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format);
+int dgm_fused_form(int hidden, int intermediate, int act_format);

@@ -624,6 +624,10 @@ int dgm_fused_workgroups(int hidden, int intermediate, int act_format) {
   return dgm_fused_grid_blocks(hidden, intermediate, act_format);
 }
 
+int dgm_fused_last_form(int hidden, int intermediate, int act_format) {
+  return dgm_fused_form(hidden, intermediate, act_format);
+}
+
 int dgm_fused_buffer_layout(int max_tokens, int num_experts, int num_local_experts, int topk,
                             int hidden, int intermediate, int act_format, DgmBufferLayout* out) {
   DGM_CHECK_ARG(out != nullptr, "null layout");
@@ -951,7 +955,7 @@ int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, 
     // (debug bit 1: phase_stamps receives the QoQ L1 accumulators instead of stamps)
     p.stamp_rows = A->phase_stamps && !(A->debug_flags & 2) ? A->phase_stamp_rows : 0;
     p.phases = phases;
-    p.debug = (int16_t)(A->debug_flags & 7);
+    p.debug = (int16_t)(A->debug_flags & 15);
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
 }

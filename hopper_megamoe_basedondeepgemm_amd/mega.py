@@ -720,6 +720,17 @@ def fused_workgroups(b):
     return _lib.load().dgm_fused_workgroups(b.hidden, b.intermediate_hidden, b.act_code)
 
 
+FUSED_FORMS = {0: "plain", 1: "in-kernel frontend", 2: "early weight streaming"}
+
+
+def fused_last_form(b):
+    """The form the persistent kernel's last launch for this buffer's shape and format ran (a
+    key of ``FUSED_FORMS``; -1 before the first). Early weight streaming is an opt-in form for
+    small routed sets (MXFP4 / MXFP8 activations, at most 32 local routes expected), turned on
+    by the buffer's ``_debug_flags`` bit 3."""
+    return _lib.load().dgm_fused_last_form(b.hidden, b.intermediate_hidden, b.act_code)
+
+
 def mxfp4_mega_moe_split(y, l1_weights, l2_weights, sym_buffer, *args, **kwargs):
     """deep_gemm/mega/__init__.py:579 split API: the same layer as separate launches (dispatch,
     L1 + SwiGLU + requant, L2, combine) with the fused path's numerics, on an "mxfp4" / "mxfp8"

@@ -292,7 +292,11 @@ typedef struct DgmMoeArgs {
    * (sum over K128 groups of s2 * sum (code - z) * x8, per route in pool order and W1 row, gate
    * rows then up rows: int32 [routes][2 I]) instead of stamps, for bit-exact tests. Bit 2: the
    * persistent kernel runs whole L2 units even where it would run half units (units filling at
-   * most half the grid), so tests cover both forms at small shapes. */
+   * most half the grid), so tests cover both forms at small shapes. Bit 3: the persistent kernel
+   * runs its early-weight-streaming form where that form applies (at most 32 local routes
+   * expected, MXFP4 / MXFP8 activations, the frontend run before the launch): the first L1
+   * unit's weight tiles are requested before the pool table is built. Measured slower than the
+   * default form at every size it applies to; kept so tests and benchmarks can compare them. */
   int32_t debug_flags;
 } DgmMoeArgs;
 
@@ -324,10 +328,12 @@ int dgm_host_device_pointer(const void* host, void** device);
 
 /* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the
  * current device. dgm_fused_workgroups: workgroups of the persistent kernel for a shape (0 before
- * its first launch). The lane-layout probes of the tests live in a library of their own
- * (include/dgm_probe.h). */
+ * its first launch). dgm_fused_last_form: the form its last launch for a shape ran, 0 plain,
+ * 1 with the in-kernel frontend, 2 with early weight streaming (-1 before its first launch).
+ * The lane-layout probes of the tests live in a library of their own (include/dgm_probe.h). */
 int dgm_device_cu_count(void);
 int dgm_fused_workgroups(int hidden, int intermediate, int act_format);
+int dgm_fused_last_form(int hidden, int intermediate, int act_format);
 
 #ifdef __cplusplus
 }
