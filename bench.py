@@ -76,10 +76,10 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
     share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
     names = ("entry", "dispatch ready", "L1 done", "first L1 seen", "L2 done", "exit")
     bufs = {}
-    # (M=2 and config 1 in both of the kernel's forms, on one buffer: the default, and the opt-in
-    # early weight streaming, debug flag bit 3)
-    for M, ep, act, flags in ((2, 1, "mxfp8", 0), (2, 1, "mxfp8", 8), (8, 1, "mxfp8", 0), (16, 1, "mxfp8", 0),
-                              (8, 8, "mxfp4", 0), (8, 8, "mxfp4", 8)):
+    # (M=2 and config 1 in the kernel's forms, on one buffer: the default, and the opt-in early
+    # weight streaming (debug flag bit 3) and, at M=2, tail half units (bit 4))
+    for M, ep, act, flags in ((2, 1, "mxfp8", 0), (2, 1, "mxfp8", 8), (2, 1, "mxfp8", 16), (8, 1, "mxfp8", 0),
+                              (16, 1, "mxfp8", 0), (8, 8, "mxfp4", 0), (8, 8, "mxfp4", 8)):
         w = share if ep > 1 else weights
         buf = bufs.get((M, ep, act))
         if buf is None:

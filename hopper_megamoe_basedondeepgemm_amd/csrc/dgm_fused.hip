@@ -208,6 +208,10 @@ struct FusedSmem {
   float xf[ACT == DGM_ACT_FP8F128 ? KT1 : 1][16];
   float slab_w[16];                    // routing weights of the staged slab's routes (L1)
   float upv[4][64][4];                 // L1: up-projection sums for the gate waves [pair][lane][i]
+  // L1 half units (TAIL form): per block pair of the half, the K-half-1 sums of its gate and up
+  // blocks [pair & 1][gate, up][lane][i]
+  static constexpr int HS = (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) && KT1 == 24 ? 2 : 1;
+  float hsum[HS][2][64][4];
   float amax[4][16];                   // L1: per-token amax of each pair's 16 features
   int claimv[3];            // [0] the claim ahead, [1] prefetch decision, [2] L2: a complete expert
 };
@@ -671,8 +675,13 @@ DGM_DEV long long wall_clock() { return (long long)__builtin_amdgcn_s_memrealtim
 // the default: measured slower at every size it applies to, since each wave's dispatch code
 // then waits behind the acceptance of its own tile requests, and the ring's second half is
 // requested no earlier.
-template <int KT1, int KT2, int ACT, bool FEIN, bool EARLY>
+// The kernel's forms (one instantiation each; the launch picks one): plain, FEIN, and the
+// opt-in EARLY and TAIL (A-MXFP at H = 3072, small routed sets: the last round of L1 units as
+// half units).
+constexpr int FORM_PLAIN = 0, FORM_FEIN = 1, FORM_EARLY = 2, FORM_TAIL = 3;
+template <int KT1, int KT2, int ACT, int FORM>
 __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
+  constexpr bool FEIN = FORM == FORM_FEIN, EARLY = FORM == FORM_EARLY, TAIL = FORM == FORM_TAIL;
   using Smem = FusedSmem<KT1, KT2, ACT>;
   __shared__ Smem s;
   constexpr int FB = ACT == DGM_ACT_MXFP4 ? 4 : 0;        // B operand format
@@ -1003,11 +1012,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int u2w = n_active * UPE2, G2 = (int)gridDim.x;
   const bool halves = RB2 == 2 && (2 * u2w <= G2 || (WIDE && u2w > G2 && 2 * (u2w - G2) <= G2)) && !(p.debug & 4);
   const int U1 = n_active * QN1, U2 = n_active * (halves ? NBL2 : UPE2);
+  // TAIL: when the last round of L1 units fills at most half the grid, its units run as two
+  // half items each (32 features; each 16-row block's K split over two waves, whose sums the
+  // gate wave adds in the whole unit's order, so the results are those of whole units bit for
+  // bit). Items: the whole units 0 .. Uw - 1, then half j of unit Uw + i as item Uw + 2 i + j.
+  // L1 arrivals count half units (a whole unit adds 2).
+  constexpr int L1W = TAIL ? 2 : 1;
+  const int rem1 = U1 % (int)gridDim.x;
+  const bool tail = TAIL && rem1 != 0 && 2 * rem1 <= (int)gridDim.x;
+  const int Uw = tail ? U1 - rem1 : U1, UI = tail ? U1 + rem1 : U1;
   // This workgroup's first L2 unit (its second is G + v0)
   const int v0 = (int)blockIdx.x;
   const int c = lane & 15, kq = lane >> 4;
   int staged = -1;          // (phase, a, slab) currently in s.bst
   int l1_pend = -1;         // the L1 phase's last unit's expert slot, signalled in the L2 phase
+  int l1_pend_w = 0;        // (and its arrival count)
   bool handed = false;      // wr[0 .. KT2) hold the first L2 unit's tiles 0 .. KT2 - 1
   // L2 item v's first 16-row block for this wave (whole units or halves)
   auto l2_blk = [wv, halves](int v) __attribute__((always_inline)) {
@@ -1032,12 +1051,27 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const uint8_t* w1v = p.w1v;
     const uint32_t* w1s = p.w1s;
     const int topk = p.topk;
-    auto tile_base = [w1v, lane, l1_blk](int u) __attribute__((always_inline)) {
-      return w1v + l1_blk(s.act[u / QN1], u % QN1) * KT1 * 1024 + lane * 16;
+    constexpr int KH = KT1 / 2;       // (TAIL) K-tiles per wave of a half item
+    static_assert(!TAIL || (KH == KR && KH % 4 == 0), "a half item fills the ring once, whole scale dwords");
+    // item q: its unit; (half items) this wave's block pair (of the unit's four) is
+    // 2 j + (w & 1), its tile (gate / up) (w >> 1) & 1 and its K half w >> 2
+    auto unit_of = [Uw](int q) __attribute__((always_inline)) { return TAIL && q >= Uw ? Uw + ((q - Uw) >> 1) : q; };
+    auto item_blk = [Uw, wv, l1_blk](int q) __attribute__((always_inline)) {
+      if (TAIL && q >= Uw) {
+        const int u = Uw + ((q - Uw) >> 1);
+        return (size_t)s.act[u / QN1] * NB1 + 2 * (4 * (u % QN1) + 2 * ((q - Uw) & 1) + (wv & 1)) + ((wv >> 1) & 1);
+      }
+      return l1_blk(s.act[q / QN1], q % QN1);
     };
-    auto load_scales = [load_scales_blk, l1_blk](int u, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
-      load_scales_blk(l1_blk(s.act[u / QN1], u % QN1), sw);
+    auto tile_base = [w1v, lane, Uw, wv, item_blk](int q) __attribute__((always_inline)) {
+      return w1v + item_blk(q) * KT1 * 1024 + (TAIL && q >= Uw ? (size_t)(wv >> 2) * KH * 1024 : 0) + lane * 16;
     };
+    // (a half item loads its block's scale dwords of both K halves; it uses its own half's)
+    auto load_scales = [load_scales_blk, item_blk](int q, uint32_t (&sw)[SW1]) __attribute__((always_inline)) {
+      load_scales_blk(item_blk(q), sw);
+    };
+    // (TAIL) an item's first K-tile for this wave
+    auto k_first = [Uw, wv](int q) __attribute__((always_inline)) { return TAIL && q >= Uw ? (wv >> 2) * KH : 0; };
     // NVFP4: the lane's scale dword of each tile (128 B of E4M3 scales per 16 x 128 tile), in a
     // ring beside the tile ring
     const int slane = (((lane >> 5) << 4) | (lane & 15)) * 4;
@@ -1060,23 +1094,24 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     // thread 0: the raw counter value of the claim ahead (unit 2 G + value), -1 for none; it is
     // used as returned (any arithmetic on it here would wait for every load issued before it)
     int ahead = -1;
-    int q0 = (int)blockIdx.x < U1 ? (int)blockIdx.x : U1;    // current unit
-    int q1 = G + (int)blockIdx.x < U1 ? G + (int)blockIdx.x : U1;   // next unit
+    int q0 = (int)blockIdx.x < UI ? (int)blockIdx.x : UI;    // current item
+    int q1 = G + (int)blockIdx.x < UI ? G + (int)blockIdx.x : UI;   // next item
     int s0 = 0;
     uint32_t sn[SW1];
     int pend = -1;            // expert slot of a finished unit whose arrival is not signalled yet
-    if (q0 < U1) {
+    int pend_w = 0;           // (and its arrival count)
+    if (q0 < UI) {
       // The first item's slab is staged before any tile load is issued: every workgroup
       // starts at once, and tile loads issued first would queue the slab loads (and so the
       // barrier, and every wave's first K loop) behind the whole ring of every wave.
       // (EARLY: all three were requested during the dispatch; q0 < U1 exactly when the mask
       // had an active expert q0 / QN1.)
       if constexpr (!EARLY) {
-        load_slab(pre, q0 / QN1, 0);
+        load_slab(pre, unit_of(q0) / QN1, 0);
         load_scales(q0, sd);
       }
       slab_store(s, pre);
-      staged = (q0 / QN1) << 16;
+      staged = (unit_of(q0) / QN1) << 16;
       __syncthreads();
       if constexpr (!EARLY) {
         const uint8_t* b = tile_base(q0);
@@ -1098,19 +1133,22 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     };
     v8i bq0 = {}, bq1 = {};
     uint32_t bs0 = 0;
-    if (q0 < U1) {
-      bq0 = bfrag(0);
-      bq1 = KT1 > 1 ? bfrag(1) : bq0;
-      bs0 = s.bsc[0][lane];
+    if (q0 < UI) {
+      const int k0 = k_first(q0);
+      bq0 = bfrag(k0);
+      bq1 = KT1 > 1 ? bfrag(k0 + 1) : bq0;
+      bs0 = s.bsc[k0 >> 2][lane];
     }
-    bool more = 2 * G < U1;   // the claim counter has not run out
-    while (q0 < U1) {
-      const int a = q0 / QN1, q = q0 % QN1;
+    bool more = 2 * G < UI;   // the claim counter has not run out
+    while (q0 < UI) {
+      const int u0 = unit_of(q0);
+      const int a = u0 / QN1, q = u0 % QN1;
+      const bool hf = TAIL && q0 >= Uw;       // a half item
       const int r0 = s.aoff[a], n = s.aoff[a + 1] - r0;
       const bool last_slab = s0 + 16 >= n;
       const int nq = last_slab ? q1 : q0, ns0 = last_slab ? 0 : s0 + 16;
-      const bool has_next = nq < U1;
-      const int na = has_next ? nq / QN1 : -1;
+      const bool has_next = nq < UI;
+      const int na = has_next ? unit_of(nq) / QN1 : -1;
       const int nkey = (na << 16) | ns0;
       const bool restage = has_next && nkey != staged;
       const uint8_t* cb = tile_base(q0);
@@ -1139,7 +1177,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       const float sx = ACT == DGM_ACT_QOQ ? s.xsc[c] : 1.f;       // QoQ: the token's activation scale
       // the unit after q1, claimed at the start of the item that finishes q0 (after its loads;
       // the value is read in this item's epilogue, by when it has returned)
-      if (tid == 0 && last_slab && q1 < U1 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && last_slab && q1 < UI && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -1260,27 +1298,43 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(xf_p, prev[i], acc[i]);
       } else {
         // two chains, K-tiles 0 .. KT1 / 2 - 1 and KT1 / 2 .., summed after the loop: the split
-        // path's L1 kernel sums the same two, so the two paths agree bit for bit for any data
+        // path's L1 kernel sums the same two, so the two paths agree bit for bit for any data.
+        // (TAIL, a half item: each wave runs one of the chains, K half w >> 2, and a K half 0
+        // wave refills its slots with the next item's tiles: a half item fills the ring once.)
         v4f acc2 = {0.f, 0.f, 0.f, 0.f};
         uint32_t bs = bs0;
+        const bool hi_wave = wv >= 4;
+        const int ro = TAIL && hf ? 0 : KR * 1024;                     // refill offset of K half 0
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
           constexpr bool HI = t >= KT1 / 2;
-          const v8i bop = bq0;
-          const uint32_t bsw = bs;
-          bq0 = bq1;
-          if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
-          if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
-          v4f& ac = HI ? acc2 : acc;
-          ac = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, ac, (int)sd[t >> 2], (int)bsw);
-          if constexpr (t + KR < KT1) wr[t % KR] = ld_stream_after(cb, (t + KR) * 1024, ac);
-          else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, ac);
-          if constexpr (t == KT1 - KR) {
-            if (has_next && nq != q0) load_scales(nq, sn);
-            if (restage) load_slab(pre, na, ns0);
+          if (!TAIL || !hf || HI == hi_wave) {
+            const v8i bop = bq0;
+            const uint32_t bsw = bs;
+            bq0 = bq1;
+            if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
+            if constexpr ((t & 3) == 3 && t + 1 < KT1) bs = s.bsc[(t + 1) >> 2][lane];
+            v4f& ac = HI ? acc2 : acc;
+            ac = mfma_scale_16x16x128_sel<4, FB, t & 3, t & 3>(as_v8i(wr[t % KR]), bop, ac, (int)sd[t >> 2], (int)bsw);
+            if constexpr (t + KR < KT1) {
+              // (a half item's K half 0: the next item's tile t, as the second half refills)
+              const uint8_t* rb = TAIL && hf ? (t < KT2 ? nb : nbd) : cb;
+              wr[t % KR] = ld_stream_after(rb, (TAIL ? ro : KR * 1024) + t * 1024, ac);
+            }
+            else wr[t % KR] = ld_stream_after(t + KR - KT1 < KT2 ? nb : nbd, (t + KR - KT1) * 1024, ac);
+            if constexpr (t == KT1 - KR || (TAIL && t == 0)) {
+              if (t == KT1 - KR || (hf && !hi_wave)) {
+                if (has_next && nq != q0) load_scales(nq, sn);
+                if (restage) load_slab(pre, na, ns0);
+              }
+            }
           }
         });
-        acc += acc2;
+        if (TAIL && hf) {
+          if (hi_wave) acc = acc2;      // (the K half 1 chain, added by the gate wave)
+        } else {
+          acc += acc2;
+        }
       }
       // all but this loop's KR youngest tile loads (and scale loads) are done: the previous
       // item's stores too
@@ -1292,38 +1346,57 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= gsc;
       }
-      if (gu == 1) {
+      // this wave's block pair (of the unit's four) and tile in the item, and whether it holds
+      // K half 1 of a half item (its sum goes to the gate wave through LDS)
+      const int ip = hf ? 2 * ((q0 - Uw) & 1) + (wv & 1) : pp;
+      const int ig = hf ? (wv >> 1) & 1 : gu;
+      const bool khi = hf && wv >= 4;
+      if (khi) {
+        if constexpr (TAIL) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s.upv[pp][lane][i] = acc[i];
+          for (int i = 0; i < 4; ++i) s.hsum[wv & 1][ig][lane][i] = acc[i];
+        }
+      } else if (ig == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s.upv[ip][lane][i] = acc[i];
       }
       // the unit after q1 (claimed at this item's start), broadcast here
-      const bool bcast = last_slab && q1 < U1;
+      const bool bcast = last_slab && q1 < UI;
       if (tid == 0 && bcast) s.claimv[0] = more ? ahead : -1;
       __syncthreads();                                   // (1) up sums visible, slab free
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], pend_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       pend = -1;
-      int q2 = U1;
+      int q2 = UI;
       if (bcast) {
         const int raw = __builtin_amdgcn_readfirstlane(s.claimv[0]);
-        q2 = raw >= 0 && 2 * G + raw < U1 ? 2 * G + raw : U1;
-        if (q2 >= U1) more = false;
+        q2 = raw >= 0 && 2 * G + raw < UI ? 2 * G + raw : UI;
+        if (q2 >= UI) more = false;
       }
       if (restage) {
         slab_store(s, pre);
         staged = nkey;
       }
       const bool valid = s0 + c < n;
-      const int pr = 4 * q + pp;                         // 16-feature block of this pair
+      const int pr = 4 * q + ip;                         // 16-feature block of this pair
       float act[4];
-      if (gu == 0) {
+      if (ig == 0 && !khi) {
         float am = 0.f;
+        if constexpr (TAIL) {
+          if (hf) {           // the K halves summed as a whole unit sums its two chains
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += s.hsum[wv & 1][0][lane][i];
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           // MXFP: gate / up rounded to bf16 (the reference's L1 output); QoQ, FP8F128: fp32
           // (tests/test_four_api_correctness.py:437-442)
           constexpr bool F32GU = ACT == DGM_ACT_QOQ || F128;
           const float g = fminf(F32GU ? acc[i] : round_bf16(acc[i]), p.clamp);
-          const float uv = s.upv[pp][lane][i];
+          float uv = s.upv[ip][lane][i];
+          if constexpr (TAIL) {
+            if (hf) uv += s.hsum[wv & 1][1][lane][i];
+          }
           const float uu = fminf(fmaxf(F32GU ? uv : round_bf16(uv), -p.clamp), p.clamp);
           const float sgm = p.fast_math ? sigmoid<true>(g) : sigmoid<false>(g);
           act[i] = valid ? ((g * sgm) * uu) * wt_r : 0.f;
@@ -1331,20 +1404,21 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         }
         am = fmaxf(am, __shfl_xor(am, 16));
         am = fmaxf(am, __shfl_xor(am, 32));
-        if (lane < 16) s.amax[pp][lane] = am;
+        if (lane < 16) s.amax[ip][lane] = am;
       }
       __syncthreads();                                   // (2) amax visible, next slab staged
       if (has_next) {
-        bq0 = bfrag(0);
-        bq1 = KT1 > 1 ? bfrag(1) : bq0;
-        bs0 = s.bsc[0][lane];
+        const int k0 = k_first(nq);
+        bq0 = bfrag(k0);
+        bq1 = KT1 > 1 ? bfrag(k0 + 1) : bq0;
+        bs0 = s.bsc[k0 >> 2][lane];
       }
-      if (gu == 0) {
+      if (ig == 0 && !khi) {
         // requant group: QoQ, FP8F128 64 features (the unit), NVFP4 16 (this pair), MXFP 32 (two
-        // pairs)
+        // pairs, both in a half item)
         const float am = ACT == DGM_ACT_QOQ || F128 ? fmaxf(fmaxf(s.amax[0][c], s.amax[1][c]), fmaxf(s.amax[2][c], s.amax[3][c]))
-                         : ACT == DGM_ACT_NVFP4 ? s.amax[pp][c]
-                                                : fmaxf(s.amax[pp][c], s.amax[pp ^ 1][c]);
+                         : ACT == DGM_ACT_NVFP4 ? s.amax[ip][c]
+                                                : fmaxf(s.amax[ip][c], s.amax[ip ^ 1][c]);
         const int row = r0 + s0 + c;
         // lane group kq holds features 16 pr + 4 kq .. +3 of column c
         if (ACT == DGM_ACT_QOQ) {
@@ -1361,7 +1435,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           const uint64_t w64 = (uint64_t)__shfl(w, src_lo) | ((uint64_t)__shfl(w, src_hi) << 32);
           if (valid && lane < 32) {
             st_agent64(p.mid + (size_t)row * MB + 16 * pr + (lane < 16 ? 0 : 8), w64);
-            if (pp == 0 && lane < 16) st_agent32(p.mid_sf + (size_t)row * (I / 16) + 4 * q, __float_as_uint(sc));
+            if (ip == 0 && lane < 16) st_agent32(p.mid_sf + (size_t)row * (I / 16) + 4 * q, __float_as_uint(sc));
           }
         } else if (ACT == DGM_ACT_NVFP4) {
           // E2M1 per 16 features: sf = E4M3 (round to nearest even) of max(amax, 1e-30) / 6,
@@ -1390,7 +1464,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
                                ((uint64_t)(__shfl(w, c + 48) & 0xffffu) << 48);
           if (valid && lane < 16) {
             st_agent64(p.mid + (size_t)row * MB + 8 * pr, w64);
-            if ((pp & 1) == 0) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
+            if ((ip & 1) == 0) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
           }
         } else {
           // E4M3 with a power-of-two scale per 32 (MXFP8: 2^ceil(log2(max(amax, 1e-30) / 448)))
@@ -1407,13 +1481,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
           const uint64_t w64 = (uint64_t)__shfl(w, src_lo) | ((uint64_t)__shfl(w, src_hi) << 32);
           if (valid && lane < 32) {
             st_agent64(p.mid + (size_t)row * MB + 16 * pr + (lane < 16 ? 0 : 8), w64);
-            if ((pp & 1) == 0 && lane < 16) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
+            if ((ip & 1) == 0 && lane < 16) st_agent8(p.mid_sf + (size_t)row * (I / 32) + (pr >> 1), (uint8_t)code);
           }
         }
       }
       if (st) l1_sig_ticks += wall_clock() - t_e0;
       if (last_slab) {
         pend = a;
+        pend_w = hf ? 1 : L1W;
         if (nq != q0) {
 #pragma unroll
           for (int g = 0; g < SW1; ++g) sd[g] = sn[g];
@@ -1427,10 +1502,11 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
     if (p.phases & 2) {
       l1_pend = pend;         // (its stores complete while the L2 phase issues its first loads)
+      l1_pend_w = pend_w;
     } else {
       wait_mem();             // the last item's stores (and the dummy ring reads)
       __syncthreads();
-      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && pend >= 0) __hip_atomic_fetch_add(&l1_done[pend * CNT_LINE], pend_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   if (st && tid == 0) st[2] = wall_clock();
@@ -1532,14 +1608,14 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       // the L1 phase's last unit: its stores have completed (every wave) -> its arrival, before
       // any wait on other workgroups' arrivals
       wait_mem();
-      if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= QN1 ? 1 : 0;
+      if (tid == 0) s.claimv[1] = q0 < U2 && pr_a >= L1W * QN1 ? 1 : 0;
       __syncthreads();
-      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid == 0 && q0 < U2 && pr_a >= QN1) ready = q0 / UPE;
+      if (tid == 0 && l1_pend >= 0) __hip_atomic_fetch_add(&l1_done[l1_pend * CNT_LINE], l1_pend_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0 && q0 < U2 && pr_a >= L1W * QN1) ready = q0 / UPE;
     }
     // (thread 0) the second unit's expert when its probe found it complete (LDS: read once, by
     // the first item's prefetch check)
-    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= QN1 ? q1 / UPE : -1;
+    if (tid == 0) s.claimv[2] = q1 < U2 && pr_n >= L1W * QN1 ? q1 / UPE : -1;
     if (q0 < U2) {
       if (!handed) {          // (unit q0 = v0: handed over by the L1 phase otherwise)
         const uint8_t* b = tile_base(q0);
@@ -1573,7 +1649,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       } else if (key != staged) {    // not prefetched: wait for the expert's L1 units, then stage
         const long long w0 = st ? wall_clock() : 0;
         if (a != ready) {
-          if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], QN1, p.spin_limit, err, p.host_err);
+          if (tid == 0 && (p.phases & 1)) spin_until2(&l1_done[a * CNT_LINE], L1W * QN1, p.spin_limit, err, p.host_err);
           ready = a;
         }
         __syncthreads();
@@ -1602,7 +1678,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       if (has_next && nkey != key) {
         if (tid == 0)
           s.claimv[1] = !(p.phases & 1) || na == ready || na == s.claimv[2] ||
-                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= QN1;
+                        __hip_atomic_load(&l1_done[na * CNT_LINE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= L1W * QN1;
         __syncthreads();
         pf = __builtin_amdgcn_readfirstlane(s.claimv[1]) != 0;
         if (pf) {
@@ -1874,7 +1950,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
 // (shape slot, format): the last launch's grid and form (the grid is what the device keeps
 // resident at once, so it depends on the device's CU count)
 constexpr int GRID_DEVICES = 64;
-struct GridCache { int blocks[3][5][3] = {}; int last[3][5] = {}; int form[3][5] = {}; };
+struct GridCache { int blocks[3][5][4] = {}; int last[3][5] = {}; int form[3][5] = {}; };
 GridCache g_grid[GRID_DEVICES];
 
 GridCache& grid_cache() {
@@ -1883,13 +1959,13 @@ GridCache& grid_cache() {
   return g_grid[dev >= 0 && dev < GRID_DEVICES ? dev : 0];
 }
 
-template <int KT1, int KT2, int ACT, bool FEIN, bool EARLY>
+template <int KT1, int KT2, int ACT, int FORM>
 int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
   GridCache& gc = grid_cache();
-  int& nb = gc.blocks[slot][ACT][FEIN ? 1 : EARLY ? 2 : 0];
+  int& nb = gc.blocks[slot][ACT][FORM];
   if (nb == 0) {
     int per_cu = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT, FEIN, EARLY>, FT, 0);
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_megamoe<KT1, KT2, ACT, FORM>, FT, 0);
     if (e != hipSuccess || per_cu < 1) per_cu = 1;
     int dev = 0, cus = 0;
     (void)hipGetDevice(&dev);
@@ -1897,8 +1973,8 @@ int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
     nb = per_cu * (cus > 0 ? cus : 256);
   }
   gc.last[slot][ACT] = nb;
-  gc.form[slot][ACT] = FEIN ? 1 : EARLY ? 2 : 0;
-  hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FEIN, EARLY>), dim3(nb), dim3(FT), 0, stream, prm);
+  gc.form[slot][ACT] = FORM;
+  hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FORM>), dim3(nb), dim3(FT), 0, stream, prm);
   return dgm_last_launch_status();
 }
 
@@ -1912,13 +1988,26 @@ bool use_early(const FusedParams& prm, int act) {
          R * prm.E_local <= 32LL * prm.E && (prm.debug & 8);
 }
 
+// Half units for the last round of L1 units (debug bit 4; A-MXFP at H = 3072, the frontend run
+// before the launch): for decode batches of up to 4 tokens at top-8 (<= 32 routes), whose units
+// end in a partial round (M=2: 320 units, M=4: 640, on 256 workgroups); the kernel applies them
+// when that round is at most half full. An opt-in form: measured slower (that round shares the
+// HBM with the other workgroups' L2 weight streams, so halving its units does not end it
+// sooner, and every half item pays a whole item's epilogue).
+bool use_tail(const FusedParams& prm) {
+  return !prm.fe_in && (prm.phases & 1) && (long long)prm.M * prm.topk <= 32 && (prm.debug & 16);
+}
+
 template <int KT1, int KT2, int ACT>
 int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream) {
   if constexpr (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) {
-    if (use_early(prm, ACT)) return launch_fused_t<KT1, KT2, ACT, false, true>(prm, slot, stream);
+    if (use_early(prm, ACT)) return launch_fused_t<KT1, KT2, ACT, FORM_EARLY>(prm, slot, stream);
+    if constexpr (KT1 == 24) {
+      if (use_tail(prm)) return launch_fused_t<KT1, KT2, ACT, FORM_TAIL>(prm, slot, stream);
+    }
   }
-  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, true, false>(prm, slot, stream)
-                   : launch_fused_t<KT1, KT2, ACT, false, false>(prm, slot, stream);
+  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, FORM_FEIN>(prm, slot, stream)
+                   : launch_fused_t<KT1, KT2, ACT, FORM_PLAIN>(prm, slot, stream);
 }
 
 }  // namespace

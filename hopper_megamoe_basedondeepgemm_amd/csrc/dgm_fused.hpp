@@ -79,7 +79,8 @@ struct FusedParams {
   int16_t phases;
   int16_t debug;            // bit 0: one bounded wait that expires (tests of the error reporting);
                             // bit 1 (QoQ): the int32 L1 accumulators to `stamps` [routes][2 I];
-                            // bit 2: whole L2 units only; bit 3: early weight streaming
+                            // bit 2: whole L2 units only; bit 3: early weight streaming;
+                            // bit 4: tail half units
 };
 
 int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream);

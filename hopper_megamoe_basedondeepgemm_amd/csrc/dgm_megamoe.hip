@@ -955,7 +955,7 @@ int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, 
     // (debug bit 1: phase_stamps receives the QoQ L1 accumulators instead of stamps)
     p.stamp_rows = A->phase_stamps && !(A->debug_flags & 2) ? A->phase_stamp_rows : 0;
     p.phases = phases;
-    p.debug = (int16_t)(A->debug_flags & 15);
+    p.debug = (int16_t)(A->debug_flags & 31);
     return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
   }
 }

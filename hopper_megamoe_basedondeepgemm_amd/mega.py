@@ -720,14 +720,16 @@ def fused_workgroups(b):
     return _lib.load().dgm_fused_workgroups(b.hidden, b.intermediate_hidden, b.act_code)
 
 
-FUSED_FORMS = {0: "plain", 1: "in-kernel frontend", 2: "early weight streaming"}
+FUSED_FORMS = {0: "plain", 1: "in-kernel frontend", 2: "early weight streaming", 3: "tail half units"}
 
 
 def fused_last_form(b):
     """The form the persistent kernel's last launch for this buffer's shape and format ran (a
-    key of ``FUSED_FORMS``; -1 before the first). Early weight streaming is an opt-in form for
-    small routed sets (MXFP4 / MXFP8 activations, at most 32 local routes expected), turned on
-    by the buffer's ``_debug_flags`` bit 3."""
+    key of ``FUSED_FORMS``; -1 before the first). Two opt-in forms, both measured slower than the
+    default: early weight streaming for small routed sets (MXFP4 / MXFP8 activations, at most 32
+    local routes expected), turned on by the buffer's ``_debug_flags`` bit 3, and tail half units
+    for up to 32 routes (A-MXFP4 / A-MXFP8 at H = 3072: the last round of L1 units, when at most
+    half full, runs as half units), bit 4."""
     return _lib.load().dgm_fused_last_form(b.hidden, b.intermediate_hidden, b.act_code)
 
 

@@ -296,7 +296,11 @@ typedef struct DgmMoeArgs {
    * runs its early-weight-streaming form where that form applies (at most 32 local routes
    * expected, MXFP4 / MXFP8 activations, the frontend run before the launch): the first L1
    * unit's weight tiles are requested before the pool table is built. Measured slower than the
-   * default form at every size it applies to; kept so tests and benchmarks can compare them. */
+   * default form at every size it applies to; kept so tests and benchmarks can compare them.
+   * Bit 4: the persistent kernel runs its tail-half-unit form where that form applies (up to 32
+   * routes, MXFP4 / MXFP8 activations, hidden 3072: the last round of L1 units, when at most half
+   * full, runs as half units of 32 features, each 16-row block's K split over two waves).
+   * Measured slower than the default form; kept so tests and benchmarks can compare them. */
   int32_t debug_flags;
 } DgmMoeArgs;
 
@@ -329,7 +333,8 @@ int dgm_host_device_pointer(const void* host, void** device);
 /* Diagnostics (no counterpart in the reference). dgm_device_cu_count: compute units of the
  * current device. dgm_fused_workgroups: workgroups of the persistent kernel for a shape (0 before
  * its first launch). dgm_fused_last_form: the form its last launch for a shape ran, 0 plain,
- * 1 with the in-kernel frontend, 2 with early weight streaming (-1 before its first launch).
+ * 1 with the in-kernel frontend, 2 with early weight streaming, 3 with tail half units (-1
+ * before its first launch).
  * The lane-layout probes of the tests live in a library of their own (include/dgm_probe.h). */
 int dgm_device_cu_count(void);
 int dgm_fused_workgroups(int hidden, int intermediate, int act_format);

@@ -194,20 +194,21 @@ def test_config2_m2_m4_balanced(mxfp4_weights):
 
 
 @pytest.mark.parametrize("fmt", ["mxfp8", "mxfp4"])
-def test_config2_small_m_early_streaming_matches_plain(mxfp4_weights, fmt):
-    """At the bench's M=2 and M=4 (forced-balanced, 384 resident experts), the opt-in early-
-    weight-streaming form (debug flag bit 3) and the default form give the same y, route outputs,
-    intermediate rows and recv stats bit for bit."""
+def test_config2_small_m_kernel_forms_match(mxfp4_weights, fmt):
+    """At the bench's M=2 and M=4 (forced-balanced, 384 resident experts: 320 and 640 L1 units on
+    256 workgroups), the default form and the opt-in early-weight-streaming (debug flag bit 3) and
+    tail-half-unit (bit 4) forms give the same y, route outputs, intermediate rows and recv stats
+    bit for bit."""
     import hopper_megamoe_basedondeepgemm_amd as dgm
     (t1, t2), _ = mxfp4_weights
     for M in (2, 4):
-        print(f"early vs plain at full size: fmt={fmt} M={M}", flush=True)
+        print(f"kernel forms at full size: fmt={fmt} M={M}", flush=True)
         rng = np.random.default_rng(520 + M)
         x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
         rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
         buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format=fmt)
         outs = []
-        for flags in (8, 0):
+        for flags in (0, 8, 16):
             buf._debug_flags = flags
             dgm.fable_router_quant_topk_frontend(x, rw, buf, force_balanced=True, select_in_mega=True)
             y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
@@ -215,12 +216,13 @@ def test_config2_small_m_early_streaming_matches_plain(mxfp4_weights, fmt):
             dgm.mxfp4_mega_moe_fused(y, t1, t2, buf, cumulative_local_expert_recv_stats=stats)
             torch.cuda.synchronize()
             assert buf.kernel_error() == 0 and buf.host_error() == 0
-            assert dgm.mega.fused_last_form(buf) == (2 if flags else 0)
+            assert dgm.mega.fused_last_form(buf) == {0: 0, 8: 2, 16: 3}[flags]
             n = int(buf.pool_table()[0].sum())
             outs.append((y.view(torch.int16).cpu(), stats.cpu(), buf.combine_partials[:, :M].view(torch.int16).cpu(),
                          buf.l2_acts[:n].view(torch.uint8).cpu(), buf.l2_acts_sf[:n].cpu()))
-        for name, u, v in zip(("y", "stats", "partials", "mid", "mid_sf"), *outs):
-            assert torch.equal(u, v), name
+        for o in outs[1:]:
+            for name, u, v in zip(("y", "stats", "partials", "mid", "mid_sf"), outs[0], o):
+                assert torch.equal(u, v), name
 
 
 def test_config3_qoq_m8_balanced(qoq_weights):
