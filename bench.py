@@ -70,7 +70,9 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
     clock at entry, dispatch table ready, L1 units done, first L1 arrival observed by the L2
     phase, L2 units done, exit; plus the L1 K-loop and epilogue ticks): for each workload the
     launch with the median event time of `reps`, each after a cache eviction, printed as
-    min / p10 / median / p90 / max over the workgroups in us from the earliest entry."""
+    min / p10 / median / p90 / max over the workgroups in us from the earliest entry. The
+    one-launch layer (frontend in the kernel; M=2 and M=8) adds its frontend stamps: router and
+    cast work done, grid-wide arrival passed (its event time covers the whole layer)."""
     flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
     flush_rd = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
     share = tuple(tuple(t[:E // 8] if t is not None else None for t in w) for w in weights)
@@ -78,8 +80,10 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
     bufs = {}
     # (M=2 and config 1 in the kernel's forms, on one buffer: the default, and the opt-in early
     # weight streaming (debug flag bit 3) and, at M=2, tail half units (bit 4))
-    for M, ep, act, flags in ((2, 1, "mxfp8", 0), (2, 1, "mxfp8", 8), (2, 1, "mxfp8", 16), (8, 1, "mxfp8", 0),
-                              (16, 1, "mxfp8", 0), (8, 8, "mxfp4", 0), (8, 8, "mxfp4", 8)):
+    # (one = the one-launch layer: the frontend runs in the fused kernel)
+    for M, ep, act, flags, one in ((2, 1, "mxfp8", 0, False), (2, 1, "mxfp8", 8, False), (2, 1, "mxfp8", 16, False),
+                                   (2, 1, "mxfp8", 0, True), (8, 1, "mxfp8", 0, False), (8, 1, "mxfp8", 0, True),
+                                   (16, 1, "mxfp8", 0, False), (8, 8, "mxfp4", 0, False), (8, 8, "mxfp4", 8, False)):
         w = share if ep > 1 else weights
         buf = bufs.get((M, ep, act))
         if buf is None:
@@ -95,11 +99,16 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
         for _ in range(reps):
             flush.fill_(1)
             flush_rd.sum()
-            dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=True, select_in_mega=True)
+            if not one:
+                dgm.fable_router_quant_topk_frontend(x, router_w, buf, force_balanced=True, select_in_mega=True)
             st.zero_()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            dgm.mxfp4_mega_moe_fused(y, w[0], w[1], buf, phase_stamps=st)
+            if one:
+                dgm.mxfp4_mega_moe_from_bf16(y, x, router_w, w[0], w[1], buf, force_balanced=True, one_launch=True,
+                                             phase_stamps=st)
+            else:
+                dgm.mxfp4_mega_moe_fused(y, w[0], w[1], buf, phase_stamps=st)
             e1.record()
             torch.cuda.synchronize()
             runs.append((e0.elapsed_time(e1) * 1e3, st.clone()))
@@ -110,9 +119,13 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
         t0 = a[:, 0].min()
         n_active = int((buf.pool_table()[0] > 0).sum())
         form = dgm.mega.FUSED_FORMS.get(dgm.mega.fused_last_form(buf), "?")
-        print(f"M={M} ep_share={ep} A-{act.upper()} ({form} form) active experts {n_active}, {G} workgroups, kernel "
+        print(f"M={M} ep_share={ep} A-{act.upper()} ({form} form{', one launch' if one else ''}) active experts "
+              f"{n_active}, {G} workgroups, kernel "
               f"{ev:.1f} us by events; us from the earliest entry (min / p10 / median / p90 / max):")
-        for c, nm in enumerate(names):
+        rows = list(enumerate(names))
+        if one:
+            rows = rows[:1] + [(6, "router+cast"), (7, "grid arrival")] + rows[1:]
+        for c, nm in rows:
             v = a[:, c]
             v = (v[v > 0] - t0) / 100.0 if c == 3 else (v - t0) / 100.0    # (0: never waited)
             if len(v):
@@ -120,7 +133,7 @@ def phase_stamps_report(torch, dgm, weights, router_w, reps=9):
                 print(f"  {nm:15s}" + "".join(f" {x:7.2f}" for x in q))
         k = a[:, 6][a[:, 6] > 0] / 100.0
         e = a[:, 7][a[:, 6] > 0] / 100.0
-        if len(k):
+        if len(k) and not one:
             print(f"  per workgroup with L1 work: L1 K loops {np.median(k):.2f} us (median), "
                   f"L1 epilogues {np.median(e):.2f} us (median)")
         sys.stdout.flush()

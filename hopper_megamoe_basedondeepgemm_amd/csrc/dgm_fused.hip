@@ -662,7 +662,9 @@ DGM_DEV void slab_store(S& s, const SlabRegs<KT, ACT, COHERENT, MIDL>& r) {
 // Phase stamps (the reference's phase_stamps facility): per workgroup, 100 MHz wall clock at
 // [0] entry, [1] dispatch table ready, [2] L1 units done, [3] first L1 arrival observed,
 // [4] L2 units done, [5] exit; [6] wall ticks in L1 K loops (matrix-core ops, including the
-// waits for their weight tiles), [7] wall ticks in L1 epilogues.
+// waits for their weight tiles), [7] wall ticks in L1 epilogues. With the in-kernel frontend,
+// [6] and [7] are instead wall clock at: this workgroup's router and cast work done (its
+// stores issued), and the grid-wide arrival passed.
 DGM_DEV long long wall_clock() { return (long long)__builtin_amdgcn_s_memrealtime(); }
 
 // FEIN: the router, token flags and activation cast run in this launch (p.fe_in); the rows they
@@ -753,6 +755,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       for (int64_t i = (int64_t)cw * 64 + lane; i < (int64_t)p.M * (H / 32) * 8; i += (int64_t)NW * G * 64)
         cast_lane_mx<true>(p.hidden, ACT, i, xq, xsf);
     }
+    if (st && tid == 0) st[6] = wall_clock();
     wait_mem();                  // this wave's stores have completed
     __syncthreads();
     if (tid == 0)
@@ -773,6 +776,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
     }
     __syncthreads();
+    if (st && tid == 0) st[7] = wall_clock();
   }
 
   // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last
@@ -1934,7 +1938,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // ---------------------------------------------------------------- teardown
   // (test hook: a bounded wait on a counter nothing sets, with a zero spin limit)
   if ((p.debug & 1) && blockIdx.x == 0 && tid == 0) spin_until(p.counters + CNT_NEVER, 1, 0, err, p.host_err);
-  if (st && tid == 0) {
+  if (!FEIN && st && tid == 0) {
     st[6] = l1_load_ticks;
     st[7] = l1_sig_ticks;
   }

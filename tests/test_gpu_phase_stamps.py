@@ -59,6 +59,32 @@ def test_phase_stamps_ordered_and_harmless(fmt, M, E):
     assert entry.max() <= ex.min()
 
 
+def test_one_launch_stamps():
+    """The one-launch layer (frontend in the fused kernel) stamps its frontend in [6] (this
+    workgroup's router and cast work done) and [7] (the grid-wide arrival passed): in order
+    with entry and the dispatch, and no workgroup passes the arrival before every workgroup has
+    done its frontend work."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests.test_gpu_l2_halves import _weights
+    M, E = 6, 16
+    t1, t2 = _weights("mxfp8", E, 7501)
+    rng = np.random.default_rng(7500)
+    x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    b = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, TOPK, H, I, act_format="mxfp8")
+    y = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    st = torch.zeros((2048, 8), dtype=torch.int64, device="cuda")
+    dgm.mxfp4_mega_moe_from_bf16(y, x, rw, t1, t2, b, one_launch=True, phase_stamps=st)
+    torch.cuda.synchronize()
+    assert b.kernel_error() == 0 and dgm.mega.fused_last_form(b) == 1
+    G = dgm.mega.fused_workgroups(b)
+    r = st.cpu().numpy()[:G]
+    entry, ready, ex, fe, arr = r[:, 0], r[:, 1], r[:, 5], r[:, 6], r[:, 7]
+    assert ((entry > 0) & (fe >= entry) & (arr >= fe) & (ready >= arr) & (ex >= ready)).all()
+    assert arr.min() >= fe.max()
+
+
 @pytest.mark.parametrize("M,act", [(8, "mxfp8"), (3, "qoq"), (64, "nvfp4")])
 def test_frontend_stamps(M, act):
     """fable_frontend_stamps (deep_gemm/mega/__init__.py:743-756) after a frontend call with
