@@ -51,7 +51,7 @@ def profiled_traffic_bytes():
     return None
 
 
-def profiled_mfma_util(kernel="k_megamoe<24,10,1,false>", workload=("M=8", "A-MXFP8")):
+def profiled_mfma_util(kernel="k_megamoe<24,10,1,0>", workload=("M=8", "A-MXFP8")):
     """Matrix-core busy fraction of the fused kernel at the headline workload, from the committed
     rocprofv3 counter summary (SQ_VALU_MFMA_BUSY_CYCLES over all SIMD cycles), or None."""
     path = os.path.join(HERE, "profiles", "k_megamoe_E384_mfma_valu_counters.txt")

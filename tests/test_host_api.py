@@ -79,7 +79,7 @@ def test_bench_reads_its_committed_profiles():
     assert t is not None and abs(t / 401.1e6 - 1) < 0.02, t
     u = bench.profiled_mfma_util()
     assert u is not None and 0 < u < 0.2, u
-    assert bench.profiled_mfma_util("k_megamoe<24,10,3,false>", ("M=64", "NVFP4")) > u   # (VALU co-bound, busier)
+    assert bench.profiled_mfma_util("k_megamoe<24,10,3,0>", ("M=64", "NVFP4")) > u   # (VALU co-bound, busier)
 
 
 def test_reorder_fp4_nibbles_refuses_rows_of_partial_words():
