@@ -24,7 +24,7 @@ EXPORTS = [
     "dgm_quantize_nvfp4", "dgm_quantize_qoq", "dgm_cast_int8_rows", "dgm_transform_fp4_weights",
     "dgm_fused_buffer_layout", "dgm_router_topk_launch", "dgm_megamoe_fused_launch",
     "dgm_megamoe_split_launch",
-    "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_fused_last_form",
+    "dgm_device_cu_count", "dgm_fused_workgroups", "dgm_fused_last_form", "dgm_abi_struct_sizes",
     "dgm_transform_qoq_weights", "dgm_transform_nvfp4_weights", "dgm_quantize_qoq_int4",
     "dgm_transform_qoq_int4_weights", "dgm_host_device_pointer", "dgm_megamoe_fused_launch_noalloc",
     "dgm_reorder_fp4_nibbles", "dgm_untransform_fp4_weights", "dgm_untransform_nvfp4_weights",
@@ -55,6 +55,9 @@ class BufferLayout(ctypes.Structure):
                 ("x_sf_row_bytes", ctypes.c_int32), ("mid_sf_row_bytes", ctypes.c_int32)]
 
 
+LAUNCH_COOPERATIVE = 1      # DGM_LAUNCH_COOPERATIVE
+
+
 class MoeArgs(ctypes.Structure):
     _fields_ = [("num_tokens", ctypes.c_int32), ("hidden", ctypes.c_int32), ("intermediate", ctypes.c_int32),
                 ("num_experts", ctypes.c_int32), ("expert_begin", ctypes.c_int32),
@@ -70,7 +73,8 @@ class MoeArgs(ctypes.Structure):
                 ("w2_row_scales", ctypes.c_void_p), ("l1_global_scales", ctypes.c_void_p),
                 ("l2_global_scales", ctypes.c_void_p), ("fe_in_mega", ctypes.c_int32),
                 ("hidden_states", ctypes.c_void_p), ("router_weight", ctypes.c_void_p),
-                ("fe_keys", ctypes.c_void_p), ("host_error", ctypes.c_void_p), ("debug_flags", ctypes.c_int32)]
+                ("fe_keys", ctypes.c_void_p), ("host_error", ctypes.c_void_p), ("debug_flags", ctypes.c_int32),
+                ("launch_flags", ctypes.c_int32)]
 
 
 _lib = None
@@ -113,6 +117,7 @@ def load():
         "dgm_device_cu_count": ([], i32),
         "dgm_fused_workgroups": ([i32, i32, i32], i32),
         "dgm_fused_last_form": ([i32, i32, i32], i32),
+        "dgm_abi_struct_sizes": ([ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)], i32),
         "dgm_transform_qoq_weights": ([vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp], i32),
         "dgm_transform_nvfp4_weights": ([vp, vp, i32, i32, i32, i32, i32, vp, vp, vp], i32),
         "dgm_host_device_pointer": ([vp, ctypes.POINTER(vp)], i32),

@@ -1964,7 +1964,7 @@ GridCache& grid_cache() {
 }
 
 template <int KT1, int KT2, int ACT, int FORM>
-int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
+int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream, bool coop) {
   GridCache& gc = grid_cache();
   int& nb = gc.blocks[slot][ACT][FORM];
   if (nb == 0) {
@@ -1978,6 +1978,20 @@ int launch_fused_t(const FusedParams& prm, int slot, hipStream_t stream) {
   }
   gc.last[slot][ACT] = nb;
   gc.form[slot][ACT] = FORM;
+  if (coop) {
+    // (the grid is the device's resident capacity, which a cooperative launch requires)
+    FusedParams arg = prm;
+    void* args[] = {&arg};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_megamoe<KT1, KT2, ACT, FORM>),
+                                                    dim3(nb), dim3(FT), args, 0, stream);
+    if (e != hipSuccess) {
+      char buf[256];
+      snprintf(buf, sizeof(buf), "cooperative launch of the persistent kernel failed: %s", hipGetErrorString(e));
+      dgm_set_error(buf);
+      return (int)e;
+    }
+    return 0;
+  }
   hipLaunchKernelGGL((k_megamoe<KT1, KT2, ACT, FORM>), dim3(nb), dim3(FT), 0, stream, prm);
   return dgm_last_launch_status();
 }
@@ -2003,15 +2017,15 @@ bool use_tail(const FusedParams& prm) {
 }
 
 template <int KT1, int KT2, int ACT>
-int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream) {
+int launch_fused_fe(const FusedParams& prm, int slot, hipStream_t stream, bool coop) {
   if constexpr (ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8) {
-    if (use_early(prm, ACT)) return launch_fused_t<KT1, KT2, ACT, FORM_EARLY>(prm, slot, stream);
+    if (use_early(prm, ACT)) return launch_fused_t<KT1, KT2, ACT, FORM_EARLY>(prm, slot, stream, coop);
     if constexpr (KT1 == 24) {
-      if (use_tail(prm)) return launch_fused_t<KT1, KT2, ACT, FORM_TAIL>(prm, slot, stream);
+      if (use_tail(prm)) return launch_fused_t<KT1, KT2, ACT, FORM_TAIL>(prm, slot, stream, coop);
     }
   }
-  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, FORM_FEIN>(prm, slot, stream)
-                   : launch_fused_t<KT1, KT2, ACT, FORM_PLAIN>(prm, slot, stream);
+  return prm.fe_in ? launch_fused_t<KT1, KT2, ACT, FORM_FEIN>(prm, slot, stream, coop)
+                   : launch_fused_t<KT1, KT2, ACT, FORM_PLAIN>(prm, slot, stream, coop);
 }
 
 }  // namespace
@@ -2029,15 +2043,16 @@ int dgm_fused_form(int hidden, int intermediate, int act_format) {
   return gc.last[slot][act_format] ? gc.form[slot][act_format] : -1;
 }
 
-int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream) {
+int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream,
+                 bool cooperative) {
 #define DGM_FUSED_SHAPE(H_, I_, SLOT)                                                          \
   if (hidden == H_ && intermediate == I_) {                                                    \
     constexpr int KA = H_ / 128, KB = I_ / 128;                                               \
-    return act == DGM_ACT_MXFP4   ? launch_fused_fe<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream) \
-           : act == DGM_ACT_MXFP8 ? launch_fused_fe<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream) \
-           : act == DGM_ACT_QOQ   ? launch_fused_fe<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream)   \
-           : act == DGM_ACT_NVFP4 ? launch_fused_fe<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream) \
-                                  : launch_fused_fe<KA, KB, DGM_ACT_FP8F128>(prm, SLOT, stream); \
+    return act == DGM_ACT_MXFP4   ? launch_fused_fe<KA, KB, DGM_ACT_MXFP4>(prm, SLOT, stream, cooperative) \
+           : act == DGM_ACT_MXFP8 ? launch_fused_fe<KA, KB, DGM_ACT_MXFP8>(prm, SLOT, stream, cooperative) \
+           : act == DGM_ACT_QOQ   ? launch_fused_fe<KA, KB, DGM_ACT_QOQ>(prm, SLOT, stream, cooperative)   \
+           : act == DGM_ACT_NVFP4 ? launch_fused_fe<KA, KB, DGM_ACT_NVFP4>(prm, SLOT, stream, cooperative) \
+                                  : launch_fused_fe<KA, KB, DGM_ACT_FP8F128>(prm, SLOT, stream, cooperative); \
   }
   DGM_FUSED_SHAPE(3072, 1280, 0)
   DGM_FUSED_SHAPE(512, 256, 1)

@@ -83,6 +83,8 @@ struct FusedParams {
                             // bit 4: tail half units
 };
 
-int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream);
+// cooperative: hipLaunchCooperativeKernel (co-residency guaranteed) instead of a plain launch
+int launch_fused(const FusedParams& prm, int hidden, int intermediate, int act, hipStream_t stream,
+                 bool cooperative = false);
 int dgm_fused_grid_blocks(int hidden, int intermediate, int act_format);
 int dgm_fused_form(int hidden, int intermediate, int act_format);

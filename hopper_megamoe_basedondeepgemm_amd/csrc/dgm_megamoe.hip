@@ -610,6 +610,13 @@ const char* dgm_last_error(void) { return g_err; }
 
 int dgm_device_cu_count(void) { return cu_count(); }
 
+int dgm_abi_struct_sizes(size_t* moe_args, size_t* buffer_layout) {
+  DGM_CHECK_ARG(moe_args && buffer_layout, "null pointer");
+  *moe_args = sizeof(DgmMoeArgs);
+  *buffer_layout = sizeof(DgmBufferLayout);
+  return 0;
+}
+
 int dgm_host_device_pointer(const void* host, void** device) {
   DGM_CHECK_ARG(host && device, "null pointer");
   hipError_t e = hipHostGetDevicePointer(device, const_cast<void*>(host), 0);
@@ -956,7 +963,8 @@ int dgm_fused_launch_ws(const DgmMoeArgs* A, int phases, const DgmWorkspace& w, 
     p.stamp_rows = A->phase_stamps && !(A->debug_flags & 2) ? A->phase_stamp_rows : 0;
     p.phases = phases;
     p.debug = (int16_t)(A->debug_flags & 31);
-    return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream);
+    return launch_fused(p, A->hidden, A->intermediate, A->act_format, stream,
+                        (A->launch_flags & DGM_LAUNCH_COOPERATIVE) != 0);
   }
 }
 

@@ -302,7 +302,16 @@ typedef struct DgmMoeArgs {
    * full, runs as half units of 32 features, each 16-row block's K split over two waves).
    * Measured slower than the default form; kept so tests and benchmarks can compare them. */
   int32_t debug_flags;
+  /* DGM_LAUNCH_* flags, 0 = the default plain launch. The persistent kernel's workgroups wait on
+   * each other (bounded), so they must all be resident at once: the plain launch sizes the grid
+   * to what the device keeps resident, which holds when no other work occupies the compute
+   * units. DGM_LAUNCH_COOPERATIVE launches it cooperatively (hipLaunchCooperativeKernel), which
+   * guarantees co-residency for callers that share the GPU with other streams or processes, at
+   * a cost of ~14-19 us per call on MI355X. No counterpart in the reference (a plain launch). */
+  int32_t launch_flags;
 } DgmMoeArgs;
+
+#define DGM_LAUNCH_COOPERATIVE 1
 
 int dgm_megamoe_fused_launch(const DgmMoeArgs* args, hipStream_t stream);
 
@@ -338,6 +347,9 @@ int dgm_host_device_pointer(const void* host, void** device);
  * The lane-layout probes of the tests live in a library of their own (include/dgm_probe.h). */
 int dgm_device_cu_count(void);
 int dgm_fused_workgroups(int hidden, int intermediate, int act_format);
+/* sizeof(DgmMoeArgs) and sizeof(DgmBufferLayout) as this library was built, so a binding can
+ * check its own struct layouts against the library's (no counterpart in the reference). */
+int dgm_abi_struct_sizes(size_t* moe_args, size_t* buffer_layout);
 int dgm_fused_last_form(int hidden, int intermediate, int act_format);
 
 #ifdef __cplusplus

@@ -354,3 +354,33 @@ def test_expired_wait_is_reported(monkeypatch):
     torch.cuda.synchronize()
     assert b.kernel_error() == 0
     np.testing.assert_array_equal(y.float().cpu().numpy(), r["y"])
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8", "qoq", "nvfp4"])
+def test_cooperative_launch_matches_plain(fmt):
+    """The opt-in cooperative launch of the persistent kernel (``buffer.cooperative`` /
+    DG_MEGA_COOPERATIVE=1: co-residency guaranteed for callers sharing the GPU) gives the plain
+    launch's y and recv stats bit for bit, on the same grid."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests.test_gpu_l2_halves import _weights, _fused
+    M, E, H, I = 12, 16, 512, 256
+    print(f"cooperative vs plain launch fmt={fmt}", flush=True)
+    rng = np.random.default_rng(7600 + len(fmt))
+    t1, t2 = _weights(fmt, E, 7601)
+    x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    b = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, 4, H, I, act_format=fmt)
+    out = []
+    for coop in (False, True):
+        b.cooperative = coop
+        assert dgm.mega.cooperative_launch(b) == coop
+        dgm.fable_router_quant_topk_frontend(x, rw, b, select_in_mega=True)
+        y = torch.full((M, H), 9.0, dtype=torch.bfloat16, device="cuda")
+        stats = torch.zeros(E, dtype=torch.int32, device="cuda")
+        _fused(dgm, fmt, y, t1, t2, b, stats)
+        torch.cuda.synchronize()
+        assert b.kernel_error() == 0 and b.host_error() == 0
+        out.append((y.view(torch.int16).cpu(), stats.cpu(), dgm.mega.fused_workgroups(b)))
+    (y0, s0, g0), (y1, s1, g1) = out
+    assert torch.equal(y0, y1) and torch.equal(s0, s1) and g0 == g1 > 0

@@ -32,6 +32,16 @@ def test_library_exports_every_declared_symbol():
     assert not any(n.startswith("dgm_probe") for n in declared_symbols("dgm_megamoe.h"))
 
 
+def test_struct_layouts_match_the_library():
+    """The ctypes mirrors of DgmMoeArgs and DgmBufferLayout have the sizes the library was built
+    with (a field added on one side only would shift every later field)."""
+    from hopper_megamoe_basedondeepgemm_amd import _lib
+    a, b = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert _lib.load().dgm_abi_struct_sizes(ctypes.byref(a), ctypes.byref(b)) == 0
+    assert a.value == ctypes.sizeof(_lib.MoeArgs) and b.value == ctypes.sizeof(_lib.BufferLayout)
+    assert _lib.MoeArgs.launch_flags.offset + 4 <= a.value
+
+
 def test_host_checks_and_layout():
     from hopper_megamoe_basedondeepgemm_amd import _lib
     lib = _lib.load()
