@@ -1950,7 +1950,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   if (st && tid == 0) st[5] = wall_clock();
 }
 
-// per device, per (shape slot, format, form: plain / FEIN / EARLY): the resident grid; per
+// per device, per (shape slot, format, form: plain / FEIN / EARLY / TAIL): the resident grid; per
 // (shape slot, format): the last launch's grid and form (the grid is what the device keeps
 // resident at once, so it depends on the device's CU count)
 constexpr int GRID_DEVICES = 64;
