@@ -75,7 +75,7 @@ def run_nvfp4(M, E, E_local, expert_begin, H, I, topk, seed, force_balanced=Fals
     codes, sfb, x_dq = moe.quant_act(x, "nvfp4")
     ref, _ = moe.moe_forward(x_dq, idx, w, W1, W2, expert_begin, "nvfp4", gs1=gs1, gs2=gs2)
     return dict(buf=buf, y=y.float().cpu().numpy(), ref=ref, idx=idx, codes=codes, sfb=sfb,
-                stats=stats.cpu().numpy(), E_local=E_local, expert_begin=expert_begin)
+                stats=stats.cpu().numpy(), E_local=E_local, expert_begin=expert_begin, t=(t1, t2), gs=(gs1, gs2))
 
 
 def check_frontend(r, M):

@@ -54,3 +54,42 @@ def test_random_shape(case):
     torch.cuda.synchronize()
     assert r["buf"].kernel_error() == 0
     np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
+
+
+@pytest.mark.parametrize("case", _cases(12, seed=2027), ids=lambda c: f"case{c[0]}")
+def test_random_shape_qoq(case):
+    """QoQ W4A8: the same random shapes (the format column ignored): frontend codes and scales,
+    pool and stats bit-exact, intermediate codes against the exact-integer L1 restatement,
+    y within tolerance."""
+    need_gpu()
+    from tests import test_gpu_qoq as tq
+    i, M, E, e_local, begin, H, I, topk, _, balanced, zero_rows, select = case
+    r = tq.run_qoq(M, E, e_local, begin, H, I, topk, seed=9300 + i, force_balanced=balanced, zero_rows=zero_rows,
+                   select_in_mega=select)
+    tq.check_frontend(r, M)
+    tq.check_mid(r)
+    tq.check_y(r, zero_rows=zero_rows)
+
+
+@pytest.mark.parametrize("case", _cases(12, seed=2028), ids=lambda c: f"case{c[0]}")
+def test_random_shape_nvfp4(case):
+    """NVFP4 W4A4 (per-expert global scales on odd cases): frontend codes and scales, pool and
+    stats bit-exact, y within tolerance; the split family (two launches) gives the fused
+    launch's y bit for bit."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests import test_gpu_nvfp4 as tn
+    i, M, E, e_local, begin, H, I, topk, _, balanced, zero_rows, select = case
+    r = tn.run_nvfp4(M, E, e_local, begin, H, I, topk, seed=9500 + i, force_balanced=balanced, zero_rows=zero_rows,
+                     select_in_mega=select, global_scales=bool(i % 2))
+    tn.check_frontend(r, M)
+    tn.check_pool(r)
+    tn.check_y(r, zero_rows=zero_rows)
+    (t1, t2), (gs1, gs2) = r["t"], r["gs"]
+    gs = {} if gs1 is None else dict(l1_global_scales=torch.from_numpy(gs1).cuda(),
+                                     l2_global_scales=torch.from_numpy(gs2).cuda())
+    y2 = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    dgm.nvfp4_mega_moe(y2, t1, t2, r["buf"], activation_clamp=10.0, kernel_family="split", **gs)
+    torch.cuda.synchronize()
+    assert r["buf"].kernel_error() == 0
+    np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
