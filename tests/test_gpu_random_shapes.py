@@ -93,3 +93,97 @@ def test_random_shape_nvfp4(case):
     torch.cuda.synchronize()
     assert r["buf"].kernel_error() == 0
     np.testing.assert_array_equal(y2.float().cpu().numpy(), r["y"])
+
+
+@pytest.mark.parametrize("case", _cases(16, seed=2029), ids=lambda c: f"case{c[0]}")
+def test_random_shape_one_launch(case):
+    """The one-launch layer (router, zero-row flags and cast in the fused kernel) against the
+    two launches on the same inputs, every activation format in turn: frontend outputs, pool
+    table and y bit for bit."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests.gpu_common import bf16_cpu, randn_bf16
+    from tests.test_gpu_one_launch import weights_for, layer_two_launch, snapshot
+    i, M, E, e_local, begin, H, I, topk, _, balanced, zero_rows, _ = case
+    fmt = ["mxfp8", "mxfp4", "qoq", "nvfp4"][i % 4]
+    print(f"one-launch random shape {i}: {fmt} M={M} E={E} local={e_local}@{begin} H={H} I={I} topk={topk} "
+          f"balanced={balanced} zero_rows={zero_rows}", flush=True)
+    rng = np.random.default_rng(9700 + i)
+    x = randn_bf16(rng, (M, H))
+    for r in zero_rows:
+        x[r] = 0.0
+    rw = randn_bf16(rng, (E, H), 0.02)
+    xs, rws = bf16_cpu(x).cuda(), bf16_cpu(rw).cuda()
+    t1, t2 = weights_for(fmt, e_local, H, I, 9701 + i)
+    bufs = [dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format=fmt, ep_size=E // e_local,
+                                                   ep_rank=begin // e_local) for _ in range(2)]
+    y2 = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+    layer_two_launch(dgm, fmt, y2, xs, rws, t1, t2, bufs[0], balanced)
+    y1 = torch.full((M, H), 7.0, dtype=torch.bfloat16, device="cuda")
+    dgm.mxfp4_mega_moe_from_bf16(y1, xs, rws, t1, t2, bufs[1], activation_clamp=10.0, force_balanced=balanced,
+                                 one_launch=True)
+    torch.cuda.synchronize()
+    assert bufs[0].kernel_error() == 0 and bufs[1].kernel_error() == 0
+    ref, got = snapshot(bufs[0], M), snapshot(bufs[1], M)
+    for k in ref:
+        a, r = got[k].cpu(), ref[k].cpu()
+        if a.dtype == torch.float32:
+            a, r = a.view(torch.int32), r.view(torch.int32)
+        assert torch.equal(a, r), k
+    for a, r in zip(bufs[1].pool_table(), bufs[0].pool_table()):
+        assert torch.equal(a, r)
+    assert torch.equal(y1.view(torch.int16).cpu(), y2.view(torch.int16).cpu())
+
+
+def _form_cases(n=8, seed=2030):
+    """Shapes where the opt-in forms apply: H = 3072, I = 1280, at most 32 routes."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        ep = [1, 2, 8][int(rng.integers(3))]
+        e_local = int(rng.integers(4, 25))
+        E = e_local * ep
+        topk = int(rng.integers(1, min(8, E) + 1))
+        M = int(rng.integers(1, 32 // topk + 1))
+        out.append((i, M, E, e_local, int(rng.integers(ep)) * e_local, topk, ["mxfp4", "mxfp8"][i % 2]))
+    return out
+
+
+@pytest.mark.parametrize("case", _form_cases(), ids=lambda c: f"case{c[0]}")
+def test_random_shape_opt_in_forms(case):
+    """The opt-in kernel forms (early weight streaming, debug bit 3; tail half units, bit 4)
+    against the default form on random small routed sets at H = 3072: y, recv stats and the
+    intermediate rows bit for bit, and each form reported as the one that ran when its rule
+    applies."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests.gpu_common import bf16_cpu, randn_bf16
+    i, M, E, e_local, begin, topk, fmt = case
+    H, I = 3072, 1280
+    print(f"forms random shape {i}: {fmt} M={M} E={E} local={e_local}@{begin} topk={topk}", flush=True)
+    rng = np.random.default_rng(9900 + i)
+    x = bf16_cpu(randn_bf16(rng, (M, H))).cuda()
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    (t1, t2), _, _ = make_weights(e_local, H, I, 9901 + i)
+    outs = {}
+    for flags in (0, 8, 16):
+        b = dgm.get_fused_symm_buffer_for_mega_moe(None, E, M, topk, H, I, act_format=fmt, ep_size=E // e_local,
+                                                   ep_rank=begin // e_local)
+        b._debug_flags = flags
+        dgm.fable_router_quant_topk_frontend(x, rw, b)
+        y = torch.full((M, H), 5.0, dtype=torch.bfloat16, device="cuda")
+        stats = torch.zeros(e_local, dtype=torch.int32, device="cuda")
+        dgm.mxfp4_mega_moe_fused(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0)
+        torch.cuda.synchronize()
+        assert b.kernel_error() == 0 and b.host_error() == 0
+        n = int(b.pool_table()[0].sum())
+        outs[flags] = (dgm.mega.fused_last_form(b), y.view(torch.int16).cpu(), stats.cpu(),
+                       b.l2_acts[:n].view(torch.uint8).cpu().clone(), b.l2_acts_sf[:n].view(torch.uint8).cpu().clone())
+    R = M * topk
+    assert outs[0][0] == 0
+    if R <= 64 and R * e_local <= 32 * E:
+        assert outs[8][0] == 2
+    assert outs[16][0] == 3
+    for flags in (8, 16):
+        for a, r in zip(outs[flags][1:], outs[0][1:]):
+            assert torch.equal(a, r), flags
