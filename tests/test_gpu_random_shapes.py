@@ -187,3 +187,66 @@ def test_random_shape_opt_in_forms(case):
     for flags in (8, 16):
         for a, r in zip(outs[flags][1:], outs[0][1:]):
             assert torch.equal(a, r), flags
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4", "mxfp8", "qoq", "nvfp4"])
+def test_random_call_sequence(fmt):
+    """One buffer through 30 calls of random token count (zero rows included) and random launch
+    form: the fused launch with the top-k from the frontend or selected in its prologue, the
+    split launches, the one-launch layer, and (A-MXFP) the early-streaming form and a
+    cooperative launch. Every call equals a fresh buffer's fused launch bit for bit (y and the
+    accumulated recv stats), with no device error: the buffer's two counter sets stay
+    consistent whatever the sequence."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from tests.gpu_common import bf16_cpu, randn_bf16
+    from tests.test_gpu_one_launch import weights_for
+    E, H, I, topk, maxm = 24, 512, 256, 4, 24
+    rng = np.random.default_rng(4300 + len(fmt))
+    t1, t2 = weights_for(fmt, E, H, I, 4301)
+    rw = bf16_cpu(randn_bf16(rng, (E, H), 0.02)).cuda()
+    fused = {"qoq": dgm.qoq_mega_moe_fused, "nvfp4": dgm.fp4_fp4_mega_moe}.get(fmt, dgm.mxfp4_mega_moe_fused)
+
+    def split(y, b, stats):
+        if fmt == "qoq":
+            dgm.qoq_mega_moe_split(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0)
+        elif fmt == "nvfp4":
+            dgm.nvfp4_mega_moe(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0,
+                               kernel_family="split")
+        else:
+            dgm.mxfp4_mega_moe_split(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0)
+
+    def run(mode, y, x, b, stats):
+        b._debug_flags = 8 if mode == "early" else 0
+        b.cooperative = mode == "coop"
+        if mode == "one":
+            dgm.mxfp4_mega_moe_from_bf16(y, x, rw, t1, t2, b, cumulative_local_expert_recv_stats=stats,
+                                         activation_clamp=10.0, one_launch=True)
+        elif mode == "split":
+            dgm.fable_router_quant_topk_frontend(x, rw, b)
+            split(y, b, stats)
+        else:
+            dgm.fable_router_quant_topk_frontend(x, rw, b, select_in_mega=(mode == "select"))
+            fused(y, t1, t2, b, cumulative_local_expert_recv_stats=stats, activation_clamp=10.0)
+
+    modes = ["fused", "select", "split", "one"] + (["early", "coop"] if fmt in ("mxfp4", "mxfp8") else [])
+    shared = dgm.get_fused_symm_buffer_for_mega_moe(None, E, maxm, topk, H, I, act_format=fmt)
+    stats = torch.zeros(E, dtype=torch.int32, device="cuda")
+    want = torch.zeros(E, dtype=torch.int32, device="cuda")
+    for i in range(30):
+        M = int(rng.integers(1, maxm + 1))
+        mode = modes[int(rng.integers(len(modes)))]
+        print(f"sequence {fmt} call {i}: M={M} mode={mode}", flush=True)
+        xh = randn_bf16(rng, (M, H))
+        if M > 3 and rng.random() < 0.5:
+            xh[int(rng.integers(M))] = 0.0
+        x = bf16_cpu(xh).cuda()
+        fresh = dgm.get_fused_symm_buffer_for_mega_moe(None, E, maxm, topk, H, I, act_format=fmt)
+        y_ref = torch.empty((M, H), dtype=torch.bfloat16, device="cuda")
+        run("fused", y_ref, x, fresh, want)
+        y = torch.full((M, H), 7.0, dtype=torch.bfloat16, device="cuda")
+        run(mode, y, x, shared, stats)
+        torch.cuda.synchronize()
+        assert fresh.kernel_error() == 0 and shared.kernel_error() == 0 and shared.host_error() == 0, (i, M, mode)
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), (i, M, mode)
+        assert torch.equal(stats, want), (i, M, mode)
