@@ -709,14 +709,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   // this launch's counter set (the other one is cleared after the dispatch); each workgroup
   // counts itself once it has read the parity: the one that counts last hands the next launch
   // the other set at its end (its count is read only then, long after it has returned)
-  // (EARLY: counted behind the early requests, which then do not wait for it)
+  // (EARLY: counted behind the early requests, which then do not wait for it; FEIN: after the
+  // grid-wide arrival, so that wave 0's router work does not wait for the parity's round trip)
   const int parity = __hip_atomic_load(p.counters + CNT_PARITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1;
   int* const cset = p.counters + CNT_SET0 + parity * CNT_SET;
   int started = 0;
   auto count_start = [&]() __attribute__((always_inline)) {
     if (tid == 0) started = __hip_atomic_fetch_add(cset + CNT_STARTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  if constexpr (!EARLY) count_start();
+  if constexpr (!EARLY && !FEIN) count_start();
   int* err = p.counters + CNT_ERROR;
   int* l1_done = cset + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
   int* comb = cset + CNT_COMB;        // pair i: comb[i * CNT_LINE]
@@ -777,6 +778,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
     __syncthreads();
     if (st && tid == 0) st[7] = wall_clock();
+    count_start();
   }
 
   // The tile ring (and the NVFP4 scale ring), shared by the two phases: the L1 phase's last

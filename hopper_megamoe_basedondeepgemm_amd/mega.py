@@ -865,7 +865,7 @@ def mxfp4_mega_moe_from_bf16(y, hidden_states, router_weight, l1, l2, b,
     ``one_launch`` (env DG_ONE_LAUNCH=1; up to 64 tokens): a single launch instead, in which the
     fused kernel computes the router logits, zero-row flags and activation cast itself (spread
     over all workgroups) and meets at a grid-wide arrival counter before its prologue; same
-    results bit for bit, 2-4 us slower than the two launches on MI355X (the grid-wide arrival
+    results bit for bit, 1.5-4.3 us slower than the two launches on MI355X (the grid-wide arrival
     and the key reload after it cost more than the second launch does)."""
     # (a qoq buffer runs the QoQ layer: the reference's DG_W4A8_INT=1 route; an nvfp4 buffer the
     # W4A4 NVFP4 layer)
