@@ -146,7 +146,8 @@ def probes_report(torch, reps=15):
       * HBM read probe: the fused kernel's streaming pattern (runs of 24 consecutive 1 KB tiles per
         wave, a ring of non-temporal loads, 256 workgroups of 8 waves) without its arithmetic, at
         the weight bytes of config 1 (50 MB) and of the headline (401 MB), ring depths 4 / 12 / 24;
-      * the launch floor: an empty kernel of 256 x 512 and 1 x 64 threads."""
+      * the launch floor: an empty kernel of 256 x 512 and 1 x 64 threads;
+      * the per-workgroup rate of the same pattern on 32 to 256 workgroups, ring depths 4 / 12 / 24."""
     from hopper_megamoe_basedondeepgemm_amd import _lib
     lib = _lib.load_probe()
     flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
@@ -178,9 +179,24 @@ def probes_report(torch, reps=15):
             print(f"  {nbytes / 1e6:7.1f} MB  ring {depth:2d}: {med:7.2f} us ({mn:7.2f} min) = "
                   f"{nbytes / (med * 1e-6) / 1e12:5.2f} TB/s")
     print("empty kernel (returns at entry), median / min of %d after a 1 GiB eviction:" % reps)
+    floor = None
     for blocks, threads in ((256, 512), (1, 64)):
         med, mn = timed(lambda: _lib.check(lib.dgm_probe_empty_launch(blocks, threads, _lib.stream())))
+        floor = med if floor is None else floor
         print(f"  {blocks:4d} x {threads:3d} threads: {med:6.2f} us ({mn:6.2f} min) by events")
+    # the same pattern on fewer workgroups (the small shapes and the tail of every shape, where
+    # the HBM is not saturated): each wave streams 4 runs (768 KB per workgroup); per-workgroup
+    # rate over the event time minus the empty kernel's
+    print("HBM read probe on fewer workgroups (4 runs of 24 x 1 KB per wave, 768 KB per workgroup), "
+          "median of %d; GB/s per workgroup over (time - empty kernel):" % reps)
+    for blocks in (32, 64, 128, 160, 256):
+        nbytes = blocks * 8 * 4 * 24 * 1024
+        row = []
+        for depth in (4, 12, 24):
+            med, _ = timed(lambda: _lib.check(lib.dgm_probe_stream_read(_lib.ptr(src), nbytes, depth, blocks,
+                                                                         _lib.ptr(sink), _lib.stream())))
+            row.append(f"ring {depth:2d} {med:6.2f} us {nbytes / blocks / ((med - floor) * 1e-6) / 1e9:5.1f}")
+        print(f"  {blocks:3d} workgroups ({nbytes / 1e6:6.1f} MB): " + " | ".join(row))
     sys.stdout.flush()
 
 
