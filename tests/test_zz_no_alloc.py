@@ -3,8 +3,9 @@ workspace in a file-scope device array instead of the caller's buffer) against t
 point dgm_megamoe_fused_launch on the same inputs, both through the C ABI: y, top-k, top-k
 weights and recv stats bit for bit, on two calls in a row (the second with fewer tokens), for the
 in-prologue selection (<= 8 tokens) and the selection launch (> 8 tokens), at the array's route
-limit (512) for MXFP8 and NVFP4; and its size limit, which is refused on the host with a clear
-message."""
+limit (512) for MXFP8 and NVFP4, and on eight seeded random shapes (every format, each of the
+kernel's three (H, I), EP shares, top-1 to top-16); and its size limit, which is refused on the
+host with a clear message."""
 import ctypes
 
 import numpy as np
@@ -89,3 +90,53 @@ def test_noalloc_size_limit():
     st = _launch("dgm_megamoe_fused_launch_noalloc", args)
     assert st == -1
     assert b"num_tokens * topk must be <= 512" in _lib.load().dgm_last_error()
+
+
+def _random_noalloc_cases(n=8, seed=2031):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        H_, I_ = [(512, 256), (1024, 512), (3072, 1280)][int(rng.integers(3))]
+        fmt = ["mxfp4", "mxfp8", "qoq", "nvfp4"][i % 4]
+        ep = [1, 2, 4][int(rng.integers(3))]
+        e_local = int(rng.integers(2, 33))
+        topk = int(rng.integers(1, min(16, e_local * ep) + 1))
+        sizes = tuple(int(v) for v in rng.integers(1, 512 // topk + 1, 2))
+        out.append((i, H_, I_, fmt, e_local * ep, ep, topk, sizes))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_noalloc_cases(), ids=lambda c: f"case{c[0]}")
+def test_noalloc_random_shapes(case):
+    """Seeded random shapes on both entry points (each of the kernel's three shapes, every
+    format, EP shares, top-1 to top-16, up to the array's 512 routes), two calls each: y,
+    top-k and stats bit for bit."""
+    need_gpu()
+    import hopper_megamoe_basedondeepgemm_amd as dgm
+    from hopper_megamoe_basedondeepgemm_amd import _lib, mega
+    from tests.test_gpu_one_launch import weights_for
+    i, H_, I_, fmt, E, ep, topk, sizes = case
+    e_local = E // ep
+    t1, t2 = weights_for(fmt, e_local, H_, I_, 1400 + i)
+    buf = dgm.get_fused_symm_buffer_for_mega_moe(None, E, max(sizes), topk, H_, I_, act_format=fmt, ep_size=ep,
+                                                 ep_rank=(i % ep))
+    rng = np.random.default_rng(1410 + i)
+    rw = bf16_cpu(randn_bf16(rng, (E, H_), 0.02)).cuda()
+    for M in sizes:
+        print(f"no-alloc random {i}: {fmt} H={H_} I={I_} M={M} E={E} local={e_local}@rank{i % ep} topk={topk}",
+              flush=True)
+        x = bf16_cpu(randn_bf16(rng, (M, H_))).cuda()
+        dgm.fable_router_quant_topk_frontend(x, rw, buf, select_in_mega=bool(i % 2))
+        out = {}
+        for entry in ("dgm_megamoe_fused_launch", "dgm_megamoe_fused_launch_noalloc"):
+            y = torch.full((M, H_), 3.0, dtype=torch.bfloat16, device="cuda")
+            stats = torch.zeros(e_local, dtype=torch.int32, device="cuda")
+            args = mega._moe_args(y, t1, t2, buf, stats, 10.0, fmt=fmt)
+            _lib.check(_launch(entry, args))
+            torch.cuda.synchronize()
+            assert buf.host_error() == 0 and buf.kernel_error() == 0
+            out[entry] = (y.view(torch.int16).cpu(), stats.cpu(), buf.topk_idx[:M].cpu().clone(),
+                          buf.topk_weights[:M].cpu().clone().view(torch.int32))
+        a, b = out.values()
+        for u, v in zip(a, b):
+            assert torch.equal(u, v)
