@@ -708,19 +708,29 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   const int R = p.M * p.topk;
   // this launch's counter set (the other one is cleared after the dispatch); each workgroup
   // counts itself once it has read the parity: the one that counts last hands the next launch
-  // the other set at its end (its count is read only then, long after it has returned)
-  // (EARLY: counted behind the early requests, which then do not wait for it; FEIN: after the
-  // grid-wide arrival, so that wave 0's router work does not wait for the parity's round trip)
-  const int parity = __hip_atomic_load(p.counters + CNT_PARITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1;
-  int* const cset = p.counters + CNT_SET0 + parity * CNT_SET;
+  // the other set at its end (its count is read only then, long after it has returned).
+  // The parity is requested here and taken into a scalar only where it is first needed: after
+  // the routing loads (keys or top-k), or (FEIN) at the grid-wide arrival. Taken at once, its
+  // round trip came before every later request of the prologue (the scalar copy and the
+  // addresses derived from it were hoisted to the load); now the two round trips overlap.
+  // (EARLY: counted behind the early requests, which then do not wait for it.)
+  int parity_v = __hip_atomic_load(p.counters + CNT_PARITY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int parity = 0;
+  int* cset = nullptr;
+  int* l1_done = nullptr;      // expert slot a: l1_done[a * CNT_LINE]
+  int* comb = nullptr;         // pair i: comb[i * CNT_LINE]
+  auto take_parity = [&]() __attribute__((always_inline)) {
+    asm volatile("" : "+v"(parity_v));    // (the wait for the load is placed here)
+    parity = __builtin_amdgcn_readfirstlane(parity_v) & 1;
+    cset = p.counters + CNT_SET0 + parity * CNT_SET;
+    l1_done = cset + CNT_L1;
+    comb = cset + CNT_COMB;
+  };
   int started = 0;
   auto count_start = [&]() __attribute__((always_inline)) {
     if (tid == 0) started = __hip_atomic_fetch_add(cset + CNT_STARTED, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
-  if constexpr (!EARLY && !FEIN) count_start();
   int* err = p.counters + CNT_ERROR;
-  int* l1_done = cset + CNT_L1;      // expert slot a: l1_done[a * CNT_LINE]
-  int* comb = cset + CNT_COMB;        // pair i: comb[i * CNT_LINE]
   long long* st = (p.stamps && (int)blockIdx.x < p.stamp_rows) ? p.stamps + (size_t)blockIdx.x * 8 : nullptr;
   long long wait_ticks = 0, l1_load_ticks = 0, l1_sig_ticks = 0;
   if (st && tid == 0) st[0] = wall_clock();
@@ -758,6 +768,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
     if (st && tid == 0) st[6] = wall_clock();
     wait_mem();                  // this wave's stores have completed
+    take_parity();
     __syncthreads();
     if (tid == 0)
       __hip_atomic_fetch_add(cset + CNT_GRID + ((int)blockIdx.x % GRID_SLOTS) * GRID_STRIDE, 1,
@@ -887,6 +898,8 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     }
   }
   for (int e = tid; e < p.E_local; e += FT) s.cnt[e] = 0;   // (shares LDS with the key staging)
+  if constexpr (!FEIN) take_parity();      // (the routing loads above have returned)
+  if constexpr (!EARLY && !FEIN) count_start();
   if constexpr (ACT == DGM_ACT_NVFP4) {
     for (int e = tid; e < p.E_local; e += FT) {
       s.gsl[0][e] = p.gs1 ? p.gs1[e] : 1.f;
