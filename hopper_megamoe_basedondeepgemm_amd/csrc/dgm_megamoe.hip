@@ -88,6 +88,11 @@ __global__ void __launch_bounds__(256) k_frontend(const uint16_t* __restrict__ x
                                                   long long* __restrict__ stamps, int stamp_rows) {
   constexpr int H = J * 512, RTOK = RT > 0 ? RT : 4;
   __shared__ uint4 xs[RT > 0 ? RT * J * 64 : 1];
+  // every argument (and the grid size) requested at entry behind one wait: left to the compiler,
+  // the loads came in four dependent rounds, two of them misses on the two argument lines
+  // (0.16-0.36 us of this kernel at 2-8 tokens)
+  asm volatile("" ::"s"(x), "s"(w), "s"(M), "s"(E), "s"(act_format), "s"(logits), "s"(keys), "s"(zero_unrouted),
+               "s"(q), "s"(sf), "s"(router), "s"(stamps), "s"(stamp_rows), "s"(gridDim.x), "s"(gridDim.y));
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ry = router ? (M + RTOK - 1) / RTOK : 0;
   const int brow = (int)(blockIdx.y * gridDim.x + blockIdx.x);
