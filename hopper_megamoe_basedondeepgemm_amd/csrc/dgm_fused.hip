@@ -459,6 +459,12 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT, MIDL>& r, const uint8_t* __re
                        int row_bytes, int n, RowOf row_of, WeightOf weight_of) {
   const int tid = threadIdx.x;
   uint32_t ok = 0;
+  // MASK: only the lanes whose column holds a real row load (the slab store zeroes the others):
+  // with one route per expert, 15 of 16 columns are empty, and their loads (of row 0) kept the
+  // memory pipeline busy for ~0.7 us at each workgroup's first slab (A-MXFP, FP8F128: 0.4-1.7
+  // us per layer call). QoQ and NVFP4 keep the unconditional loads: with the branches their
+  // kernels spill more registers (5 and 9 values) and measured slower.
+  constexpr bool MASK = ACT == DGM_ACT_MXFP4 || ACT == DGM_ACT_MXFP8 || ACT == DGM_ACT_FP8F128;
 #pragma unroll
   for (int j = 0; j < SlabRegs<KT, ACT, COHERENT, MIDL>::FR; ++j) {
     const int f = tid + j * FT;
@@ -473,15 +479,21 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT, MIDL>& r, const uint8_t* __re
     const uint8_t* q = FP4 ? src + rr * row_bytes + kt * 64 + (l >> 4) * 16
                            : src + rr * row_bytes + kt * 128 + (l >> 4) * 16;
     if (COHERENT) {
-      r.h[j][0] = ld_agent64(q);
-      r.h[j][1] = ld_agent64(q + 8);
-      if (!FP4) {
-        r.h[j][2] = ld_agent64(q + 64);
-        r.h[j][3] = ld_agent64(q + 72);
+      r.h[j][0] = r.h[j][1] = r.h[j][2] = r.h[j][3] = 0;
+      if (!MASK || have) {
+        r.h[j][0] = ld_agent64(q);
+        r.h[j][1] = ld_agent64(q + 8);
+        if (!FP4) {
+          r.h[j][2] = ld_agent64(q + 64);
+          r.h[j][3] = ld_agent64(q + 72);
+        }
       }
     } else {
-      r.v0[j] = *reinterpret_cast<const v4u*>(q);
-      if (!FP4) r.v1[j] = *reinterpret_cast<const v4u*>(q + 64);
+      r.v0[j] = r.v1[j] = v4u{0u, 0u, 0u, 0u};
+      if (!MASK || have) {
+        r.v0[j] = *reinterpret_cast<const v4u*>(q);
+        if (!FP4) r.v1[j] = *reinterpret_cast<const v4u*>(q + 64);
+      }
     }
     if constexpr (ACT == DGM_ACT_NVFP4) {
       // the two E4M3 scales of the fragment (16-blocks 8 kt + 2 g, +1; row pitch KT * 8 bytes),
@@ -525,7 +537,8 @@ DGM_DEV void slab_load(SlabRegs<KT, ACT, COHERENT, MIDL>& r, const uint8_t* __re
       const bool hb = have && kt < KT;
       ok |= hb ? 1u << (8 + j) : 0u;
       const uint32_t* q = reinterpret_cast<const uint32_t*>(ssrc + (hb ? rr * (KT * 4) + kt * 4 : 0));
-      r.sb[j] = COHERENT ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *q;
+      r.sb[j] = 0u;
+      if (!MASK || hb) r.sb[j] = COHERENT ? __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *q;
     }
   }
   r.ok = ok;
