@@ -178,6 +178,9 @@ struct FusedSmem {
   float route_w[FUSED_MAX_ROUTES];     // routing weight of each route
   int routes[FUSED_MAX_ROUTES];
   int prow[FUSED_MAX_ROUTES];          // per pool row: its route's row in `partials` (slot * part_rows + token)
+  static constexpr int PT = ACT == DGM_ACT_NVFP4 ? 1 : FUSED_MAX_ROUTES;
+  int ptok[PT];                        // per pool row: its token (not NVFP4)
+  float pw[PT];                        // per pool row: its routing weight (not NVFP4)
   int ytok[FUSED_MAX_ROUTES];          // per pool row: its token when that token has no other local
                                        // route (the L2 unit writes y itself), else -1
   int act[FUSED_MAX_LOCAL];
@@ -986,6 +989,10 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
   for (int q = tid; q < s.meta[1]; q += FT) {
     const int r = s.routes[q], t = r / p.topk;
     s.prow[q] = (r - t * p.topk) * p.part_rows + t;
+    if constexpr (ACT != DGM_ACT_NVFP4) {
+      s.ptok[q] = t;
+      s.pw[q] = s.route_w[r];
+    }
     // (NVFP4: always through the combine; its kernel has no registers to spare for the y store)
     s.ytok[q] = ACT != DGM_ACT_NVFP4 && s.nslot[t] == 1 ? t : -1;
   }
@@ -1113,11 +1120,22 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
     const uint8_t* xv = p.x;
     const uint8_t* xs = p.xsf;
     // (agent-scope loads when this launch's in-kernel frontend wrote the rows)
+    // A slab column's token and weight come from the pool-row tables the dispatch filled: one
+    // LDS read each, where route -> token / top-k and route -> weight were a dependent read and
+    // an integer division on the first slab's path (0.5-1.7 us per layer call). NVFP4 keeps the
+    // route-table reads: with the tables its kernel spills more registers.
     auto load_slab = [xv, xs, topk](SlabRegs<KT1, ACT, FEIN, false>& r, int a, int s0) __attribute__((always_inline)) {
-      const int* rts = s.routes + s.aoff[a] + s0;
-      slab_load<KT1, ACT, FEIN, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
-                                 [rts, topk](int cc) { return rts[cc] / topk; },
-                                 [rts](int cc) { return s.route_w[rts[cc]]; });
+      if constexpr (ACT == DGM_ACT_NVFP4) {
+        const int* rts = s.routes + s.aoff[a] + s0;
+        slab_load<KT1, ACT, FEIN, false>(r, xv, xs, XB, s.aoff[a + 1] - s.aoff[a] - s0,
+                                         [rts, topk](int cc) { return rts[cc] / topk; },
+                                         [rts](int cc) { return s.route_w[rts[cc]]; });
+      } else {
+        const int q0r = s.aoff[a] + s0;
+        slab_load<KT1, ACT, FEIN, false>(r, xv, xs, XB, s.aoff[a + 1] - q0r,
+                                         [q0r](int cc) { return s.ptok[q0r + cc]; },
+                                         [q0r](int cc) { return s.pw[q0r + cc]; });
+      }
     };
     // Workgroup g starts with units g and G + g (every workgroup starts at once: claims on
     // one counter would serialize them); later units are claimed one at a time from a counter
