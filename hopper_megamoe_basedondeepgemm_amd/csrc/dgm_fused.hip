@@ -1230,9 +1230,17 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
       }
       const float wt_r = s.slab_w[c];
       const float sx = ACT == DGM_ACT_QOQ ? s.xsc[c] : 1.f;       // QoQ: the token's activation scale
-      // the unit after q1, claimed at the start of the item that finishes q0 (after its loads;
-      // the value is read in this item's epilogue, by when it has returned)
-      if (tid == 0 && last_slab && q1 < UI && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the unit after q1, claimed during the item that finishes q0 (after its loads; the value
+      // is read in this item's epilogue, by when it has returned). A-MXFP8 and NVFP4 claim in
+      // the K loop, at tile CT (where the refills turn to the next item: the workgroup commits
+      // to the unit half an item later, and those kernels' registers come out no worse); the
+      // others at the loop's start (A-MXFP4, QoQ, FP8F128: mid-loop claims measured no faster or
+      // spilled registers).
+      auto claim_ahead = [&]() __attribute__((always_inline)) {
+        if (tid == 0 && last_slab && q1 < UI && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      };
+      constexpr int CT = !TAIL && (ACT == DGM_ACT_MXFP8 || ACT == DGM_ACT_NVFP4) ? KT1 - KR : -1;
+      if constexpr (CT < 0) claim_ahead();
       const long long t_k0 = st ? wall_clock() : 0;
       // ---- K loop over the ring
       v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -1258,6 +1266,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         };
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           v8i bop = bq0;
           bq0 = bq1;
           if constexpr (t + 2 < KT1) bq1 = bfrag(t + 2);
@@ -1300,6 +1309,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int j = 0; j < 4; ++j) bn[j] = s.bst[0][lane][j];
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           U4 bc[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) bc[j] = bn[j];
@@ -1327,6 +1337,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         v4f prev = {0.f, 0.f, 0.f, 0.f};
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           v8i bop = bq0;
           const uint32_t bsw = bs;
           bq0 = bq1;
@@ -1362,6 +1373,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         const int ro = TAIL && hf ? 0 : KR * 1024;                     // refill offset of K half 0
         static_for<KT1>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           constexpr bool HI = t >= KT1 / 2;
           if (!TAIL || !hf || HI == hi_wave) {
             const v8i bop = bq0;
@@ -1759,9 +1771,15 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int jb = 0; jb < RB; ++jb)
           s1r[jb] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(w2r + (blk_of(q0) + jb) * 16 + 4 * kq));
       }
-      // the unit after q1, claimed at the start of the item that finishes q0 (the value is read
-      // in this item's epilogue)
-      if (tid == 0 && last_slab && q1 < U2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // the unit after q1, claimed during the item that finishes q0 (the value is read in this
+      // item's epilogue). NVFP4 claims in the K loop, at tile CT where the refills turn to the
+      // next item (its kernel then needs 179 instead of 256 VGPRs and no scratch: 2-5 us faster
+      // at M=16-64); the others at the loop's start (A-MXFP8 measured slower, 253 VGPRs).
+      auto claim_ahead = [&]() __attribute__((always_inline)) {
+        if (tid == 0 && last_slab && q1 < U2 && more) ahead = __hip_atomic_fetch_add(claim, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      };
+      constexpr int CT = ACT == DGM_ACT_NVFP4 ? TI - KT2 : -1;
+      if constexpr (CT < 0) claim_ahead();
       // ---- K loop over the ring: tile t is K-tile t % KT2 of block t / KT2; B operands are
       // read from LDS two ops ahead
       v4f acc[RB];
@@ -1797,6 +1815,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         };
         static_for<TI>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           constexpr int k = t % KT2;
           v8i bop = bq0;
           bq0 = bq1;
@@ -1835,6 +1854,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         for (int j = 0; j < 4; ++j) bn[j] = s.bst[0][lane][j];
         static_for<TI>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           constexpr int j = t / KT2, k = t % KT2;
           U4 bc[4];
 #pragma unroll
@@ -1861,6 +1881,7 @@ __global__ void __launch_bounds__(FT) k_megamoe(FusedParams p) {
         uint32_t bs0 = s.bsc[0][lane], bs1 = s.bsc[(1 % KT2) >> 2][lane];
         static_for<TI>([&](auto tc) {
           constexpr int t = decltype(tc)::value;
+          if constexpr (t == CT) claim_ahead();
           constexpr int j = t / KT2, k = t % KT2;
           const v8i bop = bq0;
           const uint32_t bsw = bs0;
