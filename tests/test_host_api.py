@@ -88,3 +88,25 @@ def test_reorder_fp4_nibbles_refuses_rows_of_partial_words():
     from hopper_megamoe_basedondeepgemm_amd import checkpoint
     with pytest.raises(AssertionError, match="4-byte words"):
         checkpoint.reorder_fp4_nibbles(torch.zeros((3, 6), dtype=torch.uint8), "ocp", "marlin")
+
+
+def test_route_to_token_multiply_is_exact_within_the_host_limits():
+    """The fused kernel maps a route to its token as (route * ceil(2^20 / topk)) >> 20 instead of
+    an integer division (dgm_fused.hip, div_small). Exact for every route below the per-call
+    route limit and every top-k the host accepts (topk <= 16, checked before any launch): the
+    product overshoots route / topk by less than 2^-10 < 1 / topk. Checked here for all pairs,
+    with the limits read from the sources so that raising one re-runs the check at the new
+    bound."""
+    import os
+    import re
+    root = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                        "hopper_megamoe_basedondeepgemm_amd", "csrc")
+    hpp = open(os.path.join(root, "dgm_fused.hpp")).read()
+    max_routes = int(re.search(r"FUSED_MAX_ROUTES\s*=\s*(\d+)", hpp).group(1))
+    src = open(os.path.join(root, "dgm_megamoe.hip")).read()
+    assert "topk <= 16" in src
+    r = np.arange(max_routes, dtype=np.uint64)
+    for d in range(1, 17):
+        m = (0x100000 + d - 1) // d
+        assert np.array_equal((r * np.uint64(m)) >> np.uint64(20), r // np.uint64(d)), d
+        assert int(r[-1]) * m < 2 ** 32          # (the kernel multiplies in 32 bits)
